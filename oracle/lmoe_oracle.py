@@ -1,0 +1,624 @@
+"""numpy restatement of the reference LatentMoE hot path -- TEST INFRASTRUCTURE.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline``
+leg may use this module, and only as the checker / the timed CPU baseline.
+The product package never imports it.
+
+Conventions
+-----------
+* bf16 tensors are carried as float32 arrays whose values are exactly
+  representable in bf16 (``bf16_round`` is round-to-nearest-even, the rounding
+  XLA applies on every ``astype(bfloat16)`` and after every bf16 op).
+* ``dtype`` arguments are the strings ``"f32"`` or ``"bf16"``.
+* Every function cites the reference ``file:line`` it restates; paths are
+  relative to the reference repository root.  Short aliases:
+    ref.py = 05_ragged_dot_on_tpu/kimi_k3_latent_moe_reference.py
+    rd.py  = 05_ragged_dot_on_tpu/kimi_k3_latent_moe_ragged_dot.py
+    deq.py = 05_ragged_dot_on_tpu/mxfp4_dequant.py
+    odq.py = 05_ragged_dot_on_tpu/mxfp4_online_dequant_matmul_pallas.py
+    gk.py  = 05_ragged_dot_on_tpu/own_gateup_situ_pallas_kernel.py
+
+Pinning (what checks each function against something other than itself) is
+listed in ``PINNING`` at the bottom of this file and exercised by
+``tests/test_oracle_*.py``.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import NamedTuple
+
+import numpy as np
+
+F32 = np.float32
+
+# ---------------------------------------------------------------------------
+# bf16 helpers
+# ---------------------------------------------------------------------------
+
+
+def bf16_round(x) -> np.ndarray:
+  """Round float32 values to the nearest bf16 (ties to even), returned as float32.
+
+  Same rounding as XLA's f32->bf16 convert, which the reference applies on every
+  ``.astype(jnp.bfloat16)`` (e.g. ref.py:293, ref.py:310, ref.py:630).
+  NaN stays NaN (quietened); overflow past bf16 max rounds to inf.
+  """
+  x = np.ascontiguousarray(x, dtype=F32)
+  u = x.view(np.uint32)
+  bias = ((u >> np.uint32(16)) & np.uint32(1)) + np.uint32(0x7FFF)
+  r = (u + bias) & np.uint32(0xFFFF0000)
+  nan = np.isnan(x)
+  if nan.any():
+    r = np.where(nan, (u | np.uint32(0x00400000)) & np.uint32(0xFFFF0000), r)
+  return r.astype(np.uint32).view(F32)
+
+
+def bf16_bits(x) -> np.ndarray:
+  """uint16 bit patterns of bf16-valued float32 data (rounds first)."""
+  return (bf16_round(x).view(np.uint32) >> np.uint32(16)).astype(np.uint16)
+
+
+def bits_to_f32(u16) -> np.ndarray:
+  """bf16 bit patterns (uint16 / int16) -> float32 values."""
+  u = np.asarray(u16).astype(np.uint16).astype(np.uint32) << np.uint32(16)
+  return u.view(F32)
+
+
+def cast(x, dtype: str) -> np.ndarray:
+  x = np.asarray(x, dtype=F32)
+  return bf16_round(x) if dtype == "bf16" else x
+
+
+def promote(a: str, b: str) -> str:
+  """JAX dtype promotion between bf16 and f32 (f32 wins)."""
+  return "f32" if "f32" in (a, b) else "bf16"
+
+
+def matmul(a, b, dtype: str) -> np.ndarray:
+  """``a @ b`` the way XLA-CPU computes it for ``dtype`` operands: float32
+  products and accumulation, one rounding of the result to ``dtype``."""
+  out = np.matmul(np.asarray(a, F32), np.asarray(b, F32), dtype=F32)
+  return cast(out, dtype)
+
+
+# ---------------------------------------------------------------------------
+# Elementwise math (float32 throughout, like XLA-CPU)
+# ---------------------------------------------------------------------------
+
+
+def sigmoid(x) -> np.ndarray:
+  """``jax.nn.sigmoid`` in float32: 1 / (1 + exp(-x))."""
+  x = np.asarray(x, F32)
+  with np.errstate(over="ignore"):
+    return (F32(1.0) / (F32(1.0) + np.exp(-x))).astype(F32)
+
+
+def softmax(x, axis=-1) -> np.ndarray:
+  """Row softmax in float32 (the official gate's softmax branch, reference
+  06_kimi_k3_golden_validation/generate_pytorch_golden.py:151-156)."""
+  x = np.asarray(x, F32)
+  m = np.max(x, axis=axis, keepdims=True)
+  e = np.exp(x - m)
+  return (e / np.sum(e, axis=axis, keepdims=True, dtype=F32)).astype(F32)
+
+
+def situ_and_mul(gate, up, beta: float, linear_beta: float, dtype: str) -> np.ndarray:
+  """Kimi SiTU-GLU, ref.py:296-310: compute in f32, cast back to ``dtype``.
+
+  situ_gate = beta*tanh(g/beta)*sigmoid(g); bounded_up = lb*tanh(u/lb).
+  """
+  g = np.asarray(gate, F32)
+  u = np.asarray(up, F32)
+  situ_gate = F32(beta) * np.tanh(g / F32(beta)) * sigmoid(g)
+  bounded_up = F32(linear_beta) * np.tanh(u / F32(linear_beta))
+  return cast(situ_gate * bounded_up, dtype)
+
+
+def rms_norm(x, scale, eps: float, dtype: str) -> np.ndarray:
+  """ref.py:286-293: f32 mean-square, x*rsqrt(var+eps), cast to input dtype,
+  then ``* scale`` in the input dtype."""
+  xf = np.asarray(x, F32)
+  var = np.mean(xf * xf, axis=-1, keepdims=True, dtype=F32)
+  normalized = xf * (F32(1.0) / np.sqrt(var + F32(eps)))
+  normalized = cast(normalized, dtype)
+  return cast(normalized * np.asarray(scale, F32), dtype)
+
+
+# ---------------------------------------------------------------------------
+# Router (a3)
+# ---------------------------------------------------------------------------
+
+
+def top_k(values, k: int) -> np.ndarray:
+  """``jax.lax.top_k`` index semantics: descending by value, equal values ordered
+  by ascending index (stable).  Returns int32 (T, k)."""
+  v = np.asarray(values, F32)
+  order = np.argsort(-v, axis=-1, kind="stable")[..., :k]
+  return order.astype(np.int32)
+
+
+class RouterOut(NamedTuple):
+  topk_idx: np.ndarray  # (T, k) int32, global expert ids
+  topk_weight: np.ndarray  # (T, k) f32 (or bf16-valued if cast)
+  scores: np.ndarray  # (T, E) f32, activation output (before bias)
+  scores_for_choice: np.ndarray  # (T, E) f32
+
+
+def router_from_logits(logits, bias, top_k_: int, renormalize: bool, scaling: float,
+                       act: str = "sigmoid", weight_dtype: str = "f32") -> RouterOut:
+  """Gate math of ref.py:347-361 (unsharded, weights stay f32) and
+  ref.py:601-631 (``_router_gate``: weights cast to the compute dtype at 630).
+
+  scores = act(logits); choice = scores + bias; idx = top_k(choice);
+  w = scores[idx]; if k>1 and renorm: w /= sum(w)+1e-20; w *= scaling.
+  The softmax branch follows the official gate
+  (06_kimi_k3_golden_validation/generate_pytorch_golden.py:151-156).
+  """
+  logits = np.asarray(logits, F32)
+  if act == "sigmoid":
+    scores = sigmoid(logits)
+  elif act == "softmax":
+    scores = softmax(logits, axis=-1)
+  else:
+    raise NotImplementedError(act)
+  bias = np.zeros(logits.shape[-1], F32) if bias is None else np.asarray(bias, F32)
+  choice = (scores + bias[None, :]).astype(F32)
+  idx = top_k(choice, top_k_)
+  w = np.take_along_axis(scores, idx.astype(np.int64), axis=-1).astype(F32)
+  if top_k_ > 1 and renormalize:
+    denom = np.sum(w, axis=-1, keepdims=True, dtype=F32) + F32(1e-20)
+    w = (w / denom).astype(F32)
+  w = (w * F32(scaling)).astype(F32)
+  return RouterOut(idx, cast(w, weight_dtype), scores, choice)
+
+
+def router_gate(hidden, router_weight, bias, config, act: str = "sigmoid",
+                weight_dtype: str = "f32") -> tuple[RouterOut, np.ndarray]:
+  """``_router_gate`` ref.py:601-631 including the f32 logits matmul
+  (ref.py:620): logits = f32(hidden) @ f32(router_weight)."""
+  logits = matmul(hidden, router_weight, "f32")
+  r = router_from_logits(logits, bias, config.top_k, config.moe_renormalize,
+                         config.routed_scaling_factor, act, weight_dtype)
+  return r, logits
+
+
+# ---------------------------------------------------------------------------
+# Dispatch (a5, a6, a7)
+# ---------------------------------------------------------------------------
+
+MOSAIC_TILE_SIZE = 128  # ref.py:149
+
+
+def round_up_to_tile(value: int, tile_size: int = MOSAIC_TILE_SIZE) -> int:
+  """ref.py:152-153."""
+  return -(-value // tile_size) * tile_size
+
+
+def compute_m_padded(num_tokens: int, top_k_: int, num_experts: int, local_num_experts: int,
+                     capacity_factor: float = 2.0, tile_size: int = MOSAIC_TILE_SIZE) -> int:
+  """ref.py:825-826 (the jittable form, ``math.ceil`` on the Python float)."""
+  expected_total = num_tokens * top_k_ * local_num_experts / num_experts
+  return round_up_to_tile(math.ceil(expected_total * capacity_factor), tile_size)
+
+
+class ShardDispatch(NamedTuple):
+  sorted_tokens: np.ndarray  # (m_padded, lat)
+  group_sizes: np.ndarray  # (L+1,) int32
+  valid_mask: np.ndarray  # (m_padded,) bool
+  per_expert_counts: np.ndarray  # (L,) int32
+  padded_token_idx: np.ndarray  # (m_padded,) int32, -1 on padding rows
+  padded_combine_weight: np.ndarray  # (m_padded,) weight dtype, 0 on padding rows
+
+
+def filter_and_pad_to_shard(topk_idx, topk_weight, x, top_k_: int, num_experts: int,
+                            local_expert_start: int, local_num_experts: int,
+                            capacity_factor: float = 2.0, tile_size: int = MOSAIC_TILE_SIZE,
+                            m_padded: int | None = None) -> ShardDispatch:
+  """Eager ``filter_and_pad_to_shard``, ref.py:658-751.
+
+  Filter slots to [start, start+L), stable argsort by local id, truncate to
+  ``m_padded`` (drop the tail), bincount, gather x rows, pad with zero rows /
+  token -1 / weight 0.  Written filter-first exactly like the eager reference
+  so that the jittable restatement below is checked against an independent
+  formulation.
+  """
+  topk_idx = np.asarray(topk_idx)
+  num_tokens = topk_idx.shape[0]
+  flat_ids = topk_idx.reshape(-1).astype(np.int64)
+  token_of_slot = np.arange(num_tokens * top_k_) // top_k_
+  flat_w = np.asarray(topk_weight, F32).reshape(-1)
+  local_end = local_expert_start + local_num_experts
+  in_shard = (flat_ids >= local_expert_start) & (flat_ids < local_end)
+  kept_local = flat_ids[in_shard] - local_expert_start
+  kept_tok = token_of_slot[in_shard]
+  kept_w = flat_w[in_shard]
+  order = np.argsort(kept_local, kind="stable")
+  s_local, s_tok, s_w = kept_local[order], kept_tok[order], kept_w[order]
+  if m_padded is None:
+    m_padded = compute_m_padded(num_tokens, top_k_, num_experts, local_num_experts,
+                                capacity_factor, tile_size)
+  keep = min(len(s_local), m_padded)
+  counts = np.bincount(s_local[:keep], minlength=local_num_experts).astype(np.int32)
+  pad = m_padded - keep
+  group_sizes = np.concatenate([counts, np.array([pad], np.int32)]).astype(np.int32)
+  x = np.asarray(x, F32)
+  sorted_tokens = np.zeros((m_padded, x.shape[-1]), F32)
+  sorted_tokens[:keep] = x[s_tok[:keep]]
+  valid = np.zeros(m_padded, bool)
+  valid[:keep] = True
+  tok = np.full(m_padded, -1, np.int32)
+  tok[:keep] = s_tok[:keep]
+  w = np.zeros(m_padded, F32)
+  w[:keep] = s_w[:keep]
+  return ShardDispatch(sorted_tokens, group_sizes, valid, counts, tok, w)
+
+
+def filter_and_pad_to_shard_jittable(topk_idx, topk_weight, x, top_k_: int, num_experts: int,
+                                     local_expert_start: int, local_num_experts: int,
+                                     capacity_factor: float = 2.0,
+                                     tile_size: int = MOSAIC_TILE_SIZE,
+                                     m_padded: int | None = None,
+                                     return_slot_pos: bool = False):
+  """Jittable dispatch, ref.py:754-877: sentinel key L for out-of-shard slots,
+  pad keys to m_padded, stable argsort, take the first m_padded.
+
+  With ``return_slot_pos`` also returns the inverse permutation ``slot_pos``
+  (T*k,) int32: the sorted row of each (token, slot), or -1 when the slot is
+  out of shard or truncated (not a reference output; the GPU combine uses it).
+  """
+  topk_idx = np.asarray(topk_idx)
+  num_tokens = topk_idx.shape[0]
+  total = num_tokens * top_k_
+  flat_ids = topk_idx.reshape(-1).astype(np.int64)
+  token_of_slot = np.arange(total) // top_k_
+  flat_w = np.asarray(topk_weight, F32).reshape(-1)
+  local_end = local_expert_start + local_num_experts
+  in_shard = (flat_ids >= local_expert_start) & (flat_ids < local_end)
+  key = np.where(in_shard, flat_ids - local_expert_start, local_num_experts)
+  if m_padded is None:
+    m_padded = compute_m_padded(num_tokens, top_k_, num_experts, local_num_experts,
+                                capacity_factor, tile_size)
+  pad_amount = max(0, m_padded - total)
+  if pad_amount:
+    key = np.concatenate([key, np.full(pad_amount, local_num_experts)])
+    token_of_slot = np.concatenate([token_of_slot, np.zeros(pad_amount, np.int64)])
+    flat_w = np.concatenate([flat_w, np.zeros(pad_amount, F32)])
+  full_order = np.argsort(key, kind="stable")
+  order = full_order[:m_padded]
+  sorted_key = key[order]
+  valid = sorted_key < local_num_experts
+  tok_all = token_of_slot[order]
+  tok = np.where(valid, tok_all, -1).astype(np.int32)
+  w = np.where(valid, flat_w[order], F32(0)).astype(F32)
+  counts = np.bincount(sorted_key[valid], minlength=local_num_experts).astype(np.int32)
+  pad = m_padded - int(counts.sum())
+  group_sizes = np.concatenate([counts, np.array([pad], np.int32)]).astype(np.int32)
+  x = np.asarray(x, F32)
+  sorted_tokens = np.where(valid[:, None], x[tok_all], F32(0)).astype(F32)
+  out = ShardDispatch(sorted_tokens, group_sizes, valid, counts, tok, w)
+  if not return_slot_pos:
+    return out
+  slot_pos = np.full(total, -1, np.int32)
+  rows = np.nonzero(valid)[0]
+  slot_pos[order[rows]] = rows.astype(np.int32)
+  return out, slot_pos
+
+
+def unsharded_dispatch(topk_idx, x, num_experts: int):
+  """Unsharded dispatch in ``latent_moe_forward``, ref.py:369-379: stable
+  argsort of the flat expert ids, gather, bincount."""
+  topk_idx = np.asarray(topk_idx)
+  t, k = topk_idx.shape
+  flat = topk_idx.reshape(-1).astype(np.int64)
+  order = np.argsort(flat, kind="stable")
+  token_of_slot = np.arange(t * k) // k
+  sorted_token_idx = token_of_slot[order]
+  sorted_tokens = np.asarray(x, F32)[sorted_token_idx]
+  group_sizes = np.bincount(flat, minlength=num_experts).astype(np.int32)
+  return order.astype(np.int32), sorted_tokens, group_sizes
+
+
+# ---------------------------------------------------------------------------
+# Grouped GEMM (a9-a12)
+# ---------------------------------------------------------------------------
+
+
+def ragged_dot(lhs, rhs, group_sizes, dtype: str) -> np.ndarray:
+  """Per-group textbook matmul (the semantics of ``tokamax.ragged_dot`` as used at
+  rd.py:358-369): rows [cum_g, cum_g+n_g) of lhs times rhs[g]; rows past
+  sum(group_sizes) are zero; output dtype = lhs dtype."""
+  lhs = np.asarray(lhs, F32)
+  rhs = np.asarray(rhs, F32)
+  gs = np.asarray(group_sizes).astype(np.int64)
+  out = np.zeros((lhs.shape[0], rhs.shape[-1]), F32)
+  start = 0
+  for g, n in enumerate(gs):
+    n = int(n)
+    if n > 0:
+      out[start:start + n] = np.matmul(lhs[start:start + n], rhs[g], dtype=F32)
+    start += n
+  return cast(out, dtype)
+
+
+def prefuse_gateup_weights(expert_gate, expert_up) -> np.ndarray:
+  """rd.py:610-641: plain concatenation [gate | up] on the N axis."""
+  return np.concatenate([np.asarray(expert_gate, F32), np.asarray(expert_up, F32)], axis=-1)
+
+
+def ragged_dot_gateup_situ(lhs, rhs_gu, group_sizes, beta: float, linear_beta: float,
+                           dtype: str, round_before_act: bool = True) -> np.ndarray:
+  """Fused gate/up + SiTU-GLU (rd.py:644-723; epilogue convention gk.py:114-125):
+  gate/up accumulators rounded to ``dtype`` before the f32 SiTU, output ``dtype``."""
+  n2 = np.asarray(rhs_gu).shape[-1]
+  inter = n2 // 2
+  acc = ragged_dot(lhs, rhs_gu, group_sizes, "f32")
+  g, u = acc[:, :inter], acc[:, inter:]
+  if round_before_act:
+    g, u = cast(g, dtype), cast(u, dtype)
+  return situ_and_mul(g, u, beta, linear_beta, dtype)
+
+
+def situ_glu_mlp(x, w_gate, w_up, w_down, beta, linear_beta, dtype: str) -> np.ndarray:
+  """ref.py:313-327: situ_and_mul(x@Wg, x@Wu) @ Wd, each matmul rounded to dtype."""
+  g = matmul(x, w_gate, dtype)
+  u = matmul(x, w_up, dtype)
+  return matmul(situ_and_mul(g, u, beta, linear_beta, dtype), w_down, dtype)
+
+
+def local_shard_expert_ffn(sorted_tokens, expert_gate, expert_up, expert_down, group_sizes,
+                           config, dtype: str) -> np.ndarray:
+  """Naive per-expert loop, ref.py:1486-1528 (the padding bucket is just the
+  last group).  Rows past sum(group_sizes) are returned as zero."""
+  sorted_tokens = np.asarray(sorted_tokens, F32)
+  out = np.zeros((sorted_tokens.shape[0], np.asarray(expert_down).shape[-1]), F32)
+  start = 0
+  for e, n in enumerate(np.asarray(group_sizes).astype(np.int64)):
+    n = int(n)
+    if n > 0:
+      out[start:start + n] = situ_glu_mlp(
+          sorted_tokens[start:start + n], expert_gate[e], expert_up[e], expert_down[e],
+          config.activation_situ_beta, config.activation_situ_linear_beta, dtype)
+    start += n
+  return out
+
+
+# ---------------------------------------------------------------------------
+# Combine (a13)
+# ---------------------------------------------------------------------------
+
+
+def combine_shard_contribution(routed_out, shard_out, padded_token_idx, padded_combine_weight,
+                               out_dtype: str, shard_dtype: str, weight_dtype: str) -> np.ndarray:
+  """``_combine_shard_contribution``, ref.py:1113-1141:
+  routed_out.at[idx].add((shard_out * w[:, None]).astype(routed_out.dtype)).
+
+  Scatter-add semantics restated exactly: the product is formed in the
+  promoted dtype of (shard_out, w) and cast to the output dtype; updates are
+  applied one row at a time in ascending row order, each add rounded to the
+  output dtype; negative indices wrap (numpy/JAX), out-of-range rows drop.
+  """
+  routed = np.array(routed_out, dtype=F32, copy=True)
+  t = routed.shape[0]
+  prod_dtype = promote(shard_dtype, weight_dtype)
+  weighted = cast(np.asarray(shard_out, F32) * np.asarray(padded_combine_weight, F32)[:, None],
+                  prod_dtype)
+  weighted = cast(weighted, out_dtype)
+  idx = np.asarray(padded_token_idx).astype(np.int64)
+  idx = np.where(idx < 0, idx + t, idx)
+  ok = (idx >= 0) & (idx < t)
+  rows = np.nonzero(ok)[0]
+  tok = idx[rows]
+  # occurrence rank of each row among the rows of the same token (ascending row)
+  o = np.lexsort((rows, tok))
+  rows, tok = rows[o], tok[o]
+  first = np.r_[True, tok[1:] != tok[:-1]]
+  grp_start = np.maximum.accumulate(np.where(first, np.arange(len(tok)), 0))
+  rank = np.arange(len(tok)) - grp_start
+  for r in range(int(rank.max()) + 1 if len(rank) else 0):
+    sel = rank == r
+    tt, rr = tok[sel], rows[sel]
+    routed[tt] = cast(routed[tt] + weighted[rr], out_dtype)
+  return routed
+
+
+def unsharded_combine(outs, order, topk_weight, num_tokens: int, top_k_: int,
+                      compute_dtype: str) -> np.ndarray:
+  """ref.py:413-416: inverse permutation, f32 weighted sum over the k slots,
+  one cast to the compute dtype."""
+  outs = np.asarray(outs, F32)
+  unsorted = np.zeros_like(outs)
+  unsorted[np.asarray(order)] = outs
+  unsorted = unsorted.reshape(num_tokens, top_k_, -1)
+  w = np.asarray(topk_weight, F32)
+  acc = np.zeros((num_tokens, outs.shape[-1]), F32)
+  for j in range(top_k_):
+    acc = (acc + unsorted[:, j, :] * w[:, j:j + 1]).astype(F32)
+  return cast(acc, compute_dtype), unsorted
+
+
+# ---------------------------------------------------------------------------
+# Full forwards (a15, a16)
+# ---------------------------------------------------------------------------
+
+
+def latent_moe_forward(hidden, w: dict, config, dtype: str, act: str = "sigmoid"):
+  """``latent_moe_forward``, ref.py:330-435, with the 18 intermediates of
+  06_kimi_k3_golden_validation/test_jax_reference_against_pytorch_golden.py:173-275.
+
+  ``w`` holds reference-layout (in, out) arrays with keys router_weight,
+  e_score_correction_bias, down_proj, up_proj, expert_gate, expert_up,
+  expert_down, norm_scale, shared_gate, shared_up, shared_down.
+  Returns (final_output, intermediates).
+  """
+  hidden = cast(hidden, dtype)
+  inter: dict[str, np.ndarray] = {}
+  t = hidden.shape[0]
+  k = config.top_k
+  r, logits = router_gate(hidden, w["router_weight"], w["e_score_correction_bias"], config,
+                          act=act, weight_dtype="f32")
+  inter["router_logits"] = logits
+  inter["router_scores_before_bias"] = r.scores
+  inter["router_scores_for_choice"] = r.scores_for_choice
+  inter["topk_indices"] = r.topk_idx
+  inter["topk_weights"] = r.topk_weight
+  x = matmul(hidden, w["down_proj"], dtype)
+  inter["latent_projection"] = x
+  order, sorted_tokens, group_sizes = unsharded_dispatch(r.topk_idx, x, config.num_experts)
+  inter["sorted_token_indices"] = order
+  inter["group_sizes"] = group_sizes
+  lat = config.latent_size
+  inter_sz = config.intermediate_size
+  gate_o = np.zeros((t * k, inter_sz), F32)
+  up_o = np.zeros((t * k, inter_sz), F32)
+  situ_o = np.zeros((t * k, inter_sz), F32)
+  down_o = np.zeros((t * k, lat), F32)
+  start = 0
+  for e in range(config.num_experts):
+    n = int(group_sizes[e])
+    if n:
+      chunk = sorted_tokens[start:start + n]
+      g = matmul(chunk, w["expert_gate"][e], dtype)
+      u = matmul(chunk, w["expert_up"][e], dtype)
+      s = situ_and_mul(g, u, config.activation_situ_beta, config.activation_situ_linear_beta, dtype)
+      d = matmul(s, w["expert_down"][e], dtype)
+      gate_o[start:start + n], up_o[start:start + n] = g, u
+      situ_o[start:start + n], down_o[start:start + n] = s, d
+    start += n
+  inter["expert_gate_output"] = gate_o
+  inter["expert_up_output"] = up_o
+  inter["situ_output"] = situ_o
+  inter["expert_down_output"] = down_o
+  routed, unsorted = unsharded_combine(down_o, order, r.topk_weight, t, k, dtype)
+  inter["routed_output_before_combine"] = unsorted.reshape(t * k, lat)
+  inter["routed_output_after_combine"] = routed
+  normed = rms_norm(routed, w["norm_scale"], config.rms_norm_eps, dtype)
+  inter["normalized_output"] = normed
+  up = matmul(normed, w["up_proj"], dtype)
+  inter["up_projection_output"] = up
+  shared = situ_glu_mlp(hidden, w["shared_gate"], w["shared_up"], w["shared_down"],
+                        config.activation_situ_beta, config.activation_situ_linear_beta, dtype)
+  inter["shared_expert_output"] = shared
+  final = cast(up + shared, dtype)
+  inter["final_output"] = final
+  return final, inter
+
+
+def single_shard_forward(hidden, w: dict, shard_gate, shard_up, shard_down, config, dtype: str,
+                         local_expert_start: int, local_num_experts: int,
+                         capacity_factor: float = 2.0, act: str = "sigmoid",
+                         include_shared: bool = True):
+  """``latent_moe_forward_ragged_dot_single_shard_jittable``, rd.py:1035-1137,
+  with the naive per-expert FFN as the ragged_dot oracle.  ``shard_*`` have
+  L+1 experts (the last is the padding bucket).  Returns (final, stages)."""
+  hidden = cast(hidden, dtype)
+  stages: dict[str, np.ndarray] = {}
+  x = matmul(hidden, w["down_proj"], dtype)
+  stages["x"] = x
+  r, logits = router_gate(hidden, w["router_weight"], w["e_score_correction_bias"], config,
+                          act=act, weight_dtype=dtype)
+  stages["router_logits"] = logits
+  stages["topk_idx"] = r.topk_idx
+  stages["topk_weight"] = r.topk_weight
+  d = filter_and_pad_to_shard_jittable(r.topk_idx, r.topk_weight, x, config.top_k,
+                                       config.num_experts, local_expert_start,
+                                       local_num_experts, capacity_factor)
+  stages["dispatch"] = d
+  shard_out = local_shard_expert_ffn(d.sorted_tokens, shard_gate, shard_up, shard_down,
+                                     d.group_sizes, config, dtype)
+  stages["shard_out"] = shard_out
+  routed = np.zeros((hidden.shape[0], config.latent_size), F32)
+  routed = combine_shard_contribution(routed, shard_out, d.padded_token_idx,
+                                      d.padded_combine_weight, dtype, dtype, dtype)
+  stages["routed_out"] = routed
+  normed = rms_norm(routed, w["norm_scale"], config.rms_norm_eps, dtype)
+  stages["normed"] = normed
+  up = matmul(normed, w["up_proj"], dtype)
+  stages["up"] = up
+  if include_shared:
+    shared = situ_glu_mlp(hidden, w["shared_gate"], w["shared_up"], w["shared_down"],
+                          config.activation_situ_beta, config.activation_situ_linear_beta, dtype)
+    stages["shared"] = shared
+    final = cast(up + shared, dtype)
+  else:
+    final = up
+  return final, stages
+
+
+# ---------------------------------------------------------------------------
+# MXFP4 (a17, a18)
+# ---------------------------------------------------------------------------
+
+FP4_E2M1_TABLE = np.array([0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0], F32)  # deq.py:26
+
+
+def e8m0_to_f32(scale_u8) -> np.ndarray:
+  """E8M0 byte s -> 2^(s-127) as float32, deq.py:63-64 (exact for every byte:
+  byte 0 is the f32 denormal 2^-127, byte 255 overflows to inf)."""
+  s = np.asarray(scale_u8).astype(np.int64)
+  with np.errstate(over="ignore"):
+    return np.ldexp(np.float64(1.0), s - 127).astype(F32)
+
+
+def fp4_e2m1_to_f32(nibble) -> np.ndarray:
+  """deq.py:52-54: sign = bit 3, |v| = table[n & 7]; nibble 8 is -0.0."""
+  n = np.asarray(nibble).astype(np.int64)
+  mag = FP4_E2M1_TABLE[n & 7]
+  return (mag * np.where((n & 8) != 0, F32(-1.0), F32(1.0))).astype(F32)
+
+
+def dequantize_mxfp4(weight_packed, weight_scale) -> np.ndarray:
+  """``dequantize_mxfp4``, deq.py:29-67.  packed (N, K/2) u8 (low nibble =
+  element 2j, high = 2j+1), scale (N, K/gs) u8 -> (N, K) float32."""
+  p = np.asarray(weight_packed, np.uint8)
+  n_out, kh = p.shape
+  k = kh * 2
+  s = np.asarray(weight_scale, np.uint8)
+  gs = k // s.shape[1]
+  combined = np.stack([p & 0x0F, p >> 4], axis=-1).reshape(n_out, k)
+  values = fp4_e2m1_to_f32(combined)
+  scale = np.repeat(e8m0_to_f32(s), gs, axis=1)
+  with np.errstate(invalid="ignore", over="ignore"):
+    return (values * scale).astype(F32)
+
+
+def mxfp4_matmul(x, weight_packed, weight_scale, dtype: str = "bf16") -> np.ndarray:
+  """y = x @ dequant(W)^T (odq.py:1-36 orientation), bf16 weights exact,
+  f32 accumulation, one rounding to ``dtype``."""
+  wd = bf16_round(dequantize_mxfp4(weight_packed, weight_scale))
+  return matmul(x, wd.T, dtype)
+
+
+def ragged_dot_mxfp4(lhs, w_packed, w_scale, group_sizes, dtype: str = "bf16",
+                     situ: tuple[float, float] | None = None) -> np.ndarray:
+  """Grouped x @ deq(W_g)^T with W_g in checkpoint (N, K/2) layout; with
+  ``situ=(beta, lb)`` the N axis is [gate | up] and the SiTU-GLU epilogue
+  (rounded to ``dtype`` first) is applied."""
+  lhs = np.asarray(lhs, F32)
+  gs = np.asarray(group_sizes).astype(np.int64)
+  n_out = np.asarray(w_packed).shape[1]
+  acc = np.zeros((lhs.shape[0], n_out), F32)
+  start = 0
+  for g, n in enumerate(gs):
+    n = int(n)
+    if n:
+      wd = bf16_round(dequantize_mxfp4(w_packed[g], w_scale[g]))
+      acc[start:start + n] = np.matmul(lhs[start:start + n], wd.T, dtype=F32)
+    start += n
+  if situ is None:
+    return cast(acc, dtype)
+  inter = n_out // 2
+  g_, u_ = cast(acc[:, :inter], dtype), cast(acc[:, inter:], dtype)
+  return situ_and_mul(g_, u_, situ[0], situ[1], dtype)
+
+
+PINNING = {
+    "bf16_round": "closed form: exhaustive bf16 neighbours, torch.bfloat16 cast (tests/test_oracle_basics.py)",
+    "router_from_logits / router_gate": "golden bundles router_* / topk_* (6 stages), softmax closed form",
+    "filter_and_pad_to_shard(_jittable)": "literal KATs from test_sharded_routing_local.py, brute force, eager==jittable",
+    "unsharded_dispatch": "golden group_sizes + canonical sorted_token_indices",
+    "ragged_dot / situ / ffn": "golden expert_* / situ_output stages, brute-force per-row dot",
+    "combine_shard_contribution": "golden routed_output_after_combine via sharded==unsharded, literal padding KAT",
+    "rms_norm / forward": "golden normalized/up_projection/shared/final stages",
+    "dequantize_mxfp4": "closed form OCP MX E2M1/E8M0 table, exhaustive 256 bytes x edge scales",
+}
