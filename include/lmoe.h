@@ -1,0 +1,184 @@
+/*
+ * lmoe.h -- C-ABI of liblmoe.so, the MI355X (gfx950) LatentMoE expert hot path.
+ *
+ * Every pointer argument is a DEVICE pointer owned by the caller (in the Python
+ * host layer: torch tensors), except where marked "host".  Every call is
+ * stream-ordered on `stream` (a hipStream_t passed as void*; NULL = the null
+ * stream), allocates nothing, and returns an int status: LMOE_OK (0) or a
+ * negative LMOE_ERR_* code, with a message retrievable from lmoe_last_error()
+ * (thread-local).  Calls hold no global state and are safe to issue from
+ * several host threads on different streams.
+ *
+ * Data types: bf16 is stored as its 16-bit pattern (torch.bfloat16 layout),
+ * f32 as IEEE float.  Index arrays are int32.  Booleans are one byte.
+ *
+ * The reference interface each entry point replaces is cited as file:line
+ * relative to the reference repository (Yog-Sothothftgn/tokamax-tpu-kernel-lab),
+ * with these aliases:
+ *   ref.py = 05_ragged_dot_on_tpu/kimi_k3_latent_moe_reference.py
+ *   rd.py  = 05_ragged_dot_on_tpu/kimi_k3_latent_moe_ragged_dot.py
+ *   deq.py = 05_ragged_dot_on_tpu/mxfp4_dequant.py
+ *   odq.py = 05_ragged_dot_on_tpu/mxfp4_online_dequant_matmul_pallas.py
+ *   gk.py  = 05_ragged_dot_on_tpu/own_gateup_situ_pallas_kernel.py
+ */
+#ifndef LMOE_H_
+#define LMOE_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ---------------------------------------------------------*/
+#define LMOE_OK 0
+#define LMOE_ERR_INVALID -1     /* bad shape / argument (Python: ValueError) */
+#define LMOE_ERR_UNSUPPORTED -2 /* dtype / layout / size not implemented (NotImplementedError) */
+#define LMOE_ERR_HIP -3         /* HIP runtime error */
+#define LMOE_ERR_WORKSPACE -4   /* workspace missing or too small */
+
+/* ---- dtypes and enums -----------------------------------------------------*/
+#define LMOE_F32 0
+#define LMOE_BF16 1
+
+#define LMOE_RHS_GKN 0 /* rhs[g][k][n], n contiguous: the reference layout (x @ W) */
+#define LMOE_RHS_GNK 1 /* rhs[g][n][k], k contiguous: prepared / checkpoint layout */
+
+#define LMOE_ACT_SIGMOID 0
+#define LMOE_ACT_SOFTMAX 1
+
+#define LMOE_EPI_NONE 0
+#define LMOE_EPI_SITU 1 /* rhs N axis is [gate | up]; out = SiTU-GLU(gate, up), width N/2 */
+
+#define LMOE_MXFP4_LDS_DEQUANT 0 /* dequantise weight tiles to bf16 in LDS, bf16 MFMA */
+#define LMOE_MXFP4_SCALED_MFMA 1 /* native v_mfma_scale_f32_*_f8f6f4 (activations to MXFP8) */
+
+#define LMOE_COMBINE_SCATTER_ADD 0 /* sharded: sequential adds rounded to out dtype (ref.py:1113-1141) */
+#define LMOE_COMBINE_SLOT_SUM 1    /* unsharded: f32 sum over slots, one cast (ref.py:413-416) */
+
+/* ---- library ----------------------------------------------------------------*/
+const char* lmoe_last_error(void); /* host string, valid until the next call on this thread */
+int lmoe_version(void);
+int lmoe_device_arch_ok(void); /* 1 if device 0 is gfx950, else 0 (host-side query) */
+
+/* ---- a9: grouped GEMM ----------------------------------------------------------
+ * Replaces tokamax.ragged_dot(lhs, rhs, group_sizes) (call sites rd.py:358-369,
+ * rd.py:604-607; semantics in SURVEY a9): rows [cum_g, cum_g + n_g) of lhs times
+ * rhs[g]; rows past sum(group_sizes) are written as zero.  lhs (M, K) and out
+ * (M, N) row-major; out dtype may differ from lhs dtype (f32 out = the logits
+ * GEMM of ref.py:620).  group_sizes (G,) int32 is read on the device only.
+ * `zero_group` >= 0 names one group whose rows are written as zero without
+ * reading its weights (the trailing padding bucket, whose input rows are zero:
+ * ref.py:1497-1500); pass -1 to compute every group.
+ * bf16: K % 8 == 0, N % 8 == 0, 16-byte aligned lhs/rhs; f32: any shape.
+ */
+int lmoe_ragged_dot(const void* lhs, int lhs_dtype, const void* rhs, int rhs_layout,
+                    const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                    int zero_group, void* out, int out_dtype, void* stream);
+
+/* ---- a12: fused gate/up + SiTU-GLU epilogue ------------------------------------
+ * Replaces PallasMosaicTpuV2RaggedDot()(lhs, rhs_gu, group_sizes=...,
+ * fuse_gateup_activation="situ:<beta>:<beta_lin>") (rd.py:713-720) over the
+ * prefused [gate | up] weight of rd.py:610-641 (rhs_gu: (G, K, 2I) for GKN,
+ * (G, 2I, K) for GNK).  out (M, I) = SiTU(gate, up) with the epilogue of
+ * gk.py:114-125: accumulators rounded to bf16 first when round_before_act != 0.
+ * bf16 only.
+ */
+int lmoe_ragged_dot_gateup_situ(const void* lhs, const void* rhs_gu, int rhs_layout,
+                                const int32_t* group_sizes, int64_t M, int64_t K, int64_t I,
+                                int64_t G, int zero_group, float beta, float beta_lin,
+                                int round_before_act, void* out, void* stream);
+
+/* ---- a17: MXFP4 dequantisation ---------------------------------------------------
+ * Replaces dequantize_mxfp4(weight_packed, weight_scale) (deq.py:29-67):
+ * packed (N, K/2) u8 (low nibble = element 2j), scale (N, K/gs) u8 E8M0 ->
+ * out (N, K) in out_dtype (f32 or bf16), bit-exact (E2M1 * 2^(s-127)).
+ * Batched over `batch` independent matrices laid out back to back.
+ */
+int lmoe_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, int64_t batch, int64_t N,
+                       int64_t K, int64_t group_size, void* out, int out_dtype, void* stream);
+
+/* ---- a18 (+a12): grouped GEMM on MXFP4 weights ------------------------------------
+ * out = lhs @ deq(W_g)^T per group (orientation of odq.py:1-36 / odq.py:150-157,
+ * checkpoint layout W_g (N, K/2) u8 + (N, K/32) u8, group size 32).  With
+ * epilogue LMOE_EPI_SITU the N axis is [gate | up] and out is (M, N/2).
+ * lhs bf16 (M, K), out bf16.  mode: LMOE_MXFP4_LDS_DEQUANT or
+ * LMOE_MXFP4_SCALED_MFMA.
+ */
+int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_t* w_scale,
+                          const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                          int zero_group, int mode, int epilogue, float beta, float beta_lin,
+                          void* out, void* stream);
+
+/* ---- a3: router top-k --------------------------------------------------------------
+ * Replaces the gate math of _router_gate (ref.py:601-631) / latent_moe_forward
+ * step 1 (ref.py:347-361) given f32 logits (T, E): scores = act(logits);
+ * idx = top_k(scores + bias) (descending, ties -> lower index); w = scores[idx];
+ * renormalise when renorm != 0 and k > 1; w *= scale; w stored as
+ * weight_dtype.  bias may be NULL (zeros).  scores_out (T, E) f32 is optional.
+ * E <= 4096, k <= 64, k <= E.
+ */
+int lmoe_router_topk(const float* logits, const float* bias, int64_t T, int64_t E, int64_t k,
+                     int act, int renorm, float scale, int weight_dtype, int32_t* topk_idx,
+                     void* topk_w, float* scores_out, void* stream);
+
+/* ---- a7: local-shard dispatch ------------------------------------------------------
+ * Replaces filter_and_pad_to_shard_jittable (ref.py:754-877), bit-identical to
+ * the eager filter_and_pad_to_shard (ref.py:658-751): slots whose expert is in
+ * [local_start, local_start + L) are stable-sorted by local id, truncated to
+ * m_padded, and the x rows gathered.  Outputs (all device):
+ *   sorted_tokens (m_padded, lat) x_dtype, zero on padding rows
+ *   group_sizes (L+1,) int32 [counts..., m_padded - sum]
+ *   valid (m_padded,) u8, per_expert_counts (L,) int32
+ *   padded_token_idx (m_padded,) int32 (-1 on padding), padded_w (m_padded,) w_dtype
+ *   slot_pos (T*k,) int32 or NULL: sorted row of each (token, slot), -1 if not kept
+ * Workspace: lmoe_dispatch_workspace_size(T, k, L) bytes, no initialisation needed.
+ */
+int64_t lmoe_dispatch_workspace_size(int64_t T, int64_t k, int64_t L);
+int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
+                        int x_dtype, int64_t T, int64_t k, int64_t lat, int64_t local_start,
+                        int64_t L, int64_t m_padded, void* sorted_tokens, int32_t* group_sizes,
+                        uint8_t* valid, int32_t* per_expert_counts, int32_t* padded_token_idx,
+                        void* padded_w, int32_t* slot_pos, void* workspace,
+                        int64_t workspace_size, void* stream);
+
+/* ---- a13: combine -----------------------------------------------------------------
+ * lmoe_combine_scatter_add replaces _combine_shard_contribution (ref.py:1113-1141):
+ * routed_out.at[idx].add((shard_out * w[:, None]).astype(routed_out.dtype)),
+ * in place on routed_out (T, lat).  Deterministic: each token's rows are added
+ * in ascending row order, each add rounded to out_dtype (the scatter order of
+ * the reference).  idx -1 rows (padding, weight 0) are skipped, other indices
+ * outside [0, T) are dropped.  Workspace: lmoe_combine_workspace_size(m, T).
+ *
+ * lmoe_combine_slots is the same combine driven by the dispatch's slot_pos
+ * (no sort needed): mode LMOE_COMBINE_SCATTER_ADD reproduces
+ * _combine_shard_contribution (weights padded_w[row]); mode
+ * LMOE_COMBINE_SLOT_SUM reproduces the unsharded f32 weighted sum of
+ * ref.py:413-416 (weights topk_w[t, j], f32), writing routed_out.
+ */
+int64_t lmoe_combine_workspace_size(int64_t m, int64_t T);
+int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype, const int32_t* padded_token_idx,
+                             const void* padded_w, int w_dtype, int64_t m, int64_t lat, int64_t T,
+                             void* routed_out, int out_dtype, void* workspace,
+                             int64_t workspace_size, void* stream);
+int lmoe_combine_slots(const void* shard_out, int shard_dtype, const int32_t* slot_pos,
+                       const void* w, int w_dtype, int64_t T, int64_t k, int64_t lat, int mode,
+                       void* routed_out, int out_dtype, void* stream);
+
+/* ---- a14 / a10: adjacent elementwise stages -----------------------------------------
+ * lmoe_rms_norm: _rms_norm (ref.py:286-293): f32 mean square, x*rsqrt(var+eps)
+ *   cast to dtype, then * scale in dtype.  x, out (rows, n); scale (n,).
+ * lmoe_situ_and_mul: _situ_and_mul (ref.py:296-310) on separate gate/up (rows, n).
+ * lmoe_add: out = cast(a + b) elementwise (the residual add of ref.py:435).
+ */
+int lmoe_rms_norm(const void* x, const void* scale, int64_t rows, int64_t n, float eps, int dtype,
+                  void* out, void* stream);
+int lmoe_situ_and_mul(const void* gate, const void* up, int64_t count, float beta, float beta_lin,
+                      int dtype, void* out, void* stream);
+int lmoe_add(const void* a, const void* b, int64_t count, int dtype, void* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LMOE_H_ */

@@ -1,0 +1,66 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function
+include/lmoe.h declares, and rejects bad arguments with the documented status
+codes before touching the device."""
+import ctypes
+
+import pytest
+
+from lmoe import _lib
+
+
+@pytest.fixture(scope="module")
+def L():
+  return _lib.lib()
+
+
+def test_every_declared_symbol_is_exported(L):
+  declared = _lib.declared_functions()
+  assert len(declared) >= 16
+  missing = [n for n in declared if not hasattr(L, n)]
+  assert not missing, missing
+  assert set(declared) == set(_lib.SIGNATURES), set(declared) ^ set(_lib.SIGNATURES)
+
+
+def test_version_and_error_string(L):
+  assert L.lmoe_version() >= 1
+  rc = L.lmoe_router_topk(None, None, 4, 8, 9, 0, 1, 1.0, _lib.F32, None, None, None, None)
+  assert rc == _lib.ERR_INVALID
+  assert b"k=9" in L.lmoe_last_error()
+
+
+@pytest.mark.parametrize("call,code", [
+    (lambda L: L.lmoe_router_topk(None, None, 4, 8192, 2, 0, 1, 1.0, _lib.F32, None, None, None, None),
+     _lib.ERR_UNSUPPORTED),
+    (lambda L: L.lmoe_router_topk(None, None, 4, 8, 2, 7, 1, 1.0, _lib.F32, None, None, None, None),
+     _lib.ERR_INVALID),
+    (lambda L: L.lmoe_ragged_dot(None, _lib.BF16, None, 0, None, 16, 12, 16, 2, -1, None, _lib.BF16, None),
+     _lib.ERR_INVALID),
+    (lambda L: L.lmoe_ragged_dot(ctypes.c_void_p(16), _lib.BF16, ctypes.c_void_p(16), 0,
+                                 ctypes.c_void_p(16), 16, 12, 16, 2, -1, ctypes.c_void_p(16), _lib.BF16,
+                                 None), _lib.ERR_UNSUPPORTED),
+    (lambda L: L.lmoe_ragged_dot(None, _lib.BF16, None, 0, None, 16, 16, 16, 2, 5, None, _lib.BF16, None),
+     _lib.ERR_INVALID),
+    (lambda L: L.lmoe_dispatch_local(None, None, 0, None, 1, 4, 2, 8, 0, 4, 128, None, None, None, None,
+                                     None, None, None, None, 0, None), _lib.ERR_WORKSPACE),
+    (lambda L: L.lmoe_ragged_dot_mxfp4(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                       ctypes.c_void_p(16), 16, 96, 16, 1, -1, 0, 0, 0.0, 0.0,
+                                       ctypes.c_void_p(16), None), _lib.ERR_UNSUPPORTED),
+    (lambda L: L.lmoe_mxfp4_dequant(None, None, 1, 4, 33, 32, None, 0, None), _lib.ERR_INVALID),
+])
+def test_argument_validation(L, call, code):
+  assert call(L) == code
+
+
+def test_workspace_sizes(L):
+  assert L.lmoe_dispatch_workspace_size(4096, 16, 112) >= 2 * 64 * 112 * 4
+  assert L.lmoe_combine_workspace_size(16384, 4096) >= 16384 * 4
+
+
+def test_ops_refuse_cpu_tensors():
+  import torch
+  from lmoe import ops
+  with pytest.raises(ValueError):
+    ops.ragged_dot(torch.zeros(4, 8), torch.zeros(1, 8, 8), torch.zeros(1, dtype=torch.int32))
+  with pytest.raises(NotImplementedError):
+    ops.ragged_dot(torch.zeros(4, 8), torch.zeros(1, 8, 8), torch.zeros(1, dtype=torch.int32),
+                   implementation="xla")

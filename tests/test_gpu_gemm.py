@@ -1,0 +1,204 @@
+"""GPU parity: grouped GEMMs (bf16 MFMA, f32), fused gate/up + SiTU, MXFP4
+dequant (bit-exact) and the MXFP4 grouped GEMM vs the CPU oracle.
+
+Tolerances (max|d|/max|ref|, benchmark_harness.py:192-199): bf16 outputs
+2e-2, f32 outputs 1e-5.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import banner, max_rel, to_dev, to_np
+from oracle import lmoe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+BF16_TOL = 2e-2
+F32_TOL = 1e-5
+
+
+def zipf_group_sizes(rng, m, g, s=1.1, n_zero=3):
+  """Zipf(s) multinomial over a seeded permutation, at least
+  n_zero empty groups (their counts moved to the largest group)."""
+  rank = rng.permutation(g)
+  p = (rank + 1.0) ** -s
+  p /= p.sum()
+  gs = rng.multinomial(m, p)
+  zero = rng.choice(g, n_zero, replace=False)
+  big = int(np.argmax(np.where(np.isin(np.arange(g), zero), -1, gs)))
+  gs[big] += gs[zero].sum()
+  gs[zero] = 0
+  return gs.astype(np.int32)
+
+
+GEMM_CASES = [
+    # name, M, K, N, G, sizes ("zipf" | list), layout
+    ("small_tail", 200, 64, 48, 4, [50, 0, 70, 31], "gkn"),  # rows past the sum are zero
+    ("k48", 96, 48, 40, 3, [32, 32, 32], "gkn"),
+    ("zipf_gkn", 2048, 512, 256, 16, "zipf", "gkn"),
+    ("zipf_gnk", 2048, 512, 256, 16, "zipf", "gnk"),
+    ("expertlike", 1024, 256, 512, 17, "small", "gnk"),
+    ("one_group", 333, 128, 72, 1, [333], "gkn"),
+]
+
+
+def _sizes(rng, spec, m, g):
+  if spec == "zipf":
+    return zipf_group_sizes(rng, m, g)
+  if spec == "small":
+    gs = rng.integers(0, 2 * m // g, g).astype(np.int32)
+    gs[-1] = 0
+    return gs
+  return np.array(spec, np.int32)
+
+
+@pytest.mark.parametrize("name,m,k,n,g,spec,layout", GEMM_CASES)
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_ragged_dot_matches_oracle(gpu_device, name, m, k, n, g, spec, layout, dt):
+  from lmoe import ops
+  banner(f"ragged_dot {name} {dt}")
+  rng = np.random.default_rng(m + k + n + g)
+  gs = _sizes(rng, spec, m, g)
+  lhs = O.cast(rng.standard_normal((m, k)), dt)
+  rhs = O.cast(rng.standard_normal((g, k, n)) * 0.02, dt)
+  ref = O.ragged_dot(lhs, rhs, gs, dt)
+  rhs_dev = to_dev(rhs if layout == "gkn" else np.ascontiguousarray(rhs.transpose(0, 2, 1)), dt)
+  out = to_np(ops.ragged_dot(to_dev(lhs, dt), rhs_dev, to_dev(gs), rhs_layout=layout))
+  assert out.shape == ref.shape
+  assert max_rel(out, ref) <= (BF16_TOL if dt == "bf16" else F32_TOL)
+  tail = int(gs.sum())
+  assert np.all(out[tail:] == 0)
+
+
+def test_ragged_dot_config2_full(gpu_device):
+  """BASELINE config 2 at full size: M=8192, K=2048, N=1024, G=32 Zipf(1.1)."""
+  from lmoe import ops
+  rng = np.random.default_rng(2)
+  gs = zipf_group_sizes(rng, 8192, 32)
+  assert (gs == 0).sum() >= 3 and gs.sum() == 8192
+  lhs = O.bf16_round(rng.standard_normal((8192, 2048)))
+  rhs = O.bf16_round(rng.standard_normal((32, 2048, 1024)) * 0.02)
+  ref = O.ragged_dot(lhs, rhs, gs, "bf16")
+  out = to_np(ops.ragged_dot(to_dev(lhs, "bf16"), to_dev(rhs, "bf16"), to_dev(gs)))
+  assert max_rel(out, ref) <= BF16_TOL
+
+
+def test_ragged_dot_f32_out_and_zero_group(gpu_device):
+  from lmoe import ops
+  rng = np.random.default_rng(3)
+  gs = np.array([40, 25, 63], np.int32)
+  lhs = O.bf16_round(rng.standard_normal((128, 256)))
+  rhs = O.bf16_round(rng.standard_normal((3, 256, 64)) * 0.02)
+  ref = O.ragged_dot(lhs, rhs, gs, "f32")
+  out = ops.ragged_dot(to_dev(lhs, "bf16"), to_dev(rhs, "bf16"), to_dev(gs),
+                       preferred_element_type=torch.float32)
+  assert out.dtype == torch.float32
+  assert max_rel(to_np(out), ref) <= 1e-5
+  z = to_np(ops.ragged_dot(to_dev(lhs, "bf16"), to_dev(rhs, "bf16"), to_dev(gs), zero_group=1))
+  assert np.all(z[40:65] == 0)
+  assert max_rel(z[:40], O.bf16_round(ref[:40])) <= BF16_TOL
+
+
+@pytest.mark.parametrize("layout", ["gkn", "gnk"])
+def test_gateup_situ_matches_oracle(gpu_device, layout):
+  from lmoe import ops
+  rng = np.random.default_rng(4)
+  m, k, inter, g = 700, 256, 192, 9
+  gs = rng.integers(0, 120, g).astype(np.int32)
+  gs[3] = 0
+  lhs = O.bf16_round(rng.standard_normal((m, k)))
+  wg = O.bf16_round(rng.standard_normal((g, k, inter)) * 0.05)
+  wu = O.bf16_round(rng.standard_normal((g, k, inter)) * 0.05)
+  fused = O.prefuse_gateup_weights(wg, wu)
+  ref = O.ragged_dot_gateup_situ(lhs, fused, gs, 4.0, 25.0, "bf16")
+  rhs = fused if layout == "gkn" else np.ascontiguousarray(fused.transpose(0, 2, 1))
+  out = to_np(ops.ragged_dot_gateup_situ(to_dev(lhs, "bf16"), to_dev(rhs, "bf16"), to_dev(gs), 4.0, 25.0,
+                                         rhs_layout=layout))
+  assert max_rel(out, ref) <= BF16_TOL
+  # the unfused oracle (separate rounded gate/up) is the same function
+  unfused = O.situ_and_mul(O.ragged_dot(lhs, wg, gs, "bf16"), O.ragged_dot(lhs, wu, gs, "bf16"), 4.0, 25.0,
+                           "bf16")
+  assert np.array_equal(unfused, ref)
+
+
+def test_mxfp4_dequant_bit_exact(gpu_device):
+  """Every byte value x edge scale bytes (0 -> 2^-127 denormal, 255 -> inf)."""
+  from lmoe import ops
+  scales = np.array([0, 1, 2, 100, 119, 126, 127, 128, 129, 200, 252, 253, 254, 255], np.uint8)
+  packed = np.tile(np.arange(256, dtype=np.uint8), (len(scales), 1))  # (14, 256) -> K = 512
+  scale = np.repeat(scales[:, None], 512 // 32, axis=1)
+  ref = O.dequantize_mxfp4(packed, scale)
+  got32 = to_np(ops.dequantize_mxfp4(to_dev(packed), to_dev(scale)))
+  got16 = to_np(ops.dequantize_mxfp4(to_dev(packed), to_dev(scale), out_dtype=torch.bfloat16))
+  for got in (got32, got16):
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32))
+
+
+def test_mxfp4_dequant_group_sizes_and_batch(gpu_device):
+  from lmoe import ops
+  rng = np.random.default_rng(5)
+  packed = rng.integers(0, 256, (3, 40, 64), dtype=np.uint8)
+  for gs in (32, 16, 128):
+    scale = rng.integers(119, 130, (3, 40, 128 // gs), dtype=np.uint8)
+    ref = np.stack([O.dequantize_mxfp4(packed[i], scale[i]) for i in range(3)])
+    got = to_np(ops.dequantize_mxfp4(to_dev(packed), to_dev(scale)))
+    assert np.array_equal(got, ref)
+
+
+def _mx_weights(rng, g, n, k):
+  packed = rng.integers(0, 256, (g, n, k // 2), dtype=np.uint8)
+  scale = rng.integers(119, 130, (g, n, k // 32), dtype=np.uint8)  # exponents -8..2
+  return packed, scale
+
+
+@pytest.mark.parametrize("m,k,n,g,situ", [
+    (300, 256, 128, 5, False), (300, 256, 128, 5, True), (1024, 1024, 256, 9, True),
+    (64, 7168, 256, 1, False)])
+def test_ragged_dot_mxfp4_lds_dequant(gpu_device, m, k, n, g, situ):
+  from lmoe import ops
+  banner(f"mxfp4 m={m} k={k} n={n} g={g} situ={situ}")
+  rng = np.random.default_rng(m + k + n)
+  gs = rng.multinomial(m, np.ones(g) / g).astype(np.int32)
+  if g > 2:
+    gs[1] = 0
+    gs[0] += m - gs.sum()
+  lhs = O.bf16_round(rng.standard_normal((m, k)))
+  packed, scale = _mx_weights(rng, g, n, k)
+  ref = O.ragged_dot_mxfp4(lhs, packed, scale, gs, "bf16", (4.0, 25.0) if situ else None)
+  out = to_np(ops.ragged_dot_mxfp4(to_dev(lhs, "bf16"), to_dev(packed), to_dev(scale), to_dev(gs),
+                                   fuse_gateup_activation="situ:4.0:25.0" if situ else None))
+  assert out.shape == ref.shape
+  assert max_rel(out, ref) <= BF16_TOL
+
+
+def test_mxfp4_gemm_equals_dequant_then_bf16_gemm(gpu_device):
+  """In-LDS dequant == dequantise to bf16 first, then the bf16 grouped GEMM."""
+  from lmoe import ops
+  rng = np.random.default_rng(6)
+  m, k, n, g = 512, 512, 128, 4
+  gs = np.array([100, 200, 0, 212], np.int32)
+  lhs = to_dev(O.bf16_round(rng.standard_normal((m, k))), "bf16")
+  packed, scale = _mx_weights(rng, g, n, k)
+  wdq = ops.dequantize_mxfp4(to_dev(packed), to_dev(scale), out_dtype=torch.bfloat16)  # (g, n, k)
+  a = ops.ragged_dot_mxfp4(lhs, to_dev(packed), to_dev(scale), to_dev(gs))
+  b = ops.ragged_dot(lhs, wdq, to_dev(gs), rhs_layout="gnk")
+  assert torch.equal(a, b)
+
+
+def test_elementwise_rms_norm_and_situ(gpu_device):
+  from lmoe import ops
+  rng = np.random.default_rng(7)
+  x = O.bf16_round(rng.standard_normal((64, 1024)))
+  s = O.bf16_round(rng.standard_normal(1024))
+  ref = O.rms_norm(x, s, 1e-5, "bf16")
+  out = to_np(ops._rms_norm(to_dev(x, "bf16"), to_dev(s, "bf16"), 1e-5))
+  assert max_rel(out, ref) <= BF16_TOL
+  xf = rng.standard_normal((16, 300)).astype(np.float32)
+  sf = rng.standard_normal(300).astype(np.float32)
+  assert max_rel(to_np(ops._rms_norm(to_dev(xf), to_dev(sf), 1e-5)), O.rms_norm(xf, sf, 1e-5, "f32")) <= F32_TOL
+  g = (rng.standard_normal(5000) * 6).astype(np.float32)
+  u = (rng.standard_normal(5000) * 30).astype(np.float32)
+  got = to_np(ops._situ_and_mul(to_dev(g), to_dev(u), 4.0, 25.0))
+  assert max_rel(got, O.situ_and_mul(g, u, 4.0, 25.0, "f32")) <= F32_TOL

@@ -1,0 +1,213 @@
+"""GPU parity: router top-k, local-shard dispatch and combine vs the CPU oracle.
+
+Integer / index outputs (top-k ids, group sizes, permutations, gathered rows,
+masks) must be bit-exact; f32 weights within 1e-5 relative; the combine
+reproduces the oracle's rounding sequence, so it is compared exactly too.
+"""
+import numpy as np
+import pytest
+import torch
+
+from _util import banner, max_rel, to_dev, to_np
+from oracle import lmoe_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _logits(rng, t, e, kind):
+  if kind == "normal":
+    return rng.standard_normal((t, e)).astype(np.float32)
+  if kind == "ties":  # integer logits: many exactly tied scores
+    return rng.integers(-3, 4, (t, e)).astype(np.float32)
+  if kind == "skew":
+    rank = rng.permutation(e)
+    return (rng.standard_normal((t, e)) - 1.2 * np.log(rank + 1)).astype(np.float32)
+  raise ValueError(kind)
+
+
+def _near_tie_tokens(choice, k, eps=4e-7):
+  """Tokens whose k-th and (k+1)-th selection scores are within a few ulp: a
+  1-ulp difference in exp() may legitimately order them either way."""
+  if choice.shape[1] <= k:
+    return np.zeros(choice.shape[0], bool)
+  s = -np.sort(-choice, axis=1)
+  gap = np.abs(s[:, k - 1] - s[:, k])
+  # exact ties are deterministic on both sides (lower expert id first)
+  return (gap > 0) & (gap <= eps * np.maximum(np.abs(s[:, k - 1]), 1e-30))
+
+
+@pytest.mark.parametrize("t,e,k,kind,act,wdt", [
+    (2048, 896, 16, "normal", "sigmoid", "bf16"),  # config 3 router
+    (512, 896, 16, "skew", "sigmoid", "f32"),
+    (257, 8, 2, "normal", "sigmoid", "f32"),
+    (300, 64, 16, "ties", "sigmoid", "f32"),
+    (300, 64, 6, "ties", "softmax", "f32"),
+    (128, 8, 2, "normal", "softmax", "f32"),  # config 1 router (BASELINE: softmax)
+    (64, 4096, 64, "normal", "sigmoid", "f32"),
+    (33, 5, 5, "normal", "sigmoid", "bf16"),
+    (16, 896, 1, "normal", "sigmoid", "f32"),
+])
+def test_router_topk_matches_oracle(gpu_device, t, e, k, kind, act, wdt):
+  from lmoe import ops
+  banner(f"router t={t} e={e} k={k} {kind} {act} {wdt}")
+  rng = np.random.default_rng(t * 7 + e)
+  logits = _logits(rng, t, e, kind)
+  bias = np.zeros(e, np.float32)
+  if kind == "ties":
+    bias[::7] = 0.25
+  ref = O.router_from_logits(logits, bias, k, True, 1.0, act, wdt)
+  idx, w, scores = ops.router_topk_from_logits(
+      to_dev(logits), to_dev(bias), k, True, 1.0, act,
+      torch.bfloat16 if wdt == "bf16" else torch.float32, return_scores=True)
+  idx, w, scores = to_np(idx), to_np(w), to_np(scores)
+  skip = _near_tie_tokens(ref.scores_for_choice, k)
+  assert skip.sum() <= max(1, t // 1000), skip.sum()
+  assert np.array_equal(idx[~skip], ref.topk_idx[~skip])
+  tol = 1e-5 if wdt == "f32" else 8e-3
+  assert max_rel(w[~skip], ref.topk_weight[~skip]) <= tol
+  assert max_rel(scores, ref.scores) <= 1e-5
+
+
+def test_router_golden_bias(gpu_device):
+  """The golden bundles' uninitialised bias (1.36e5, denormals) through the GPU gate."""
+  import _golden
+  from lmoe import ops
+  config, dtype, hidden, w, golden = _golden.load("golden_bundle_small")
+  idx, wt = ops.router_topk_from_logits(to_dev(golden["router_logits"]),
+                                        to_dev(w["e_score_correction_bias"]), 2, True, 1.0)
+  g = np.sort(golden["topk_indices"], axis=1)
+  assert np.array_equal(np.sort(to_np(idx), axis=1), g)
+
+
+DISPATCH_CASES = [
+    # name, T, k, E, start, L, cf, tile, wdt
+    ("config3", 2048, 16, 896, 0, 112, 2.0, 128, "bf16"),
+    ("offset137", 256, 16, 896, 137, 64, 4.0, 128, "f32"),
+    ("overflow", 256, 16, 896, 137, 64, 0.05, 1, "f32"),
+    ("decode_t1", 1, 16, 896, 0, 112, 2.0, 128, "bf16"),
+    ("all_local", 100, 4, 16, 0, 16, 1.0, 1, "f32"),
+    ("last_shard", 64, 2, 24, 18, 6, 4.0, 128, "f32"),
+    ("big_chunks", 4096, 16, 896, 448, 112, 2.0, 128, "bf16"),
+]
+
+
+def _run_dispatch(topk_idx, topk_w, x, wdt, start, L, m_padded):
+  from lmoe import ops
+  return ops.dispatch_local(to_dev(topk_idx), to_dev(topk_w, wdt), to_dev(x, "bf16"), start, L, m_padded)
+
+
+@pytest.mark.parametrize("name,t,k,e,start,L,cf,tile,wdt", DISPATCH_CASES)
+def test_dispatch_matches_oracle_bit_exact(gpu_device, name, t, k, e, start, L, cf, tile, wdt):
+  banner(f"dispatch {name}")
+  rng = np.random.default_rng(len(name) * 31 + t)
+  topk_idx = np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
+  topk_w = O.cast(rng.uniform(size=(t, k)), wdt)
+  x = O.bf16_round(rng.standard_normal((t, 64)))
+  m_padded = O.compute_m_padded(t, k, e, L, cf, tile)
+  ref, slot_pos = O.filter_and_pad_to_shard_jittable(topk_idx, topk_w, x, k, e, start, L, cf, tile,
+                                                     return_slot_pos=True)
+  got = _run_dispatch(topk_idx, topk_w, x, wdt, start, L, m_padded)
+  for field in ("sorted_tokens", "group_sizes", "valid_mask", "per_expert_counts", "padded_token_idx",
+                "padded_combine_weight"):
+    a, b = to_np(getattr(got, field)), getattr(ref, field)
+    assert a.shape == b.shape, field
+    assert np.array_equal(a, b), field
+  assert np.array_equal(to_np(got.slot_pos), slot_pos)
+
+
+@pytest.mark.parametrize("case", ["empty_shard", "extreme_skew", "boundary"])
+def test_dispatch_literal_kats(gpu_device, case):
+  """test_sharded_routing_local.py literal inputs (62-99, 102-125, 232-266)."""
+  if case == "empty_shard":
+    ti = np.array([[0, 1], [1, 2], [6, 7], [7, 0], [2, 3]], np.int32)
+    tw, start, L, e = np.full((5, 2), 0.5, np.float32), 4, 2, 8
+  elif case == "extreme_skew":
+    ti, tw, start, L, e = np.full((50, 1), 5, np.int32), np.full((50, 1), 0.7, np.float32), 3, 5, 16
+  else:
+    ti = np.array([[4], [5], [8], [9]], np.int32)
+    tw, start, L, e = np.array([[0.1], [0.2], [0.3], [0.4]], np.float32), 5, 4, 20
+  t, k = ti.shape
+  x = O.bf16_round(np.random.default_rng(5).standard_normal((t, 32)))
+  m_padded = O.compute_m_padded(t, k, e, L, 4.0, 1)
+  ref = O.filter_and_pad_to_shard(ti, tw, x, k, e, start, L, 4.0, 1)
+  got = _run_dispatch(ti, tw, x, "f32", start, L, m_padded)
+  for a, b in zip(got[:6], ref):
+    assert np.array_equal(to_np(a), b)
+
+
+@pytest.mark.parametrize("odt", ["bf16", "f32"])
+def test_combine_slots_scatter_add_bit_exact(gpu_device, odt):
+  from lmoe import ops
+  rng = np.random.default_rng(11)
+  t, k, e, L = 512, 16, 896, 112
+  topk_idx = np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
+  topk_w = O.cast(rng.uniform(size=(t, k)), odt)
+  x = O.bf16_round(rng.standard_normal((t, 64)))
+  d, slot_pos = O.filter_and_pad_to_shard_jittable(topk_idx, topk_w, x, k, e, 0, L, 2.0, 128,
+                                                   return_slot_pos=True)
+  shard_out = O.cast(rng.standard_normal(d.sorted_tokens.shape), odt)
+  ref = O.combine_shard_contribution(np.zeros((t, 64), np.float32), shard_out, d.padded_token_idx,
+                                     d.padded_combine_weight, odt, odt, odt)
+  got = ops.combine_slots(to_dev(shard_out, odt), to_dev(slot_pos), to_dev(d.padded_combine_weight, odt),
+                          t, k, mode="scatter_add",
+                          out_dtype=torch.bfloat16 if odt == "bf16" else torch.float32)
+  assert np.array_equal(to_np(got), ref)
+
+
+def test_combine_slot_sum_bit_exact(gpu_device):
+  from lmoe import ops
+  rng = np.random.default_rng(12)
+  t, k, e = 300, 4, 16
+  topk_idx = np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
+  topk_w = rng.uniform(size=(t, k)).astype(np.float32)
+  order, _, gs = O.unsharded_dispatch(topk_idx, np.zeros((t, 8), np.float32), e)
+  outs = O.bf16_round(rng.standard_normal((t * k, 48)))
+  ref, _ = O.unsharded_combine(outs, order, topk_w, t, k, "bf16")
+  slot_pos = np.empty(t * k, np.int32)
+  slot_pos[order] = np.arange(t * k, dtype=np.int32)
+  got = ops.combine_slots(to_dev(outs, "bf16"), to_dev(slot_pos), to_dev(topk_w), t, k, mode="slot_sum",
+                          out_dtype=torch.bfloat16)
+  assert np.array_equal(to_np(got), ref)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f32"])
+def test_generic_combine_scatter_add(gpu_device, dt):
+  """_combine_shard_contribution on arbitrary indices: duplicates, -1 padding
+  rows with non-zero content (test_sharded_routing_local.py:170-194), a
+  non-zero running accumulator, and one token hit 300 times (> LDS batch)."""
+  from lmoe import ops
+  rng = np.random.default_rng(13)
+  t, m, lat = 40, 1000, 24
+  idx = rng.integers(-1, t, m).astype(np.int32)
+  idx[:300] = 7
+  w = O.cast(rng.uniform(size=m), dt)
+  w[idx < 0] = 0
+  shard = O.cast(rng.standard_normal((m, lat)), dt)
+  routed0 = O.cast(rng.standard_normal((t, lat)), dt)
+  ref = O.combine_shard_contribution(routed0, shard, idx, w, dt, dt, dt)
+  got = ops._combine_shard_contribution(to_dev(routed0, dt), to_dev(shard, dt), to_dev(idx), to_dev(w, dt))
+  assert np.array_equal(to_np(got), ref)  # value equality (-1 rows add +-0 in the reference)
+
+
+def test_combine_padding_literal(gpu_device):
+  from lmoe import ops
+  shard = np.random.default_rng(3).standard_normal((6, 8)).astype(np.float32)
+  idx = np.array([0, 1, 2, 3, -1, -1], np.int32)
+  w = np.array([0.5, 0.5, 0.5, 0.5, 0.0, 0.0], np.float32)
+  got = ops._combine_shard_contribution(to_dev(np.zeros((4, 8), np.float32)), to_dev(shard), to_dev(idx),
+                                        to_dev(w))
+  assert np.max(np.abs(to_np(got) - shard[:4] * 0.5)) < 1e-6
+
+
+def test_dispatch_deterministic_rerun(gpu_device):
+  """Same inputs twice -> identical bytes (no atomics in the ordering)."""
+  rng = np.random.default_rng(14)
+  t, k, e, L = 4096, 16, 896, 112
+  ti = np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
+  tw = O.bf16_round(rng.uniform(size=(t, k)))
+  x = O.bf16_round(rng.standard_normal((t, 128)))
+  m = O.compute_m_padded(t, k, e, L)
+  a = _run_dispatch(ti, tw, x, "bf16", 0, L, m)
+  b = _run_dispatch(ti, tw, x, "bf16", 0, L, m)
+  for u, v in zip(a, b):
+    assert torch.equal(u, v)

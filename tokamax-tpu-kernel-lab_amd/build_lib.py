@@ -1,0 +1,87 @@
+"""Build liblmoe.so (gfx950) from csrc/*.hip with hipcc, in-tree.
+
+Objects go to ``_build/`` next to this file, the shared library to
+``lmoe/liblmoe.so``.  Every build recompiles every source (the driver's
+"does it build" check); ``--jobs`` controls parallel compiles.
+
+  python build_lib.py [--jobs N] [--verbose]
+"""
+
+from __future__ import annotations
+
+import argparse
+import concurrent.futures as cf
+import os
+import shutil
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+BUILD = os.path.join(HERE, "_build")
+OUT = os.path.join(HERE, "lmoe", "liblmoe.so")
+ARCH = "gfx950"
+
+HIPCC_FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-fPIC",
+    "-std=c++17",
+    "-ffp-contract=off",
+    # packed-fp32 instructions have given silent wrong results on these boxes
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    "-Wno-unused-function",
+    "-Wno-unused-variable",
+]
+
+
+def hipcc() -> str:
+  for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+    if cand and os.path.exists(cand):
+      return cand
+  raise RuntimeError("hipcc not found")
+
+
+def _compile(src: str, verbose: bool) -> str:
+  obj = os.path.join(BUILD, os.path.basename(src) + ".o")
+  cmd = [hipcc(), *HIPCC_FLAGS, "-I", CSRC, "-c", src, "-o", obj]
+  if verbose:
+    print(" ".join(cmd), flush=True)
+  r = subprocess.run(cmd, capture_output=True, text=True)
+  err = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+  if r.returncode != 0:
+    raise RuntimeError(f"hipcc failed on {src}:\n{err}")
+  if err.strip() and verbose:
+    print(err)
+  return obj
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> str:
+  os.makedirs(BUILD, exist_ok=True)
+  srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+  jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4)))
+  with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
+    objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
+  tmp = OUT + ".tmp"
+  cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+  r = subprocess.run(cmd, capture_output=True, text=True)
+  if r.returncode != 0:
+    raise RuntimeError(f"link failed:\n{r.stderr}")
+  os.replace(tmp, OUT)
+  if verbose:
+    print(f"built {OUT}")
+  return OUT
+
+
+def main() -> int:
+  ap = argparse.ArgumentParser()
+  ap.add_argument("--jobs", type=int, default=None)
+  ap.add_argument("--verbose", action="store_true")
+  a = ap.parse_args()
+  build(a.jobs, a.verbose)
+  return 0
+
+
+if __name__ == "__main__":
+  sys.exit(main())

@@ -1,0 +1,286 @@
+// Weighted top-k combine (reference _combine_shard_contribution,
+// ref.py:1113-1141, and the unsharded combine of latent_moe_forward,
+// ref.py:413-416).
+//
+// Atomic-free and deterministic: one 64-wide wavefront owns one token and
+// accumulates that token's contributing rows itself, in ascending row order,
+// which is the order the reference's scatter-add applies its updates.  The
+// rows of a token come either from the dispatch's slot_pos (k slots per token,
+// sorted in-wave) or, for arbitrary padded_token_idx, from a stable counting
+// sort by token (csort.h).
+#include "csort.h"
+
+namespace lmoe {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kTokensPerBlock = 4;
+constexpr int kMaxRowsInLds = 256;
+
+// The LDS staging arrays are private to one wavefront, so only wave-level
+// ordering is needed (waves of a block work on different tokens and may run
+// different trip counts, so a block barrier would be wrong here).
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}
+
+// Accumulation state for VEC consecutive output elements of one lane.
+template <int VEC>
+struct Acc {
+  float v[VEC];
+};
+
+template <int VEC>
+__device__ __forceinline__ void load_vec(const void* p, int64_t i, int dtype, float* out) {
+  if (dtype == LMOE_BF16) {
+    const uint16_t* q = static_cast<const uint16_t*>(p) + i;
+    if constexpr (VEC == 8) {
+      const uint4 raw = *reinterpret_cast<const uint4*>(q);
+      const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        out[2 * j] = __uint_as_float(w[j] << 16);
+        out[2 * j + 1] = __uint_as_float(w[j] & 0xffff0000u);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) out[j] = bf16_to_f32(q[j]);
+    }
+  } else {
+    const float* q = static_cast<const float*>(p) + i;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) out[j] = q[j];
+  }
+}
+
+template <int VEC>
+__device__ __forceinline__ void store_vec(void* p, int64_t i, int dtype, const float* v) {
+  if (dtype == LMOE_BF16) {
+    uint16_t* q = static_cast<uint16_t*>(p) + i;
+    if constexpr (VEC == 8) {
+      uint4 raw;
+      raw.x = f32_to_bf16(v[0]) | (static_cast<uint32_t>(f32_to_bf16(v[1])) << 16);
+      raw.y = f32_to_bf16(v[2]) | (static_cast<uint32_t>(f32_to_bf16(v[3])) << 16);
+      raw.z = f32_to_bf16(v[4]) | (static_cast<uint32_t>(f32_to_bf16(v[5])) << 16);
+      raw.w = f32_to_bf16(v[6]) | (static_cast<uint32_t>(f32_to_bf16(v[7])) << 16);
+      *reinterpret_cast<uint4*>(q) = raw;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) q[j] = f32_to_bf16(v[j]);
+    }
+  } else {
+    float* q = static_cast<float*>(p) + i;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) q[j] = v[j];
+  }
+}
+
+// Adds the rows rows[0..n) (ascending) with weights wts[] into routed_out[t]
+// with the scatter-add rounding: product in promoted(shard, w) dtype, cast to
+// out dtype, each add rounded to out dtype.
+template <int VEC>
+__device__ void accumulate_token(const void* shard, int sdt, const int32_t* rows, const float* wts,
+                                 int n, int64_t lat, void* out, int odt, int64_t t, int prod_dt,
+                                 int lane) {
+  for (int64_t c0 = static_cast<int64_t>(lane) * VEC; c0 < lat; c0 += kWave * VEC) {
+    float acc[VEC];
+    load_vec<VEC>(out, t * lat + c0, odt, acc);
+    for (int r = 0; r < n; ++r) {
+      float x[VEC];
+      load_vec<VEC>(shard, static_cast<int64_t>(rows[r]) * lat + c0, sdt, x);
+      const float w = wts[r];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) {
+        float v = round_to(__fmul_rn(x[j], w), prod_dt);
+        v = round_to(v, odt);
+        acc[j] = round_to(__fadd_rn(acc[j], v), odt);
+      }
+    }
+    store_vec<VEC>(out, t * lat + c0, odt, acc);
+  }
+}
+
+template <int VEC>
+__global__ __launch_bounds__(256) void combine_slots_kernel(
+    const void* __restrict__ shard, int sdt, const int32_t* __restrict__ slot_pos,
+    const void* __restrict__ w, int wdt, int T, int k, int64_t lat, int mode, void* __restrict__ out,
+    int odt) {
+  __shared__ int32_t rows_s[kTokensPerBlock][kWave];
+  __shared__ float wts_s[kTokensPerBlock][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int t = blockIdx.x * kTokensPerBlock + wave;
+  if (t >= T) return;
+  int p = -1;
+  if (lane < k) p = slot_pos[static_cast<int64_t>(t) * k + lane];
+  if (mode == LMOE_COMBINE_SLOT_SUM) {
+    // f32 weighted sum over slots j = 0..k-1, one cast at the end (ref.py:413-416).
+    float wj = lane < k ? load_as_f32(w, static_cast<int64_t>(t) * k + lane, wdt) : 0.0f;
+    rows_s[wave][lane] = p;
+    wts_s[wave][lane] = wj;
+    wave_sync();
+    for (int64_t c0 = static_cast<int64_t>(lane) * VEC; c0 < lat; c0 += kWave * VEC) {
+      float acc[VEC];
+#pragma unroll
+      for (int j = 0; j < VEC; ++j) acc[j] = 0.0f;
+      for (int j = 0; j < k; ++j) {
+        const int row = rows_s[wave][j];
+        if (row < 0) continue;
+        float x[VEC];
+        load_vec<VEC>(shard, static_cast<int64_t>(row) * lat + c0, sdt, x);
+        const float wv = wts_s[wave][j];
+#pragma unroll
+        for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(x[q], wv));
+      }
+      store_vec<VEC>(out, static_cast<int64_t>(t) * lat + c0, odt, acc);
+    }
+    return;
+  }
+  // Scatter-add mode: order this token's kept rows ascending (k <= 64).
+  const bool valid = lane < k && p >= 0;
+  int rank = 0;
+  for (int j = 0; j < k; ++j) {
+    const int pj = __shfl(p, j, kWave);
+    rank += (pj >= 0 && pj < p) ? 1 : 0;
+  }
+  const int n = __popcll(__ballot(valid));
+  if (valid) {
+    rows_s[wave][rank] = p;
+    wts_s[wave][rank] = load_as_f32(w, p, wdt);
+  }
+  wave_sync();
+  const int prod_dt = (sdt == LMOE_F32 || wdt == LMOE_F32) ? LMOE_F32 : LMOE_BF16;
+  accumulate_token<VEC>(shard, sdt, rows_s[wave], wts_s[wave], n, lat, out, odt, t, prod_dt, lane);
+}
+
+// ---- generic scatter-add over an arbitrary padded_token_idx --------------------
+
+struct TokenKey {
+  const int32_t* idx;
+  int T;
+  __device__ __forceinline__ int operator()(int64_t s) const {
+    const int t = idx[s];
+    return (t >= 0 && t < T) ? t : T;
+  }
+};
+
+struct OrderSink {
+  int32_t* order;
+  __device__ __forceinline__ void operator()(int64_t s, int key, int pos, bool real) const {
+    if (real) order[pos] = static_cast<int32_t>(s);
+  }
+};
+
+template <int VEC>
+__global__ __launch_bounds__(256) void combine_csr_kernel(
+    const void* __restrict__ shard, int sdt, const int32_t* __restrict__ order,
+    const int32_t* __restrict__ offsets, const void* __restrict__ w, int wdt, int T, int64_t lat,
+    void* __restrict__ out, int odt) {
+  __shared__ int32_t rows_s[kTokensPerBlock][kMaxRowsInLds];
+  __shared__ float wts_s[kTokensPerBlock][kMaxRowsInLds];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int t = blockIdx.x * kTokensPerBlock + wave;
+  if (t >= T) return;
+  const int prod_dt = (sdt == LMOE_F32 || wdt == LMOE_F32) ? LMOE_F32 : LMOE_BF16;
+  const int b = offsets[t], e = offsets[t + 1];
+  // Rows are consumed in batches that fit the LDS staging area; the running
+  // sum lives in routed_out between batches, so the add order is unchanged.
+  for (int q0 = b; q0 < e; q0 += kMaxRowsInLds) {
+    const int n = (e - q0) < kMaxRowsInLds ? (e - q0) : kMaxRowsInLds;
+    for (int i = lane; i < n; i += kWave) {
+      const int row = order[q0 + i];
+      rows_s[wave][i] = row;
+      wts_s[wave][i] = load_as_f32(w, row, wdt);
+    }
+    wave_sync();
+    accumulate_token<VEC>(shard, sdt, rows_s[wave], wts_s[wave], n, lat, out, odt, t, prod_dt, lane);
+    wave_sync();
+  }
+}
+
+int64_t combine_ws_bytes(int64_t m, int64_t T) {
+  const int64_t chunks = csort::num_chunks(m > 0 ? m : 1);
+  return (2 * chunks * T + (T + 1) + m + 64) * static_cast<int64_t>(sizeof(int32_t));
+}
+
+bool vec8_ok(const void* a, const void* b, int64_t lat, int adt, int bdt) {
+  return lat % 8 == 0 && aligned(a, adt == LMOE_BF16 ? 16 : 32) && aligned(b, bdt == LMOE_BF16 ? 16 : 32);
+}
+
+}  // namespace
+}  // namespace lmoe
+
+extern "C" int64_t lmoe_combine_workspace_size(int64_t m, int64_t T) {
+  return lmoe::combine_ws_bytes(m, T);
+}
+
+extern "C" int lmoe_combine_slots(const void* shard_out, int shard_dtype, const int32_t* slot_pos,
+                                  const void* w, int w_dtype, int64_t T, int64_t k, int64_t lat,
+                                  int mode, void* routed_out, int out_dtype, void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(T >= 0 && k > 0 && lat > 0, "combine_slots: bad sizes");
+  LMOE_CHECK_SUPPORTED(k <= 64, "combine_slots: k=%lld > 64", (long long)k);
+  LMOE_CHECK_ARG(valid_dtype(shard_dtype) && valid_dtype(w_dtype) && valid_dtype(out_dtype),
+                 "combine_slots: bad dtype");
+  LMOE_CHECK_ARG(mode == LMOE_COMBINE_SCATTER_ADD || mode == LMOE_COMBINE_SLOT_SUM,
+                 "combine_slots: bad mode %d", mode);
+  LMOE_CHECK_SUPPORTED(T < (1ll << 31), "combine_slots: T too large");
+  if (T == 0) return LMOE_OK;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>(ceil_div(T, kTokensPerBlock));
+  if (vec8_ok(shard_out, routed_out, lat, shard_dtype, out_dtype))
+    combine_slots_kernel<8><<<blocks, 256, 0, st>>>(shard_out, shard_dtype, slot_pos, w, w_dtype,
+                                                   (int)T, (int)k, lat, mode, routed_out, out_dtype);
+  else
+    combine_slots_kernel<1><<<blocks, 256, 0, st>>>(shard_out, shard_dtype, slot_pos, w, w_dtype,
+                                                   (int)T, (int)k, lat, mode, routed_out, out_dtype);
+  LMOE_CHECK_LAUNCH("combine_slots");
+  return LMOE_OK;
+}
+
+extern "C" int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype,
+                                        const int32_t* padded_token_idx, const void* padded_w,
+                                        int w_dtype, int64_t m, int64_t lat, int64_t T,
+                                        void* routed_out, int out_dtype, void* workspace,
+                                        int64_t workspace_size, void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(m >= 0 && lat > 0 && T >= 0, "combine_scatter_add: bad sizes");
+  LMOE_CHECK_ARG(valid_dtype(shard_dtype) && valid_dtype(w_dtype) && valid_dtype(out_dtype),
+                 "combine_scatter_add: bad dtype");
+  LMOE_CHECK_SUPPORTED(T + 1 <= 16384, "combine_scatter_add: T=%lld exceeds the LDS histogram",
+                       (long long)T);
+  LMOE_CHECK_SUPPORTED(m < (1ll << 31), "combine_scatter_add: m too large");
+  if (T == 0 || m == 0) return LMOE_OK;
+  const int64_t need = combine_ws_bytes(m, T);
+  if (!workspace || workspace_size < need)
+    return fail(LMOE_ERR_WORKSPACE, "combine_scatter_add: workspace %lld < %lld",
+                (long long)workspace_size, (long long)need);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t chunks = csort::num_chunks(m);
+  int32_t* ws = static_cast<int32_t*>(workspace);
+  int32_t* hist = ws;
+  int32_t* base = hist + chunks * T;
+  int32_t* offsets = base + chunks * T;
+  int32_t* order = offsets + (T + 1);
+  int32_t* num_kept = order + m;
+  const int Ti = static_cast<int>(T);
+  TokenKey key{padded_token_idx, Ti};
+  csort::hist_kernel<<<dim3(static_cast<unsigned>(chunks)), 256, (T + 1) * sizeof(int32_t), st>>>(
+      key, m, Ti, hist);
+  LMOE_CHECK_LAUNCH("combine_hist");
+  csort::scan_kernel<<<1, csort::kScanThreads, 0, st>>>(hist, static_cast<int>(chunks), Ti,
+                                                        (1ll << 40), base, nullptr, offsets, num_kept);
+  LMOE_CHECK_LAUNCH("combine_scan");
+  csort::place_kernel<<<dim3(static_cast<unsigned>(chunks)), 64, T * sizeof(int32_t), st>>>(
+      key, m, Ti, csort::key_bits_for(Ti), base, OrderSink{order});
+  LMOE_CHECK_LAUNCH("combine_place");
+  const unsigned blocks = static_cast<unsigned>(ceil_div(T, kTokensPerBlock));
+  if (vec8_ok(shard_out, routed_out, lat, shard_dtype, out_dtype))
+    combine_csr_kernel<8><<<blocks, 256, 0, st>>>(shard_out, shard_dtype, order, offsets, padded_w,
+                                                 w_dtype, Ti, lat, routed_out, out_dtype);
+  else
+    combine_csr_kernel<1><<<blocks, 256, 0, st>>>(shard_out, shard_dtype, order, offsets, padded_w,
+                                                 w_dtype, Ti, lat, routed_out, out_dtype);
+  LMOE_CHECK_LAUNCH("combine_csr");
+  return LMOE_OK;
+}

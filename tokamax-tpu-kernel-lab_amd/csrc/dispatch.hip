@@ -1,0 +1,164 @@
+// Local-shard dispatch (reference filter_and_pad_to_shard_jittable,
+// ref.py:754-877, bit-identical to the eager filter_and_pad_to_shard,
+// ref.py:658-751).
+//
+// Slot s = t*k + j carries key = local expert id if the global id is in
+// [local_start, local_start + L), else the sentinel L.  A stable counting
+// sort (csort.h) gives each in-shard slot its row in expert-major order; rows
+// >= m_padded are dropped (tail truncation), and rows past the kept count are
+// the padding bucket.  Then one gather pass copies x rows into sorted_tokens
+// and fills the padding rows (zero row, token -1, weight 0, valid 0).
+#include "csort.h"
+
+namespace lmoe {
+namespace {
+
+struct DispatchKey {
+  const int32_t* idx;
+  int start;
+  int L;
+  __device__ __forceinline__ int operator()(int64_t s) const {
+    const int g = idx[s];
+    return (g >= start && g < start + L) ? g - start : L;
+  }
+};
+
+struct DispatchSink {
+  int k;
+  const uint8_t* w;
+  int wsize;
+  int32_t* tok_out;
+  uint8_t* w_out;
+  int32_t* slot_pos;
+  int64_t limit;
+  __device__ __forceinline__ void operator()(int64_t s, int key, int pos, bool real) const {
+    const bool kept = real && pos < limit;
+    if (kept) {
+      tok_out[pos] = static_cast<int32_t>(s / k);
+      if (wsize == 4)
+        reinterpret_cast<uint32_t*>(w_out)[pos] = reinterpret_cast<const uint32_t*>(w)[s];
+      else
+        reinterpret_cast<uint16_t*>(w_out)[pos] = reinterpret_cast<const uint16_t*>(w)[s];
+    }
+    if (slot_pos) slot_pos[s] = kept ? pos : -1;
+  }
+};
+
+constexpr int kGatherRows = 16;
+
+template <typename VT>
+__global__ __launch_bounds__(256) void gather_kernel(
+    const VT* __restrict__ x, int64_t row_vecs, const int32_t* __restrict__ num_kept_p,
+    int64_t m_padded, VT* __restrict__ out, uint8_t* __restrict__ valid, int32_t* __restrict__ tok,
+    uint8_t* __restrict__ w_out, int wsize, int32_t* __restrict__ group_sizes,
+    int32_t* __restrict__ per_expert, int L) {
+  const int nk = *num_kept_p;
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < L; i += blockDim.x) per_expert[i] = group_sizes[i];
+    if (threadIdx.x == 0) group_sizes[L] = static_cast<int32_t>(m_padded - nk);
+  }
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kGatherRows;
+  const int64_t r1 = r0 + kGatherRows < m_padded ? r0 + kGatherRows : m_padded;
+  for (int64_t p = r0 + threadIdx.x; p < r1; p += blockDim.x) {
+    valid[p] = p < nk ? 1 : 0;
+    if (p >= nk) {
+      tok[p] = -1;
+      if (wsize == 4)
+        reinterpret_cast<uint32_t*>(w_out)[p] = 0;
+      else
+        reinterpret_cast<uint16_t*>(w_out)[p] = 0;
+    }
+  }
+  const int64_t total = (r1 - r0) * row_vecs;
+  for (int64_t i = threadIdx.x; i < total; i += blockDim.x) {
+    const int64_t p = r0 + i / row_vecs;
+    const int64_t v = i % row_vecs;
+    VT val{};
+    if (p < nk) {
+      const int32_t t = tok[p];
+      val = x[static_cast<int64_t>(t) * row_vecs + v];
+    }
+    out[p * row_vecs + v] = val;
+  }
+}
+
+struct Workspace {
+  int32_t* hist;
+  int32_t* base;
+  int32_t* num_kept;
+};
+
+int64_t workspace_bytes(int64_t n, int64_t L) {
+  const int64_t chunks = csort::num_chunks(n > 0 ? n : 1);
+  return (2 * chunks * L + 64) * static_cast<int64_t>(sizeof(int32_t));
+}
+
+}  // namespace
+}  // namespace lmoe
+
+extern "C" int64_t lmoe_dispatch_workspace_size(int64_t T, int64_t k, int64_t L) {
+  return lmoe::workspace_bytes(T * k, L);
+}
+
+extern "C" int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, int w_dtype,
+                                   const void* x, int x_dtype, int64_t T, int64_t k, int64_t lat,
+                                   int64_t local_start, int64_t L, int64_t m_padded,
+                                   void* sorted_tokens, int32_t* group_sizes, uint8_t* valid,
+                                   int32_t* per_expert_counts, int32_t* padded_token_idx,
+                                   void* padded_w, int32_t* slot_pos, void* workspace,
+                                   int64_t workspace_size, void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(T >= 0 && k > 0 && lat > 0 && L > 0 && m_padded >= 0 && local_start >= 0,
+                 "dispatch_local: bad sizes T=%lld k=%lld lat=%lld L=%lld m_padded=%lld",
+                 (long long)T, (long long)k, (long long)lat, (long long)L, (long long)m_padded);
+  LMOE_CHECK_ARG(valid_dtype(w_dtype) && valid_dtype(x_dtype), "dispatch_local: bad dtype");
+  LMOE_CHECK_SUPPORTED(T * k < (1ll << 31) && m_padded < (1ll << 31) && L < (1 << 20),
+                       "dispatch_local: sizes exceed int32 indexing");
+  LMOE_CHECK_SUPPORTED(L + 1 <= 12288, "dispatch_local: L=%lld exceeds the LDS histogram", (long long)L);
+  const int64_t need = workspace_bytes(T * k, L);
+  if (!workspace || workspace_size < need)
+    return fail(LMOE_ERR_WORKSPACE, "dispatch_local: workspace %lld bytes < %lld", (long long)workspace_size,
+                (long long)need);
+  LMOE_CHECK_ARG(group_sizes && valid && per_expert_counts && padded_token_idx && padded_w &&
+                     (sorted_tokens || m_padded == 0),
+                 "dispatch_local: null output");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = T * k;
+  const int64_t chunks = csort::num_chunks(n > 0 ? n : 1);
+  int32_t* ws = static_cast<int32_t*>(workspace);
+  Workspace w{ws, ws + chunks * L, ws + 2 * chunks * L};
+  const int Li = static_cast<int>(L);
+  DispatchKey key{topk_idx, static_cast<int>(local_start), Li};
+  // With n == 0 the single chunk still writes an all-zero histogram.
+  csort::hist_kernel<<<dim3(static_cast<unsigned>(chunks)), 256, (L + 1) * sizeof(int32_t), st>>>(
+      key, n, Li, w.hist);
+  LMOE_CHECK_LAUNCH("dispatch_hist");
+  csort::scan_kernel<<<1, csort::kScanThreads, 0, st>>>(w.hist, static_cast<int>(chunks), Li,
+                                                        m_padded, w.base, group_sizes, nullptr,
+                                                        w.num_kept);
+  LMOE_CHECK_LAUNCH("dispatch_scan");
+  if (n > 0) {
+    DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
+                      padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
+    csort::place_kernel<<<dim3(static_cast<unsigned>(chunks)), 64, L * sizeof(int32_t), st>>>(
+        key, n, Li, csort::key_bits_for(Li), w.base, sink);
+    LMOE_CHECK_LAUNCH("dispatch_place");
+  }
+  // The gather also finalises group_sizes[L] and per_expert_counts (block 0),
+  // so it runs even when m_padded == 0.
+  const int64_t row_bytes = lat * dtype_size(x_dtype);
+  const unsigned blocks = static_cast<unsigned>(m_padded > 0 ? ceil_div(m_padded, kGatherRows) : 1);
+  if (row_bytes % 16 == 0 && aligned(x, 16) && aligned(sorted_tokens, 16)) {
+    gather_kernel<uint4><<<blocks, 256, 0, st>>>(
+        static_cast<const uint4*>(x), row_bytes / 16, w.num_kept, m_padded,
+        static_cast<uint4*>(sorted_tokens), valid, padded_token_idx, static_cast<uint8_t*>(padded_w),
+        dtype_size(w_dtype), group_sizes, per_expert_counts, Li);
+  } else {
+    gather_kernel<uint16_t><<<blocks, 256, 0, st>>>(
+        static_cast<const uint16_t*>(x), row_bytes / 2, w.num_kept, m_padded,
+        static_cast<uint16_t*>(sorted_tokens), valid, padded_token_idx,
+        static_cast<uint8_t*>(padded_w), dtype_size(w_dtype), group_sizes, per_expert_counts, Li);
+  }
+  LMOE_CHECK_LAUNCH("dispatch_gather");
+  return LMOE_OK;
+}

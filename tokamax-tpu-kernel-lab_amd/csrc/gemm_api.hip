@@ -1,0 +1,133 @@
+// C-ABI entry points of the grouped GEMMs and the MXFP4 dequantisation.
+#include "gemm_tile.h"
+
+namespace lmoe {
+namespace gemm {
+int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* name);
+int run_f32(const Params& p, int layout, hipStream_t st, const char* name);
+int run_mxfp4_scaled(const Params& p, int epi, hipStream_t st, const char* name);
+
+namespace {
+
+// Dequantise one packed byte per thread pair: thread handles 16 packed bytes
+// (32 values) when the scale group is 32, else one byte.
+__global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __restrict__ packed,
+                                                            const uint8_t* __restrict__ scale,
+                                                            int64_t rows, int64_t K, int64_t gs,
+                                                            void* __restrict__ out, int odt) {
+  const int64_t kh = K / 2;
+  const int64_t total = rows * kh;
+  const int64_t ng = K / gs;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / kh, j = i % kh;
+    const uint32_t byte = packed[i];
+    const int64_t k = 2 * j;
+    const float sc0 = e8m0_to_float(scale[r * ng + k / gs]);
+    const float sc1 = e8m0_to_float(scale[r * ng + (k + 1) / gs]);
+    const uint32_t b0 = fp4_to_bf16_bits(byte & 15u, sc0);
+    const uint32_t b1 = fp4_to_bf16_bits(byte >> 4, sc1);
+    if (odt == LMOE_BF16) {
+      reinterpret_cast<uint32_t*>(out)[i] = b0 | (b1 << 16);
+    } else {
+      float* o = static_cast<float*>(out) + r * K + k;
+      o[0] = __uint_as_float(b0 << 16);
+      o[1] = __uint_as_float(b1 << 16);
+    }
+  }
+}
+
+int check_common(const void* lhs, const void* rhs, const int32_t* gs, int64_t M, int64_t K,
+                 int64_t N, int64_t G, int zero_group, const void* out, const char* name) {
+  LMOE_CHECK_ARG(M >= 0 && K > 0 && N > 0 && G > 0, "%s: bad sizes M=%lld K=%lld N=%lld G=%lld", name,
+                 (long long)M, (long long)K, (long long)N, (long long)G);
+  LMOE_CHECK_ARG(zero_group >= -1 && zero_group < G, "%s: bad zero_group %d", name, zero_group);
+  LMOE_CHECK_ARG(M == 0 || (lhs && rhs && gs && out), "%s: null pointer", name);
+  return LMOE_OK;
+}
+
+}  // namespace
+}  // namespace gemm
+}  // namespace lmoe
+
+using namespace lmoe;
+using namespace lmoe::gemm;
+
+extern "C" int lmoe_ragged_dot(const void* lhs, int lhs_dtype, const void* rhs, int rhs_layout,
+                               const int32_t* group_sizes, int64_t M, int64_t K, int64_t N,
+                               int64_t G, int zero_group, void* out, int out_dtype, void* stream) {
+  const char* name = "ragged_dot";
+  int rc = check_common(lhs, rhs, group_sizes, M, K, N, G, zero_group, out, name);
+  if (rc) return rc;
+  LMOE_CHECK_ARG(valid_dtype(lhs_dtype) && valid_dtype(out_dtype), "%s: bad dtype", name);
+  LMOE_CHECK_ARG(rhs_layout == LMOE_RHS_GKN || rhs_layout == LMOE_RHS_GNK, "%s: bad layout %d", name,
+                 rhs_layout);
+  Params p{static_cast<const uint16_t*>(lhs), rhs, nullptr, group_sizes, M, K, N, G, zero_group,
+           out, out_dtype, 0.f, 0.f, 0};
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (lhs_dtype == LMOE_F32) return run_f32(p, rhs_layout == LMOE_RHS_GKN ? kGKN : kGNK, st, name);
+  LMOE_CHECK_SUPPORTED(K % 8 == 0 && N % 8 == 0, "%s: bf16 needs K %% 8 == 0 and N %% 8 == 0 (K=%lld N=%lld)",
+                       name, (long long)K, (long long)N);
+  LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(rhs, 16), "%s: lhs/rhs must be 16-byte aligned", name);
+  return run_bf16(p, rhs_layout == LMOE_RHS_GKN ? kGKN : kGNK, kEpiNone, st, name);
+}
+
+extern "C" int lmoe_ragged_dot_gateup_situ(const void* lhs, const void* rhs_gu, int rhs_layout,
+                                           const int32_t* group_sizes, int64_t M, int64_t K,
+                                           int64_t I, int64_t G, int zero_group, float beta,
+                                           float beta_lin, int round_before_act, void* out,
+                                           void* stream) {
+  const char* name = "ragged_dot_gateup_situ";
+  int rc = check_common(lhs, rhs_gu, group_sizes, M, K, 2 * I, G, zero_group, out, name);
+  if (rc) return rc;
+  LMOE_CHECK_ARG(rhs_layout == LMOE_RHS_GKN || rhs_layout == LMOE_RHS_GNK, "%s: bad layout %d", name,
+                 rhs_layout);
+  LMOE_CHECK_SUPPORTED(K % 8 == 0 && I % 8 == 0, "%s: needs K %% 8 == 0 and I %% 8 == 0", name);
+  LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(rhs_gu, 16), "%s: lhs/rhs must be 16-byte aligned", name);
+  Params p{static_cast<const uint16_t*>(lhs), rhs_gu, nullptr, group_sizes, M, K, 2 * I, G, zero_group,
+           out, LMOE_BF16, beta, beta_lin, round_before_act};
+  return run_bf16(p, rhs_layout == LMOE_RHS_GKN ? kGKN : kGNK, kEpiSitu,
+                  static_cast<hipStream_t>(stream), name);
+}
+
+extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_t* w_scale,
+                                     const int32_t* group_sizes, int64_t M, int64_t K, int64_t N,
+                                     int64_t G, int zero_group, int mode, int epilogue, float beta,
+                                     float beta_lin, void* out, void* stream) {
+  const char* name = "ragged_dot_mxfp4";
+  int rc = check_common(lhs, w_packed, group_sizes, M, K, N, G, zero_group, out, name);
+  if (rc) return rc;
+  LMOE_CHECK_ARG(w_scale || M == 0, "%s: null scale", name);
+  LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
+  LMOE_CHECK_SUPPORTED(K % 64 == 0, "%s: needs K %% 64 == 0 (K=%lld)", name, (long long)K);
+  LMOE_CHECK_SUPPORTED(N % (epilogue == LMOE_EPI_SITU ? 16 : 8) == 0, "%s: N=%lld", name, (long long)N);
+  LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(w_packed, 16), "%s: 16-byte alignment", name);
+  Params p{static_cast<const uint16_t*>(lhs), w_packed, w_scale, group_sizes, M, K, N, G, zero_group,
+           out, LMOE_BF16, beta, beta_lin, 1};
+  const int epi = epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (mode == LMOE_MXFP4_LDS_DEQUANT) return run_bf16(p, kMXFP4, epi, st, name);
+  if (mode == LMOE_MXFP4_SCALED_MFMA) return run_mxfp4_scaled(p, epi, st, name);
+  return fail(LMOE_ERR_INVALID, "%s: bad mode %d", name, mode);
+}
+
+extern "C" int lmoe_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, int64_t batch,
+                                  int64_t N, int64_t K, int64_t group_size, void* out, int out_dtype,
+                                  void* stream) {
+  const char* name = "mxfp4_dequant";
+  LMOE_CHECK_ARG(batch >= 0 && N >= 0 && K > 0 && K % 2 == 0 && group_size > 0 && K % group_size == 0,
+                 "%s: bad sizes N=%lld K=%lld gs=%lld", name, (long long)N, (long long)K,
+                 (long long)group_size);
+  LMOE_CHECK_ARG(valid_dtype(out_dtype), "%s: bad dtype", name);
+  const int64_t rows = batch * N;
+  if (rows == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(packed && scale && out, "%s: null pointer", name);
+  LMOE_CHECK_SUPPORTED(out_dtype == LMOE_F32 || aligned(out, 4), "%s: out alignment", name);
+  const int64_t total = rows * (K / 2);
+  const int64_t blocks64 = ceil_div(total, 256);
+  const unsigned blocks = static_cast<unsigned>(blocks64 < 65536 * 4 ? blocks64 : 65536 * 4);
+  mxfp4_dequant_kernel<<<blocks, 256, 0, static_cast<hipStream_t>(stream)>>>(packed, scale, rows, K,
+                                                                             group_size, out, out_dtype);
+  LMOE_CHECK_LAUNCH(name);
+  return LMOE_OK;
+}

@@ -1,0 +1,169 @@
+// Grouped (ragged) GEMM tile machinery for gfx950: bf16 MFMA 16x16x32, LDS
+// tiles kept K-contiguous, per-group tile scheduling computed on the device.
+//
+// A block owns one BM x BN output tile of one group.  blockIdx.y enumerates
+// the m-tiles of all groups back to back (group g has ceil(n_g / BM) of them),
+// followed by "tail" tiles that zero rows past sum(group_sizes); each block
+// finds its group with a wavefront prefix scan over group_sizes, so no host
+// synchronisation or schedule buffer is needed.  blockIdx.x is the n-tile.
+//
+// Weight tiles reach LDS in one of three ways (the only part that differs
+// between layouts):
+//   GKN   rhs[g][k][n] (n contiguous, the reference's x @ W layout): each
+//         thread loads a 4(k) x 8(n) block with four 16-byte loads and writes
+//         it transposed as eight 8-byte LDS stores, so LDS holds B^T.
+//   GNK   rhs[g][n][k] (k contiguous): straight 16-byte copies.
+//   MXFP4 packed[g][n][k/2] + scale[g][n][k/32]: each thread expands 16 packed
+//         bytes (one 32-element scale block) to 32 bf16 in registers.
+// The MFMA loop then reads 16-byte A and B fragments from LDS.
+#pragma once
+
+#include "lmoe_common.h"
+
+namespace lmoe {
+namespace gemm {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kBK = 64;
+constexpr int kPad = 8;             // bf16 elements of padding per LDS row
+constexpr int kLdsRow = kBK + kPad;  // LDS row stride (elements)
+
+enum BLayout { kGKN = 0, kGNK = 1, kMXFP4 = 2 };
+enum Epilogue { kEpiNone = 0, kEpiSitu = 1 };
+
+struct Params {
+  const uint16_t* lhs;     // (M, K) bf16
+  const void* rhs;         // layout-dependent
+  const uint8_t* scale;    // MXFP4 scales (G, N, K/32)
+  const int32_t* group_sizes;
+  int64_t M, K, N, G;      // N = full rhs width (2I for SiTU)
+  int zero_group;
+  void* out;               // (M, N) or (M, N/2) for SiTU
+  int out_dtype;
+  float beta, beta_lin;
+  int round_before_act;
+};
+
+struct TileInfo {
+  int group;     // -1: no work
+  int64_t row0;  // first output row
+  int rows;      // valid rows in this tile
+  bool zero;     // write zeros without computing
+};
+
+// Find (group, first row, rows) of m-tile `mt`.  Executed by wave 0.
+template <int BM>
+__device__ TileInfo locate_tile(const int32_t* __restrict__ gs, int64_t G, int64_t M, int zero_group,
+                                int64_t mt) {
+  const int lane = threadIdx.x % 64;
+  int64_t cum_tiles = 0, cum_rows = 0;
+  TileInfo info{-1, 0, 0, false};
+  for (int64_t g0 = 0; g0 < G; g0 += 64) {
+    const int64_t g = g0 + lane;
+    int64_t n = g < G ? gs[g] : 0;
+    n = n < 0 ? 0 : n;
+    // rows past M are never computed
+    int64_t tiles = (n + BM - 1) / BM;
+    int64_t incl_t = tiles, incl_r = n;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const int64_t yt = __shfl_up(incl_t, off, 64);
+      const int64_t yr = __shfl_up(incl_r, off, 64);
+      if (lane >= off) {
+        incl_t += yt;
+        incl_r += yr;
+      }
+    }
+    const int64_t excl_t = cum_tiles + incl_t - tiles;
+    const int64_t excl_r = cum_rows + incl_r - n;
+    if (g < G && mt >= excl_t && mt < excl_t + tiles) {
+      const int64_t local = mt - excl_t;
+      info.group = static_cast<int>(g);
+      info.row0 = excl_r + local * BM;
+      const int64_t left = n - local * BM;
+      info.rows = static_cast<int>(left < BM ? left : BM);
+      info.zero = (g == zero_group);
+    }
+    cum_tiles += __shfl(incl_t, 63, 64);
+    cum_rows += __shfl(incl_r, 63, 64);
+  }
+  // broadcast the (single) hit
+  const uint64_t hit = __ballot(info.group >= 0);
+  if (hit) {
+    const int src = __ffsll(static_cast<long long>(hit)) - 1;
+    info.group = __shfl(info.group, src, 64);
+    info.row0 = __shfl(info.row0, src, 64);
+    info.rows = __shfl(info.rows, src, 64);
+    info.zero = __shfl(static_cast<int>(info.zero), src, 64) != 0;
+  } else {
+    // tail tiles: zero rows [sum(group_sizes), M)
+    const int64_t q = mt - cum_tiles;
+    const int64_t r0 = cum_rows + q * BM;
+    if (r0 < M) {
+      info.group = 0;
+      info.row0 = r0;
+      const int64_t left = M - r0;
+      info.rows = static_cast<int>(left < BM ? left : BM);
+      info.zero = true;
+    }
+  }
+  // never touch rows >= M (group sizes summing past M are clipped)
+  if (info.group >= 0) {
+    if (info.row0 >= M) {
+      info.group = -1;
+    } else if (info.row0 + info.rows > M) {
+      info.rows = static_cast<int>(M - info.row0);
+    }
+  }
+  return info;
+}
+
+__device__ __forceinline__ float situ(float g, float u, float beta, float beta_lin) {
+  // ref.py:305-310: beta*tanh(g/beta)*sigmoid(g) * beta_lin*tanh(u/beta_lin)
+  const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-g)));
+  const float sg = __fmul_rn(__fmul_rn(beta, tanhf(__fdiv_rn(g, beta))), sig);
+  const float bu = __fmul_rn(beta_lin, tanhf(__fdiv_rn(u, beta_lin)));
+  return __fmul_rn(sg, bu);
+}
+
+// E2M1 nibble with E8M0 scale byte s -> bf16 bits, exact (value has <= 2
+// significant bits, so the f32 product truncates to bf16 without rounding).
+__device__ __forceinline__ uint32_t fp4_to_bf16_bits(uint32_t nib, float scale) {
+  const uint32_t e = (nib >> 1) & 3u, m = nib & 1u;
+  uint32_t bits;
+  if (e == 0)
+    bits = m ? 0x3f000000u : 0u;  // 0.5 or 0
+  else
+    bits = ((e + 126u) << 23) | (m << 22);  // 2^(e-1) * (1 + m/2)
+  float v = __uint_as_float(bits) * scale;
+  uint32_t r = __float_as_uint(v) >> 16;
+  return r | ((nib & 8u) << 12);  // sign (also for zero: -0.0)
+}
+
+__device__ __forceinline__ float e8m0_to_float(uint32_t s) {
+  if (s == 0) return __uint_as_float(0x00400000u);  // 2^-127 (denormal)
+  if (s == 255) return __uint_as_float(0x7f800000u);  // 2^128 overflows to inf
+  return __uint_as_float(s << 23);
+}
+
+// 16 packed bytes (32 e2m1 values, low nibble first) -> 32 bf16 (as 16 u32).
+__device__ __forceinline__ void dequant32(const uint4 p, uint32_t scale_byte, uint32_t* o) {
+  const float sc = e8m0_to_float(scale_byte);
+  const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (w[d] >> (8 * b)) & 0xffu;
+      const uint32_t lo = fp4_to_bf16_bits(byte & 15u, sc);
+      const uint32_t hi = fp4_to_bf16_bits(byte >> 4, sc);
+      o[d * 4 + b] = lo | (hi << 16);
+    }
+  }
+}
+
+}  // namespace gemm
+}  // namespace lmoe

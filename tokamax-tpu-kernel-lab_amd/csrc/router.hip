@@ -1,0 +1,188 @@
+// Router top-k (reference _router_gate, ref.py:601-631, and latent_moe_forward
+// step 1, ref.py:347-361): one 64-wide wavefront per token.
+//
+// Each lane owns the experts e = c*64 + lane (c < EPL), so the logits row is read
+// with fully coalesced loads.  Selection is k rounds of a wavefront arg-max over
+// a 64-bit key (order-preserving float bits << 32 | ~expert), which gives
+// "descending value, ties to the lower expert id" -- jax.lax.top_k's order --
+// in one max.  Only the winning lane rescans its EPL candidates per round.
+#include <cmath>
+
+#include "lmoe_common.h"
+
+namespace lmoe {
+namespace {
+
+constexpr int kWave = 64;
+constexpr int kWavesPerBlock = 4;
+
+__device__ __forceinline__ uint32_t ordered_bits(float f) {
+  if (f == 0.0f) f = 0.0f;  // -0 and +0 compare equal: canonicalise
+  uint32_t u = __float_as_uint(f);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
+    uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
+    uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
+    v = o > v ? o : v;
+  }
+  return v;
+}
+
+__device__ __forceinline__ float wave_max_f32(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum_f32(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+template <int EPL>
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int k, int act,
+    int renorm, float scale, int wdtype, int32_t* __restrict__ idx_out, void* __restrict__ w_out,
+    float* __restrict__ scores_out) {
+  const int lane = threadIdx.x % kWave;
+  const int t = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
+  if (t >= T) return;
+  const float* row = logits + static_cast<int64_t>(t) * E;
+
+  float s[EPL];
+  uint32_t key[EPL];
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = c * kWave + lane;
+    s[c] = e < E ? row[e] : -INFINITY;
+  }
+  if (act == LMOE_ACT_SOFTMAX) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) m = fmaxf(m, s[c]);
+    m = wave_max_f32(m);
+    float sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      const int e = c * kWave + lane;
+      s[c] = e < E ? expf(__fsub_rn(s[c], m)) : 0.0f;
+      sum = __fadd_rn(sum, s[c]);
+    }
+    sum = wave_sum_f32(sum);
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) s[c] = __fdiv_rn(s[c], sum);
+  } else {
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) s[c] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-s[c])));
+  }
+  uint64_t taken = 0;
+#pragma unroll
+  for (int c = 0; c < EPL; ++c) {
+    const int e = c * kWave + lane;
+    if (e < E) {
+      if (scores_out) scores_out[static_cast<int64_t>(t) * E + e] = s[c];
+      const float sel = bias ? __fadd_rn(s[c], bias[e]) : __fadd_rn(s[c], 0.0f);
+      key[c] = ordered_bits(sel);
+    } else {
+      key[c] = 0;
+      taken |= 1ull << c;
+    }
+  }
+
+  auto local_best = [&]() -> uint64_t {
+    uint64_t best = 0;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      if (!((taken >> c) & 1ull)) {
+        const uint32_t e = static_cast<uint32_t>(c * kWave + lane);
+        const uint64_t cand = (static_cast<uint64_t>(key[c]) << 32) | static_cast<uint32_t>(~e);
+        best = cand > best ? cand : best;
+      }
+    }
+    return best;
+  };
+
+  uint64_t mine = local_best();
+  int my_idx = 0;
+  float my_w = 0.0f;
+  float sum = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    const uint64_t win = wave_max_u64(mine);
+    const int e = static_cast<int>(~static_cast<uint32_t>(win));
+    const int wl = e % kWave;
+    const int wc = e / kWave;
+    float v = 0.0f;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) v = (c == wc) ? s[c] : v;
+    const float w = __shfl(v, wl, kWave);
+    if (lane == wl) {
+      taken |= 1ull << wc;
+      mine = local_best();
+    }
+    if (lane == j) {
+      my_idx = e;
+      my_w = w;
+    }
+    sum = __fadd_rn(sum, w);
+  }
+  if (lane < k) {
+    float w = my_w;
+    if (renorm && k > 1) w = __fdiv_rn(w, __fadd_rn(sum, 1e-20f));
+    w = __fmul_rn(w, scale);
+    const int64_t o = static_cast<int64_t>(t) * k + lane;
+    idx_out[o] = my_idx;
+    store_from_f32(w_out, o, w, wdtype);
+  }
+}
+
+template <int EPL>
+void launch_router(const float* logits, const float* bias, int T, int E, int k, int act, int renorm,
+                   float scale, int wdtype, int32_t* idx, void* w, float* scores, hipStream_t st) {
+  dim3 grid(static_cast<unsigned>(ceil_div(T, kWavesPerBlock)));
+  router_topk_kernel<EPL><<<grid, 256, 0, st>>>(logits, bias, T, E, k, act, renorm, scale, wdtype,
+                                                 idx, w, scores);
+}
+
+}  // namespace
+}  // namespace lmoe
+
+extern "C" int lmoe_router_topk(const float* logits, const float* bias, int64_t T, int64_t E,
+                                int64_t k, int act, int renorm, float scale, int weight_dtype,
+                                int32_t* topk_idx, void* topk_w, float* scores_out, void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(T >= 0 && E > 0 && k > 0, "router_topk: bad sizes T=%lld E=%lld k=%lld",
+                 (long long)T, (long long)E, (long long)k);
+  LMOE_CHECK_ARG(k <= E, "router_topk: k=%lld > E=%lld", (long long)k, (long long)E);
+  LMOE_CHECK_SUPPORTED(k <= 64, "router_topk: k=%lld > 64", (long long)k);
+  LMOE_CHECK_SUPPORTED(E <= 4096, "router_topk: E=%lld > 4096", (long long)E);
+  LMOE_CHECK_ARG(act == LMOE_ACT_SIGMOID || act == LMOE_ACT_SOFTMAX, "router_topk: bad act %d", act);
+  LMOE_CHECK_ARG(valid_dtype(weight_dtype), "router_topk: bad weight dtype %d", weight_dtype);
+  LMOE_CHECK_ARG(T <= (1ll << 30), "router_topk: T too large");
+  if (T == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(logits && topk_idx && topk_w, "router_topk: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int epl = static_cast<int>(ceil_div(E, 64));
+  const int Ti = static_cast<int>(T), Ei = static_cast<int>(E), ki = static_cast<int>(k);
+#define LMOE_ROUTER_CASE(N)                                                                   \
+  if (epl <= N) {                                                                             \
+    launch_router<N>(logits, bias, Ti, Ei, ki, act, renorm, scale, weight_dtype, topk_idx,    \
+                     topk_w, scores_out, st);                                                 \
+    LMOE_CHECK_LAUNCH("router_topk");                                                         \
+    return LMOE_OK;                                                                           \
+  }
+  LMOE_ROUTER_CASE(1)
+  LMOE_ROUTER_CASE(2)
+  LMOE_ROUTER_CASE(4)
+  LMOE_ROUTER_CASE(8)
+  LMOE_ROUTER_CASE(16)
+  LMOE_ROUTER_CASE(32)
+  LMOE_ROUTER_CASE(64)
+#undef LMOE_ROUTER_CASE
+  return fail(LMOE_ERR_UNSUPPORTED, "router_topk: E=%lld", (long long)E);
+}

@@ -1,0 +1,201 @@
+"""LatentMoE forwards on the HIP kernels, keeping the reference's entry points.
+
+* ``latent_moe_forward`` / ``latent_moe_forward_ragged_dot`` -- the unsharded
+  8-step forward (ref.py:330-435, rd.py:317-391): dispatch over all E experts,
+  f32 weighted combine.
+* ``latent_moe_forward_ragged_dot_single_shard_jittable`` -- one local shard
+  as the whole routed population (rd.py:1035-1137), the production path.
+* ``LocalShardLatentMoE`` -- the same single-shard forward on weights prepared
+  once (k-contiguous bf16 or MXFP4 checkpoint layout), used by the benchmark.
+
+ref.py = 05_ragged_dot_on_tpu/kimi_k3_latent_moe_reference.py,
+rd.py = 05_ragged_dot_on_tpu/kimi_k3_latent_moe_ragged_dot.py.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import ops
+from .config import LatentMoEConfig, LatentMoEWeights
+
+
+def _stage_order_from_slot_pos(slot_pos: torch.Tensor, m: int) -> torch.Tensor:
+  """Dispatch permutation (row -> flat slot) from its inverse, for reporting."""
+  order = torch.full((m,), -1, dtype=torch.int64, device=slot_pos.device)
+  s = torch.arange(slot_pos.numel(), device=slot_pos.device)
+  keep = slot_pos >= 0
+  order[slot_pos[keep].long()] = s[keep]
+  return order
+
+
+def latent_moe_forward(hidden_states: torch.Tensor, weights: LatentMoEWeights, config: LatentMoEConfig,
+                       act: str = "sigmoid", return_intermediates: bool = False,
+                       implementation: str | None = None):
+  """Unsharded forward, ref.py:330-435.  Gate math in f32, combine weight kept
+  f32 through the weighted sum (ref.py:357-361, 413-416)."""
+  if implementation not in (None, "hip"):
+    raise NotImplementedError(f"implementation={implementation!r}")
+  W = weights
+  t = hidden_states.shape[0]
+  k, e = config.top_k, config.num_experts
+  b, bl = config.activation_situ_beta, config.activation_situ_linear_beta
+  logits = ops.router_logits(hidden_states, W.router_weight)
+  idx, w, scores = ops.router_topk_from_logits(logits, W.e_score_correction_bias, k, config.moe_renormalize,
+                                               config.routed_scaling_factor, act, torch.float32,
+                                               return_scores=True)
+  x = ops.dense(hidden_states, W.down_proj)
+  d = ops.dispatch_local(idx, w, x, 0, e, t * k)  # every slot kept: no truncation, empty pad group
+  gs = d.group_sizes[:e]
+  gate = ops.ragged_dot(d.sorted_tokens, W.expert_gate, gs)
+  up = ops.ragged_dot(d.sorted_tokens, W.expert_up, gs)
+  situ = ops._situ_and_mul(gate, up, b, bl)
+  down = ops.ragged_dot(situ, W.expert_down, gs)
+  routed = ops.combine_slots(down, d.slot_pos, w, t, k, mode="slot_sum", out_dtype=hidden_states.dtype)
+  normed = ops._rms_norm(routed, W.norm_scale, config.rms_norm_eps)
+  up_out = ops.dense(normed, W.up_proj)
+  shared = ops._situ_glu_mlp(hidden_states, W.shared_gate, W.shared_up, W.shared_down, b, bl)
+  final = ops.add(up_out, shared)
+  if not return_intermediates:
+    return final
+  bias = W.e_score_correction_bias
+  inter = {
+      "router_logits": logits,
+      "router_scores_before_bias": scores,
+      "router_scores_for_choice": scores + (bias.float() if bias is not None else 0.0),
+      "topk_indices": idx,
+      "topk_weights": w,
+      "latent_projection": x,
+      "sorted_token_indices": _stage_order_from_slot_pos(d.slot_pos, t * k),
+      "group_sizes": gs,
+      "expert_gate_output": gate,
+      "expert_up_output": up,
+      "situ_output": situ,
+      "expert_down_output": down,
+      "routed_output_before_combine": down[d.slot_pos.long()],
+      "routed_output_after_combine": routed,
+      "normalized_output": normed,
+      "up_projection_output": up_out,
+      "shared_expert_output": shared,
+      "final_output": final,
+  }
+  return final, inter
+
+
+def latent_moe_forward_ragged_dot(hidden_states, weights, config, implementation=None, **kw):
+  """rd.py:317-391 -- the same forward with the expert FFN as three ragged_dots."""
+  return latent_moe_forward(hidden_states, weights, config, implementation=implementation, **kw)
+
+
+def latent_moe_forward_ragged_dot_single_shard_jittable(
+    hidden_states, router_weight, e_score_correction_bias, down_proj, shard_expert_gate,
+    shard_expert_up, shard_expert_down, norm_scale, up_proj, shared_gate, shared_up, shared_down,
+    config: LatentMoEConfig, local_expert_start: int, local_num_experts: int,
+    capacity_factor: float = 2.0, implementation: str | None = None, act: str = "sigmoid",
+    return_stages: bool = False, fused_gateup: bool = False):
+  """rd.py:1035-1137.  shard_expert_* carry local_num_experts + 1 rows (the
+  last is the padding bucket, computed as exact zeros without reading its
+  weights).  shared_* may be None when the layer has no shared experts."""
+  if implementation not in (None, "hip"):
+    raise NotImplementedError(f"implementation={implementation!r}")
+  t = hidden_states.shape[0]
+  L = local_num_experts
+  dt = hidden_states.dtype
+  b, bl = config.activation_situ_beta, config.activation_situ_linear_beta
+  x = ops.dense(hidden_states, down_proj)
+  logits = ops.router_logits(hidden_states, router_weight)
+  idx, w = ops.router_topk_from_logits(logits, e_score_correction_bias, config.top_k,
+                                       config.moe_renormalize, config.routed_scaling_factor, act, dt)
+  m_padded = ops.compute_m_padded(t, config.top_k, config.num_experts, L, capacity_factor)
+  d = ops.dispatch_local(idx, w, x, local_expert_start, L, m_padded)
+  if fused_gateup:
+    shard_out = ops._local_shard_expert_ffn_ragged_dot_fused_gateup(
+        d.sorted_tokens, shard_expert_gate, shard_expert_up, shard_expert_down, d.group_sizes, config,
+        zero_group=L)
+  else:
+    shard_out = ops._local_shard_expert_ffn_ragged_dot(d.sorted_tokens, shard_expert_gate,
+                                                       shard_expert_up, shard_expert_down,
+                                                       d.group_sizes, config, zero_group=L)
+  routed = ops.combine_slots(shard_out, d.slot_pos, d.padded_combine_weight, t, config.top_k,
+                             mode="scatter_add", out_dtype=dt)
+  normed = ops._rms_norm(routed, norm_scale, config.rms_norm_eps)
+  up = ops.dense(normed, up_proj)
+  if shared_gate is not None:
+    shared = ops._situ_glu_mlp(hidden_states, shared_gate, shared_up, shared_down, b, bl)
+    final = ops.add(up, shared)
+  else:
+    final = up
+  if not return_stages:
+    return final
+  return final, {"x": x, "router_logits": logits, "topk_idx": idx, "topk_weight": w, "dispatch": d,
+                 "shard_out": shard_out, "routed_out": routed, "normed": normed, "up": up}
+
+
+class LocalShardLatentMoE:
+  """Single-shard LatentMoE layer on weights prepared once.
+
+  ``expert_format``: "bf16" (gate/up prefused to (L+1, 2I, K) and down to
+  (L+1, lat, I), k-contiguous) or "mxfp4" (checkpoint layout: gate/up packed
+  (L+1, 2I, lat/2) + scales (L+1, 2I, lat/32), down (L+1, lat, I/2) +
+  (L+1, lat, I/32)).  Dense projections are stored (N, K).  Stages:
+  router logits GEMM, down-projection GEMM, top-k, dispatch, fused gate/up +
+  SiTU GEMM, down GEMM, combine, RMSNorm, up-projection GEMM (+ the shared
+  expert MLP when given).
+  """
+
+  def __init__(self, config: LatentMoEConfig, *, router_weight, e_score_correction_bias, down_proj,
+               up_proj, norm_scale, local_expert_start: int, local_num_experts: int,
+               expert_format: str, experts: dict, shared: dict | None = None,
+               capacity_factor: float = 2.0, act: str = "sigmoid", mxfp4_mode: str = "lds_dequant"):
+    self.config = config
+    self.L = local_num_experts
+    self.start = local_expert_start
+    self.cf = capacity_factor
+    self.act = act
+    self.expert_format = expert_format
+    self.mxfp4_mode = mxfp4_mode
+    self.router_nk = router_weight.t().contiguous()
+    self.bias = e_score_correction_bias.float().contiguous()
+    self.down_nk = down_proj.t().contiguous()
+    self.up_nk = up_proj.t().contiguous()
+    self.norm_scale = norm_scale.contiguous()
+    self.experts = experts
+    self.shared = shared
+
+  def _dense(self, x, w_nk, out_dtype=None):
+    return ops.dense(x, w_nk, out_dtype=out_dtype, w_layout="nk")
+
+  def forward(self, hidden: torch.Tensor, return_stages: bool = False):
+    c = self.config
+    t = hidden.shape[0]
+    b, bl = c.activation_situ_beta, c.activation_situ_linear_beta
+    logits = self._dense(hidden, self.router_nk, torch.float32)
+    x = self._dense(hidden, self.down_nk)
+    idx, w = ops.router_topk_from_logits(logits, self.bias, c.top_k, c.moe_renormalize,
+                                         c.routed_scaling_factor, self.act, hidden.dtype)
+    m_padded = ops.compute_m_padded(t, c.top_k, c.num_experts, self.L, self.cf)
+    d = ops.dispatch_local(idx, w, x, self.start, self.L, m_padded)
+    E = self.experts
+    if self.expert_format == "mxfp4":
+      act = ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed"], E["gu_scale"], d.group_sizes,
+                                 fuse_gateup_activation=f"situ:{b}:{bl}", mode=self.mxfp4_mode,
+                                 zero_group=self.L)
+      shard_out = ops.ragged_dot_mxfp4(act, E["down_packed"], E["down_scale"], d.group_sizes,
+                                       mode=self.mxfp4_mode, zero_group=self.L)
+    else:
+      act = ops.ragged_dot_gateup_situ(d.sorted_tokens, E["gu_nk"], d.group_sizes, b, bl,
+                                       rhs_layout="gnk", zero_group=self.L)
+      shard_out = ops.ragged_dot(act, E["down_nk"], d.group_sizes, rhs_layout="gnk", zero_group=self.L)
+    routed = ops.combine_slots(shard_out, d.slot_pos, d.padded_combine_weight, t, c.top_k,
+                               mode="scatter_add", out_dtype=hidden.dtype)
+    normed = ops._rms_norm(routed, self.norm_scale, c.rms_norm_eps)
+    out = self._dense(normed, self.up_nk)
+    if self.shared is not None:
+      S = self.shared
+      sact = ops.ragged_dot_gateup_situ(hidden, S["gu_nk"], ops._ones_group(t, hidden.device), b, bl,
+                                        rhs_layout="gnk")
+      out = ops.add(out, self._dense(sact, S["down_nk"]))
+    if not return_stages:
+      return out
+    return out, {"router_logits": logits, "x": x, "topk_idx": idx, "topk_weight": w, "dispatch": d,
+                 "act": act, "shard_out": shard_out, "routed_out": routed, "normed": normed}

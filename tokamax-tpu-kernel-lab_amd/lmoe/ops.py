@@ -1,0 +1,509 @@
+"""Reference-shaped operators of the LatentMoE expert hot path on the HIP kernels.
+
+Each function keeps the name, argument meaning, output dtype and error
+behaviour of the reference function it replaces (cited file:line, reference
+paths relative to the reference repository; ref.py =
+05_ragged_dot_on_tpu/kimi_k3_latent_moe_reference.py, rd.py =
+05_ragged_dot_on_tpu/kimi_k3_latent_moe_ragged_dot.py).  Tensors are torch
+tensors on the GPU; outputs are new tensors (the reference's JAX arrays are
+immutable).  Every operator runs a kernel of liblmoe.so on the current torch
+stream; nothing falls back to torch or the CPU.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import NamedTuple
+
+import torch
+
+from . import _lib
+from ._lib import check, lib
+
+MOSAIC_TILE_SIZE = 128  # ref.py:149
+
+_DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
+
+
+def _dt(t: torch.Tensor) -> int:
+  try:
+    return _DT[t.dtype]
+  except KeyError:
+    raise NotImplementedError(f"dtype {t.dtype} is not supported (bf16 / f32 only)") from None
+
+
+def _dev(*ts: torch.Tensor) -> None:
+  for t in ts:
+    if t is None:
+      continue
+    if not t.is_cuda:
+      raise ValueError("LatentMoE operators need GPU tensors (no CPU fallback)")
+    if not t.is_contiguous():
+      raise ValueError("LatentMoE operators need contiguous tensors")
+
+
+def _p(t: torch.Tensor | None) -> int | None:
+  return None if t is None else t.data_ptr()
+
+
+def _stream() -> int:
+  return torch.cuda.current_stream().cuda_stream
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor:
+  return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+# ---------------------------------------------------------------------------
+# a9 / a12: grouped GEMMs
+# ---------------------------------------------------------------------------
+
+
+def ragged_dot(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor, precision=None,
+               implementation: str | None = None, preferred_element_type: torch.dtype | None = None,
+               *, rhs_layout: str = "gkn", zero_group: int = -1) -> torch.Tensor:
+  """``tokamax.ragged_dot(lhs, rhs, group_sizes)`` (call shape rd.py:358-369).
+
+  lhs (M, K); rhs (G, K, N) for ``rhs_layout="gkn"`` (the reference layout) or
+  (G, N, K) for ``"gnk"`` (prepared, k-contiguous); group_sizes (G,) int32 on
+  the device (never read on the host).  Output (M, N) in lhs dtype (or
+  ``preferred_element_type``); rows past sum(group_sizes) are zero.
+  ``implementation`` accepts only None / "hip": there is one backend.
+  ``precision`` is accepted for signature compatibility: f32 operands are
+  always computed at full f32 precision (the reference needs
+  Precision.HIGHEST for that, trg.py:150-163).
+  ``zero_group`` names a group computed as exact zeros without reading its
+  weights (the padding bucket, whose rows are zero).
+  """
+  if implementation not in (None, "hip"):
+    raise NotImplementedError(f"implementation={implementation!r}: only the HIP backend exists")
+  _dev(lhs, rhs, group_sizes)
+  if lhs.dim() != 2 or rhs.dim() != 3:
+    raise ValueError(f"ragged_dot: lhs {tuple(lhs.shape)} / rhs {tuple(rhs.shape)} ranks")
+  if group_sizes.dtype != torch.int32:
+    raise ValueError("group_sizes must be int32")
+  m, k = lhs.shape
+  g = rhs.shape[0]
+  if rhs_layout == "gkn":
+    layout, kk, n = _lib.RHS_GKN, rhs.shape[1], rhs.shape[2]
+  elif rhs_layout == "gnk":
+    layout, n, kk = _lib.RHS_GNK, rhs.shape[1], rhs.shape[2]
+  else:
+    raise ValueError(f"rhs_layout {rhs_layout!r}")
+  if kk != k or group_sizes.shape != (g,):
+    raise ValueError(f"ragged_dot: shapes lhs {tuple(lhs.shape)} rhs {tuple(rhs.shape)} "
+                     f"group_sizes {tuple(group_sizes.shape)}")
+  if rhs.dtype != lhs.dtype:
+    raise NotImplementedError(f"mixed lhs {lhs.dtype} / rhs {rhs.dtype}")
+  out_dtype = preferred_element_type or lhs.dtype
+  out = torch.empty((m, n), dtype=out_dtype, device=lhs.device)
+  check(lib().lmoe_ragged_dot(_p(lhs), _dt(lhs), _p(rhs), layout, _p(group_sizes), m, k, n, g,
+                              zero_group, _p(out), _dt(out), _stream()), "ragged_dot")
+  return out
+
+
+def parse_fused_activation(spec: str) -> tuple[float, float]:
+  """"situ:<beta>:<linear_beta>" (the op-class string of rd.py:713-720)."""
+  parts = spec.split(":")
+  if len(parts) != 3 or parts[0] != "situ":
+    raise NotImplementedError(f"fuse_gateup_activation={spec!r}: only 'situ:<beta>:<beta_lin>'")
+  return float(parts[1]), float(parts[2])
+
+
+def ragged_dot_gateup_situ(lhs: torch.Tensor, rhs_gu: torch.Tensor, group_sizes: torch.Tensor,
+                           beta: float, linear_beta: float, *, rhs_layout: str = "gkn",
+                           zero_group: int = -1, round_before_act: bool = True) -> torch.Tensor:
+  """One grouped GEMM against the prefused [gate | up] weight with the SiTU-GLU
+  epilogue in registers (rd.py:644-723; gate/up rounded to bf16 before SiTU as
+  in gk.py:114-125).  rhs_gu (G, K, 2I) ("gkn") or (G, 2I, K) ("gnk"); out (M, I)."""
+  _dev(lhs, rhs_gu, group_sizes)
+  if lhs.dtype != torch.bfloat16 or rhs_gu.dtype != torch.bfloat16:
+    raise NotImplementedError("fused gate/up SiTU is bf16 only")
+  m, k = lhs.shape
+  g = rhs_gu.shape[0]
+  if rhs_layout == "gkn":
+    layout, kk, n2 = _lib.RHS_GKN, rhs_gu.shape[1], rhs_gu.shape[2]
+  elif rhs_layout == "gnk":
+    layout, n2, kk = _lib.RHS_GNK, rhs_gu.shape[1], rhs_gu.shape[2]
+  else:
+    raise ValueError(f"rhs_layout {rhs_layout!r}")
+  if kk != k or n2 % 2:
+    raise ValueError(f"gateup shapes lhs {tuple(lhs.shape)} rhs {tuple(rhs_gu.shape)}")
+  inter = n2 // 2
+  out = torch.empty((m, inter), dtype=torch.bfloat16, device=lhs.device)
+  check(lib().lmoe_ragged_dot_gateup_situ(_p(lhs), _p(rhs_gu), layout, _p(group_sizes), m, k, inter,
+                                          g, zero_group, beta, linear_beta, int(round_before_act),
+                                          _p(out), _stream()), "ragged_dot_gateup_situ")
+  return out
+
+
+class HipRaggedDot:
+  """Op-class form of the grouped GEMM, mirroring how the reference reaches
+  the fused and scaled paths through ``PallasMosaicTpuV2RaggedDot()(...)``
+  (rd.py:713-720, rd.py:2804-2811): ``op(lhs, rhs, group_sizes=...,
+  fuse_gateup_activation="situ:b:bl", rhs_scale=...)``.  With ``rhs_scale``
+  the rhs is MXFP4 in checkpoint layout (G, N, K/2) u8 and rhs_scale is
+  (G, N, K/32) u8 E8M0."""
+
+  def __init__(self, mxfp4_mode: str = "lds_dequant"):
+    self.mxfp4_mode = mxfp4_mode
+
+  def __call__(self, lhs, rhs, *, group_sizes, rhs_scale=None, fuse_gateup_activation=None,
+               maybe_quantize_lhs=False, rhs_layout="gkn", zero_group=-1):
+    if maybe_quantize_lhs:
+      raise NotImplementedError("maybe_quantize_lhs")
+    if rhs_scale is not None:
+      return ragged_dot_mxfp4(lhs, rhs, rhs_scale, group_sizes,
+                              fuse_gateup_activation=fuse_gateup_activation, mode=self.mxfp4_mode,
+                              zero_group=zero_group)
+    if fuse_gateup_activation is not None:
+      b, bl = parse_fused_activation(fuse_gateup_activation)
+      return ragged_dot_gateup_situ(lhs, rhs, group_sizes, b, bl, rhs_layout=rhs_layout,
+                                    zero_group=zero_group)
+    return ragged_dot(lhs, rhs, group_sizes, rhs_layout=rhs_layout, zero_group=zero_group)
+
+
+def prefuse_gateup_weights(expert_gate: torch.Tensor, expert_up: torch.Tensor) -> torch.Tensor:
+  """rd.py:610-641: plain concatenation [gate | up] on the last (N) axis."""
+  return torch.cat([expert_gate, expert_up], dim=-1).contiguous()
+
+
+def prefuse_gateup_weights_gnk(expert_gate: torch.Tensor, expert_up: torch.Tensor) -> torch.Tensor:
+  """The same prefused weight in the k-contiguous (G, 2I, K) layout the MFMA
+  tiles read with plain 16-byte loads; done once at weight-load time."""
+  return torch.cat([expert_gate, expert_up], dim=-1).transpose(1, 2).contiguous()
+
+
+def to_gnk(w: torch.Tensor) -> torch.Tensor:
+  """(G, K, N) -> (G, N, K) contiguous (weight preparation, outside timed regions)."""
+  return w.transpose(1, 2).contiguous()
+
+
+# ---------------------------------------------------------------------------
+# a17 / a18: MXFP4
+# ---------------------------------------------------------------------------
+
+
+def dequantize_mxfp4(weight_packed: torch.Tensor, weight_scale: torch.Tensor,
+                     out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+  """``dequantize_mxfp4`` (mxfp4_dequant.py:29-67): packed (..., N, K/2) u8,
+  scale (..., N, K/gs) u8 -> (..., N, K) float32 (bit-exact)."""
+  _dev(weight_packed, weight_scale)
+  if weight_packed.dtype != torch.uint8 or weight_scale.dtype != torch.uint8:
+    raise ValueError("packed / scale must be uint8")
+  *lead, n, kh = weight_packed.shape
+  k = kh * 2
+  ng = weight_scale.shape[-1]
+  if tuple(weight_scale.shape[:-1]) != (*lead, n) or ng == 0 or k % ng:
+    raise ValueError(f"scale shape {tuple(weight_scale.shape)} vs packed {tuple(weight_packed.shape)}")
+  batch = math.prod(lead) if lead else 1
+  out = torch.empty((*lead, n, k), dtype=out_dtype, device=weight_packed.device)
+  check(lib().lmoe_mxfp4_dequant(_p(weight_packed), _p(weight_scale), batch, n, k, k // ng, _p(out),
+                                 _dt(out), _stream()), "mxfp4_dequant")
+  return out
+
+
+_MX_MODES = {"lds_dequant": _lib.MXFP4_LDS_DEQUANT, "scaled_mfma": _lib.MXFP4_SCALED_MFMA}
+
+
+def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+                     group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
+                     mode: str = "lds_dequant", zero_group: int = -1) -> torch.Tensor:
+  """Grouped lhs @ deq(W_g)^T with W_g in checkpoint (N, K/2) layout
+  (orientation of mxfp4_online_dequant_matmul_pallas.py:1-36), block-32 E8M0
+  scales (G, N, K/32).  With ``fuse_gateup_activation`` the N axis is
+  [gate | up] and the SiTU-GLU epilogue is applied (output width N/2)."""
+  _dev(lhs, w_packed, w_scale, group_sizes)
+  if lhs.dtype != torch.bfloat16:
+    raise NotImplementedError("MXFP4 GEMM takes bf16 activations")
+  m, k = lhs.shape
+  g, n, kh = w_packed.shape
+  if kh * 2 != k or tuple(w_scale.shape) != (g, n, k // 32):
+    raise ValueError(f"mxfp4 shapes lhs {tuple(lhs.shape)} packed {tuple(w_packed.shape)} "
+                     f"scale {tuple(w_scale.shape)}")
+  epi, b, bl = _lib.EPI_NONE, 0.0, 0.0
+  width = n
+  if fuse_gateup_activation is not None:
+    b, bl = parse_fused_activation(fuse_gateup_activation)
+    epi, width = _lib.EPI_SITU, n // 2
+  if mode not in _MX_MODES:
+    raise ValueError(f"mode {mode!r}")
+  out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
+  check(lib().lmoe_ragged_dot_mxfp4(_p(lhs), _p(w_packed), _p(w_scale), _p(group_sizes), m, k, n, g,
+                                    zero_group, _MX_MODES[mode], epi, b, bl, _p(out), _stream()),
+        "ragged_dot_mxfp4")
+  return out
+
+
+# ---------------------------------------------------------------------------
+# a3 / a4: router
+# ---------------------------------------------------------------------------
+
+_ACTS = {"sigmoid": _lib.ACT_SIGMOID, "softmax": _lib.ACT_SOFTMAX}
+
+
+def router_topk_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top_k: int,
+                            renormalize: bool = True, scaling: float = 1.0, act: str = "sigmoid",
+                            weight_dtype: torch.dtype = torch.float32, return_scores: bool = False):
+  """Gate math of ref.py:347-361 / ref.py:601-631 on given f32 logits (T, E):
+  returns (topk_idx int32 (T, k), topk_weight (T, k) weight_dtype[, scores])."""
+  _dev(logits, bias)
+  if logits.dtype != torch.float32:
+    raise ValueError("router logits must be float32 (the reference's gate runs in f32)")
+  if bias is not None and bias.dtype != torch.float32:
+    bias = bias.float().contiguous()
+  t, e = logits.shape
+  idx = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
+  w = torch.empty((t, top_k), dtype=weight_dtype, device=logits.device)
+  scores = torch.empty((t, e), dtype=torch.float32, device=logits.device) if return_scores else None
+  check(lib().lmoe_router_topk(_p(logits), _p(bias), t, e, top_k, _ACTS[act], int(renormalize),
+                               scaling, _dt(w), _p(idx), _p(w), _p(scores), _stream()), "router_topk")
+  return (idx, w, scores) if return_scores else (idx, w)
+
+
+def _ones_group(m: int, device) -> torch.Tensor:
+  return torch.tensor([m], dtype=torch.int32, device=device)
+
+
+def dense(x: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None,
+          w_layout: str = "kn") -> torch.Tensor:
+  """x @ w as a one-group grouped GEMM on the same kernels (w (K, N), or
+  (N, K) with w_layout="nk")."""
+  rhs = w.unsqueeze(0)
+  return ragged_dot(x, rhs, _ones_group(x.shape[0], x.device), preferred_element_type=out_dtype,
+                    rhs_layout="gkn" if w_layout == "kn" else "gnk")
+
+
+def router_logits(hidden: torch.Tensor, router_weight: torch.Tensor) -> torch.Tensor:
+  """``f32(hidden) @ f32(router_weight)`` (ref.py:620).  For bf16 operands the
+  products are exact in f32, so the bf16 MFMA with f32 accumulation computes
+  the same f32 matmul (up to summation order)."""
+  if hidden.dtype == router_weight.dtype:
+    return dense(hidden, router_weight, out_dtype=torch.float32)
+  return dense(hidden.float(), router_weight.float(), out_dtype=torch.float32)
+
+
+def _router_gate(hidden_states: torch.Tensor, router_weight: torch.Tensor,
+                 e_score_correction_bias: torch.Tensor, config, act: str = "sigmoid"):
+  """ref.py:601-631: f32 gate math, combine weight cast to the compute dtype."""
+  logits = router_logits(hidden_states, router_weight)
+  return router_topk_from_logits(logits, e_score_correction_bias, config.top_k,
+                                 config.moe_renormalize, config.routed_scaling_factor, act,
+                                 hidden_states.dtype)
+
+
+def router_and_projection(hidden_states, router_weight, e_score_correction_bias, down_proj, config):
+  """ref.py:634-655: _router_gate plus x = hidden @ down_proj."""
+  topk_idx, topk_weight = _router_gate(hidden_states, router_weight, e_score_correction_bias, config)
+  return topk_idx, topk_weight, dense(hidden_states, down_proj)
+
+
+# ---------------------------------------------------------------------------
+# a6 / a7: local-shard dispatch
+# ---------------------------------------------------------------------------
+
+
+def round_up_to_tile(value: int, tile_size: int = MOSAIC_TILE_SIZE) -> int:
+  """ref.py:152-153."""
+  return -(-value // tile_size) * tile_size
+
+
+def compute_m_padded(num_tokens: int, top_k: int, num_experts: int, local_num_experts: int,
+                     capacity_factor: float = 2.0, tile_size: int = MOSAIC_TILE_SIZE) -> int:
+  """ref.py:825-826: round_up(ceil(T*k*L/E * cf), tile), static per config."""
+  expected_total = num_tokens * top_k * local_num_experts / num_experts
+  return round_up_to_tile(math.ceil(expected_total * capacity_factor), tile_size)
+
+
+class Dispatch(NamedTuple):
+  sorted_tokens: torch.Tensor
+  group_sizes: torch.Tensor
+  valid_mask: torch.Tensor
+  per_expert_counts: torch.Tensor
+  padded_token_idx: torch.Tensor
+  padded_combine_weight: torch.Tensor
+  slot_pos: torch.Tensor
+
+
+def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.Tensor,
+                   local_expert_start: int, local_num_experts: int, m_padded: int) -> Dispatch:
+  """The GPU dispatch with an explicit m_padded; also returns slot_pos (T*k,)."""
+  _dev(topk_idx, topk_weight, x)
+  if topk_idx.dtype != torch.int32:
+    raise ValueError("topk_idx must be int32")
+  t, k = topk_idx.shape
+  lat = x.shape[-1]
+  dev = x.device
+  L = local_num_experts
+  sorted_tokens = torch.empty((m_padded, lat), dtype=x.dtype, device=dev)
+  group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
+  valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
+  counts = torch.empty((L,), dtype=torch.int32, device=dev)
+  tok = torch.empty((m_padded,), dtype=torch.int32, device=dev)
+  w = torch.empty((m_padded,), dtype=topk_weight.dtype, device=dev)
+  slot_pos = torch.empty((t * k,), dtype=torch.int32, device=dev)
+  ws_bytes = lib().lmoe_dispatch_workspace_size(t, k, L)
+  ws = _workspace(ws_bytes, dev)
+  check(lib().lmoe_dispatch_local(_p(topk_idx), _p(topk_weight), _dt(topk_weight), _p(x), _dt(x), t, k,
+                                  lat, local_expert_start, L, m_padded, _p(sorted_tokens),
+                                  _p(group_sizes), _p(valid), _p(counts), _p(tok), _p(w), _p(slot_pos),
+                                  _p(ws), ws.numel(), _stream()), "dispatch_local")
+  return Dispatch(sorted_tokens, group_sizes, valid, counts, tok, w, slot_pos)
+
+
+def filter_and_pad_to_shard_jittable(topk_idx, topk_weight, x, config, local_expert_start: int,
+                                     local_num_experts: int, capacity_factor: float = 2.0,
+                                     tile_size: int = MOSAIC_TILE_SIZE):
+  """ref.py:754-877: returns (sorted_tokens, group_sizes, valid_mask,
+  per_expert_counts, padded_token_idx, padded_combine_weight)."""
+  m_padded = compute_m_padded(topk_idx.shape[0], config.top_k, config.num_experts, local_num_experts,
+                              capacity_factor, tile_size)
+  return tuple(dispatch_local(topk_idx, topk_weight, x, local_expert_start, local_num_experts,
+                              m_padded)[:6])
+
+
+def filter_and_pad_to_shard(topk_idx, topk_weight, x, config, local_expert_start: int,
+                            local_num_experts: int, capacity_factor: float = 2.0,
+                            tile_size: int = MOSAIC_TILE_SIZE):
+  """ref.py:658-751.  The reference proves its eager and jittable dispatches
+  bit-identical (ref.py:880-939), so both names run the same fixed-shape GPU
+  dispatch (no host sync); the eager overflow warning print is not emitted."""
+  return filter_and_pad_to_shard_jittable(topk_idx, topk_weight, x, config, local_expert_start,
+                                          local_num_experts, capacity_factor, tile_size)
+
+
+def route_and_filter_to_local_shard_jittable(hidden_states, x, router_weight, e_score_correction_bias,
+                                             config, local_expert_start, local_num_experts,
+                                             capacity_factor=2.0, tile_size=MOSAIC_TILE_SIZE):
+  """ref.py:1382-1416: _router_gate then the jittable dispatch."""
+  topk_idx, topk_weight = _router_gate(hidden_states, router_weight, e_score_correction_bias, config)
+  return filter_and_pad_to_shard_jittable(topk_idx, topk_weight, x, config, local_expert_start,
+                                          local_num_experts, capacity_factor, tile_size)
+
+
+route_and_filter_to_local_shard = route_and_filter_to_local_shard_jittable  # ref.py:1144-1187
+
+
+# ---------------------------------------------------------------------------
+# a13: combine
+# ---------------------------------------------------------------------------
+
+
+def _combine_shard_contribution(routed_out: torch.Tensor, shard_out: torch.Tensor,
+                                padded_token_idx: torch.Tensor,
+                                padded_combine_weight: torch.Tensor) -> torch.Tensor:
+  """ref.py:1113-1141: routed_out.at[idx].add((shard_out * w).astype(routed_out.dtype)),
+  returned as a new tensor.  Rows are added per token in ascending row order
+  with the output dtype's rounding after every add (the reference's scatter
+  order); idx -1 rows (padding, weight 0) are skipped."""
+  _dev(routed_out, shard_out, padded_token_idx, padded_combine_weight)
+  out = routed_out.clone()
+  m, lat = shard_out.shape
+  t = routed_out.shape[0]
+  ws = _workspace(lib().lmoe_combine_workspace_size(m, t), routed_out.device)
+  check(lib().lmoe_combine_scatter_add(_p(shard_out), _dt(shard_out), _p(padded_token_idx),
+                                       _p(padded_combine_weight), _dt(padded_combine_weight), m, lat, t,
+                                       _p(out), _dt(out), _p(ws), ws.numel(), _stream()),
+        "combine_scatter_add")
+  return out
+
+
+def combine_slots(shard_out: torch.Tensor, slot_pos: torch.Tensor, weights: torch.Tensor,
+                  num_tokens: int, top_k: int, *, mode: str, routed_out: torch.Tensor | None = None,
+                  out_dtype: torch.dtype | None = None) -> torch.Tensor:
+  """Combine driven by the dispatch's slot_pos.  mode="scatter_add": adds into a
+  copy of routed_out exactly like _combine_shard_contribution (weights are the
+  padded per-row weights); mode="slot_sum": the unsharded f32 weighted sum of
+  ref.py:413-416 (weights are topk_weight (T, k) f32)."""
+  _dev(shard_out, slot_pos, weights)
+  lat = shard_out.shape[-1]
+  if mode == "scatter_add":
+    if routed_out is None:
+      routed_out = torch.zeros((num_tokens, lat), dtype=out_dtype or shard_out.dtype,
+                               device=shard_out.device)
+    out = routed_out.clone()
+    m = _lib.COMBINE_SCATTER_ADD
+  elif mode == "slot_sum":
+    out = torch.empty((num_tokens, lat), dtype=out_dtype or shard_out.dtype, device=shard_out.device)
+    m = _lib.COMBINE_SLOT_SUM
+  else:
+    raise ValueError(mode)
+  check(lib().lmoe_combine_slots(_p(shard_out), _dt(shard_out), _p(slot_pos), _p(weights),
+                                 _dt(weights), num_tokens, top_k, lat, m, _p(out), _dt(out),
+                                 _stream()), "combine_slots")
+  return out
+
+
+# ---------------------------------------------------------------------------
+# a10 / a14: elementwise stages
+# ---------------------------------------------------------------------------
+
+
+def _rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
+  """ref.py:286-293."""
+  _dev(x, scale)
+  out = torch.empty_like(x)
+  n = x.shape[-1]
+  check(lib().lmoe_rms_norm(_p(x), _p(scale.to(x.dtype).contiguous()), x.numel() // n, n, eps, _dt(x),
+                            _p(out), _stream()), "rms_norm")
+  return out
+
+
+def _situ_and_mul(gate: torch.Tensor, up: torch.Tensor, beta: float, linear_beta: float) -> torch.Tensor:
+  """ref.py:296-310: f32 SiTU-GLU, cast back to the input dtype."""
+  _dev(gate, up)
+  out = torch.empty_like(gate)
+  check(lib().lmoe_situ_and_mul(_p(gate), _p(up), gate.numel(), beta, linear_beta, _dt(gate), _p(out),
+                                _stream()), "situ_and_mul")
+  return out
+
+
+def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+  """a + b rounded to the dtype (the residual add of ref.py:435)."""
+  _dev(a, b)
+  out = torch.empty_like(a)
+  check(lib().lmoe_add(_p(a), _p(b), a.numel(), _dt(a), _p(out), _stream()), "add")
+  return out
+
+
+def _situ_glu_mlp(x, w_gate, w_up, w_down, beta, linear_beta):
+  """ref.py:313-327 on dense weights (in, out): situ(x@Wg, x@Wu) @ Wd."""
+  return dense(_situ_and_mul(dense(x, w_gate), dense(x, w_up), beta, linear_beta), w_down)
+
+
+# ---------------------------------------------------------------------------
+# a11: expert FFN over one shard
+# ---------------------------------------------------------------------------
+
+
+def _local_shard_expert_ffn_ragged_dot(sorted_tokens, expert_gate, expert_up, expert_down,
+                                       group_sizes, config, implementation=None, zero_group=-1):
+  """rd.py:580-607: gate / up ragged_dots, SiTU-GLU, down ragged_dot."""
+  b, bl = config.activation_situ_beta, config.activation_situ_linear_beta
+  gate = ragged_dot(sorted_tokens, expert_gate, group_sizes, implementation=implementation,
+                    zero_group=zero_group)
+  up = ragged_dot(sorted_tokens, expert_up, group_sizes, implementation=implementation,
+                  zero_group=zero_group)
+  return ragged_dot(_situ_and_mul(gate, up, b, bl), expert_down, group_sizes,
+                    implementation=implementation, zero_group=zero_group)
+
+
+def _local_shard_expert_ffn_ragged_dot_fused_gateup(sorted_tokens, expert_gate, expert_up, expert_down,
+                                                    group_sizes, config, zero_group=-1):
+  """rd.py:726-748: prefuse then the fused gate/up + SiTU GEMM and the down GEMM."""
+  fused = prefuse_gateup_weights(expert_gate, expert_up)
+  return _fused_gateup_expert_ffn_from_prefused_weights(
+      sorted_tokens, fused, expert_down, group_sizes, config.activation_situ_beta,
+      config.activation_situ_linear_beta, zero_group=zero_group)
+
+
+def _fused_gateup_expert_ffn_from_prefused_weights(sorted_tokens, fused_expert_gate_up, expert_down,
+                                                   group_sizes, beta, linear_beta,
+                                                   implementation=None, zero_group=-1,
+                                                   rhs_layout="gkn"):
+  """rd.py:644-723 on an already-prefused weight."""
+  if implementation not in (None, "hip"):
+    raise NotImplementedError(f"implementation={implementation!r}")
+  act = ragged_dot_gateup_situ(sorted_tokens, fused_expert_gate_up, group_sizes, beta, linear_beta,
+                               rhs_layout=rhs_layout, zero_group=zero_group)
+  return ragged_dot(act, expert_down, group_sizes, rhs_layout=rhs_layout, zero_group=zero_group)
