@@ -1,0 +1,196 @@
+#!/usr/bin/env python3
+"""LatentMoE layer benchmark on one MI355X.
+
+One step = one full local-shard LatentMoE forward over 4096 tokens: router
+logits GEMM (7168 -> 896, f32 out), down-projection (7168 -> 1024), top-16
+router, local-shard dispatch (experts 0..111), fused gate/up + SiTU-GLU and
+down grouped GEMMs on MXFP4 expert weights, combine, RMSNorm and the
+up-projection (1024 -> 7168).  Inputs are resident in HBM before timing.
+
+Prints ONE JSON line with the layer throughput, the roofline of the dominant
+kernel (the MXFP4 gate/up grouped GEMM, timed in place with HIP events on its
+stream) and the CPU baseline (the oracle's restatement of the reference
+forward on a bounded token sample, timed on this host).
+
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--mxfp4-mode lds_dequant]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tokamax-tpu-kernel-lab_amd"))
+sys.path.insert(0, ROOT)
+
+METRIC = "LatentMoE layer tokens/s @1 GPU; grouped-GEMM TFLOP/s as % of MFMA peak"
+HBM_PEAK_GBS = 8000.0
+PEAK_TFLOPS = {"bf16": 2500.0, "mxfp4": 10100.0}
+
+
+def log(msg):
+  print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def gateup_algorithmic(c, group_sizes):
+  """Algorithmic FLOPs / HBM bytes of one MXFP4 gate/up + SiTU launch:
+  valid rows only, each touched expert's weights read once."""
+  import numpy as np
+  gs = np.asarray(group_sizes)[: c.local_experts]
+  rows = int(gs.sum())
+  lat, inter = c.latent, c.intermediate
+  experts_hit = int((gs > 0).sum())
+  w_bytes = experts_hit * 2 * inter * lat * (0.5 + 1.0 / 32)
+  act_bytes = rows * lat * 2 + rows * inter * 2
+  flops = 2.0 * rows * lat * 2 * inter
+  return rows, experts_hit, flops, w_bytes + act_bytes
+
+
+def load_traffic(name):
+  path = os.path.join(ROOT, "profiles", name)
+  if not os.path.exists(path):
+    return None
+  with open(path) as f:
+    return json.load(f)
+
+
+def cpu_baseline(layer, hidden, w, c, sample_tokens, reps):
+  """Oracle restatement of the reference single-shard forward on the host:
+  the same weights (MXFP4 experts dequantised to bf16, as the reference does
+  offline), ``sample_tokens`` of the 4096 tokens, median of ``reps`` runs."""
+  import numpy as np
+  import torch
+
+  from lmoe import ops
+  from oracle import lmoe_oracle as O
+  try:
+    from threadpoolctl import threadpool_info
+    threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+  except Exception:  # noqa: BLE001
+    threads = len(os.sched_getaffinity(0))
+  E = layer.experts
+  L, I = c.local_experts, c.intermediate
+  gu = ops.dequantize_mxfp4(E["gu_packed"], E["gu_scale"], out_dtype=torch.bfloat16)  # (L+1, 2I, lat)
+  dn = ops.dequantize_mxfp4(E["down_packed"], E["down_scale"], out_dtype=torch.bfloat16)  # (L+1, lat, I)
+  f = lambda t: t.float().cpu().numpy()
+  gu_h, dn_h = f(gu), f(dn)
+  del gu, dn
+  gate = gu_h[:, :I, :].transpose(0, 2, 1)
+  up = gu_h[:, I:, :].transpose(0, 2, 1)
+  down = dn_h.transpose(0, 2, 1)
+  wd = {k: f(v) for k, v in w.items()}
+  cfg = c.config()
+  h = f(hidden[:sample_tokens])
+  run = lambda: O.single_shard_forward(h, wd, gate, up, down, cfg, "bf16", c.local_start, L,
+                                       c.capacity_factor, include_shared=False)
+  run()
+  times = []
+  for _ in range(reps):
+    t0 = time.perf_counter()
+    run()
+    times.append(time.perf_counter() - t0)
+  med = statistics.median(times)
+  return {"value": round(sample_tokens / med, 2), "unit": "tokens/s", "cores": int(threads),
+          "kind": "port",
+          "sample": f"{sample_tokens} of {c.tokens} tokens through the numpy oracle's single-shard "
+                    f"forward (all stages, bf16 rounding emulated), median of {reps} runs "
+                    f"({med:.2f} s each)"}
+
+
+def main():
+  ap = argparse.ArgumentParser()
+  ap.add_argument("--gpus", type=int, default=1)
+  ap.add_argument("--steps", type=int, default=20)
+  ap.add_argument("--warmup", type=int, default=5)
+  ap.add_argument("--mxfp4-mode", default="lds_dequant", choices=["lds_dequant", "scaled_mfma"])
+  ap.add_argument("--cpu-sample-tokens", type=int, default=512)
+  ap.add_argument("--cpu-reps", type=int, default=3)
+  ap.add_argument("--no-cpu-baseline", action="store_true")
+  args = ap.parse_args()
+  if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+    print("bench.py measures one GPU only: this build has no multi-GPU path "
+          "(the expert-parallel all-reduce is design-only; see DESIGN.md).", file=sys.stderr)
+    sys.exit(2)
+
+  import numpy as np
+  import torch
+
+  from lmoe import _lib
+  from lmoe.forward import LocalShardLatentMoE
+  from lmoe.workloads import Config5, make_config5
+
+  _lib.lib()
+  dev = torch.device("cuda:0")
+  c = Config5()
+  log("generating config 5 inputs and MXFP4 expert weights")
+  hidden, w, experts = make_config5(dev, c, "mxfp4")
+  layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                              e_score_correction_bias=w["e_score_correction_bias"],
+                              down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                              local_expert_start=c.local_start, local_num_experts=c.local_experts,
+                              expert_format="mxfp4", experts=experts, capacity_factor=c.capacity_factor,
+                              mxfp4_mode=args.mxfp4_mode)
+  torch.cuda.synchronize()
+  _, st = layer.forward(hidden, return_stages=True)
+  gs = st["dispatch"].group_sizes.cpu().numpy()
+  rows, hit, flops, nbytes = gateup_algorithmic(c, gs)
+  m_padded = int(gs.sum())
+  log(f"routed rows R={rows} of m_padded={m_padded}, experts hit {hit}/{c.local_experts}, "
+      f"group sizes min/max {gs[:c.local_experts].min()}/{gs[:c.local_experts].max()}")
+
+  for _ in range(args.warmup):
+    layer.forward(hidden)
+  torch.cuda.synchronize()
+  events = [{"gateup": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))}
+            for _ in range(args.steps)]
+  t0 = time.perf_counter()
+  for i in range(args.steps):
+    layer.forward(hidden, kernel_events=events[i])
+  torch.cuda.synchronize()
+  t1 = time.perf_counter()
+  ms_per_step = (t1 - t0) * 1000.0 / args.steps
+  gateup_ms = statistics.mean(e["gateup"][0].elapsed_time(e["gateup"][1]) for e in events)
+  tokens_per_s = c.tokens / (ms_per_step / 1000.0)
+  log(f"{ms_per_step:.3f} ms/step, gate/up kernel {gateup_ms * 1000:.1f} us")
+
+  achieved = nbytes / (gateup_ms / 1000.0) / 1e9
+  tflops = flops / (gateup_ms / 1000.0) / 1e12
+  traffic = load_traffic("traffic_cfg5_gateup_mxfp4.json")
+  roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+              "frac": round(achieved / HBM_PEAK_GBS, 4),
+              "traffic": traffic.get("bytes_per_launch") if traffic else None,
+              "kernel": "grouped_gemm_kernel<MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
+              "algorithmic_bytes": int(nbytes), "algorithmic_flops": flops,
+              "kernel_us": round(gateup_ms * 1000.0, 2)}
+  grouped = {"tflops": round(tflops, 2),
+             "pct_mxfp4_peak": round(100 * tflops / PEAK_TFLOPS["mxfp4"], 2),
+             "pct_bf16_peak": round(100 * tflops / PEAK_TFLOPS["bf16"], 2),
+             "mfma_path": args.mxfp4_mode}
+
+  cpu = None
+  if not args.no_cpu_baseline:
+    log(f"cpu baseline on {args.cpu_sample_tokens} tokens")
+    cpu = cpu_baseline(layer, hidden, w, c, args.cpu_sample_tokens, args.cpu_reps)
+
+  line = {
+      "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
+      "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4),
+      "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+      "data": "synthetic (seeded; random-init weights, experts quantised to MXFP4)",
+      "config": {"workload": "cfg5: full local-shard LatentMoE forward (BASELINE config 5)",
+                 "tokens": c.tokens, "d_model": c.hidden, "latent": c.latent,
+                 "intermediate": c.intermediate, "experts": c.experts, "top_k": c.top_k,
+                 "local_experts": f"{c.local_start}..{c.local_start + c.local_experts - 1}",
+                 "expert_weights": "mxfp4 (e2m1, e8m0 block-32)", "capacity_factor": c.capacity_factor,
+                 "m_padded": m_padded, "routed_rows": rows, "router_skew": "zipf(1.2) on logits",
+                 "shared_experts": 0, "parallelism": "single GPU (one expert shard)"},
+      "roofline": roofline, "grouped_gemm": grouped, "cpu_baseline": cpu,
+  }
+  print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+  main()

@@ -165,8 +165,12 @@ class LocalShardLatentMoE:
   def _dense(self, x, w_nk, out_dtype=None):
     return ops.dense(x, w_nk, out_dtype=out_dtype, w_layout="nk")
 
-  def forward(self, hidden: torch.Tensor, return_stages: bool = False):
+  def forward(self, hidden: torch.Tensor, return_stages: bool = False, kernel_events: dict | None = None):
+    """``kernel_events`` optionally maps a stage name ("gateup", "down") to a
+    (start, end) pair of torch.cuda.Event recorded around that kernel on the
+    current stream (used by the benchmark to time one kernel in place)."""
     c = self.config
+    ev = kernel_events or {}
     t = hidden.shape[0]
     b, bl = c.activation_situ_beta, c.activation_situ_linear_beta
     logits = self._dense(hidden, self.router_nk, torch.float32)
@@ -176,16 +180,26 @@ class LocalShardLatentMoE:
     m_padded = ops.compute_m_padded(t, c.top_k, c.num_experts, self.L, self.cf)
     d = ops.dispatch_local(idx, w, x, self.start, self.L, m_padded)
     E = self.experts
+    if "gateup" in ev:
+      ev["gateup"][0].record()
     if self.expert_format == "mxfp4":
       act = ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed"], E["gu_scale"], d.group_sizes,
                                  fuse_gateup_activation=f"situ:{b}:{bl}", mode=self.mxfp4_mode,
                                  zero_group=self.L)
-      shard_out = ops.ragged_dot_mxfp4(act, E["down_packed"], E["down_scale"], d.group_sizes,
-                                       mode=self.mxfp4_mode, zero_group=self.L)
     else:
       act = ops.ragged_dot_gateup_situ(d.sorted_tokens, E["gu_nk"], d.group_sizes, b, bl,
                                        rhs_layout="gnk", zero_group=self.L)
+    if "gateup" in ev:
+      ev["gateup"][1].record()
+    if "down" in ev:
+      ev["down"][0].record()
+    if self.expert_format == "mxfp4":
+      shard_out = ops.ragged_dot_mxfp4(act, E["down_packed"], E["down_scale"], d.group_sizes,
+                                       mode=self.mxfp4_mode, zero_group=self.L)
+    else:
       shard_out = ops.ragged_dot(act, E["down_nk"], d.group_sizes, rhs_layout="gnk", zero_group=self.L)
+    if "down" in ev:
+      ev["down"][1].record()
     routed = ops.combine_slots(shard_out, d.slot_pos, d.padded_combine_weight, t, c.top_k,
                                mode="scatter_add", out_dtype=hidden.dtype)
     normed = ops._rms_norm(routed, self.norm_scale, c.rms_norm_eps)

@@ -261,8 +261,19 @@ def router_topk_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top
   return (idx, w, scores) if return_scores else (idx, w)
 
 
+_GROUP_CACHE: dict = {}
+
+
 def _ones_group(m: int, device) -> torch.Tensor:
-  return torch.tensor([m], dtype=torch.int32, device=device)
+  """Cached one-group group_sizes tensor [m] (no per-call host->device copy)."""
+  key = (m, str(device))
+  t = _GROUP_CACHE.get(key)
+  if t is None:
+    if len(_GROUP_CACHE) > 256:
+      _GROUP_CACHE.clear()
+    t = torch.full((1,), m, dtype=torch.int32, device=device)
+    _GROUP_CACHE[key] = t
+  return t
 
 
 def dense(x: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None,

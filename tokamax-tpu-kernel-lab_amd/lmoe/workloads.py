@@ -1,0 +1,169 @@
+"""Seeded synthetic inputs for the BASELINE.json configurations, plus the OCP
+MX (v1.0) MXFP4 weight quantiser used to produce MXFP4 expert weights.
+
+Large tensors are generated with torch's Philox generator directly on the
+target device (fast at 4096 x 7168); small ones may be generated on the CPU
+and moved.  Every generator takes an explicit seed, so the same workload is
+reproducible on any box.  These are benchmark inputs, not reference data.
+"""
+
+from __future__ import annotations
+
+import dataclasses
+
+import numpy as np
+import torch
+
+from .config import LatentMoEConfig
+
+# ---------------------------------------------------------------------------
+# MXFP4 quantisation (OCP Microscaling Formats v1.0, section 6.3)
+# ---------------------------------------------------------------------------
+
+_E2M1_MAG = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+
+
+def quantize_mxfp4(w: torch.Tensor, block: int = 32) -> tuple[torch.Tensor, torch.Tensor]:
+  """w (..., N, K) float -> (packed (..., N, K/2) uint8, scale (..., N, K/block) uint8).
+
+  Per block of ``block`` consecutive K elements: shared exponent
+  X = floor(log2(amax)) - emax_elem (emax_elem = 2 for E2M1; an all-zero block
+  uses amax = 1), clamped to [-127, 127] and stored as the E8M0 byte X + 127;
+  elements are v / 2^X rounded to the nearest E2M1 value, ties to the even
+  code, saturating at +-6.  Low nibble = element 2j, high nibble = 2j+1 (the
+  checkpoint packing of mxfp4_dequant.py:14-17)."""
+  *lead, n, k = w.shape
+  if k % block or k % 2:
+    raise ValueError(f"K={k} must be a multiple of {block}")
+  x = w.float().reshape(*lead, n, k // block, block)
+  amax = x.abs().amax(-1, keepdim=True)
+  amax = torch.where(amax > 0, amax, torch.ones_like(amax))
+  e = torch.floor(torch.log2(amax)) - 2.0
+  e = e.clamp(-127.0, 127.0)
+  q = x * torch.exp2(-e)
+  a = q.abs()
+  code = ((a > 0.25).to(torch.uint8) + (a >= 0.75).to(torch.uint8) + (a > 1.25).to(torch.uint8) +
+          (a >= 1.75).to(torch.uint8) + (a > 2.5).to(torch.uint8) + (a >= 3.5).to(torch.uint8) +
+          (a > 5.0).to(torch.uint8))
+  code = code | (torch.signbit(q) & (code > 0)).to(torch.uint8) << 3
+  code = code.reshape(*lead, n, k)
+  packed = (code[..., 0::2] | (code[..., 1::2] << 4)).contiguous()
+  scale = (e.squeeze(-1) + 127.0).to(torch.uint8).contiguous()
+  return packed, scale
+
+
+def random_mxfp4(g: int, n: int, k: int, device, seed: int, scale_lo: int = 119,
+                 scale_hi: int = 129) -> tuple[torch.Tensor, torch.Tensor]:
+  """BASELINE config 4 weights: codes uniform over the 16 E2M1 values (both
+  nibbles of every byte uniform), scale exponents uniform in
+  [scale_lo-127, scale_hi-127] (default -8..2)."""
+  gen = torch.Generator(device=device).manual_seed(seed)
+  packed = torch.randint(0, 256, (g, n, k // 2), generator=gen, device=device, dtype=torch.int32)
+  scale = torch.randint(scale_lo, scale_hi + 1, (g, n, k // 32), generator=gen, device=device,
+                        dtype=torch.int32)
+  return packed.to(torch.uint8), scale.to(torch.uint8)
+
+
+# ---------------------------------------------------------------------------
+# Workloads
+# ---------------------------------------------------------------------------
+
+
+def zipf_group_sizes(m: int, g: int, seed: int, s: float = 1.1, n_zero: int = 3) -> np.ndarray:
+  """BASELINE config 2 group sizes: multinomial(m, p) with p_g ~ (rank_g+1)^-s
+  over a seeded permutation of ranks; n_zero seeded groups emptied into the
+  largest remaining group (so sum == m)."""
+  rng = np.random.default_rng(seed)
+  rank = rng.permutation(g)
+  p = (rank + 1.0) ** -s
+  p /= p.sum()
+  gs = rng.multinomial(m, p)
+  zero = rng.choice(g, n_zero, replace=False)
+  big = int(np.argmax(np.where(np.isin(np.arange(g), zero), -1, gs)))
+  gs[big] += gs[zero].sum()
+  gs[zero] = 0
+  return gs.astype(np.int32)
+
+
+def _normal(shape, std, gen, device, dtype=torch.bfloat16):
+  return (torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
+
+
+@dataclasses.dataclass
+class Config5:
+  """full local-shard LatentMoE forward."""
+  tokens: int = 4096
+  hidden: int = 7168
+  latent: int = 1024
+  intermediate: int = 2048
+  experts: int = 896
+  top_k: int = 16
+  local_start: int = 0
+  local_experts: int = 112
+  capacity_factor: float = 2.0
+  zipf_skew: float = 1.2
+  seed: int = 0
+
+  def config(self) -> LatentMoEConfig:
+    return LatentMoEConfig(hidden_size=self.hidden, latent_size=self.latent,
+                           intermediate_size=self.intermediate, num_experts=self.experts,
+                           top_k=self.top_k, num_shared_experts=0)
+
+
+def make_config5(device, c: Config5 | None = None, expert_format: str = "mxfp4"):
+  """Inputs and prepared weights of config 5.
+
+  Router skew: the reference's only skew mechanism is e_score_correction_bias
+  (selection-only, ref.py:350-352); BASELINE asks for "logits plus a Zipf(1.2)
+  per-expert bias".  The bias is folded into the router *logits* by a seeded
+  per-expert offset -1.2*ln(rank+1) added through an extra hidden feature:
+  hidden[:, -1] = 1 and router_weight[-1, e] = offset_e, so the logits carry
+  the skew and the combine weights see it (the "bias on logits" reading).
+  Expert weights: N(0, 0.02^2) quantised to MXFP4 with the OCP rule.
+  Returns (hidden, weights dict, experts dict) on ``device``."""
+  c = c or Config5()
+  gen = torch.Generator(device=device).manual_seed(c.seed)
+  hidden = torch.randn((c.tokens, c.hidden), generator=gen, device=device).to(torch.bfloat16)
+  router = _normal((c.hidden, c.experts), 0.02, gen, device)
+  rng = np.random.default_rng(c.seed + 1)
+  rank = rng.permutation(c.experts)
+  offset = torch.from_numpy((-c.zipf_skew * np.log(rank + 1.0)).astype(np.float32)).to(device)
+  hidden[:, -1] = 1.0
+  router[-1, :] = offset.to(torch.bfloat16)
+  w = {
+      "router_weight": router,
+      "e_score_correction_bias": torch.zeros(c.experts, device=device),
+      "down_proj": _normal((c.hidden, c.latent), 0.02, gen, device),
+      "up_proj": _normal((c.latent, c.hidden), 0.02, gen, device),
+      "norm_scale": torch.ones(c.latent, device=device, dtype=torch.bfloat16),
+  }
+  L = c.local_experts
+  experts = {}
+  # gate/up as one [gate; up] (L+1, 2I, lat) matrix in checkpoint (out, in)
+  # layout; the trailing expert is the zero padding bucket.
+  gu = _normal((L + 1, 2 * c.intermediate, c.latent), 0.02, gen, device, torch.float32)
+  gu[L] = 0
+  dn = _normal((L + 1, c.latent, c.intermediate), 0.02, gen, device, torch.float32)
+  dn[L] = 0
+  if expert_format == "mxfp4":
+    experts["gu_packed"], experts["gu_scale"] = _quantize_chunked(gu)
+    experts["down_packed"], experts["down_scale"] = _quantize_chunked(dn)
+  else:
+    experts["gu_nk"] = gu.to(torch.bfloat16).contiguous()
+    experts["down_nk"] = dn.to(torch.bfloat16).contiguous()
+  del gu, dn
+  return hidden, w, experts
+
+
+def _quantize_chunked(w: torch.Tensor, chunk: int = 8):
+  packs, scales = [], []
+  for i in range(0, w.shape[0], chunk):
+    p, s = quantize_mxfp4(w[i:i + chunk])
+    packs.append(p)
+    scales.append(s)
+  return torch.cat(packs).contiguous(), torch.cat(scales).contiguous()
+
+
+def routed_rows(topk_idx: torch.Tensor, start: int, L: int) -> int:
+  """Number of (token, slot) assignments that land in [start, start+L)."""
+  return int(((topk_idx >= start) & (topk_idx < start + L)).sum().item())
