@@ -106,7 +106,7 @@ def main():
   ap.add_argument("--steps", type=int, default=20)
   ap.add_argument("--warmup", type=int, default=5)
   ap.add_argument("--mxfp4-mode", default="lds_dequant", choices=["lds_dequant", "scaled_mfma"])
-  ap.add_argument("--cpu-sample-tokens", type=int, default=512)
+  ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
   ap.add_argument("--cpu-reps", type=int, default=3)
   ap.add_argument("--no-cpu-baseline", action="store_true")
   args = ap.parse_args()

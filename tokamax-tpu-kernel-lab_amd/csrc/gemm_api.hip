@@ -23,10 +23,17 @@ __global__ __launch_bounds__(256) void mxfp4_dequant_kernel(const uint8_t* __res
     const int64_t r = i / kh, j = i % kh;
     const uint32_t byte = packed[i];
     const int64_t k = 2 * j;
-    const float sc0 = e8m0_to_float(scale[r * ng + k / gs]);
-    const float sc1 = e8m0_to_float(scale[r * ng + (k + 1) / gs]);
-    const uint32_t b0 = fp4_to_bf16_bits(byte & 15u, sc0);
-    const uint32_t b1 = fp4_to_bf16_bits(byte >> 4, sc1);
+    const uint32_t s0 = scale[r * ng + k / gs];
+    const uint32_t s1 = scale[r * ng + (k + 1) / gs];
+    uint32_t b0, b1;
+    if (s0 == s1) {
+      const uint32_t both = dequant_byte(byte, s0);
+      b0 = both & 0xffffu;
+      b1 = both >> 16;
+    } else {
+      b0 = fp4_to_bf16_bits(byte & 15u, e8m0_to_float(s0));
+      b1 = fp4_to_bf16_bits(byte >> 4, e8m0_to_float(s1));
+    }
     if (odt == LMOE_BF16) {
       reinterpret_cast<uint32_t*>(out)[i] = b0 | (b1 << 16);
     } else {

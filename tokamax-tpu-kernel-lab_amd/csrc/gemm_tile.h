@@ -54,6 +54,27 @@ struct TileInfo {
   bool zero;     // write zeros without computing
 };
 
+// Total m-tiles of the problem: every group's ceil(n_g / BM) tiles plus the
+// tail tiles that zero rows [sum(group_sizes), M).  Executed by one wave.
+template <int BM>
+__device__ int64_t total_m_tiles(const int32_t* __restrict__ gs, int64_t G, int64_t M) {
+  const int lane = threadIdx.x % 64;
+  int64_t tiles = 0, rows = 0;
+  for (int64_t g = lane; g < G; g += 64) {
+    int64_t n = gs[g];
+    n = n < 0 ? 0 : n;
+    tiles += (n + BM - 1) / BM;
+    rows += n;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    tiles += __shfl_xor(tiles, off, 64);
+    rows += __shfl_xor(rows, off, 64);
+  }
+  const int64_t tail = rows < M ? M - rows : 0;
+  return tiles + (tail + BM - 1) / BM;
+}
+
 // Find (group, first row, rows) of m-tile `mt`.  Executed by wave 0.
 template <int BM>
 __device__ TileInfo locate_tile(const int32_t* __restrict__ gs, int64_t G, int64_t M, int zero_group,
@@ -129,6 +150,27 @@ __device__ __forceinline__ float situ(float g, float u, float beta, float beta_l
   return __fmul_rn(sg, bu);
 }
 
+// tanh for the fused epilogue: odd Taylor polynomial below |x| = 1/8
+// (relative error < 1e-8), (1 - e^-2|x|) / (1 + e^-2|x|) above, with the
+// hardware exp / reciprocal (a few f32 ulp, below bf16 output resolution).
+__device__ __forceinline__ float tanh_fast(float x) {
+  const float ax = fabsf(x);
+  const float x2 = x * x;
+  const float poly = x * (1.0f - x2 * (0.333333333f - x2 * (0.133333333f - x2 * 0.053968254f)));
+  const float e = __expf(-2.0f * ax);
+  const float t = copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
+  return ax < 0.125f ? poly : t;
+}
+
+// SiTU-GLU with hardware transcendentals, used where the result is rounded to
+// bf16 right away (the fused gate/up epilogue).
+__device__ __forceinline__ float situ_fast(float g, float u, float beta, float beta_lin) {
+  const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+  const float sg = beta * tanh_fast(g * __builtin_amdgcn_rcpf(beta)) * sig;
+  const float bu = beta_lin * tanh_fast(u * __builtin_amdgcn_rcpf(beta_lin));
+  return sg * bu;
+}
+
 // E2M1 nibble with E8M0 scale byte s -> bf16 bits, exact (value has <= 2
 // significant bits, so the f32 product truncates to bf16 without rounding).
 __device__ __forceinline__ uint32_t fp4_to_bf16_bits(uint32_t nib, float scale) {
@@ -149,10 +191,33 @@ __device__ __forceinline__ float e8m0_to_float(uint32_t s) {
   return __uint_as_float(s << 23);
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
 // 16 packed bytes (32 e2m1 values, low nibble first) -> 32 bf16 (as 16 u32).
+// Scale bytes 3..252 use gfx950's v_cvt_scalef32_pk_bf16_fp4 (two values per
+// instruction, exact: every product is a normal bf16 with <= 2 significant
+// bits); the edge bytes, whose products can be denormal (0..2) or overflow
+// (253..255), take the bit-level path.
+__device__ __forceinline__ bool hw_scale_ok(uint32_t s) { return s - 3u <= 249u; }
+
 __device__ __forceinline__ void dequant32(const uint4 p, uint32_t scale_byte, uint32_t* o) {
-  const float sc = e8m0_to_float(scale_byte);
   const uint32_t w[4] = {p.x, p.y, p.z, p.w};
+  if (hw_scale_ok(scale_byte)) {
+    const float sc = __uint_as_float(scale_byte << 23);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      bf16x2_t r0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], sc, 0);
+      bf16x2_t r1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], sc, 1);
+      bf16x2_t r2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], sc, 2);
+      bf16x2_t r3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w[d], sc, 3);
+      o[d * 4 + 0] = __builtin_bit_cast(uint32_t, r0);
+      o[d * 4 + 1] = __builtin_bit_cast(uint32_t, r1);
+      o[d * 4 + 2] = __builtin_bit_cast(uint32_t, r2);
+      o[d * 4 + 3] = __builtin_bit_cast(uint32_t, r3);
+    }
+    return;
+  }
+  const float sc = e8m0_to_float(scale_byte);
 #pragma unroll
   for (int d = 0; d < 4; ++d) {
 #pragma unroll
@@ -163,6 +228,16 @@ __device__ __forceinline__ void dequant32(const uint4 p, uint32_t scale_byte, ui
       o[d * 4 + b] = lo | (hi << 16);
     }
   }
+}
+
+// Same conversion for one packed byte (two values) -> one u32 of two bf16.
+__device__ __forceinline__ uint32_t dequant_byte(uint32_t byte, uint32_t scale_byte) {
+  if (hw_scale_ok(scale_byte)) {
+    const float sc = __uint_as_float(scale_byte << 23);
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(byte, sc, 0));
+  }
+  const float sc = e8m0_to_float(scale_byte);
+  return fp4_to_bf16_bits(byte & 15u, sc) | (fp4_to_bf16_bits(byte >> 4, sc) << 16);
 }
 
 }  // namespace gemm

@@ -1,0 +1,190 @@
+"""Per-kernel benchmarks of the BASELINE configurations on one GPU.
+
+Mirrors the reference's measurement protocol (hw_session_common.py:120-175:
+warm-up, then rounds of back-to-back calls timed with device events, median
+over rounds) and its metrics (bf16 TFLOP/s, GB/s, fraction of the binding
+roofline, SURVEY 8(d) formulas: valid rows only, each weight byte once).
+
+  python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5] [--rounds 10] [--calls 20]
+
+Prints one JSON object per measured kernel.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import statistics
+
+import numpy as np
+import torch
+
+from . import ops
+from .workloads import Config5, make_config5, random_mxfp4, zipf_group_sizes
+
+HBM_GBS = 8000.0
+PEAK = {"bf16": 2500.0, "fp8": 5000.0, "mxfp4": 10100.0}
+
+
+_FILTER = None  # substring: only kernels whose name contains it are run
+_PROFILE = False  # run each selected kernel a few times, no timing
+
+
+def time_fn(fn, rounds=10, calls=20, name=""):
+  """Median per-call ms over `rounds` rounds of `calls` pipelined calls."""
+  if _FILTER and _FILTER not in name:
+    return None
+  if _PROFILE:
+    for _ in range(5):
+      fn()
+    torch.cuda.synchronize()
+    return None
+  fn()
+  torch.cuda.synchronize()
+  per = []
+  for _ in range(rounds):
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(calls):
+      fn()
+    b.record()
+    b.synchronize()
+    per.append(a.elapsed_time(b) / calls)
+  return statistics.median(per)
+
+
+def report(name, ms, flops, nbytes, peak_key="bf16", **extra):
+  if ms is None:
+    return None
+  t = ms / 1000.0
+  tf = flops / t / 1e12 if flops else 0.0
+  gbs = nbytes / t / 1e9
+  t_roof = max(flops / (PEAK[peak_key] * 1e12), nbytes / (HBM_GBS * 1e9))
+  rec = {"kernel": name, "us": round(ms * 1000, 2), "tflops": round(tf, 2), "gbs": round(gbs, 1),
+         "mfma_util": round(tf / PEAK[peak_key], 4), "roofline_frac": round(t_roof / t, 4),
+         "bound": "hbm" if nbytes / (HBM_GBS * 1e9) >= flops / (PEAK[peak_key] * 1e12) else "mfma"}
+  rec.update(extra)
+  print(json.dumps(rec), flush=True)
+  return rec
+
+
+def bench_cfg2(dev, rounds, calls):
+  gs = zipf_group_sizes(8192, 32, seed=2)
+  gen = torch.Generator(device=dev).manual_seed(2)
+  lhs = torch.randn((8192, 2048), generator=gen, device=dev).to(torch.bfloat16)
+  rhs = (torch.randn((32, 2048, 1024), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+  g = torch.from_numpy(gs).to(dev)
+  flops = 2.0 * 2048 * 1024 * gs.sum()
+  nbytes = (gs > 0).sum() * 2048 * 1024 * 2 + 8192 * 2048 * 2 + 8192 * 1024 * 2
+  ms = time_fn(lambda: ops.ragged_dot(lhs, rhs, g), rounds, calls, name="cfg2 ragged_dot bf16 (GKN reference layout)")
+  report("cfg2 ragged_dot bf16 (GKN reference layout)", ms, flops, nbytes)
+  rhs_nk = ops.to_gnk(rhs)
+  ms = time_fn(lambda: ops.ragged_dot(lhs, rhs_nk, g, rhs_layout="gnk"), rounds, calls, name="cfg2 ragged_dot bf16 (GNK prepared layout)")
+  report("cfg2 ragged_dot bf16 (GNK prepared layout)", ms, flops, nbytes)
+
+
+def bench_cfg3(dev, rounds, calls):
+  t, e, k, L, lat, inter = 2048, 896, 16, 112, 1024, 2048
+  gen = torch.Generator(device=dev).manual_seed(3)
+  logits = torch.randn((t, e), generator=gen, device=dev)
+  x = torch.randn((t, lat), generator=gen, device=dev).to(torch.bfloat16)
+  gu = (torch.randn((L + 1, 2 * inter, lat), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+  dn = (torch.randn((L + 1, lat, inter), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+  idx, w = ops.router_topk_from_logits(logits, None, k, True, 1.0, "sigmoid", torch.bfloat16)
+  m_padded = ops.compute_m_padded(t, k, e, L)
+  d = ops.dispatch_local(idx, w, x, 0, L, m_padded)
+  gs = d.group_sizes.cpu().numpy()
+  rows, hit = int(gs[:L].sum()), int((gs[:L] > 0).sum())
+  ms = time_fn(lambda: ops.router_topk_from_logits(logits, None, k, True, 1.0, "sigmoid", torch.bfloat16),
+               rounds, calls, name="cfg3 router_topk (2048x896, k=16)")
+  report("cfg3 router_topk (2048x896, k=16)", ms, 0, t * e * 4 + t * k * 6)
+  ms = time_fn(lambda: ops.dispatch_local(idx, w, x, 0, L, m_padded), rounds, calls, name="cfg3 dispatch (hist+scan+place+gather)")
+  report("cfg3 dispatch (hist+scan+place+gather)", ms, 0,
+         t * k * 4 + rows * lat * 2 * 2 + (m_padded - rows) * lat * 2 + m_padded * 11, rows=rows)
+  f_gu = 2.0 * rows * lat * 2 * inter
+  b_gu = hit * 2 * inter * lat * 2 + rows * lat * 2 + rows * inter * 2
+  ms = time_fn(lambda: ops.ragged_dot_gateup_situ(d.sorted_tokens, gu, d.group_sizes, 4.0, 25.0,
+                                                  rhs_layout="gnk", zero_group=L), rounds, calls, name="cfg3 gate/up+SiTU bf16 grouped GEMM")
+  report("cfg3 gate/up+SiTU bf16 grouped GEMM", ms, f_gu, b_gu, rows=rows, experts_hit=hit)
+  act = ops.ragged_dot_gateup_situ(d.sorted_tokens, gu, d.group_sizes, 4.0, 25.0, rhs_layout="gnk",
+                                   zero_group=L)
+  f_dn = 2.0 * rows * inter * lat
+  b_dn = hit * inter * lat * 2 + rows * inter * 2 + rows * lat * 2
+  ms = time_fn(lambda: ops.ragged_dot(act, dn, d.group_sizes, rhs_layout="gnk", zero_group=L), rounds,
+               calls, name="cfg3 down bf16 grouped GEMM")
+  report("cfg3 down bf16 grouped GEMM", ms, f_dn, b_dn, rows=rows)
+  out = ops.ragged_dot(act, dn, d.group_sizes, rhs_layout="gnk", zero_group=L)
+  ms = time_fn(lambda: ops.combine_slots(out, d.slot_pos, d.padded_combine_weight, t, k,
+                                         mode="scatter_add", out_dtype=torch.bfloat16), rounds, calls, name="cfg3 combine (slot scatter-add)")
+  report("cfg3 combine (slot scatter-add)", ms, 0, rows * lat * 2 + t * lat * 2 * 2 + t * k * 4)
+
+
+def bench_cfg4(dev, rounds, calls):
+  k_, n_ = 7168, 2048
+  packed, scale = random_mxfp4(1, n_, k_, dev, seed=4)
+  for m in (1, 16, 128, 1024, 4096):
+    gen = torch.Generator(device=dev).manual_seed(m)
+    a = torch.randn((m, k_), generator=gen, device=dev).to(torch.bfloat16)
+    g = torch.tensor([m], dtype=torch.int32, device=dev)
+    flops = 2.0 * m * k_ * n_
+    nbytes = n_ * k_ * (0.5 + 1 / 32) + m * k_ * 2 + m * n_ * 2
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, packed, scale, g), rounds, calls, name=f"cfg4 mxfp4 matmul lds_dequant M={m}")
+    report(f"cfg4 mxfp4 matmul lds_dequant M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
+
+
+def bench_cfg5(dev, rounds, calls):
+  from .forward import LocalShardLatentMoE
+  c = Config5()
+  hidden, w, experts = make_config5(dev, c, "mxfp4")
+  layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                              e_score_correction_bias=w["e_score_correction_bias"],
+                              down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                              local_expert_start=0, local_num_experts=c.local_experts,
+                              expert_format="mxfp4", experts=experts)
+  _, st = layer.forward(hidden, return_stages=True)
+  d = st["dispatch"]
+  gs = d.group_sizes.cpu().numpy()
+  L, lat, inter, H, T = c.local_experts, c.latent, c.intermediate, c.hidden, c.tokens
+  rows, hit = int(gs[:L].sum()), int((gs[:L] > 0).sum())
+  ms = time_fn(lambda: layer.forward(hidden), rounds, max(1, calls // 4), name="cfg5 full layer")
+  report("cfg5 full layer", ms, 0, 0, tokens_per_s=round(T / (ms / 1000)) if ms else None, rows=rows)
+  ms = time_fn(lambda: layer._dense(hidden, layer.router_nk, torch.float32), rounds, calls, name="cfg5 router logits GEMM 4096x7168x896 (f32 out)")
+  report("cfg5 router logits GEMM 4096x7168x896 (f32 out)", ms, 2.0 * T * H * c.experts,
+         T * H * 2 + H * c.experts * 2 + T * c.experts * 4)
+  ms = time_fn(lambda: layer._dense(hidden, layer.down_nk), rounds, calls, name="cfg5 down-proj GEMM 4096x7168x1024")
+  report("cfg5 down-proj GEMM 4096x7168x1024", ms, 2.0 * T * H * lat, T * H * 2 + H * lat * 2 + T * lat * 2)
+  f_gu = 2.0 * rows * lat * 2 * inter
+  b_gu = hit * 2 * inter * lat * (0.5 + 1 / 32) + rows * lat * 2 + rows * inter * 2
+  for mode in ("lds_dequant",):
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(d.sorted_tokens, experts["gu_packed"], experts["gu_scale"],
+                                              d.group_sizes, fuse_gateup_activation="situ:4.0:25.0",
+                                              mode=mode, zero_group=L), rounds, calls, name=f"cfg5 mxfp4 gate/up+SiTU grouped GEMM ({mode})")
+    report(f"cfg5 mxfp4 gate/up+SiTU grouped GEMM ({mode})", ms, f_gu, b_gu, rows=rows, experts_hit=hit)
+  act = st["act"]
+  f_dn = 2.0 * rows * inter * lat
+  b_dn = hit * lat * inter * (0.5 + 1 / 32) + rows * inter * 2 + rows * lat * 2
+  ms = time_fn(lambda: ops.ragged_dot_mxfp4(act, experts["down_packed"], experts["down_scale"],
+                                            d.group_sizes, zero_group=L), rounds, calls, name="cfg5 mxfp4 down grouped GEMM (lds_dequant)")
+  report("cfg5 mxfp4 down grouped GEMM (lds_dequant)", ms, f_dn, b_dn, rows=rows)
+  normed = st["normed"]
+  ms = time_fn(lambda: layer._dense(normed, layer.up_nk), rounds, calls, name="cfg5 up-proj GEMM 4096x1024x7168")
+  report("cfg5 up-proj GEMM 4096x1024x7168", ms, 2.0 * T * lat * H, T * lat * 2 + lat * H * 2 + T * H * 2)
+
+
+def main():
+  ap = argparse.ArgumentParser()
+  ap.add_argument("--only", default="cfg2,cfg3,cfg4,cfg5")
+  ap.add_argument("--rounds", type=int, default=10)
+  ap.add_argument("--calls", type=int, default=20)
+  ap.add_argument("--kernel", default=None, help="only kernels whose name contains this")
+  ap.add_argument("--profile", action="store_true", help="run the selected kernels 5x, untimed")
+  a = ap.parse_args()
+  global _FILTER, _PROFILE
+  _FILTER, _PROFILE = a.kernel, a.profile
+  dev = torch.device("cuda:0")
+  for name in a.only.split(","):
+    globals()[f"bench_{name}"](dev, a.rounds, a.calls)
+
+
+if __name__ == "__main__":
+  main()
