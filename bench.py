@@ -112,7 +112,7 @@ def main():
   args = ap.parse_args()
   if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
     print("bench.py measures one GPU only: this build has no multi-GPU path "
-          "(the expert-parallel all-reduce is design-only; see DESIGN.md).", file=sys.stderr)
+          "(the expert-parallel all-reduce across GPUs is not built).", file=sys.stderr)
     sys.exit(2)
 
   import numpy as np

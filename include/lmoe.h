@@ -63,7 +63,7 @@ int lmoe_device_arch_ok(void); /* 1 if device 0 is gfx950, else 0 (host-side que
 
 /* ---- a9: grouped GEMM ----------------------------------------------------------
  * Replaces tokamax.ragged_dot(lhs, rhs, group_sizes) (call sites rd.py:358-369,
- * rd.py:604-607; semantics in SURVEY a9): rows [cum_g, cum_g + n_g) of lhs times
+ * rd.py:604-607): rows [cum_g, cum_g + n_g) of lhs times
  * rhs[g]; rows past sum(group_sizes) are written as zero.  lhs (M, K) and out
  * (M, N) row-major; out dtype may differ from lhs dtype (f32 out = the logits
  * GEMM of ref.py:620).  group_sizes (G,) int32 is read on the device only.

@@ -3,7 +3,7 @@
 Mirrors the reference's measurement protocol (hw_session_common.py:120-175:
 warm-up, then rounds of back-to-back calls timed with device events, median
 over rounds) and its metrics (bf16 TFLOP/s, GB/s, fraction of the binding
-roofline, SURVEY 8(d) formulas: valid rows only, each weight byte once).
+roofline: valid rows only, each weight byte counted once).
 
   python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5] [--rounds 10] [--calls 20]
 
