@@ -39,6 +39,11 @@ GEMM_CASES = [
     ("zipf_gnk", 2048, 512, 256, 16, "zipf", "gnk"),
     ("expertlike", 1024, 256, 512, 17, "small", "gnk"),
     ("one_group", 333, 128, 72, 1, [333], "gkn"),
+    # k-contiguous weights with K % 64 == 0 take the direct-to-LDS kernel,
+    # other K the register-staged one
+    ("gnk_k64_partial_n", 300, 64, 72, 5, "small", "gnk"),
+    ("gnk_k96_regs", 150, 96, 40, 3, [50, 0, 70], "gnk"),
+    ("gnk_one_group_tail", 333, 192, 136, 1, [300], "gnk"),
 ]
 
 
@@ -83,18 +88,20 @@ def test_ragged_dot_config2_full(gpu_device):
   assert max_rel(out, ref) <= BF16_TOL
 
 
-def test_ragged_dot_f32_out_and_zero_group(gpu_device):
+@pytest.mark.parametrize("layout", ["gkn", "gnk"])
+def test_ragged_dot_f32_out_and_zero_group(gpu_device, layout):
   from lmoe import ops
   rng = np.random.default_rng(3)
   gs = np.array([40, 25, 63], np.int32)
   lhs = O.bf16_round(rng.standard_normal((128, 256)))
   rhs = O.bf16_round(rng.standard_normal((3, 256, 64)) * 0.02)
   ref = O.ragged_dot(lhs, rhs, gs, "f32")
-  out = ops.ragged_dot(to_dev(lhs, "bf16"), to_dev(rhs, "bf16"), to_dev(gs),
-                       preferred_element_type=torch.float32)
+  rhs_dev = to_dev(rhs if layout == "gkn" else np.ascontiguousarray(rhs.transpose(0, 2, 1)), "bf16")
+  out = ops.ragged_dot(to_dev(lhs, "bf16"), rhs_dev, to_dev(gs), preferred_element_type=torch.float32,
+                       rhs_layout=layout)
   assert out.dtype == torch.float32
   assert max_rel(to_np(out), ref) <= 1e-5
-  z = to_np(ops.ragged_dot(to_dev(lhs, "bf16"), to_dev(rhs, "bf16"), to_dev(gs), zero_group=1))
+  z = to_np(ops.ragged_dot(to_dev(lhs, "bf16"), rhs_dev, to_dev(gs), zero_group=1, rhs_layout=layout))
   assert np.all(z[40:65] == 0)
   assert max_rel(z[:40], O.bf16_round(ref[:40])) <= BF16_TOL
 
@@ -185,6 +192,87 @@ def test_mxfp4_gemm_equals_dequant_then_bf16_gemm(gpu_device):
   a = ops.ragged_dot_mxfp4(lhs, to_dev(packed), to_dev(scale), to_dev(gs))
   b = ops.ragged_dot(lhs, wdq, to_dev(gs), rhs_layout="gnk")
   assert torch.equal(a, b)
+
+
+def test_mxfp4_tile_scales_layout(gpu_device):
+  """(G, N, K/32) -> (G, K/64, N, 2): out[g, s, n, h] = scale[g, n, 2s + h]."""
+  from lmoe import ops
+  rng = np.random.default_rng(7)
+  g, n, k = 3, 40, 448
+  scale = rng.integers(0, 256, (g, n, k // 32), dtype=np.uint8)
+  got = to_np(ops.mxfp4_tile_scales(to_dev(scale)))
+  assert got.shape == (g, k // 64, n, 2)
+  for s_ in range(k // 64):
+    for h in range(2):
+      assert np.array_equal(got[:, s_, :, h], scale[:, :, 2 * s_ + h])
+
+
+MX_TILED_CASES = [
+    # m, k, n, g, situ, zero_group
+    (300, 256, 128, 5, False, -1),
+    (300, 256, 128, 5, True, -1),
+    (1024, 1024, 256, 9, True, 8),     # trailing padding bucket skipped
+    (200, 64, 80, 3, True, -1),        # one k step; I = 40: partial n tile
+    (130, 128, 8, 2, False, -1),       # narrowest N
+    (333, 7168, 256, 1, False, -1),    # one group: m-tile groups of 4 per XCD slot
+    (96, 2048, 1024, 4, False, 3),     # cfg5 down-projection shape
+]
+
+
+@pytest.mark.parametrize("m,k,n,g,situ,zg", MX_TILED_CASES)
+def test_ragged_dot_mxfp4_tiled_scales(gpu_device, m, k, n, g, situ, zg):
+  """Direct-to-LDS MXFP4 kernel: parity with the oracle, and bit-identical to
+  the checkpoint-scale kernel (same MFMA sequence)."""
+  from lmoe import ops
+  banner(f"mxfp4 tiled m={m} k={k} n={n} g={g} situ={situ} zero_group={zg}")
+  rng = np.random.default_rng(m * 7 + k + n)
+  gs = rng.multinomial(m - 17, np.ones(g) / g).astype(np.int32)  # 17 tail rows
+  if g > 2:
+    gs[1] = 0
+  lhs = O.bf16_round(rng.standard_normal((m, k)))
+  if zg >= 0:
+    start = int(gs[:zg].sum())
+    lhs[start:start + gs[zg]] = 0.0  # padding-bucket rows are zero in the layer
+  packed, scale = _mx_weights(rng, g, n, k)
+  epi = (4.0, 25.0) if situ else None
+  ref = O.ragged_dot_mxfp4(lhs, packed, scale, gs, "bf16", epi)
+  fa = "situ:4.0:25.0" if situ else None
+  lhs_d, pk_d, gs_d = to_dev(lhs, "bf16"), to_dev(packed), to_dev(gs)
+  tiled = ops.mxfp4_tile_scales(to_dev(scale))
+  out = ops.ragged_dot_mxfp4(lhs_d, pk_d, tiled, gs_d, fuse_gateup_activation=fa, zero_group=zg,
+                             scale_layout="tiled")
+  chk = ops.ragged_dot_mxfp4(lhs_d, pk_d, to_dev(scale), gs_d, fuse_gateup_activation=fa, zero_group=zg)
+  o = to_np(out)
+  assert o.shape == ref.shape
+  assert max_rel(o, ref) <= BF16_TOL
+  assert np.all(o[int(gs.sum()):] == 0)
+  assert torch.equal(out, chk)
+
+
+def test_mxfp4_tiled_edge_scales(gpu_device):
+  """Scale bytes 0..2 (denormal products) and 253..255 (overflow to inf) take
+  the exact per-byte conversion: NaN-aware bit equality with the
+  checkpoint-scale kernel and with dequantise-then-bf16-GEMM."""
+  from lmoe import ops
+  rng = np.random.default_rng(8)
+  m, k, n, g = 160, 256, 128, 2
+  gs = np.array([70, 90], np.int32)
+  lhs = to_dev(O.bf16_round(rng.standard_normal((m, k))), "bf16")
+  packed = rng.integers(0, 256, (g, n, k // 2), dtype=np.uint8)
+  scale = rng.integers(120, 128, (g, n, k // 32), dtype=np.uint8)
+  edge = np.array([0, 1, 2, 3, 252, 253, 254, 255], np.uint8)
+  scale[0, ::5, 1] = edge[rng.integers(0, 8, scale[0, ::5, 1].shape)]
+  scale[1, 7, :] = 0
+  scale[1, 64:70, 3] = 255
+  tiled = ops.mxfp4_tile_scales(to_dev(scale))
+  a = ops.ragged_dot_mxfp4(lhs, to_dev(packed), tiled, to_dev(gs), scale_layout="tiled")
+  b = ops.ragged_dot_mxfp4(lhs, to_dev(packed), to_dev(scale), to_dev(gs))
+  wdq = ops.dequantize_mxfp4(to_dev(packed), to_dev(scale), out_dtype=torch.bfloat16)
+  c = ops.ragged_dot(lhs, wdq, to_dev(gs), rhs_layout="gnk")
+  for x in (b, c):
+    assert torch.equal(torch.isnan(a), torch.isnan(x))
+    fin = ~torch.isnan(a)
+    assert torch.equal(a[fin], x[fin])
 
 
 def test_elementwise_rms_norm_and_situ(gpu_device):

@@ -6,6 +6,8 @@ namespace gemm {
 int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* name);
 int run_f32(const Params& p, int layout, hipStream_t st, const char* name);
 int run_mxfp4_scaled(const Params& p, int epi, hipStream_t st, const char* name);
+int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name);
+int tile_scales(const uint8_t* in, int64_t G, int64_t N, int64_t K, uint8_t* out, hipStream_t st);
 
 namespace {
 
@@ -114,6 +116,10 @@ extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, c
   const int epi = epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (mode == LMOE_MXFP4_LDS_DEQUANT) return run_bf16(p, kMXFP4, epi, st, name);
+  if (mode == LMOE_MXFP4_LDS_DEQUANT_TILED) {
+    LMOE_CHECK_SUPPORTED(aligned(w_scale, 16), "%s: tiled scales must be 16-byte aligned", name);
+    return M == 0 ? LMOE_OK : run_dma(p, kMXFP4, epi, st, name);
+  }
   if (mode == LMOE_MXFP4_SCALED_MFMA) return run_mxfp4_scaled(p, epi, st, name);
   return fail(LMOE_ERR_INVALID, "%s: bad mode %d", name, mode);
 }
@@ -137,4 +143,14 @@ extern "C" int lmoe_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, i
                                                                              group_size, out, out_dtype);
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;
+}
+
+extern "C" int lmoe_mxfp4_tile_scales(const uint8_t* scale, int64_t G, int64_t N, int64_t K, uint8_t* out,
+                                      void* stream) {
+  const char* name = "mxfp4_tile_scales";
+  LMOE_CHECK_ARG(G >= 0 && N >= 0 && K > 0, "%s: bad sizes", name);
+  LMOE_CHECK_SUPPORTED(K % 64 == 0, "%s: needs K %% 64 == 0 (K=%lld)", name, (long long)K);
+  if (G * N == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(scale && out, "%s: null pointer", name);
+  return tile_scales(scale, G, N, K, out, static_cast<hipStream_t>(stream));
 }

@@ -17,6 +17,7 @@
 // (n-tile outer, m-tile inner).  Blocks that run together on one XCD then share
 // A rows (and, with GM > 1, B columns) in that XCD's L2.
 #include <cstdlib>
+#include <cstring>
 #include <utility>
 
 #include "gemm_tile.h"
@@ -392,7 +393,20 @@ int dispatch_shape(const Params& p, hipStream_t st, const char* name) {
 
 }  // namespace
 
+int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name);
+
+// LMOE_GEMM_PATH=regs keeps k-contiguous bf16 weights on the register-staged
+// kernel above (for A/B timing); the default sends them to the DMA kernel.
+static bool use_dma_path() {
+  static const bool v = [] {
+    const char* e = std::getenv("LMOE_GEMM_PATH");
+    return !(e && std::strcmp(e, "regs") == 0);
+  }();
+  return v;
+}
+
 int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* name) {
+  if (layout == kGNK && p.K % 64 == 0 && use_dma_path()) return run_dma(p, layout, epi, st, name);
   if (layout == kGKN && epi == kEpiNone) return dispatch_shape<kGKN, kEpiNone>(p, st, name);
   if (layout == kGKN && epi == kEpiSitu) return dispatch_shape<kGKN, kEpiSitu>(p, st, name);
   if (layout == kGNK && epi == kEpiNone) return dispatch_shape<kGNK, kEpiNone>(p, st, name);
