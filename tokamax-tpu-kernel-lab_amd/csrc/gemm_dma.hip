@@ -29,6 +29,8 @@
 // Layouts: A (M, K) bf16 row-major; B either bf16 (G, N, K) ("GNK") or MXFP4
 // packed (G, N, K/2) with scales re-tiled once to (G, K/64, N, 2)
 // (lmoe_mxfp4_tile_scales).  K % 64 == 0.
+#include <cstdlib>
+#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -81,9 +83,11 @@ __device__ __forceinline__ void wait_and_barrier() {
 
 enum DmaLayout { kDGNK = 0, kDMX = 1 };
 
+// 4 waves side by side along N (each wave: all BM rows x BN/4 columns), so
+// every weight fragment is expanded by exactly one wave.
 template <int BM, int BN, int LAYOUT, int EPI, int NS>
 struct DCfg {
-  static constexpr int kWM = 2, kWN = 2;
+  static constexpr int kWM = 1, kWN = 4;
   static constexpr int kWTM = BM / kWM, kWTN = BN / kWN;
   static constexpr int kTM = kWTM / 16, kTN = kWTN / 16;
   static constexpr int kABytes = BM * 128;                       // A slot
@@ -93,12 +97,17 @@ struct DCfg {
   // DMA instructions per wave per step
   static constexpr int kAOps = BM * 8 / 256;                     // 16-byte chunks / 256 lanes
   static constexpr int kBOps = LAYOUT == kDGNK ? BN * 8 / 256 : BN * 2 / 256;
-  static constexpr int kSOps = LAYOUT == kDMX ? 1 : 0;           // 4 lanes x 16 B per wave
+  static constexpr int kSOps = LAYOUT == kDMX ? 1 : 0;           // BN/32 lanes x 16 B per wave
+  static constexpr int kSLanes = BN / 32;
   static constexpr int kOps = kAOps + kBOps + kSOps;
   static_assert(BM * 8 % 256 == 0 && (LAYOUT == kDGNK ? BN * 8 : BN * 2) % 256 == 0, "DMA split");
-  static_assert(LAYOUT != kDMX || BN * 2 == 4 * 4 * 16, "scale DMA: 4 waves x 4 lanes x 16 B");
+  static_assert(LAYOUT != kDMX || (BN % 32 == 0 && BN <= 2048), "scale DMA: 4 waves x BN/32 lanes x 16 B");
   static_assert((NS - 2) * kOps < 64, "vmcnt range");
   static_assert(EPI != kEpiSitu || kTN % 2 == 0, "SiTU pairs gate/up sub-tiles");
+  // blocks per CU the LDS ring allows (160 KB per CU); the register budget is
+  // capped so that the same number of waves fits on each SIMD
+  static constexpr int kLdsBlocks = 163840 / (NS * kSlot + 64);
+  static constexpr int kWavesPerEu = kLdsBlocks < 1 ? 1 : (kLdsBlocks > 8 ? 8 : kLdsBlocks);
 };
 
 template <int BN, int TN, int EPI>
@@ -126,7 +135,8 @@ __device__ __forceinline__ int64_t drhs_col(int64_t nt, int c, int64_t N) {
 }
 
 template <int BM, int BN, int LAYOUT, int EPI, int NS>
-__global__ __launch_bounds__(kThreads) void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, LAYOUT, EPI, NS>::kWavesPerEu)))
+void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
   using C = DCfg<BM, BN, LAYOUT, EPI, NS>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ TileInfo s_tile;
@@ -204,9 +214,9 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma_kernel(Params p, in
     const uint8_t* s_src = nullptr;
     bool s_active = false;
     if constexpr (LAYOUT == kDMX) {
-      const int sl = lane & 3;
-      s_active = lane < 4;
-      const int c0 = wave * 32 + sl * 8;  // 8 consecutive LDS columns
+      const int sl = lane % C::kSLanes;
+      s_active = lane < C::kSLanes;
+      const int c0 = wave * (BN / 4) + sl * 8;  // 8 consecutive LDS columns
       // LDS columns c0..c0+7 are 8 consecutive global columns (BN/2 is a
       // multiple of 8); a run past the matrix edge reads the last in-bounds
       // run instead (its values are never stored).  N % 16 == 0 for SiTU and
@@ -237,8 +247,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma_kernel(Params p, in
         dma16(b_src[u] + s * b_step,
               __builtin_amdgcn_readfirstlane(base + C::kABytes + (wave * 64 + u * 256) * 16));
       if constexpr (LAYOUT == kDMX) {
-        // lanes 0..3 only: one operation per wave either way
-        const uint32_t sbase = __builtin_amdgcn_readfirstlane(base + C::kABytes + C::kBBytes + wave * 64);
+        // lanes 0..BN/32-1 only: one operation per wave either way
+        const uint32_t sbase = __builtin_amdgcn_readfirstlane(base + C::kABytes + C::kBBytes + wave * (BN / 2));
         if (s_active) dma16(s_src + s * s_step, sbase);
       }
     };
@@ -330,7 +340,24 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma_kernel(Params p, in
   }
 
   // Epilogue: lane holds column (lane % 16) and rows 4*(lane/16) + r.
-  if constexpr (EPI == kEpiSitu) {
+  if (EPI == kEpiSitu && tile.zero) {
+    // padding bucket: zeros, no activation math (SiTU(0, 0) == 0)
+    const int64_t I = N / 2;
+    constexpr int half = C::kTN / 2;
+#pragma unroll
+    for (int i = 0; i < C::kTM; ++i) {
+#pragma unroll
+      for (int j = 0; j < half; ++j) {
+        const int64_t col = nt * (BN / 2) + wn * half * 16 + j * 16 + (lane % 16);
+        if (col >= I) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = wm * C::kWTM + i * 16 + 4 * (lane / 16) + r;
+          if (row < tile.rows) static_cast<uint16_t*>(p.out)[(tile.row0 + row) * I + col] = 0;
+        }
+      }
+    }
+  } else if constexpr (EPI == kEpiSitu) {
     const int64_t I = N / 2;
     constexpr int half = C::kTN / 2;
 #pragma unroll
@@ -348,7 +375,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_dma_kernel(Params p, in
             gv = round_bf16(gv);
             uv = round_bf16(uv);
           }
-          const float v = tile.zero ? 0.0f : situ_fast(gv, uv, p.beta, p.beta_lin);
+          const float v = situ_fast(gv, uv, p.beta, p.beta_lin);
           static_cast<uint16_t*>(p.out)[(tile.row0 + row) * I + col] = f32_to_bf16(v);
         }
       }
@@ -409,14 +436,40 @@ __global__ __launch_bounds__(256) void tile_scales_kernel(const uint8_t* __restr
   }
 }
 
+// Tile shape / ring depth of the MXFP4 kernel: LMOE_DMA_CFG = "BMxBNxNS"
+// picks one of the instantiated variants (tuning sweeps); default 64x128x4.
+int mx_variant() {
+  static const int v = [] {
+    const char* e = std::getenv("LMOE_DMA_CFG");
+    if (!e) return 0;
+    const char* names[] = {"64x128x4", "64x128x6", "64x256x4", "64x256x6", "128x128x4", "128x256x3"};
+    for (int i = 0; i < 6; ++i)
+      if (std::strcmp(e, names[i]) == 0) return i;
+    return 0;
+  }();
+  return v;
+}
+
+template <int EPI>
+int run_mx(const Params& p, hipStream_t st, const char* name) {
+  switch (mx_variant()) {
+    case 1: return launch_dma<64, 128, kDMX, EPI, 6>(p, st, name);
+    case 2: return launch_dma<64, 256, kDMX, EPI, 4>(p, st, name);
+    case 3: return launch_dma<64, 256, kDMX, EPI, 6>(p, st, name);
+    case 4: return launch_dma<128, 128, kDMX, EPI, 4>(p, st, name);
+    case 5: return launch_dma<128, 256, kDMX, EPI, 3>(p, st, name);
+    default: return launch_dma<64, 128, kDMX, EPI, 4>(p, st, name);
+  }
+}
+
 }  // namespace
 
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name) {
   constexpr int BM = 64, BN = 128;
   if (layout == kGNK && epi == kEpiNone) return launch_dma<BM, BN, kDGNK, kEpiNone, 3>(p, st, name);
   if (layout == kGNK && epi == kEpiSitu) return launch_dma<BM, BN, kDGNK, kEpiSitu, 3>(p, st, name);
-  if (layout == kMXFP4 && epi == kEpiNone) return launch_dma<BM, BN, kDMX, kEpiNone, 4>(p, st, name);
-  if (layout == kMXFP4 && epi == kEpiSitu) return launch_dma<BM, BN, kDMX, kEpiSitu, 4>(p, st, name);
+  if (layout == kMXFP4 && epi == kEpiNone) return run_mx<kEpiNone>(p, st, name);
+  if (layout == kMXFP4 && epi == kEpiSitu) return run_mx<kEpiSitu>(p, st, name);
   return fail(LMOE_ERR_UNSUPPORTED, "%s: DMA path layout %d epilogue %d", name, layout, epi);
 }
 

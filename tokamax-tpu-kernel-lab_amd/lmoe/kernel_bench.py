@@ -5,7 +5,7 @@ warm-up, then rounds of back-to-back calls timed with device events, median
 over rounds) and its metrics (bf16 TFLOP/s, GB/s, fraction of the binding
 roofline: valid rows only, each weight byte counted once).
 
-  python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5] [--rounds 10] [--calls 20]
+  python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5,copy] [--rounds 10] [--calls 20]
 
 Prints one JSON object per measured kernel.
 """
@@ -122,14 +122,18 @@ def bench_cfg3(dev, rounds, calls):
 def bench_cfg4(dev, rounds, calls):
   k_, n_ = 7168, 2048
   packed, scale = random_mxfp4(1, n_, k_, dev, seed=4)
+  tiled = ops.mxfp4_tile_scales(scale)
   for m in (1, 16, 128, 1024, 4096):
     gen = torch.Generator(device=dev).manual_seed(m)
     a = torch.randn((m, k_), generator=gen, device=dev).to(torch.bfloat16)
     g = torch.tensor([m], dtype=torch.int32, device=dev)
     flops = 2.0 * m * k_ * n_
     nbytes = n_ * k_ * (0.5 + 1 / 32) + m * k_ * 2 + m * n_ * 2
-    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, packed, scale, g), rounds, calls, name=f"cfg4 mxfp4 matmul lds_dequant M={m}")
-    report(f"cfg4 mxfp4 matmul lds_dequant M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, packed, scale, g), rounds, calls, name=f"cfg4 mxfp4 matmul checkpoint scales M={m}")
+    report(f"cfg4 mxfp4 matmul checkpoint scales M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, packed, tiled, g, scale_layout="tiled"), rounds, calls,
+                 name=f"cfg4 mxfp4 matmul tiled scales M={m}")
+    report(f"cfg4 mxfp4 matmul tiled scales M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
 
 
 def bench_cfg5(dev, rounds, calls):
@@ -155,20 +159,34 @@ def bench_cfg5(dev, rounds, calls):
   report("cfg5 down-proj GEMM 4096x7168x1024", ms, 2.0 * T * H * lat, T * H * 2 + H * lat * 2 + T * lat * 2)
   f_gu = 2.0 * rows * lat * 2 * inter
   b_gu = hit * 2 * inter * lat * (0.5 + 1 / 32) + rows * lat * 2 + rows * inter * 2
-  for mode in ("lds_dequant",):
-    ms = time_fn(lambda: ops.ragged_dot_mxfp4(d.sorted_tokens, experts["gu_packed"], experts["gu_scale"],
+  E = layer.experts
+  for lay, sfx in (("checkpoint", ""), ("tiled", "_tiled")):
+    nm = f"cfg5 mxfp4 gate/up+SiTU grouped GEMM ({lay} scales)"
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed"], E["gu_scale" + sfx],
                                               d.group_sizes, fuse_gateup_activation="situ:4.0:25.0",
-                                              mode=mode, zero_group=L), rounds, calls, name=f"cfg5 mxfp4 gate/up+SiTU grouped GEMM ({mode})")
-    report(f"cfg5 mxfp4 gate/up+SiTU grouped GEMM ({mode})", ms, f_gu, b_gu, rows=rows, experts_hit=hit)
+                                              zero_group=L, scale_layout=lay), rounds, calls, name=nm)
+    report(nm, ms, f_gu, b_gu, rows=rows, experts_hit=hit)
   act = st["act"]
   f_dn = 2.0 * rows * inter * lat
   b_dn = hit * lat * inter * (0.5 + 1 / 32) + rows * inter * 2 + rows * lat * 2
-  ms = time_fn(lambda: ops.ragged_dot_mxfp4(act, experts["down_packed"], experts["down_scale"],
-                                            d.group_sizes, zero_group=L), rounds, calls, name="cfg5 mxfp4 down grouped GEMM (lds_dequant)")
-  report("cfg5 mxfp4 down grouped GEMM (lds_dequant)", ms, f_dn, b_dn, rows=rows)
+  for lay, sfx in (("checkpoint", ""), ("tiled", "_tiled")):
+    nm = f"cfg5 mxfp4 down grouped GEMM ({lay} scales)"
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(act, E["down_packed"], E["down_scale" + sfx], d.group_sizes,
+                                              zero_group=L, scale_layout=lay), rounds, calls, name=nm)
+    report(nm, ms, f_dn, b_dn, rows=rows)
   normed = st["normed"]
   ms = time_fn(lambda: layer._dense(normed, layer.up_nk), rounds, calls, name="cfg5 up-proj GEMM 4096x1024x7168")
   report("cfg5 up-proj GEMM 4096x1024x7168", ms, 2.0 * T * lat * H, T * lat * 2 + lat * H * 2 + T * H * 2)
+
+
+def bench_copy(dev, rounds, calls):
+  """Plain 256 MiB device copy: the calibration kernel for the HBM traffic
+  counters (FETCH_SIZE / WRITE_SIZE should read 256 MiB each)."""
+  n = 256 << 20
+  a = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+  b = torch.empty_like(a)
+  ms = time_fn(lambda: b.copy_(a), rounds, calls, name="copy 256MiB")
+  report("copy 256MiB", ms, 0, 2 * n)
 
 
 def main():
