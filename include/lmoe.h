@@ -52,7 +52,7 @@ extern "C" {
 
 #define LMOE_MXFP4_LDS_DEQUANT 0 /* dequantise weight tiles to bf16 in LDS, bf16 MFMA */
 #define LMOE_MXFP4_SCALED_MFMA 1 /* native v_mfma_scale_f32_*_f8f6f4 (activations to MXFP8) */
-#define LMOE_MXFP4_LDS_DEQUANT_TILED 2 /* as LDS_DEQUANT, w_scale from lmoe_mxfp4_tile_scales */
+#define LMOE_MXFP4_LDS_DEQUANT_TILED 2 /* as LDS_DEQUANT, weights re-tiled by lmoe_mxfp4_tile */
 
 #define LMOE_COMBINE_SCATTER_ADD 0 /* sharded: sequential adds rounded to out dtype (ref.py:1113-1141) */
 #define LMOE_COMBINE_SLOT_SUM 1    /* unsharded: f32 sum over slots, one cast (ref.py:413-416) */
@@ -104,23 +104,25 @@ int lmoe_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, int64_t batc
  * checkpoint layout W_g (N, K/2) u8 + (N, K/32) u8, group size 32).  With
  * epilogue LMOE_EPI_SITU the N axis is [gate | up] and out is (M, N/2).
  * lhs bf16 (M, K), out bf16.  mode: LMOE_MXFP4_LDS_DEQUANT,
- * LMOE_MXFP4_LDS_DEQUANT_TILED (same result; w_scale in the (G, K/64, N, 2)
- * layout of lmoe_mxfp4_tile_scales, which lets weight tiles stream straight
- * into LDS) or LMOE_MXFP4_SCALED_MFMA.
+ * LMOE_MXFP4_LDS_DEQUANT_TILED (same result; w_packed (G, K/64, N, 32) and
+ * w_scale (G, K/64, N, 2) from lmoe_mxfp4_tile, which lets each k step's
+ * weight tile stream into LDS as one contiguous read) or
+ * LMOE_MXFP4_SCALED_MFMA.
  */
 int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_t* w_scale,
                           const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
                           int zero_group, int mode, int epilogue, float beta, float beta_lin,
                           void* out, void* stream);
 
-/* ---- a18: MXFP4 scale preparation -------------------------------------------------
+/* ---- a18: MXFP4 weight preparation ------------------------------------------------
  * One-time weight preparation, the MXFP4 counterpart of prefuse_gateup_weights
- * (rd.py:610-641): E8M0 scales (G, N, K/32) -> out (G, K/64, N, 2), so that
- * the scales of one 64-wide k step of all N columns are contiguous.
- * K % 64 == 0.  out must not alias scale.
+ * (rd.py:610-641): k-step-major re-tiling of checkpoint-layout weights,
+ * packed (G, N, K/2) -> packed_out (G, K/64, N, 32) and E8M0 scales
+ * (G, N, K/32) -> scale_out (G, K/64, N, 2).  K % 64 == 0; outputs must not
+ * alias inputs; packed buffers 16-byte aligned.
  */
-int lmoe_mxfp4_tile_scales(const uint8_t* scale, int64_t G, int64_t N, int64_t K, uint8_t* out,
-                           void* stream);
+int lmoe_mxfp4_tile(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K,
+                    uint8_t* packed_out, uint8_t* scale_out, void* stream);
 
 /* ---- a3: router top-k --------------------------------------------------------------
  * Replaces the gate math of _router_gate (ref.py:601-631) / latent_moe_forward

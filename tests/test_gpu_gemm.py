@@ -194,17 +194,20 @@ def test_mxfp4_gemm_equals_dequant_then_bf16_gemm(gpu_device):
   assert torch.equal(a, b)
 
 
-def test_mxfp4_tile_scales_layout(gpu_device):
-  """(G, N, K/32) -> (G, K/64, N, 2): out[g, s, n, h] = scale[g, n, 2s + h]."""
+def test_mxfp4_tile_weights_layout(gpu_device):
+  """k-step-major re-tiling: packed[g, s, n, b] = checkpoint[g, n, 32 s + b],
+  scale[g, s, n, h] = checkpoint[g, n, 2 s + h]."""
   from lmoe import ops
   rng = np.random.default_rng(7)
   g, n, k = 3, 40, 448
+  packed = rng.integers(0, 256, (g, n, k // 2), dtype=np.uint8)
   scale = rng.integers(0, 256, (g, n, k // 32), dtype=np.uint8)
-  got = to_np(ops.mxfp4_tile_scales(to_dev(scale)))
-  assert got.shape == (g, k // 64, n, 2)
+  pk, sc = (to_np(t) for t in ops.mxfp4_tile_weights(to_dev(packed), to_dev(scale)))
+  assert pk.shape == (g, k // 64, n, 32) and sc.shape == (g, k // 64, n, 2)
   for s_ in range(k // 64):
+    assert np.array_equal(pk[:, s_], packed[:, :, 32 * s_:32 * s_ + 32])
     for h in range(2):
-      assert np.array_equal(got[:, s_, :, h], scale[:, :, 2 * s_ + h])
+      assert np.array_equal(sc[:, s_, :, h], scale[:, :, 2 * s_ + h])
 
 
 MX_TILED_CASES = [
@@ -220,7 +223,7 @@ MX_TILED_CASES = [
 
 
 @pytest.mark.parametrize("m,k,n,g,situ,zg", MX_TILED_CASES)
-def test_ragged_dot_mxfp4_tiled_scales(gpu_device, m, k, n, g, situ, zg):
+def test_ragged_dot_mxfp4_tiled_weights(gpu_device, m, k, n, g, situ, zg):
   """Direct-to-LDS MXFP4 kernel: parity with the oracle, and bit-identical to
   the checkpoint-scale kernel (same MFMA sequence)."""
   from lmoe import ops
@@ -238,9 +241,9 @@ def test_ragged_dot_mxfp4_tiled_scales(gpu_device, m, k, n, g, situ, zg):
   ref = O.ragged_dot_mxfp4(lhs, packed, scale, gs, "bf16", epi)
   fa = "situ:4.0:25.0" if situ else None
   lhs_d, pk_d, gs_d = to_dev(lhs, "bf16"), to_dev(packed), to_dev(gs)
-  tiled = ops.mxfp4_tile_scales(to_dev(scale))
-  out = ops.ragged_dot_mxfp4(lhs_d, pk_d, tiled, gs_d, fuse_gateup_activation=fa, zero_group=zg,
-                             scale_layout="tiled")
+  tpk, tsc = ops.mxfp4_tile_weights(pk_d, to_dev(scale))
+  out = ops.ragged_dot_mxfp4(lhs_d, tpk, tsc, gs_d, fuse_gateup_activation=fa, zero_group=zg,
+                             weight_layout="tiled")
   chk = ops.ragged_dot_mxfp4(lhs_d, pk_d, to_dev(scale), gs_d, fuse_gateup_activation=fa, zero_group=zg)
   o = to_np(out)
   assert o.shape == ref.shape
@@ -264,8 +267,8 @@ def test_mxfp4_tiled_edge_scales(gpu_device):
   scale[0, ::5, 1] = edge[rng.integers(0, 8, scale[0, ::5, 1].shape)]
   scale[1, 7, :] = 0
   scale[1, 64:70, 3] = 255
-  tiled = ops.mxfp4_tile_scales(to_dev(scale))
-  a = ops.ragged_dot_mxfp4(lhs, to_dev(packed), tiled, to_dev(gs), scale_layout="tiled")
+  tpk, tsc = ops.mxfp4_tile_weights(to_dev(packed), to_dev(scale))
+  a = ops.ragged_dot_mxfp4(lhs, tpk, tsc, to_dev(gs), weight_layout="tiled")
   b = ops.ragged_dot_mxfp4(lhs, to_dev(packed), to_dev(scale), to_dev(gs))
   wdq = ops.dequantize_mxfp4(to_dev(packed), to_dev(scale), out_dtype=torch.bfloat16)
   c = ops.ragged_dot(lhs, wdq, to_dev(gs), rhs_layout="gnk")

@@ -7,7 +7,8 @@ int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* n
 int run_f32(const Params& p, int layout, hipStream_t st, const char* name);
 int run_mxfp4_scaled(const Params& p, int epi, hipStream_t st, const char* name);
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name);
-int tile_scales(const uint8_t* in, int64_t G, int64_t N, int64_t K, uint8_t* out, hipStream_t st);
+int tile_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K, uint8_t* packed_out,
+               uint8_t* scale_out, hipStream_t st);
 
 namespace {
 
@@ -118,6 +119,7 @@ extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, c
   if (mode == LMOE_MXFP4_LDS_DEQUANT) return run_bf16(p, kMXFP4, epi, st, name);
   if (mode == LMOE_MXFP4_LDS_DEQUANT_TILED) {
     LMOE_CHECK_SUPPORTED(aligned(w_scale, 16), "%s: tiled scales must be 16-byte aligned", name);
+    // w_packed (G, K/64, N, 32) and w_scale (G, K/64, N, 2) from lmoe_mxfp4_tile
     return M == 0 ? LMOE_OK : run_dma(p, kMXFP4, epi, st, name);
   }
   if (mode == LMOE_MXFP4_SCALED_MFMA) return run_mxfp4_scaled(p, epi, st, name);
@@ -145,12 +147,14 @@ extern "C" int lmoe_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, i
   return LMOE_OK;
 }
 
-extern "C" int lmoe_mxfp4_tile_scales(const uint8_t* scale, int64_t G, int64_t N, int64_t K, uint8_t* out,
-                                      void* stream) {
-  const char* name = "mxfp4_tile_scales";
+extern "C" int lmoe_mxfp4_tile(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K,
+                               uint8_t* packed_out, uint8_t* scale_out, void* stream) {
+  const char* name = "mxfp4_tile";
   LMOE_CHECK_ARG(G >= 0 && N >= 0 && K > 0, "%s: bad sizes", name);
   LMOE_CHECK_SUPPORTED(K % 64 == 0, "%s: needs K %% 64 == 0 (K=%lld)", name, (long long)K);
   if (G * N == 0) return LMOE_OK;
-  LMOE_CHECK_ARG(scale && out, "%s: null pointer", name);
-  return tile_scales(scale, G, N, K, out, static_cast<hipStream_t>(stream));
+  LMOE_CHECK_ARG(packed && scale && packed_out && scale_out, "%s: null pointer", name);
+  LMOE_CHECK_SUPPORTED(aligned(packed, 16) && aligned(packed_out, 16), "%s: packed buffers must be 16-byte aligned",
+                       name);
+  return tile_mxfp4(packed, scale, G, N, K, packed_out, scale_out, static_cast<hipStream_t>(stream));
 }

@@ -27,8 +27,9 @@
 // B fragment is expanded in registers with v_cvt_scalef32_pk_bf16_fp4.
 //
 // Layouts: A (M, K) bf16 row-major; B either bf16 (G, N, K) ("GNK") or MXFP4
-// packed (G, N, K/2) with scales re-tiled once to (G, K/64, N, 2)
-// (lmoe_mxfp4_tile_scales).  K % 64 == 0.
+// re-tiled once by lmoe_mxfp4_tile into k-step-major order: packed
+// (G, K/64, N, 32) and scales (G, K/64, N, 2), so that one step's weights for
+// a run of columns are one contiguous stretch of memory.  K % 64 == 0.
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -57,12 +58,21 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
 }
 
-// One 16-byte DMA per active lane: LDS[base + 16 * lane] = *g.  `base` must be
-// wave-uniform.  M0 is written immediately before use (one wait state).
-__device__ __forceinline__ void dma16(const void* g, uint32_t base) {
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+// Wave-uniform copy of a pointer (lives in an SGPR pair).
+__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// One 16-byte DMA per active lane: LDS[lds + 16 * lane] = *(sbase + off).
+// `sbase` and `lds` are wave-uniform (SGPRs); M0 is written immediately
+// before use (one wait state).
+__device__ __forceinline__ void dma16s(uint32_t off, const uint8_t* sbase, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
                :
-               : "v"(g), "s"(base)
+               : "v"(off), "s"(uniform_ptr(sbase)), "s"(__builtin_amdgcn_readfirstlane(lds))
                : "memory");
 }
 
@@ -73,21 +83,40 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 // Wait until at most N of this wave's vector memory operations are in flight
-// and all its LDS reads have returned, then barrier.  The LDS-read wait keeps a
-// slot's last fragment reads ahead of the DMA that the next step issues into it.
+// and all its LDS reads have returned.  The LDS-read wait keeps a slot's last
+// fragment reads ahead of the DMA that the next step issues into it.
 template <int N>
-__device__ __forceinline__ void wait_and_barrier() {
+__device__ __forceinline__ void wait_vm_lgkm() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)\n\ts_barrier" : : "n"(N) : "memory");
+  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" : : "n"(N) : "memory");
+}
+
+__device__ __forceinline__ void barrier() { asm volatile("s_barrier" : : : "memory"); }
+
+// Wait for the DMA of step kt when `ahead` (0 .. NS-2) later steps, of OPS
+// operations each for this wave, have been issued after it.
+template <int NS, int OPS>
+__device__ __forceinline__ void wait_step(int ahead) {
+  if (ahead >= NS - 2) {
+    wait_vm_lgkm<(NS - 2) * OPS>();
+  } else {
+    static_for<NS - 2>([&](auto a) __attribute__((always_inline)) {
+      constexpr int A = decltype(a)::value;
+      if (ahead == A) wait_vm_lgkm<A * OPS>();
+      return true;
+    });
+  }
 }
 
 enum DmaLayout { kDGNK = 0, kDMX = 1 };
 
-// 4 waves side by side along N (each wave: all BM rows x BN/4 columns), so
-// every weight fragment is expanded by exactly one wave.
-template <int BM, int BN, int LAYOUT, int EPI, int NS>
+// WM x WN waves; wave (wm, wn) owns rows [wm*BM/WM, ...) and columns
+// [wn*BN/WN, ...) of the tile.  With WM == 1 every weight fragment is expanded
+// by exactly one wave.
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4>
 struct DCfg {
-  static constexpr int kWM = 1, kWN = 4;
+  static constexpr int kWM = WM, kWN = WN;
+  static constexpr int kWaves = WM * WN, kThreads = 64 * WM * WN;
   static constexpr int kWTM = BM / kWM, kWTN = BN / kWN;
   static constexpr int kTM = kWTM / 16, kTN = kWTN / 16;
   static constexpr int kABytes = BM * 128;                       // A slot
@@ -95,19 +124,25 @@ struct DCfg {
   static constexpr int kSBytes = LAYOUT == kDMX ? BN * 2 : 0;    // scale slot
   static constexpr int kSlot = kABytes + kBBytes + ((kSBytes + 15) / 16) * 16;
   // DMA instructions per wave per step
-  static constexpr int kAOps = BM * 8 / 256;                     // 16-byte chunks / 256 lanes
-  static constexpr int kBOps = LAYOUT == kDGNK ? BN * 8 / 256 : BN * 2 / 256;
-  static constexpr int kSOps = LAYOUT == kDMX ? 1 : 0;           // BN/32 lanes x 16 B per wave
-  static constexpr int kSLanes = BN / 32;
-  static constexpr int kOps = kAOps + kBOps + kSOps;
-  static_assert(BM * 8 % 256 == 0 && (LAYOUT == kDGNK ? BN * 8 : BN * 2) % 256 == 0, "DMA split");
-  static_assert(LAYOUT != kDMX || (BN % 32 == 0 && BN <= 2048), "scale DMA: 4 waves x BN/32 lanes x 16 B");
-  static_assert((NS - 2) * kOps < 64, "vmcnt range");
+  static constexpr int kAOps = BM * 8 / kThreads;  // 16-byte chunks per thread
+  static constexpr int kBOps = LAYOUT == kDGNK ? BN * 8 / kThreads : BN * 2 / kThreads;
+  // scales: BN columns x 2 bytes per step, fetched by wave 0 alone (kSLanes
+  // lanes x 16 B) -- one instruction instead of one per wave
+  static constexpr int kSOps = LAYOUT == kDMX ? 1 : 0;
+  static constexpr int kSLanes = BN / 8;
+  static constexpr int kOps = kAOps + kBOps;       // per step, every wave
+  static constexpr int kOps0 = kAOps + kBOps + kSOps;  // per step, wave 0
+  static_assert(kAOps >= 1 && BM * 8 % kThreads == 0, "A DMA split");
+  static_assert(kBOps >= 1 && (LAYOUT == kDGNK ? BN * 8 : BN * 2) % kThreads == 0, "B DMA split");
+  static_assert(LAYOUT != kDMX || (BN % 8 == 0 && kSLanes <= 64), "scale DMA split");
+  static_assert(kTM >= 1 && kTN >= 1 && kWTM % 16 == 0 && kWTN % 16 == 0, "wave tile");
+  static_assert((NS - 2) * kOps0 < 64, "vmcnt range");
   static_assert(EPI != kEpiSitu || kTN % 2 == 0, "SiTU pairs gate/up sub-tiles");
   // blocks per CU the LDS ring allows (160 KB per CU); the register budget is
   // capped so that the same number of waves fits on each SIMD
   static constexpr int kLdsBlocks = 163840 / (NS * kSlot + 64);
-  static constexpr int kWavesPerEu = kLdsBlocks < 1 ? 1 : (kLdsBlocks > 8 ? 8 : kLdsBlocks);
+  static constexpr int kWavesPerEuRaw = kLdsBlocks * kWaves / 4;
+  static constexpr int kWavesPerEu = kWavesPerEuRaw < 1 ? 1 : (kWavesPerEuRaw > 8 ? 8 : kWavesPerEuRaw);
 };
 
 template <int BN, int TN, int EPI>
@@ -134,31 +169,52 @@ __device__ __forceinline__ int64_t drhs_col(int64_t nt, int c, int64_t N) {
   }
 }
 
-template <int BM, int BN, int LAYOUT, int EPI, int NS>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, LAYOUT, EPI, NS>::kWavesPerEu)))
-void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
-  using C = DCfg<BM, BN, LAYOUT, EPI, NS>;
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM, int WN>
+__global__ __launch_bounds__((DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>::kThreads))
+__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>::kWavesPerEu)))
+void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtual) {
+  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ TileInfo s_tile;
   __shared__ int64_t s_nt;
 
-  const int tid = threadIdx.x;
+  const int64_t tm = threadIdx.x < 64 ? total_m_tiles<BM>(p.group_sizes, p.G, p.M) : 0;  // used by wave 0
+  // Persistent blocks: block b takes virtual tiles b, b + gridDim.x, ... (the
+  // grid is a multiple of the XCD count, so a virtual tile keeps its XCD).
+  for (int64_t vb = blockIdx.x; vb < n_virtual; vb += gridDim.x) {
+  // The thread index is re-read per tile through an opaque move so that no
+  // per-lane address math is hoisted out of the tile loop: those values would
+  // stay live across every tile and push the kernel past its register budget.
+  int tid;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(static_cast<int>(threadIdx.x)));
   const int lane = tid % 64, wave = tid / 64;
   const int wm = wave / C::kWN, wn = wave % C::kWN;
+  __syncthreads();  // the previous tile's LDS slots and s_tile are no longer read
   if (wave == 0) {
-    const int64_t tm = total_m_tiles<BM>(p.group_sizes, p.G, p.M);
-    const int64_t b = blockIdx.x;
+    const int64_t b = vb;
     const int64_t xcd = b % kXcds, slot = b / kXcds;
-    const int64_t span = static_cast<int64_t>(gm) * n_tiles;
-    const int64_t m_base = ((slot / span) * kXcds + xcd) * gm;
-    const int64_t r = slot % span;
     TileInfo ti{-1, 0, 0, false};
     int64_t nt = 0;
-    if (m_base < tm) {
-      const int64_t gm_eff = tm - m_base < gm ? tm - m_base : gm;
-      if (r < gm_eff * n_tiles) {
-        nt = r / gm_eff;
-        ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, m_base + r % gm_eff);
+    if (gm == 0) {
+      // n-tiles striped over the XCDs: each weight column slice is read by
+      // one XCD only, and the m-tiles of a group (which share it) follow each
+      // other there, so its second and later reads hit that XCD's L2
+      const int64_t per = n_tiles / kXcds;
+      const int64_t mt = slot / per;
+      nt = xcd + kXcds * (slot % per);
+      if (mt < tm) ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, mt);
+    } else {
+      // groups of gm m-tiles round-robin over the XCDs, all n-tiles of a group
+      // on one XCD (the A rows are read by one XCD only)
+      const int64_t span = static_cast<int64_t>(gm) * n_tiles;
+      const int64_t m_base = ((slot / span) * kXcds + xcd) * gm;
+      const int64_t r = slot % span;
+      if (m_base < tm) {
+        const int64_t gm_eff = tm - m_base < gm ? tm - m_base : gm;
+        if (r < gm_eff * n_tiles) {
+          nt = r / gm_eff;
+          ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, m_base + r % gm_eff);
+        }
       }
     }
     if (lane == 0) {
@@ -168,7 +224,7 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
   }
   __syncthreads();
   const TileInfo tile = s_tile;
-  if (tile.group < 0) return;
+  if (tile.group < 0) continue;
   const int64_t nt = s_nt;
   const int64_t K = p.K, N = p.N;
   const int64_t g = tile.group;
@@ -183,40 +239,44 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
     const uint32_t smem0 = lds_offset(smem);
     const int64_t nk = K / kSK;
 
-    // Per-thread DMA sources for step 0; step s adds s * (bytes per step).
-    // A: LDS chunk position q = tid + 256 * v of the slot <- row q/8, logical
-    // chunk (q%8) ^ (row&7).  Rows past the tile read row 0 of the tile.
-    const uint8_t* a_src[C::kAOps];
+    // DMA addressing: a wave-uniform (SGPR) base per operand that advances by
+    // one k step per step, plus a loop-invariant 32-bit per-lane offset.
+    // A: LDS chunk position q = tid + kThreads * v of the slot <- row q/8,
+    // logical chunk (q%8) ^ (row&7).  Rows past the tile read row 0 of the tile.
+    const uint8_t* a_base = uniform_ptr(p.lhs + tile.row0 * K);
+    uint32_t a_off[C::kAOps];
 #pragma unroll
     for (int v = 0; v < C::kAOps; ++v) {
-      const int q = tid + 256 * v;
+      const int q = tid + C::kThreads * v;
       const int row = q / 8, kc = (q % 8) ^ (row & 7);
-      const int64_t rr = row < tile.rows ? row : 0;
-      a_src[v] = reinterpret_cast<const uint8_t*>(p.lhs + (tile.row0 + rr) * K) + kc * 16;
+      const int rr = row < tile.rows ? row : 0;
+      a_off[v] = static_cast<uint32_t>(rr * K * 2 + kc * 16);
     }
-    const uint8_t* b_src[C::kBOps];
+    // GNK: row n of group g at (g*N + n) * 2K bytes; MXFP4 (k-step-major):
+    // column n of step s of group g at ((g*K/64 + s)*N + n) * 32 bytes
+    const int64_t b_row = LAYOUT == kDGNK ? K * 2 : 32;
+    const uint8_t* b_base = uniform_ptr(static_cast<const uint8_t*>(p.rhs) + g * N * (LAYOUT == kDGNK ? K * 2 : K / 2));
+    uint32_t b_off[C::kBOps];
 #pragma unroll
     for (int u = 0; u < C::kBOps; ++u) {
-      const int q = tid + 256 * u;
+      const int q = tid + C::kThreads * u;
       if constexpr (LAYOUT == kDGNK) {
         const int c = q / 8, kc = (q % 8) ^ (c & 7);
-        const int64_t n = drhs_col<BN, EPI>(nt, c, N);
-        b_src[u] = reinterpret_cast<const uint8_t*>(static_cast<const uint16_t*>(p.rhs) + (g * N + n) * K) +
-                   kc * 16;
+        b_off[u] = static_cast<uint32_t>(drhs_col<BN, EPI>(nt, c, N) * b_row + kc * 16);
       } else {
         const int c = q / 2, ch = (q % 2) ^ ((c >> 3) & 1);
-        const int64_t n = drhs_col<BN, EPI>(nt, c, N);
-        b_src[u] = static_cast<const uint8_t*>(p.rhs) + (g * N + n) * (K / 2) + ch * 16;
+        b_off[u] = static_cast<uint32_t>(drhs_col<BN, EPI>(nt, c, N) * b_row + ch * 16);
       }
     }
-    // Scales (tiled (G, K/64, N, 2)): wave w's lanes 0..3 fetch 16 bytes =
-    // 8 columns' two scale bytes; wave w covers columns [32w, 32w + 32).
-    const uint8_t* s_src = nullptr;
+    // Scales (tiled (G, K/64, N, 2)): lanes 0..kSLanes-1 of wave 0 each fetch
+    // 16 bytes = 8 LDS columns' two scale bytes.
+    const uint8_t* s_base = nullptr;
+    uint32_t s_off = 0;
     bool s_active = false;
     if constexpr (LAYOUT == kDMX) {
       const int sl = lane % C::kSLanes;
       s_active = lane < C::kSLanes;
-      const int c0 = wave * (BN / 4) + sl * 8;  // 8 consecutive LDS columns
+      const int c0 = sl * 8;  // 8 consecutive LDS columns
       // LDS columns c0..c0+7 are 8 consecutive global columns (BN/2 is a
       // multiple of 8); a run past the matrix edge reads the last in-bounds
       // run instead (its values are never stored).  N % 16 == 0 for SiTU and
@@ -231,25 +291,29 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
         n0 = nt * BN + c0;
         n0 = n0 <= N - 8 ? n0 : N - 8;
       }
-      s_src = p.scale + (g * (K / 64) * N + n0) * 2;
+      s_base = uniform_ptr(p.scale + g * (K / 64) * N * 2);
+      s_off = static_cast<uint32_t>(n0 * 2);
     }
-    const int64_t a_step = kSK * 2, b_step = LAYOUT == kDGNK ? kSK * 2 : kSK / 2;
+    const int64_t b_step = LAYOUT == kDGNK ? kSK * 2 : N * 32;
     const int64_t s_step = N * 2;
+    // LDS destination of this wave's chunk 0 (M0 must be wave-uniform)
+    const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(smem0 + wave * 64 * 16);
 
+    // DMA of step `step` into ring slot `slot`; nothing past the last step.
     auto issue = [&](int64_t step, int slot) __attribute__((always_inline)) {
-      const int64_t s = step < nk ? step : nk - 1;  // past the end: reload (unused)
-      const uint32_t base = smem0 + slot * C::kSlot;
+      if (step >= nk) return;
+      const int64_t s = step;
+      const uint32_t base = lds_wave + slot * C::kSlot;
 #pragma unroll
-      for (int v = 0; v < C::kAOps; ++v)
-        dma16(a_src[v] + s * a_step, __builtin_amdgcn_readfirstlane(base + (wave * 64 + v * 256) * 16));
+      for (int v = 0; v < C::kAOps; ++v) dma16s(a_off[v], a_base + s * (kSK * 2), base + v * C::kThreads * 16);
 #pragma unroll
       for (int u = 0; u < C::kBOps; ++u)
-        dma16(b_src[u] + s * b_step,
-              __builtin_amdgcn_readfirstlane(base + C::kABytes + (wave * 64 + u * 256) * 16));
+        dma16s(b_off[u], b_base + s * b_step, base + C::kABytes + u * C::kThreads * 16);
       if constexpr (LAYOUT == kDMX) {
-        // lanes 0..BN/32-1 only: one operation per wave either way
-        const uint32_t sbase = __builtin_amdgcn_readfirstlane(base + C::kABytes + C::kBBytes + wave * (BN / 2));
-        if (s_active) dma16(s_src + s * s_step, sbase);
+        if (wave == 0) {
+          const uint32_t sbase = base + C::kABytes + C::kBBytes;  // wave 0: base is the slot start
+          if (s_active) dma16s(s_off, s_base + s * s_step, sbase);
+        }
       }
     };
 
@@ -270,17 +334,19 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
 #pragma unroll
       for (int ks = 0; ks < kSK / 32; ++ks) {
         const int kc = ks * 4 + (lane / 16);  // logical 16-byte chunk of this lane
-        bf16x8_t af[C::kTM], bfr[C::kTN];
+        bf16x8_t af[C::kTM];
 #pragma unroll
         for (int i = 0; i < C::kTM; ++i) {
           const int r = wm * C::kWTM + i * 16 + (lane % 16);
           af[i] = *reinterpret_cast<const bf16x8_t*>(as + r * 128 + ((kc ^ (r & 7)) * 16));
         }
+        // B fragments one at a time: read, expand, feed the column of MFMAs
 #pragma unroll
         for (int j = 0; j < C::kTN; ++j) {
           const int c = dlds_col<BN, C::kTN, EPI>(wn, j) + (lane % 16);
+          bf16x8_t bfr;
           if constexpr (LAYOUT == kDGNK) {
-            bfr[j] = *reinterpret_cast<const bf16x8_t*>(bs + c * 128 + ((kc ^ (c & 7)) * 16));
+            bfr = *reinterpret_cast<const bf16x8_t*>(bs + c * 128 + ((kc ^ (c & 7)) * 16));
           } else {
             const uint32_t w =
                 *reinterpret_cast<const uint32_t*>(bs + c * 32 + ((ks ^ ((c >> 3) & 1)) * 16) + (lane / 16) * 4);
@@ -296,168 +362,233 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm) {
 #pragma unroll
               for (int b = 0; b < 4; ++b) o[b] = dequant_byte((w >> (8 * b)) & 0xffu, sb);
             }
-            bfr[j] = __builtin_bit_cast(bf16x8_t, uint4{o[0], o[1], o[2], o[3]});
+            bfr = __builtin_bit_cast(bf16x8_t, uint4{o[0], o[1], o[2], o[3]});
           }
+#pragma unroll
+          for (int i = 0; i < C::kTM; ++i)
+            // weight fragment first: the accumulator holds the transposed
+            // sub-tile (a lane owns one row and four adjacent columns)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, af[i], acc[i][j], 0, 0, 0);
         }
-#pragma unroll
-        for (int i = 0; i < C::kTM; ++i)
-#pragma unroll
-          for (int j = 0; j < C::kTN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
       }
     };
 
-    for (int64_t kt0 = 0; kt0 < nk; kt0 += NS) {
-      static_for<NS>([&](auto sc) __attribute__((always_inline)) {
-        constexpr int st = decltype(sc)::value;
-        const int64_t kt = kt0 + st;
-        if (kt >= nk) return false;
-        wait_and_barrier<(NS - 2) * C::kOps>();
-        issue(kt + NS - 1, (st + NS - 1) % NS);
-        uint32_t s2[C::kTN];
-        if constexpr (LAYOUT == kDMX) {
-          const uint8_t* ss = smem + st * C::kSlot + C::kABytes + C::kBBytes;
-          bool edge = false;
+    // One pipeline step per iteration; the slot index is a run-time value so
+    // the accumulators keep one register assignment across steps.
+    int cur = 0;  // slot of step kt
+    for (int64_t kt = 0; kt < nk; ++kt) {
+      const int ahead = static_cast<int>(nk - 1 - kt < NS - 2 ? nk - 1 - kt : NS - 2);
+      if (wave == 0)
+        wait_step<NS, C::kOps0>(ahead);
+      else
+        wait_step<NS, C::kOps>(ahead);
+      barrier();
+      issue(kt + NS - 1, cur == 0 ? NS - 1 : cur - 1);
+      uint32_t s2[C::kTN];
+      if constexpr (LAYOUT == kDMX) {
+        const uint8_t* ss = smem + cur * C::kSlot + C::kABytes + C::kBBytes;
+        bool edge = false;
 #pragma unroll
-          for (int j = 0; j < C::kTN; ++j) {
-            const int c = dlds_col<BN, C::kTN, EPI>(wn, j) + (lane % 16);
-            s2[j] = *reinterpret_cast<const uint16_t*>(ss + c * 2);
-            edge |= !hw_scale_ok(s2[j] & 0xffu) || !hw_scale_ok(s2[j] >> 8);
-          }
-          if (__builtin_amdgcn_ballot_w64(edge) != 0)
-            compute(st, s2, std::true_type{});
-          else
-            compute(st, s2, std::false_type{});
-        } else {
-#pragma unroll
-          for (int j = 0; j < C::kTN; ++j) s2[j] = 0;
-          compute(st, s2, std::false_type{});
+        for (int j = 0; j < C::kTN; ++j) {
+          const int c = dlds_col<BN, C::kTN, EPI>(wn, j) + (lane % 16);
+          s2[j] = *reinterpret_cast<const uint16_t*>(ss + c * 2);
+          edge |= !hw_scale_ok(s2[j] & 0xffu) || !hw_scale_ok(s2[j] >> 8);
         }
-        return true;
-      });
+        if (__builtin_amdgcn_ballot_w64(edge) != 0)
+          compute(cur, s2, std::true_type{});
+        else
+          compute(cur, s2, std::false_type{});
+      } else {
+#pragma unroll
+        for (int j = 0; j < C::kTN; ++j) s2[j] = 0;
+        compute(cur, s2, std::false_type{});
+      }
+      cur = cur == NS - 1 ? 0 : cur + 1;
     }
-    wait_vmcnt<0>();  // drain the dummy tail loads before the block can exit
+    // every DMA of this tile has been waited for by the last step
   }
 
-  // Epilogue: lane holds column (lane % 16) and rows 4*(lane/16) + r.
-  if (EPI == kEpiSitu && tile.zero) {
-    // padding bucket: zeros, no activation math (SiTU(0, 0) == 0)
+  // Epilogue.  A lane holds output row (lane % 16) of row sub-tile i and the
+  // four adjacent columns 4*(lane/16) .. +3 of column sub-tile j: one 8-byte
+  // (bf16) or 16-byte (f32) store per sub-tile.  Column counts are multiples
+  // of 8 (checked on the host), so a group of four is in or out as a whole.
+  const int r_in = lane % 16, c_in = 4 * (lane / 16);
+  if constexpr (EPI == kEpiSitu) {
     const int64_t I = N / 2;
     constexpr int half = C::kTN / 2;
+    const SituConsts sc = situ_consts(p.beta, p.beta_lin);
 #pragma unroll
     for (int i = 0; i < C::kTM; ++i) {
+      const int row = wm * C::kWTM + i * 16 + r_in;
+      if (row >= tile.rows) continue;
+      uint16_t* orow = static_cast<uint16_t*>(p.out) + (tile.row0 + row) * I;
 #pragma unroll
       for (int j = 0; j < half; ++j) {
-        const int64_t col = nt * (BN / 2) + wn * half * 16 + j * 16 + (lane % 16);
+        const int64_t col = nt * (BN / 2) + wn * half * 16 + j * 16 + c_in;
         if (col >= I) continue;
+        uint2 packed{0u, 0u};  // padding bucket: zeros (SiTU(0, 0) == 0)
+        if (!tile.zero) {
+          float v[4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = wm * C::kWTM + i * 16 + 4 * (lane / 16) + r;
-          if (row < tile.rows) static_cast<uint16_t*>(p.out)[(tile.row0 + row) * I + col] = 0;
-        }
-      }
-    }
-  } else if constexpr (EPI == kEpiSitu) {
-    const int64_t I = N / 2;
-    constexpr int half = C::kTN / 2;
-#pragma unroll
-    for (int i = 0; i < C::kTM; ++i) {
-#pragma unroll
-      for (int j = 0; j < half; ++j) {
-        const int64_t col = nt * (BN / 2) + wn * half * 16 + j * 16 + (lane % 16);
-        if (col >= I) continue;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = wm * C::kWTM + i * 16 + 4 * (lane / 16) + r;
-          if (row >= tile.rows) continue;
-          float gv = acc[i][j][r], uv = acc[i][j + half][r];
-          if (p.round_before_act) {
-            gv = round_bf16(gv);
-            uv = round_bf16(uv);
+          for (int r = 0; r < 4; ++r) {
+            float gv = acc[i][j][r], uv = acc[i][j + half][r];
+            if (p.round_before_act) {
+              gv = static_cast<float>(static_cast<__bf16>(gv));
+              uv = static_cast<float>(static_cast<__bf16>(uv));
+            }
+            v[r] = situ_epi(gv, uv, sc);
           }
-          const float v = situ_fast(gv, uv, p.beta, p.beta_lin);
-          static_cast<uint16_t*>(p.out)[(tile.row0 + row) * I + col] = f32_to_bf16(v);
+          packed = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
         }
+        *reinterpret_cast<uint2*>(orow + col) = packed;
       }
     }
   } else {
 #pragma unroll
     for (int i = 0; i < C::kTM; ++i) {
+      const int row = wm * C::kWTM + i * 16 + r_in;
+      if (row >= tile.rows) continue;
+      const int64_t obase = (tile.row0 + row) * N;
 #pragma unroll
       for (int j = 0; j < C::kTN; ++j) {
-        const int64_t col = nt * BN + wn * C::kTN * 16 + j * 16 + (lane % 16);
+        const int64_t col = nt * BN + wn * C::kTN * 16 + j * 16 + c_in;
         if (col >= N) continue;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = wm * C::kWTM + i * 16 + 4 * (lane / 16) + r;
-          if (row >= tile.rows) continue;
-          store_from_f32(p.out, (tile.row0 + row) * N + col, acc[i][j][r], p.out_dtype);
+        const floatx4 a = acc[i][j];
+        if (p.out_dtype == LMOE_F32) {
+          *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + col) = float4{a[0], a[1], a[2], a[3]};
+        } else {
+          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+              uint2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
         }
       }
     }
   }
+  }  // persistent tile loop
 }
 
-template <int BM, int BN, int LAYOUT, int EPI, int NS>
+// Compute units of the current device (cached per device).
+int cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    cache[dev] = v;
+  }
+  return cache[dev];
+}
+
+// LMOE_PERSIST=1 launches only as many blocks as fit on the device at once,
+// each looping over tiles; the default launches one block per tile (measured
+// equal or faster on the expert shapes, where the hardware's block refill
+// overlaps one block's epilogue with its neighbours' main loops).
+bool persistent_blocks() {
+  static const bool v = [] {
+    const char* e = std::getenv("LMOE_PERSIST");
+    return e && std::strcmp(e, "1") == 0;
+  }();
+  return v;
+}
+
+// LMOE_XCD_MAP=mtile keeps m-tile groups per XCD for grouped problems (A/B
+// timing); the default stripes n-tiles over the XCDs when they divide evenly.
+bool xcd_stripe_n() {
+  static const bool v = [] {
+    const char* e = std::getenv("LMOE_XCD_MAP");
+    return !(e && std::strcmp(e, "mtile") == 0);
+  }();
+  return v;
+}
+
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4>
 int launch_dma(const Params& p, hipStream_t st, const char* name) {
-  using C = DCfg<BM, BN, LAYOUT, EPI, NS>;
+  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>;
   const int64_t out_cols = EPI == kEpiSitu ? p.N / 2 : p.N;
   const int64_t cols_per_tile = EPI == kEpiSitu ? BN / 2 : BN;
   const int64_t ntiles = ceil_div(out_cols, cols_per_tile);
   const int64_t mtiles = ceil_div(p.M, BM) + p.G + 1;
   if (ntiles == 0 || p.M == 0) return LMOE_OK;
-  const int gm = p.G == 1 ? 4 : 1;
-  const int64_t groups_per_xcd = ceil_div(ceil_div(mtiles, gm), kXcds);
-  const int64_t blocks = kXcds * groups_per_xcd * gm * ntiles;
+  int gm = p.G == 1 ? 4 : 1;
+  int64_t blocks = kXcds * ceil_div(ceil_div(mtiles, gm), kXcds) * gm * ntiles;
+  if (p.G > 1 && ntiles % kXcds == 0 && xcd_stripe_n()) {
+    gm = 0;  // n-tiles striped over the XCDs
+    blocks = mtiles * ntiles;
+  }
   LMOE_CHECK_SUPPORTED(blocks < (1ll << 31), "%s: grid too large", name);
+  // per-lane DMA offsets are 32-bit: one group's weights and one tile's rows
+  const int64_t w_bytes = p.N * (LAYOUT == kDGNK ? p.K * 2 : p.K / 2);
+  LMOE_CHECK_SUPPORTED(w_bytes < (1ll << 32) && BM * p.K * 2 < (1ll << 32), "%s: group too large for the DMA path",
+                       name);
   const size_t lds = static_cast<size_t>(NS) * C::kSlot;
   static const hipError_t attr_rc =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr_rc != hipSuccess)
     return fail(LMOE_ERR_HIP, "%s: LDS size attribute (%zu bytes): %s", name, lds, hipGetErrorString(attr_rc));
-  grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS>
-      <<<dim3(static_cast<unsigned>(blocks)), kThreads, lds, st>>>(p, ntiles, gm);
+  int64_t grid = blocks;
+  if (persistent_blocks()) {
+    const int64_t resident = kXcds * ((static_cast<int64_t>(cu_count()) * C::kLdsBlocks) / kXcds);
+    if (resident >= kXcds && resident < grid) grid = resident;
+  }
+  grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN>
+      <<<dim3(static_cast<unsigned>(grid)), C::kThreads, lds, st>>>(p, ntiles, gm, blocks);
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;
 }
 
-// Re-tile E8M0 scales (G, N, K/32) -> (G, K/64, N, 2).
-__global__ __launch_bounds__(256) void tile_scales_kernel(const uint8_t* __restrict__ in, int64_t G,
-                                                          int64_t N, int64_t K, uint8_t* __restrict__ out) {
+// Re-tile MXFP4 weights to k-step-major order: packed (G, N, K/2) ->
+// (G, K/64, N, 32) and E8M0 scales (G, N, K/32) -> (G, K/64, N, 2).  One
+// thread per (group, step, column): two 16-byte copies and one 2-byte copy.
+__global__ __launch_bounds__(256) void tile_mxfp4_kernel(const uint8_t* __restrict__ packed,
+                                                         const uint8_t* __restrict__ scale, int64_t G, int64_t N,
+                                                         int64_t K, uint8_t* __restrict__ packed_out,
+                                                         uint8_t* __restrict__ scale_out) {
   const int64_t kb64 = K / 64;
   const int64_t total = G * kb64 * N;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < total;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t n = i % N, s = (i / N) % kb64, g = i / (N * kb64);
-    const uint8_t* src = in + (g * N + n) * (K / 32) + 2 * s;
-    out[2 * i] = src[0];
-    out[2 * i + 1] = src[1];
+    const uint4* src = reinterpret_cast<const uint4*>(packed + (g * N + n) * (K / 2) + 32 * s);
+    uint4* dst = reinterpret_cast<uint4*>(packed_out + 32 * i);
+    dst[0] = src[0];
+    dst[1] = src[1];
+    const uint8_t* ss = scale + (g * N + n) * (K / 32) + 2 * s;
+    scale_out[2 * i] = ss[0];
+    scale_out[2 * i + 1] = ss[1];
   }
 }
 
 // Tile shape / ring depth of the MXFP4 kernel: LMOE_DMA_CFG = "BMxBNxNS"
-// picks one of the instantiated variants (tuning sweeps); default 64x128x4.
+// picks one of the instantiated variants (tuning sweeps).  Defaults, from
+// sweeps on the LatentMoE expert shapes: 64x256x4 with the fused SiTU
+// epilogue (gate/up: each activation tile feeds 128 gate + 128 up columns),
+// 64x128x4 without (down projection: more blocks in flight).
 int mx_variant() {
   static const int v = [] {
     const char* e = std::getenv("LMOE_DMA_CFG");
-    if (!e) return 0;
-    const char* names[] = {"64x128x4", "64x128x6", "64x256x4", "64x256x6", "128x128x4", "128x256x3"};
-    for (int i = 0; i < 6; ++i)
+    if (!e) return -1;
+    const char* names[] = {"64x128x4", "64x128x6", "64x256x4", "64x256x3", "64x128x3", "32x128x4", "32x256x4",
+                           "64x256x5"};
+    for (int i = 0; i < 8; ++i)
       if (std::strcmp(e, names[i]) == 0) return i;
-    return 0;
+    return -1;
   }();
   return v;
 }
 
 template <int EPI>
 int run_mx(const Params& p, hipStream_t st, const char* name) {
-  switch (mx_variant()) {
+  int v = mx_variant();
+  if (v < 0) v = EPI == kEpiSitu ? 2 : 0;
+  switch (v) {
     case 1: return launch_dma<64, 128, kDMX, EPI, 6>(p, st, name);
     case 2: return launch_dma<64, 256, kDMX, EPI, 4>(p, st, name);
-    case 3: return launch_dma<64, 256, kDMX, EPI, 6>(p, st, name);
-    case 4: return launch_dma<128, 128, kDMX, EPI, 4>(p, st, name);
-    case 5: return launch_dma<128, 256, kDMX, EPI, 3>(p, st, name);
+    case 3: return launch_dma<64, 256, kDMX, EPI, 3>(p, st, name);
+    case 4: return launch_dma<64, 128, kDMX, EPI, 3>(p, st, name);
+    case 5: return launch_dma<32, 128, kDMX, EPI, 4>(p, st, name);
+    case 6: return launch_dma<32, 256, kDMX, EPI, 4>(p, st, name);
+    case 7: return launch_dma<64, 256, kDMX, EPI, 5>(p, st, name);
     default: return launch_dma<64, 128, kDMX, EPI, 4>(p, st, name);
   }
 }
@@ -473,12 +604,14 @@ int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* na
   return fail(LMOE_ERR_UNSUPPORTED, "%s: DMA path layout %d epilogue %d", name, layout, epi);
 }
 
-int tile_scales(const uint8_t* in, int64_t G, int64_t N, int64_t K, uint8_t* out, hipStream_t st) {
+int tile_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K, uint8_t* packed_out,
+               uint8_t* scale_out, hipStream_t st) {
   const int64_t total = G * (K / 64) * N;
   if (total == 0) return LMOE_OK;
   const int64_t b = ceil_div(total, 256);
-  tile_scales_kernel<<<static_cast<unsigned>(b < 65536 ? b : 65536), 256, 0, st>>>(in, G, N, K, out);
-  LMOE_CHECK_LAUNCH("mxfp4_tile_scales");
+  tile_mxfp4_kernel<<<static_cast<unsigned>(b < 65536 ? b : 65536), 256, 0, st>>>(packed, scale, G, N, K,
+                                                                                  packed_out, scale_out);
+  LMOE_CHECK_LAUNCH("mxfp4_tile");
   return LMOE_OK;
 }
 

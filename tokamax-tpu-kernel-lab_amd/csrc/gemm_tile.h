@@ -171,6 +171,53 @@ __device__ __forceinline__ float situ_fast(float g, float u, float beta, float b
   return sg * bu;
 }
 
+// Two f32 -> packed bf16 pair (round to nearest even, hardware conversion).
+typedef __bf16 bf16x2_pack_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  const bf16x2_pack_t v = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// SiTU-GLU for the fused epilogue (ref.py:305-310):
+//   beta*tanh(g/beta)*sigmoid(g) * beta_lin*tanh(u/beta_lin)
+// with two reciprocals: tanh(x) = (e^2x - 1) / (e^2x + 1) and
+// sigmoid(g) = 1 / (1 + e^-g), so
+//   SiTU = beta*beta_lin * (e1 - 1)(e2 - 1) / ((e1 + 1)(e2 + 1)) / (1 + e0).
+// tanh arguments are clamped to |x| <= 9 (tanh(9) = 1 - 3e-8) so that the
+// tanh product cannot overflow (the sigmoid factor keeps its own reciprocal
+// and goes to 0 only where e^-g overflows); below |x| = 2^-6 the numerator
+// is replaced by
+// (e + 1) * x(1 - x^2/3 + 2x^4/15) (relative error < 1e-10), avoiding the
+// cancellation in e - 1.  Hardware exp2 / reciprocal: a few f32 ulp, far below
+// the bf16 rounding of the result.  NaN inputs give NaN.
+struct SituConsts {
+  float ib2, ibl2;   // 2*log2(e)/beta, 2*log2(e)/beta_lin
+  float ib, ibl;     // 1/beta, 1/beta_lin
+  float bbl;         // beta*beta_lin
+};
+__device__ __forceinline__ SituConsts situ_consts(float beta, float beta_lin) {
+  const float ib = 1.0f / beta, ibl = 1.0f / beta_lin;
+  return SituConsts{2.0f * 1.44269504088896341f * ib, 2.0f * 1.44269504088896341f * ibl, ib, ibl, beta * beta_lin};
+}
+__device__ __forceinline__ void tanh_frac(float x, float e, float& num, float& den) {
+  den = e + 1.0f;
+  const float t = x * x;
+  const float poly = __builtin_fmaf(t * x, __builtin_fmaf(t, 0.133333333f, -0.333333333f), x);
+  num = __builtin_fabsf(x) < 0.015625f ? den * poly : e - 1.0f;
+}
+__device__ __forceinline__ float situ_epi(float g, float u, const SituConsts& c) {
+  const float x1 = __builtin_amdgcn_fmed3f(g * c.ib, -9.0f, 9.0f);
+  const float x2 = __builtin_amdgcn_fmed3f(u * c.ibl, -9.0f, 9.0f);
+  const float e1 = __builtin_amdgcn_exp2f(x1 * 2.88539008177792682f);
+  const float e2 = __builtin_amdgcn_exp2f(x2 * 2.88539008177792682f);
+  const float e0 = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  float n1, d1, n2, d2;
+  tanh_frac(x1, e1, n1, d1);
+  tanh_frac(x2, e2, n2, d2);
+  const float r = c.bbl * n1 * n2 * __builtin_amdgcn_rcpf(d1 * d2) * __builtin_amdgcn_rcpf(1.0f + e0);
+  return (g != g || u != u) ? __builtin_nanf("") : r;
+}
+
 // E2M1 nibble with E8M0 scale byte s -> bf16 bits, exact (value has <= 2
 // significant bits, so the f32 product truncates to bf16 without rounding).
 __device__ __forceinline__ uint32_t fp4_to_bf16_bits(uint32_t nib, float scale) {

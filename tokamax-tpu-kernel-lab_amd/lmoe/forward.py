@@ -161,12 +161,14 @@ class LocalShardLatentMoE:
     self.norm_scale = norm_scale.contiguous()
     self.experts = dict(experts)
     self.shared = shared
-    # MXFP4 scales re-tiled once so weight tiles stream straight into LDS
-    self.scale_layout, self._sfx = "checkpoint", ""
+    # MXFP4 weights re-tiled once (k-step-major) so each k step's weight tile
+    # streams into LDS as one contiguous read
+    self.weight_layout, self._sfx = "checkpoint", ""
     if expert_format == "mxfp4" and mxfp4_mode == "lds_dequant":
-      self.experts["gu_scale_tiled"] = ops.mxfp4_tile_scales(experts["gu_scale"])
-      self.experts["down_scale_tiled"] = ops.mxfp4_tile_scales(experts["down_scale"])
-      self.scale_layout, self._sfx = "tiled", "_tiled"
+      for w in ("gu", "down"):
+        pk, sc = ops.mxfp4_tile_weights(experts[f"{w}_packed"], experts[f"{w}_scale"])
+        self.experts[f"{w}_packed_tiled"], self.experts[f"{w}_scale_tiled"] = pk, sc
+      self.weight_layout, self._sfx = "tiled", "_tiled"
 
   def _dense(self, x, w_nk, out_dtype=None):
     return ops.dense(x, w_nk, out_dtype=out_dtype, w_layout="nk")
@@ -189,9 +191,10 @@ class LocalShardLatentMoE:
     if "gateup" in ev:
       ev["gateup"][0].record()
     if self.expert_format == "mxfp4":
-      act = ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed"], E["gu_scale" + self._sfx], d.group_sizes,
+      act = ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed" + self._sfx], E["gu_scale" + self._sfx],
+                                 d.group_sizes,
                                  fuse_gateup_activation=f"situ:{b}:{bl}", mode=self.mxfp4_mode,
-                                 zero_group=self.L, scale_layout=self.scale_layout)
+                                 zero_group=self.L, weight_layout=self.weight_layout)
     else:
       act = ops.ragged_dot_gateup_situ(d.sorted_tokens, E["gu_nk"], d.group_sizes, b, bl,
                                        rhs_layout="gnk", zero_group=self.L)
@@ -200,9 +203,10 @@ class LocalShardLatentMoE:
     if "down" in ev:
       ev["down"][0].record()
     if self.expert_format == "mxfp4":
-      shard_out = ops.ragged_dot_mxfp4(act, E["down_packed"], E["down_scale" + self._sfx], d.group_sizes,
+      shard_out = ops.ragged_dot_mxfp4(act, E["down_packed" + self._sfx], E["down_scale" + self._sfx],
+                                       d.group_sizes,
                                        mode=self.mxfp4_mode, zero_group=self.L,
-                                       scale_layout=self.scale_layout)
+                                       weight_layout=self.weight_layout)
     else:
       shard_out = ops.ragged_dot(act, E["down_nk"], d.group_sizes, rhs_layout="gnk", zero_group=self.L)
     if "down" in ev:

@@ -122,7 +122,7 @@ def bench_cfg3(dev, rounds, calls):
 def bench_cfg4(dev, rounds, calls):
   k_, n_ = 7168, 2048
   packed, scale = random_mxfp4(1, n_, k_, dev, seed=4)
-  tiled = ops.mxfp4_tile_scales(scale)
+  tpk, tsc = ops.mxfp4_tile_weights(packed, scale)
   for m in (1, 16, 128, 1024, 4096):
     gen = torch.Generator(device=dev).manual_seed(m)
     a = torch.randn((m, k_), generator=gen, device=dev).to(torch.bfloat16)
@@ -131,9 +131,9 @@ def bench_cfg4(dev, rounds, calls):
     nbytes = n_ * k_ * (0.5 + 1 / 32) + m * k_ * 2 + m * n_ * 2
     ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, packed, scale, g), rounds, calls, name=f"cfg4 mxfp4 matmul checkpoint scales M={m}")
     report(f"cfg4 mxfp4 matmul checkpoint scales M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
-    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, packed, tiled, g, scale_layout="tiled"), rounds, calls,
-                 name=f"cfg4 mxfp4 matmul tiled scales M={m}")
-    report(f"cfg4 mxfp4 matmul tiled scales M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled"), rounds, calls,
+                 name=f"cfg4 mxfp4 matmul tiled weights M={m}")
+    report(f"cfg4 mxfp4 matmul tiled weights M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
 
 
 def bench_cfg5(dev, rounds, calls):
@@ -161,18 +161,18 @@ def bench_cfg5(dev, rounds, calls):
   b_gu = hit * 2 * inter * lat * (0.5 + 1 / 32) + rows * lat * 2 + rows * inter * 2
   E = layer.experts
   for lay, sfx in (("checkpoint", ""), ("tiled", "_tiled")):
-    nm = f"cfg5 mxfp4 gate/up+SiTU grouped GEMM ({lay} scales)"
-    ms = time_fn(lambda: ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed"], E["gu_scale" + sfx],
+    nm = f"cfg5 mxfp4 gate/up+SiTU grouped GEMM ({lay} weights)"
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed" + sfx], E["gu_scale" + sfx],
                                               d.group_sizes, fuse_gateup_activation="situ:4.0:25.0",
-                                              zero_group=L, scale_layout=lay), rounds, calls, name=nm)
+                                              zero_group=L, weight_layout=lay), rounds, calls, name=nm)
     report(nm, ms, f_gu, b_gu, rows=rows, experts_hit=hit)
   act = st["act"]
   f_dn = 2.0 * rows * inter * lat
   b_dn = hit * lat * inter * (0.5 + 1 / 32) + rows * inter * 2 + rows * lat * 2
   for lay, sfx in (("checkpoint", ""), ("tiled", "_tiled")):
-    nm = f"cfg5 mxfp4 down grouped GEMM ({lay} scales)"
-    ms = time_fn(lambda: ops.ragged_dot_mxfp4(act, E["down_packed"], E["down_scale" + sfx], d.group_sizes,
-                                              zero_group=L, scale_layout=lay), rounds, calls, name=nm)
+    nm = f"cfg5 mxfp4 down grouped GEMM ({lay} weights)"
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(act, E["down_packed" + sfx], E["down_scale" + sfx], d.group_sizes,
+                                              zero_group=L, weight_layout=lay), rounds, calls, name=nm)
     report(nm, ms, f_dn, b_dn, rows=rows)
   normed = st["normed"]
   ms = time_fn(lambda: layer._dense(normed, layer.up_nk), rounds, calls, name="cfg5 up-proj GEMM 4096x1024x7168")

@@ -206,45 +206,53 @@ def dequantize_mxfp4(weight_packed: torch.Tensor, weight_scale: torch.Tensor,
 _MX_MODES = {"lds_dequant": _lib.MXFP4_LDS_DEQUANT, "scaled_mfma": _lib.MXFP4_SCALED_MFMA}
 
 
-def mxfp4_tile_scales(w_scale: torch.Tensor) -> torch.Tensor:
+def mxfp4_tile_weights(w_packed: torch.Tensor, w_scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
   """One-time weight preparation (the MXFP4 counterpart of
-  ``prefuse_gateup_weights``, rd.py:610-641): E8M0 scales (G, N, K/32) ->
-  (G, K/64, N, 2), the scales of one 64-wide k step of all columns
-  contiguous, as ``ragged_dot_mxfp4(..., scale_layout="tiled")`` reads them."""
-  _dev(w_scale)
-  if w_scale.dtype != torch.uint8 or w_scale.dim() != 3 or w_scale.shape[2] % 2:
-    raise ValueError(f"scale {tuple(w_scale.shape)} {w_scale.dtype}: need (G, N, K/32) uint8, K % 64 == 0")
-  g, n, nb = w_scale.shape
-  w_scale = w_scale.contiguous()
-  out = torch.empty((g, nb // 2, n, 2), dtype=torch.uint8, device=w_scale.device)
-  check(lib().lmoe_mxfp4_tile_scales(_p(w_scale), g, n, nb * 32, _p(out), _stream()), "mxfp4_tile_scales")
-  return out
+  ``prefuse_gateup_weights``, rd.py:610-641): checkpoint-layout packed
+  (G, N, K/2) and E8M0 scales (G, N, K/32) -> k-step-major (G, K/64, N, 32)
+  and (G, K/64, N, 2), as ``ragged_dot_mxfp4(..., weight_layout="tiled")``
+  streams them (one contiguous read per k step and column run)."""
+  _dev(w_packed, w_scale)
+  if w_packed.dtype != torch.uint8 or w_scale.dtype != torch.uint8 or w_packed.dim() != 3:
+    raise ValueError("packed / scale must be uint8 (G, N, K/2) / (G, N, K/32)")
+  g, n, kh = w_packed.shape
+  k = kh * 2
+  if k % 64 or tuple(w_scale.shape) != (g, n, k // 32):
+    raise ValueError(f"packed {tuple(w_packed.shape)} scale {tuple(w_scale.shape)}: need K % 64 == 0")
+  w_packed, w_scale = w_packed.contiguous(), w_scale.contiguous()
+  pk = torch.empty((g, k // 64, n, 32), dtype=torch.uint8, device=w_packed.device)
+  sc = torch.empty((g, k // 64, n, 2), dtype=torch.uint8, device=w_packed.device)
+  check(lib().lmoe_mxfp4_tile(_p(w_packed), _p(w_scale), g, n, k, _p(pk), _p(sc), _stream()), "mxfp4_tile")
+  return pk, sc
 
 
 def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
                      group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
                      mode: str = "lds_dequant", zero_group: int = -1,
-                     scale_layout: str = "checkpoint") -> torch.Tensor:
+                     weight_layout: str = "checkpoint") -> torch.Tensor:
   """Grouped lhs @ deq(W_g)^T with W_g in checkpoint (N, K/2) layout
-  (orientation of mxfp4_online_dequant_matmul_pallas.py:1-36), block-32 E8M0
-  scales (G, N, K/32), or (G, K/64, N, 2) from ``mxfp4_tile_scales`` with
-  ``scale_layout="tiled"`` (same result, faster kernel).  With
-  ``fuse_gateup_activation`` the N axis is [gate | up] and the SiTU-GLU
-  epilogue is applied (output width N/2)."""
+  (orientation of mxfp4_online_dequant_matmul_pallas.py:1-36) and block-32
+  E8M0 scales (G, N, K/32), or with ``weight_layout="tiled"`` the
+  (G, K/64, N, 32) / (G, K/64, N, 2) pair from ``mxfp4_tile_weights`` (same
+  result, faster kernel).  With ``fuse_gateup_activation`` the N axis is
+  [gate | up] and the SiTU-GLU epilogue is applied (output width N/2)."""
   _dev(lhs, w_packed, w_scale, group_sizes)
   if lhs.dtype != torch.bfloat16:
     raise NotImplementedError("MXFP4 GEMM takes bf16 activations")
   m, k = lhs.shape
-  g, n, kh = w_packed.shape
-  if scale_layout == "tiled":
-    want = (g, k // 64, n, 2)
-  elif scale_layout == "checkpoint":
-    want = (g, n, k // 32)
+  if weight_layout == "tiled":
+    if w_packed.dim() != 4 or w_packed.shape[3] != 32:
+      raise ValueError(f"tiled packed weights must be (G, K/64, N, 32), got {tuple(w_packed.shape)}")
+    g, _, n, _ = w_packed.shape
+    want = ((g, k // 64, n, 32), (g, k // 64, n, 2))
+  elif weight_layout == "checkpoint":
+    g, n, _ = w_packed.shape
+    want = ((g, n, k // 2), (g, n, k // 32))
   else:
-    raise ValueError(f"scale_layout {scale_layout!r}")
-  if kh * 2 != k or tuple(w_scale.shape) != want:
+    raise ValueError(f"weight_layout {weight_layout!r}")
+  if (tuple(w_packed.shape), tuple(w_scale.shape)) != want:
     raise ValueError(f"mxfp4 shapes lhs {tuple(lhs.shape)} packed {tuple(w_packed.shape)} "
-                     f"scale {tuple(w_scale.shape)} ({scale_layout} layout wants {want})")
+                     f"scale {tuple(w_scale.shape)} ({weight_layout} layout wants {want})")
   epi, b, bl = _lib.EPI_NONE, 0.0, 0.0
   width = n
   if fuse_gateup_activation is not None:
@@ -253,9 +261,9 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   if mode not in _MX_MODES:
     raise ValueError(f"mode {mode!r}")
   mode_id = _MX_MODES[mode]
-  if scale_layout == "tiled":
+  if weight_layout == "tiled":
     if mode != "lds_dequant":
-      raise NotImplementedError(f"tiled scales with mode {mode!r}")
+      raise NotImplementedError(f"tiled weights with mode {mode!r}")
     mode_id = _lib.MXFP4_LDS_DEQUANT_TILED
   out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
   check(lib().lmoe_ragged_dot_mxfp4(_p(lhs), _p(w_packed), _p(w_scale), _p(group_sizes), m, k, n, g,
