@@ -51,7 +51,7 @@ extern "C" {
 #define LMOE_EPI_SITU 1 /* rhs N axis is [gate | up]; out = SiTU-GLU(gate, up), width N/2 */
 
 #define LMOE_MXFP4_LDS_DEQUANT 0 /* dequantise weight tiles to bf16 in LDS, bf16 MFMA */
-#define LMOE_MXFP4_SCALED_MFMA 1 /* native v_mfma_scale_f32_*_f8f6f4 (activations to MXFP8) */
+#define LMOE_MXFP4_SCALED_MFMA 1 /* native scaled MFMA: use lmoe_quantize_mxfp8 + lmoe_ragged_dot_mxfp8_mxfp4 */
 #define LMOE_MXFP4_LDS_DEQUANT_TILED 2 /* as LDS_DEQUANT, weights re-tiled by lmoe_mxfp4_tile */
 
 #define LMOE_COMBINE_SCATTER_ADD 0 /* sharded: sequential adds rounded to out dtype (ref.py:1113-1141) */
@@ -123,6 +123,31 @@ int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_
  */
 int lmoe_mxfp4_tile(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K,
                     uint8_t* packed_out, uint8_t* scale_out, void* stream);
+
+/* ---- a18 native: MXFP8 activations x MXFP4 weights on the block-scaled MFMA ----------
+ * The reference has no counterpart (its MXFP4 paths dequantise to bf16,
+ * odq.py:65-172); this is the native scaled-MFMA path of the north star, with
+ * OCP MX semantics: E4M3 activations with one E8M0 scale per 32 along K.
+ *
+ * lmoe_quantize_mxfp8: x (M, K) bf16/f32 -> q (M, K) E4M3 codes, and scale_t,
+ * the E8M0 scales in the k-step-major layout (K/128, roundup(M, 4), 4) of
+ * lmoe_mxfp8_scale_bytes(M, K) bytes (pad rows 0).  Shared exponent
+ * floor(log2 max|x|) - 8 per block of 32 (finite values; all-zero block -> 0),
+ * elements round-to-nearest-even, saturating to +-448, NaN -> 0x7F.  K % 128 == 0.
+ *
+ * lmoe_ragged_dot_mxfp8_mxfp4: grouped deq(q) @ deq(W_g)^T with weights from
+ * lmoe_mxfp4_tile ((G, K/64, N, 32) + (G, K/64, N, 2)); out (M, N) in out_dtype,
+ * or (M, N/2) bf16 with LMOE_EPI_SITU (gate/up rounded to bf16 first).  Rows
+ * past sum(group_sizes) are written as zero; zero_group as in lmoe_ragged_dot.
+ * E8M0 byte 255 is NaN here (OCP MX), unlike dequantize_mxfp4's 2^128.
+ */
+int64_t lmoe_mxfp8_scale_bytes(int64_t M, int64_t K);
+int lmoe_quantize_mxfp8(const void* x, int x_dtype, int64_t M, int64_t K, uint8_t* q, uint8_t* scale_t,
+                        void* stream);
+int lmoe_ragged_dot_mxfp8_mxfp4(const uint8_t* lhs_q, const uint8_t* lhs_scale_t, const uint8_t* w_packed_t,
+                                const uint8_t* w_scale_t, const int32_t* group_sizes, int64_t M, int64_t K,
+                                int64_t N, int64_t G, int zero_group, int epilogue, float beta, float beta_lin,
+                                void* out, int out_dtype, void* stream);
 
 /* ---- a3: router top-k --------------------------------------------------------------
  * Replaces the gate math of _router_gate (ref.py:601-631) / latent_moe_forward

@@ -612,6 +612,102 @@ def ragged_dot_mxfp4(lhs, w_packed, w_scale, group_sizes, dtype: str = "bf16",
   return situ_and_mul(g_, u_, situ[0], situ[1], dtype)
 
 
+# ---------------------------------------------------------------------------
+# MXFP8 activations x MXFP4 weights: the native scaled-MFMA path
+# ---------------------------------------------------------------------------
+# The reference has no such path (its MXFP4 paths dequantise to bf16); this is
+# the build's own definition, following the OCP Microscaling (MX) v1.0
+# specification: E4M3 ("fn": no infinities, 0x7F/0xFF NaN, max 448) elements
+# with one E8M0 scale per 32 consecutive elements along K; conversion picks the
+# shared exponent floor(log2(amax)) - emax_elem (emax_elem = 8 for E4M3), then
+# rounds each scaled element to nearest-even and saturates to +-448.
+
+E4M3_MAX = 448.0
+
+
+def fp8_e4m3_to_f32(code) -> np.ndarray:
+  """OCP E4M3 (fn) byte -> float32: sign bit 7, exponent bits 6..3 (bias 7),
+  mantissa bits 2..0; exponent 0 is subnormal (m/8 * 2^-6); 0x7F / 0xFF NaN."""
+  c = np.asarray(code).astype(np.int64)
+  e = (c >> 3) & 15
+  m = c & 7
+  mag = np.where(e == 0, m / 8.0 * 2.0 ** -6, (1.0 + m / 8.0) * np.ldexp(1.0, e - 7))
+  mag = np.where((c & 0x7F) == 0x7F, np.nan, mag)
+  return (np.where((c & 0x80) != 0, -mag, mag)).astype(F32)
+
+
+def f32_to_fp8_e4m3(x) -> np.ndarray:
+  """float -> OCP E4M3 byte, round to nearest even, saturating to +-448
+  (infinities saturate too); NaN -> 0x7F."""
+  x = np.asarray(x, np.float64)
+  sign = np.where(np.signbit(x), 0x80, 0).astype(np.int64)
+  a = np.minimum(np.abs(np.nan_to_num(x, nan=0.0, posinf=E4M3_MAX, neginf=-E4M3_MAX)), E4M3_MAX)
+  with np.errstate(divide="ignore"):
+    e = np.floor(np.log2(np.where(a > 0, a, 1.0)))
+  e = np.maximum(e, -6.0)  # below 2^-6: subnormal grid of 2^-9
+  quantum = np.ldexp(1.0, (e - 3).astype(np.int64))
+  q = np.rint(a / quantum) * quantum  # numpy rint: ties to even
+  q = np.minimum(q, E4M3_MAX)
+  with np.errstate(divide="ignore"):
+    qe = np.floor(np.log2(np.where(q > 0, q, 1.0))).astype(np.int64)
+  normal = q >= 2.0 ** -6
+  code_n = ((qe + 7) << 3) | np.rint((q / np.ldexp(1.0, qe) - 1.0) * 8.0).astype(np.int64)
+  code_s = np.rint(q / 2.0 ** -9).astype(np.int64)
+  code = np.where(normal, code_n, code_s) | sign
+  code = np.where(np.isnan(x), 0x7F, code)
+  return code.astype(np.uint8)
+
+
+def quantize_mxfp8(x) -> tuple[np.ndarray, np.ndarray]:
+  """(M, K) float -> (codes (M, K) u8 E4M3, scales (M, K/32) u8 E8M0), blocks of
+  32 along K.  Shared exponent floor(log2(max|x|)) - 8 over the block's finite
+  values, clamped to [-127, 127] (an all-zero block gets byte 0); elements are
+  x * 2^-exp converted by ``f32_to_fp8_e4m3``."""
+  x = np.asarray(x, np.float64)
+  m, k = x.shape
+  blocks = x.reshape(m, k // 32, 32)
+  fin = np.where(np.isfinite(blocks), np.abs(blocks), 0.0)
+  amax = fin.max(axis=-1)
+  with np.errstate(divide="ignore"):
+    ex = np.where(amax > 0, np.floor(np.log2(np.where(amax > 0, amax, 1.0))) - 8, -127)
+  ex = np.clip(ex, -127, 127).astype(np.int64)
+  scaled = blocks * np.ldexp(1.0, -ex)[..., None]
+  codes = f32_to_fp8_e4m3(scaled).reshape(m, k)
+  return codes, (ex + 127).astype(np.uint8)
+
+
+def dequantize_mxfp8(codes, scales) -> np.ndarray:
+  """E4M3 codes (M, K) x E8M0 scales (M, K/32) -> float64 values (exact)."""
+  v = fp8_e4m3_to_f32(codes).astype(np.float64)
+  s = np.ldexp(1.0, np.asarray(scales).astype(np.int64) - 127)
+  return v * np.repeat(s, 32, axis=-1)
+
+
+def ragged_dot_mxfp8_mxfp4(lhs_codes, lhs_scales, w_packed, w_scale, group_sizes, dtype: str = "f32",
+                           situ: tuple[float, float] | None = None) -> np.ndarray:
+  """Grouped deq(A) @ deq(W_g)^T with MXFP8 activations and MXFP4 weights in
+  checkpoint (N, K/2) layout.  Every product is exact; the sums are taken in
+  float64 and rounded once to ``dtype`` (``situ``: gate/up rounded to bf16,
+  SiTU-GLU, output bf16, as in the bf16 fused epilogue).  Rows past
+  sum(group_sizes) are zero."""
+  a = dequantize_mxfp8(lhs_codes, lhs_scales)
+  gs = np.asarray(group_sizes).astype(np.int64)
+  n_out = np.asarray(w_packed).shape[1]
+  acc = np.zeros((a.shape[0], n_out), np.float64)
+  start = 0
+  for g, n in enumerate(gs):
+    n = int(n)
+    if n:
+      wd = dequantize_mxfp4(w_packed[g], w_scale[g]).astype(np.float64)
+      acc[start:start + n] = a[start:start + n] @ wd.T
+    start += n
+  if situ is None:
+    return cast(acc.astype(F32), dtype)
+  inter = n_out // 2
+  g_, u_ = bf16_round(acc[:, :inter].astype(F32)), bf16_round(acc[:, inter:].astype(F32))
+  return situ_and_mul(g_, u_, situ[0], situ[1], "bf16")
+
+
 PINNING = {
     "bf16_round": "closed form: exhaustive bf16 neighbours, torch.bfloat16 cast (tests/test_oracle_basics.py)",
     "router_from_logits / router_gate": "golden bundles router_* / topk_* (6 stages), softmax closed form",
@@ -621,4 +717,7 @@ PINNING = {
     "combine_shard_contribution": "golden routed_output_after_combine via sharded==unsharded, literal padding KAT",
     "rms_norm / forward": "golden normalized/up_projection/shared/final stages",
     "dequantize_mxfp4": "closed form OCP MX E2M1/E8M0 table, exhaustive 256 bytes x edge scales",
+    "fp8_e4m3_to_f32 / f32_to_fp8_e4m3": "all 256 codes and a dense sweep incl. ties and subnormals vs torch.float8_e4m3fn",
+    "quantize_mxfp8": "OCP MX closed form (exponent choice, saturation, zero block), grid values round-trip exactly",
+    "ragged_dot_mxfp8_mxfp4": "brute-force triple loop on small inputs; equals the bf16 oracle when the activations are on the E4M3 grid",
 }

@@ -5,7 +5,6 @@ namespace lmoe {
 namespace gemm {
 int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* name);
 int run_f32(const Params& p, int layout, hipStream_t st, const char* name);
-int run_mxfp4_scaled(const Params& p, int epi, hipStream_t st, const char* name);
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name);
 int tile_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K, uint8_t* packed_out,
                uint8_t* scale_out, hipStream_t st);
@@ -122,7 +121,10 @@ extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, c
     // w_packed (G, K/64, N, 32) and w_scale (G, K/64, N, 2) from lmoe_mxfp4_tile
     return M == 0 ? LMOE_OK : run_dma(p, kMXFP4, epi, st, name);
   }
-  if (mode == LMOE_MXFP4_SCALED_MFMA) return run_mxfp4_scaled(p, epi, st, name);
+  if (mode == LMOE_MXFP4_SCALED_MFMA)
+    return fail(LMOE_ERR_UNSUPPORTED,
+                "%s: the scaled-MFMA path takes MXFP8 activations: lmoe_quantize_mxfp8 + lmoe_ragged_dot_mxfp8_mxfp4",
+                name);
   return fail(LMOE_ERR_INVALID, "%s: bad mode %d", name, mode);
 }
 

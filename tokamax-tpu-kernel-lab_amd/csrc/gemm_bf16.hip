@@ -26,7 +26,6 @@ namespace lmoe {
 namespace gemm {
 namespace {
 
-constexpr int kXcds = 8;
 
 // Calls f(integral_constant<int, 0>) ... f(integral_constant<int, N-1>) in
 // order while f returns true, so register-ring indices are compile-time.

@@ -35,78 +35,16 @@
 #include <type_traits>
 #include <utility>
 
+#include "dma_util.h"
 #include "gemm_tile.h"
 
 namespace lmoe {
 namespace gemm {
 namespace {
 
-constexpr int kXcds = 8;
+using namespace lmoe::dma;
+
 constexpr int kSK = 64;  // K per pipeline step
-
-template <class F, int... I>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
-  (void)(f(std::integral_constant<int, I>{}) && ...);
-}
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  static_for_impl(f, std::make_integer_sequence<int, N>{});
-}
-
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return static_cast<uint32_t>(
-      reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
-}
-
-// Wave-uniform copy of a pointer (lives in an SGPR pair).
-__device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
-  const uint64_t v = reinterpret_cast<uint64_t>(p);
-  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
-  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
-  return reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
-}
-
-// One 16-byte DMA per active lane: LDS[lds + 16 * lane] = *(sbase + off).
-// `sbase` and `lds` are wave-uniform (SGPRs); M0 is written immediately
-// before use (one wait state).
-__device__ __forceinline__ void dma16s(uint32_t off, const uint8_t* sbase, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :
-               : "v"(off), "s"(uniform_ptr(sbase)), "s"(__builtin_amdgcn_readfirstlane(lds))
-               : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" : : "n"(N) : "memory");
-}
-
-// Wait until at most N of this wave's vector memory operations are in flight
-// and all its LDS reads have returned.  The LDS-read wait keeps a slot's last
-// fragment reads ahead of the DMA that the next step issues into it.
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0) lgkmcnt(0)" : : "n"(N) : "memory");
-}
-
-__device__ __forceinline__ void barrier() { asm volatile("s_barrier" : : : "memory"); }
-
-// Wait for the DMA of step kt when `ahead` (0 .. NS-2) later steps, of OPS
-// operations each for this wave, have been issued after it.
-template <int NS, int OPS>
-__device__ __forceinline__ void wait_step(int ahead) {
-  if (ahead >= NS - 2) {
-    wait_vm_lgkm<(NS - 2) * OPS>();
-  } else {
-    static_for<NS - 2>([&](auto a) __attribute__((always_inline)) {
-      constexpr int A = decltype(a)::value;
-      if (ahead == A) wait_vm_lgkm<A * OPS>();
-      return true;
-    });
-  }
-}
 
 enum DmaLayout { kDGNK = 0, kDMX = 1 };
 
@@ -191,32 +129,8 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
   const int wm = wave / C::kWN, wn = wave % C::kWN;
   __syncthreads();  // the previous tile's LDS slots and s_tile are no longer read
   if (wave == 0) {
-    const int64_t b = vb;
-    const int64_t xcd = b % kXcds, slot = b / kXcds;
-    TileInfo ti{-1, 0, 0, false};
     int64_t nt = 0;
-    if (gm == 0) {
-      // n-tiles striped over the XCDs: each weight column slice is read by
-      // one XCD only, and the m-tiles of a group (which share it) follow each
-      // other there, so its second and later reads hit that XCD's L2
-      const int64_t per = n_tiles / kXcds;
-      const int64_t mt = slot / per;
-      nt = xcd + kXcds * (slot % per);
-      if (mt < tm) ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, mt);
-    } else {
-      // groups of gm m-tiles round-robin over the XCDs, all n-tiles of a group
-      // on one XCD (the A rows are read by one XCD only)
-      const int64_t span = static_cast<int64_t>(gm) * n_tiles;
-      const int64_t m_base = ((slot / span) * kXcds + xcd) * gm;
-      const int64_t r = slot % span;
-      if (m_base < tm) {
-        const int64_t gm_eff = tm - m_base < gm ? tm - m_base : gm;
-        if (r < gm_eff * n_tiles) {
-          nt = r / gm_eff;
-          ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, m_base + r % gm_eff);
-        }
-      }
-    }
+    const TileInfo ti = schedule_tile<BM>(p, n_tiles, gm, vb, tm, nt);
     if (lane == 0) {
       s_tile = ti;
       s_nt = nt;

@@ -35,7 +35,7 @@ enum BLayout { kGKN = 0, kGNK = 1, kMXFP4 = 2 };
 enum Epilogue { kEpiNone = 0, kEpiSitu = 1 };
 
 struct Params {
-  const uint16_t* lhs;     // (M, K) bf16
+  const uint16_t* lhs;     // (M, K) bf16 (MXFP8 path: E4M3 codes, read as bytes)
   const void* rhs;         // layout-dependent
   const uint8_t* scale;    // MXFP4 scales (G, N, K/32)
   const int32_t* group_sizes;
@@ -45,6 +45,7 @@ struct Params {
   int out_dtype;
   float beta, beta_lin;
   int round_before_act;
+  const uint8_t* lhs_scale = nullptr;  // MXFP8 path: E8M0 (K/128, roundup(M, 4), 4)
 };
 
 struct TileInfo {
@@ -140,6 +141,39 @@ __device__ TileInfo locate_tile(const int32_t* __restrict__ gs, int64_t G, int64
     }
   }
   return info;
+}
+
+constexpr int kXcds = 8;  // MI355X: 8 XCDs; consecutive blocks go to consecutive XCDs
+
+// Virtual tile vb -> (m-tile, n-tile) with an XCD-aware order; executed by
+// wave 0 (tm = total_m_tiles).  gm == 0: n-tiles striped over the XCDs (each
+// weight column slice is read by one XCD only, and the m-tiles of a group,
+// which share it, follow each other there so its later reads hit that XCD's
+// L2); gm > 0: groups of gm m-tiles round-robin over the XCDs with all n-tiles
+// of a group on one XCD (the A rows are read by one XCD only).
+template <int BM>
+__device__ TileInfo schedule_tile(const Params& p, int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt) {
+  const int64_t xcd = vb % kXcds, slot = vb / kXcds;
+  TileInfo ti{-1, 0, 0, false};
+  nt = 0;
+  if (gm == 0) {
+    const int64_t per = n_tiles / kXcds;
+    const int64_t mt = slot / per;
+    nt = xcd + kXcds * (slot % per);
+    if (mt < tm) ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, mt);
+  } else {
+    const int64_t span = static_cast<int64_t>(gm) * n_tiles;
+    const int64_t m_base = ((slot / span) * kXcds + xcd) * gm;
+    const int64_t r = slot % span;
+    if (m_base < tm) {
+      const int64_t gm_eff = tm - m_base < gm ? tm - m_base : gm;
+      if (r < gm_eff * n_tiles) {
+        nt = r / gm_eff;
+        ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, m_base + r % gm_eff);
+      }
+    }
+  }
+  return ti;
 }
 
 __device__ __forceinline__ float situ(float g, float u, float beta, float beta_lin) {

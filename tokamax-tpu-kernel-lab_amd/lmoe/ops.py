@@ -226,6 +226,54 @@ def mxfp4_tile_weights(w_packed: torch.Tensor, w_scale: torch.Tensor) -> tuple[t
   return pk, sc
 
 
+def quantize_mxfp8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+  """OCP MX E4M3 quantisation of activations (no reference counterpart; the
+  native scaled-MFMA path): x (M, K) bf16/f32 -> codes (M, K) uint8 and E8M0
+  scales (K/128, roundup(M, 4), 4) uint8 (the k-step-major layout the scaled
+  GEMM streams).  One shared exponent floor(log2 max|x|) - 8 per 32 along K."""
+  _dev(x)
+  if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float32):
+    raise ValueError(f"x must be (M, K) bf16/f32, got {tuple(x.shape)} {x.dtype}")
+  m, k = x.shape
+  if k % 128:
+    raise NotImplementedError(f"MXFP8 quantisation needs K % 128 == 0 (K={k})")
+  x = x.contiguous()
+  m4 = (m + 3) // 4 * 4
+  q = torch.empty((m, k), dtype=torch.uint8, device=x.device)
+  sc = torch.empty((k // 128, m4, 4), dtype=torch.uint8, device=x.device)
+  check(lib().lmoe_quantize_mxfp8(_p(x), _dt(x), m, k, _p(q), _p(sc), _stream()), "quantize_mxfp8")
+  return q, sc
+
+
+def ragged_dot_mxfp8_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packed: torch.Tensor,
+                           w_scale: torch.Tensor, group_sizes: torch.Tensor, *,
+                           fuse_gateup_activation: str | None = None, zero_group: int = -1,
+                           out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+  """Grouped deq(A) @ deq(W_g)^T on the block-scaled MFMA: A from
+  ``quantize_mxfp8``, W from ``mxfp4_tile_weights``.  With
+  ``fuse_gateup_activation`` the N axis is [gate | up] and the SiTU-GLU epilogue
+  is applied (bf16 output of width N/2)."""
+  _dev(lhs_q, lhs_scale, w_packed, w_scale, group_sizes)
+  m, k = lhs_q.shape
+  if w_packed.dim() != 4 or w_packed.shape[3] != 32:
+    raise ValueError(f"weights must be tiled (G, K/64, N, 32), got {tuple(w_packed.shape)}")
+  g, _, n, _ = w_packed.shape
+  m4 = (m + 3) // 4 * 4
+  if (lhs_q.dtype != torch.uint8 or tuple(lhs_scale.shape) != (k // 128, m4, 4)
+      or tuple(w_packed.shape) != (g, k // 64, n, 32) or tuple(w_scale.shape) != (g, k // 64, n, 2)):
+    raise ValueError(f"shapes: lhs {tuple(lhs_q.shape)} scale {tuple(lhs_scale.shape)} "
+                     f"w {tuple(w_packed.shape)} w_scale {tuple(w_scale.shape)}")
+  epi, b, bl, width = _lib.EPI_NONE, 0.0, 0.0, n
+  if fuse_gateup_activation is not None:
+    b, bl = parse_fused_activation(fuse_gateup_activation)
+    epi, width, out_dtype = _lib.EPI_SITU, n // 2, torch.bfloat16
+  out = torch.empty((m, width), dtype=out_dtype, device=lhs_q.device)
+  check(lib().lmoe_ragged_dot_mxfp8_mxfp4(_p(lhs_q), _p(lhs_scale), _p(w_packed), _p(w_scale), _p(group_sizes),
+                                          m, k, n, g, zero_group, epi, b, bl, _p(out), _dt(out), _stream()),
+        "ragged_dot_mxfp8_mxfp4")
+  return out
+
+
 def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
                      group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
                      mode: str = "lds_dequant", zero_group: int = -1,
@@ -261,9 +309,13 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   if mode not in _MX_MODES:
     raise ValueError(f"mode {mode!r}")
   mode_id = _MX_MODES[mode]
+  if mode == "scaled_mfma":
+    if weight_layout != "tiled":
+      raise NotImplementedError("the scaled-MFMA path streams weights from mxfp4_tile_weights (weight_layout='tiled')")
+    q, qs = quantize_mxfp8(lhs)
+    return ragged_dot_mxfp8_mxfp4(q, qs, w_packed, w_scale, group_sizes,
+                                  fuse_gateup_activation=fuse_gateup_activation, zero_group=zero_group)
   if weight_layout == "tiled":
-    if mode != "lds_dequant":
-      raise NotImplementedError(f"tiled weights with mode {mode!r}")
     mode_id = _lib.MXFP4_LDS_DEQUANT_TILED
   out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
   check(lib().lmoe_ragged_dot_mxfp4(_p(lhs), _p(w_packed), _p(w_scale), _p(group_sizes), m, k, n, g,
