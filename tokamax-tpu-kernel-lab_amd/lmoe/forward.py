@@ -162,9 +162,10 @@ class LocalShardLatentMoE:
     self.experts = dict(experts)
     self.shared = shared
     # MXFP4 weights re-tiled once (k-step-major) so each k step's weight tile
-    # streams into LDS as one contiguous read
+    # streams into LDS as one contiguous read; the scaled-MFMA mode reads only
+    # this layout
     self.weight_layout, self._sfx = "checkpoint", ""
-    if expert_format == "mxfp4" and mxfp4_mode == "lds_dequant":
+    if expert_format == "mxfp4" and mxfp4_mode in ("lds_dequant", "scaled_mfma"):
       for w in ("gu", "down"):
         pk, sc = ops.mxfp4_tile_weights(experts[f"{w}_packed"], experts[f"{w}_scale"])
         self.experts[f"{w}_packed_tiled"], self.experts[f"{w}_scale_tiled"] = pk, sc

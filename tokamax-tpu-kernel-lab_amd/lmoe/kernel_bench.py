@@ -134,6 +134,13 @@ def bench_cfg4(dev, rounds, calls):
     ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled"), rounds, calls,
                  name=f"cfg4 mxfp4 matmul tiled weights M={m}")
     report(f"cfg4 mxfp4 matmul tiled weights M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
+    ms = time_fn(lambda: ops.quantize_mxfp8(a), rounds, calls, name=f"cfg4 mxfp8 quantise M={m}")
+    report(f"cfg4 mxfp8 quantise M={m}", ms, 0, m * k_ * (2 + 1 + 1 / 32), m=m)
+    q, qs = ops.quantize_mxfp8(a)
+    ms = time_fn(lambda: ops.ragged_dot_mxfp8_mxfp4(q, qs, tpk, tsc, g), rounds, calls,
+                 name=f"cfg4 mxfp8 x mxfp4 scaled MFMA M={m}")
+    report(f"cfg4 mxfp8 x mxfp4 scaled MFMA M={m}", ms, flops, nbytes - m * k_ * (1 - 1 / 32),
+           peak_key="fp8", m=m)
 
 
 def bench_cfg5(dev, rounds, calls):
@@ -166,6 +173,14 @@ def bench_cfg5(dev, rounds, calls):
                                               d.group_sizes, fuse_gateup_activation="situ:4.0:25.0",
                                               zero_group=L, weight_layout=lay), rounds, calls, name=nm)
     report(nm, ms, f_gu, b_gu, rows=rows, experts_hit=hit)
+  ms = time_fn(lambda: ops.quantize_mxfp8(d.sorted_tokens), rounds, calls, name="cfg5 mxfp8 quantise sorted tokens")
+  report("cfg5 mxfp8 quantise sorted tokens", ms, 0, d.sorted_tokens.numel() * (3 + 1 / 32))
+  q, qs = ops.quantize_mxfp8(d.sorted_tokens)
+  nm = "cfg5 mxfp8 x mxfp4 gate/up+SiTU scaled MFMA"
+  ms = time_fn(lambda: ops.ragged_dot_mxfp8_mxfp4(q, qs, E["gu_packed_tiled"], E["gu_scale_tiled"], d.group_sizes,
+                                                  fuse_gateup_activation="situ:4.0:25.0", zero_group=L),
+               rounds, calls, name=nm)
+  report(nm, ms, f_gu, b_gu - rows * lat * (1 - 1 / 32), peak_key="fp8", rows=rows, experts_hit=hit)
   act = st["act"]
   f_dn = 2.0 * rows * inter * lat
   b_dn = hit * lat * inter * (0.5 + 1 / 32) + rows * inter * 2 + rows * lat * 2
@@ -174,6 +189,11 @@ def bench_cfg5(dev, rounds, calls):
     ms = time_fn(lambda: ops.ragged_dot_mxfp4(act, E["down_packed" + sfx], E["down_scale" + sfx], d.group_sizes,
                                               zero_group=L, weight_layout=lay), rounds, calls, name=nm)
     report(nm, ms, f_dn, b_dn, rows=rows)
+  q, qs = ops.quantize_mxfp8(act)
+  nm = "cfg5 mxfp8 x mxfp4 down scaled MFMA"
+  ms = time_fn(lambda: ops.ragged_dot_mxfp8_mxfp4(q, qs, E["down_packed_tiled"], E["down_scale_tiled"], d.group_sizes,
+                                                  zero_group=L), rounds, calls, name=nm)
+  report(nm, ms, f_dn, b_dn - rows * inter * (1 - 1 / 32), peak_key="fp8", rows=rows)
   normed = st["normed"]
   ms = time_fn(lambda: layer._dense(normed, layer.up_nk), rounds, calls, name="cfg5 up-proj GEMM 4096x1024x7168")
   report("cfg5 up-proj GEMM 4096x1024x7168", ms, 2.0 * T * lat * H, T * lat * 2 + lat * H * 2 + T * H * 2)
