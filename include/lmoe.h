@@ -118,8 +118,10 @@ int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_
  * One-time weight preparation, the MXFP4 counterpart of prefuse_gateup_weights
  * (rd.py:610-641): k-step-major re-tiling of checkpoint-layout weights,
  * packed (G, N, K/2) -> packed_out (G, K/64, N, 32) and E8M0 scales
- * (G, N, K/32) -> scale_out (G, K/64, N, 2).  K % 64 == 0; outputs must not
- * alias inputs; packed buffers 16-byte aligned.
+ * (G, N, K/32) -> scale_out (G, K/64, N, 2).  Each 32-byte record (one column,
+ * 64 k values) holds the checkpoint's eight 4-byte groups in the order
+ * 0, 2, 4, 6, 1, 3, 5, 7 (one 16-byte LDS read per MFMA lane and k step).
+ * K % 64 == 0; outputs must not alias inputs; packed buffers 16-byte aligned.
  */
 int lmoe_mxfp4_tile(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K,
                     uint8_t* packed_out, uint8_t* scale_out, void* stream);

@@ -195,7 +195,8 @@ def test_mxfp4_gemm_equals_dequant_then_bf16_gemm(gpu_device):
 
 
 def test_mxfp4_tile_weights_layout(gpu_device):
-  """k-step-major re-tiling: packed[g, s, n, b] = checkpoint[g, n, 32 s + b],
+  """k-step-major re-tiling: record packed[g, s, n] = the 8 dwords of
+  checkpoint[g, n, 32 s : 32 s + 32] in the order 0, 2, 4, 6, 1, 3, 5, 7;
   scale[g, s, n, h] = checkpoint[g, n, 2 s + h]."""
   from lmoe import ops
   rng = np.random.default_rng(7)
@@ -205,7 +206,8 @@ def test_mxfp4_tile_weights_layout(gpu_device):
   pk, sc = (to_np(t) for t in ops.mxfp4_tile_weights(to_dev(packed), to_dev(scale)))
   assert pk.shape == (g, k // 64, n, 32) and sc.shape == (g, k // 64, n, 2)
   for s_ in range(k // 64):
-    assert np.array_equal(pk[:, s_], packed[:, :, 32 * s_:32 * s_ + 32])
+    natural = packed[:, :, 32 * s_:32 * s_ + 32].reshape(g, n, 8, 4)
+    assert np.array_equal(pk[:, s_], natural[:, :, [0, 2, 4, 6, 1, 3, 5, 7]].reshape(g, n, 32))
     for h in range(2):
       assert np.array_equal(sc[:, s_, :, h], scale[:, :, 2 * s_ + h])
 

@@ -7,23 +7,24 @@
 // occupancy; here an NS-deep LDS ring holds the in-flight steps and VGPRs only
 // hold accumulators and MFMA fragments.
 //
-// Pipeline (one s_barrier per K step):
-//   prologue: issue DMA for steps 0 .. NS-2
-//   step kt:  s_waitcnt vmcnt(<DMA ops of the NS-2 younger steps>)
-//             s_barrier            -- step kt landed for all waves, and every
-//                                     wave finished step kt-1's math
-//             issue DMA for step kt+NS-1 into the slot of step kt-1
-//             MFMAs on slot kt % NS
+// Pipeline (one s_barrier per K step, NS-slot LDS ring):
+//   prologue: issue DMA for steps 0 .. NS-1; wait for step 0, barrier, read
+//             step 0's operand fragments into registers
+//   step k:   s_waitcnt vmcnt(<DMA ops of the younger steps>) lgkmcnt(0)
+//             s_barrier            -- step k+1 landed for all waves, and every
+//                                     wave holds step k's fragments
+//             issue DMA for step k+NS into slot k % NS
+//             read step k+1's fragments (LDS -> registers)
+//             conversions + MFMAs of step k from registers
 // The DMA is issued from inline asm, so the compiler neither sees the LDS
 // writes nor inserts its conservative vmcnt(0) before LDS reads; all vector
 // memory operations inside the K loop are these DMAs, so the wait counts are
-// exact.  Steps past the end re-load a valid address (data unused) so every
-// step issues the same number of operations.
+// exact.  No DMA is issued past the last step.
 //
 // LDS rows are 128 bytes (64 bf16) with 16-byte chunks XOR-swizzled by
-// (row & 7), which makes the MFMA fragment reads (16 rows x 16 bytes at one
-// logical chunk) bank-conflict free.  MXFP4 weights stay packed in LDS (32
-// bytes per row and step, chunks swizzled by bit 3 of the row) and each MFMA
+// swz8(row), which makes the MFMA fragment reads (16 rows x 16 bytes at one
+// logical chunk per 16-lane group) bank-conflict free.  MXFP4 weights stay
+// packed in LDS (the 32-byte tiled records, copied as they are) and each MFMA
 // B fragment is expanded in registers with v_cvt_scalef32_pk_bf16_fp4.
 //
 // Layouts: A (M, K) bf16 row-major; B either bf16 (G, N, K) ("GNK") or MXFP4
@@ -50,13 +51,19 @@ enum DmaLayout { kDGNK = 0, kDMX = 1 };
 
 // WM x WN waves; wave (wm, wn) owns rows [wm*BM/WM, ...) and columns
 // [wn*BN/WN, ...) of the tile.  With WM == 1 every weight fragment is expanded
-// by exactly one wave.
-template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4>
+// by exactly one wave.  MF is the MFMA tile edge: 32 (v_mfma_f32_32x32x16_bf16,
+// the one a single wave issues at the full matrix rate) or 16
+// (v_mfma_f32_16x16x32_bf16, which one wave issues at half rate).
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32, bool PIPE = false>
 struct DCfg {
-  static constexpr int kWM = WM, kWN = WN;
+  static constexpr int kWM = WM, kWN = WN, kMF = MF;
+  static constexpr bool kPipe = PIPE;  // operand fragments read one step ahead
   static constexpr int kWaves = WM * WN, kThreads = 64 * WM * WN;
   static constexpr int kWTM = BM / kWM, kWTN = BN / kWN;
-  static constexpr int kTM = kWTM / 16, kTN = kWTN / 16;
+  static constexpr int kTM = kWTM / MF, kTN = kWTN / MF;
+  static constexpr int kKS = kSK / (MF == 32 ? 16 : 32);  // MFMA k sub-steps per pipeline step
+  static constexpr int kAccN = MF == 32 ? 16 : 4;         // accumulator floats per lane per sub-tile
+  using Acc = std::conditional_t<MF == 32, floatx16, floatx4>;
   static constexpr int kABytes = BM * 128;                       // A slot
   static constexpr int kBBytes = LAYOUT == kDGNK ? BN * 128 : BN * 32;  // B slot
   static constexpr int kSBytes = LAYOUT == kDMX ? BN * 2 : 0;    // scale slot
@@ -73,23 +80,29 @@ struct DCfg {
   static_assert(kAOps >= 1 && BM * 8 % kThreads == 0, "A DMA split");
   static_assert(kBOps >= 1 && (LAYOUT == kDGNK ? BN * 8 : BN * 2) % kThreads == 0, "B DMA split");
   static_assert(LAYOUT != kDMX || (BN % 8 == 0 && kSLanes <= 64), "scale DMA split");
-  static_assert(kTM >= 1 && kTN >= 1 && kWTM % 16 == 0 && kWTN % 16 == 0, "wave tile");
-  static_assert((NS - 2) * kOps0 < 64, "vmcnt range");
+  static_assert(MF == 16 || MF == 32, "MFMA shape");
+  static_assert(kTM >= 1 && kTN >= 1 && kWTM % MF == 0 && kWTN % MF == 0, "wave tile");
+  static_assert((NS - 1) * kOps0 < 64, "vmcnt range");
   static_assert(EPI != kEpiSitu || kTN % 2 == 0, "SiTU pairs gate/up sub-tiles");
   // blocks per CU the LDS ring allows (160 KB per CU); the register budget is
   // capped so that the same number of waves fits on each SIMD
   static constexpr int kLdsBlocks = 163840 / (NS * kSlot + 64);
   static constexpr int kWavesPerEuRaw = kLdsBlocks * kWaves / 4;
-  static constexpr int kWavesPerEu = kWavesPerEuRaw < 1 ? 1 : (kWavesPerEuRaw > 8 ? 8 : kWavesPerEuRaw);
+  // at most 2 waves per SIMD: the two fragment sets of the software pipeline
+  // plus the accumulators need up to 256 VGPRs
+  static constexpr int kWavesPerEu = kWavesPerEuRaw < 1 ? 1 : (kWavesPerEuRaw > 2 ? 2 : kWavesPerEuRaw);
 };
 
-template <int BN, int TN, int EPI>
+// First LDS column of column sub-tile j of wave wn.  With the SiTU epilogue
+// the first half of a wave's sub-tiles are gate columns and the second half
+// the matching up columns (LDS columns BN/2 ...), so a lane holds both.
+template <int BN, int TN, int EPI, int MF>
 __device__ __forceinline__ int dlds_col(int wn, int j) {
   if constexpr (EPI == kEpiSitu) {
     constexpr int half = TN / 2;
-    return j < half ? wn * half * 16 + j * 16 : BN / 2 + wn * half * 16 + (j - half) * 16;
+    return j < half ? wn * half * MF + j * MF : BN / 2 + wn * half * MF + (j - half) * MF;
   } else {
-    return wn * TN * 16 + j * 16;
+    return wn * TN * MF + j * MF;
   }
 }
 
@@ -107,11 +120,11 @@ __device__ __forceinline__ int64_t drhs_col(int64_t nt, int c, int64_t N) {
   }
 }
 
-template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM, int WN>
-__global__ __launch_bounds__((DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>::kThreads))
-__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>::kWavesPerEu)))
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM, int WN, int MF, bool PIPE>
+__global__ __launch_bounds__((DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>::kThreads))
+__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>::kWavesPerEu)))
 void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtual) {
-  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>;
+  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ TileInfo s_tile;
   __shared__ int64_t s_nt;
@@ -143,11 +156,13 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
   const int64_t K = p.K, N = p.N;
   const int64_t g = tile.group;
 
-  floatx4 acc[C::kTM][C::kTN];
+  typename C::Acc acc[C::kTM][C::kTN];
 #pragma unroll
   for (int i = 0; i < C::kTM; ++i)
 #pragma unroll
-    for (int j = 0; j < C::kTN; ++j) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < C::kTN; ++j)
+#pragma unroll
+      for (int e = 0; e < C::kAccN; ++e) acc[i][j][e] = 0.f;
 
   if (!tile.zero) {
     const uint32_t smem0 = lds_offset(smem);
@@ -156,13 +171,13 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
     // DMA addressing: a wave-uniform (SGPR) base per operand that advances by
     // one k step per step, plus a loop-invariant 32-bit per-lane offset.
     // A: LDS chunk position q = tid + kThreads * v of the slot <- row q/8,
-    // logical chunk (q%8) ^ (row&7).  Rows past the tile read row 0 of the tile.
+    // logical chunk (q%8) ^ swz8(row).  Rows past the tile read row 0 of the tile.
     const uint8_t* a_base = uniform_ptr(p.lhs + tile.row0 * K);
     uint32_t a_off[C::kAOps];
 #pragma unroll
     for (int v = 0; v < C::kAOps; ++v) {
       const int q = tid + C::kThreads * v;
-      const int row = q / 8, kc = (q % 8) ^ (row & 7);
+      const int row = q / 8, kc = (q % 8) ^ swz8(row);
       const int rr = row < tile.rows ? row : 0;
       a_off[v] = static_cast<uint32_t>(rr * K * 2 + kc * 16);
     }
@@ -175,10 +190,10 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
     for (int u = 0; u < C::kBOps; ++u) {
       const int q = tid + C::kThreads * u;
       if constexpr (LAYOUT == kDGNK) {
-        const int c = q / 8, kc = (q % 8) ^ (c & 7);
+        const int c = q / 8, kc = (q % 8) ^ swz8(c);
         b_off[u] = static_cast<uint32_t>(drhs_col<BN, EPI>(nt, c, N) * b_row + kc * 16);
       } else {
-        const int c = q / 2, ch = (q % 2) ^ ((c >> 3) & 1);
+        const int c = q / 2, ch = q % 2;
         b_off[u] = static_cast<uint32_t>(drhs_col<BN, EPI>(nt, c, N) * b_row + ch * 16);
       }
     }
@@ -231,150 +246,274 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
       }
     };
 
-    static_for<NS - 1>([&](auto sc) __attribute__((always_inline)) {
+    // Software pipeline over K steps (PIPE; otherwise each step lands, refills
+    // the slot of the previous step and reads + computes its own fragments).
+    // The ring has NS slots; the prologue fills all of them (steps
+    // 0 .. NS-1).  Step k's operand fragments are read from LDS into
+    // registers one step early, so iteration k
+    //   waits for step k+1's DMA (s_waitcnt vmcnt) and s_barrier: step k+1
+    //     has landed for every wave, and every wave has its step-k
+    //     fragments in registers (lgkmcnt(0) before the barrier), so slot
+    //     k % NS is free;
+    //   issues the DMA of step k+NS into slot k % NS;
+    //   issues the LDS reads of step k+1's fragments;
+    //   runs step k's conversions and MFMAs from registers, overlapping the
+    //     LDS latency of those reads and NS-1 steps of DMA.
+    static_for<PIPE ? NS : NS - 1>([&](auto sc) __attribute__((always_inline)) {
       constexpr int s = decltype(sc)::value;
       issue(s, s);
       return true;
     });
 
-    // MFMAs of one pipeline step.  `s2[j]` holds the two scale bytes (k
-    // halves) of this lane's column in B fragment j; kEdge selects the exact
-    // per-byte conversion for scale bytes outside 3..252, taken only when some
-    // lane of the wave has one (a wave-uniform branch).
-    auto compute = [&](int slot, const uint32_t(&s2)[C::kTN], auto edge_tag) __attribute__((always_inline)) {
-      constexpr bool kEdge = decltype(edge_tag)::value;
+    // MF-row sub-tiles of this wave past the tile's valid rows are skipped
+    // (no MFMAs), so the last tile of a group costs what its rows need.
+    // Wave-uniform (scalar) value.
+    const int tm_eff = __builtin_amdgcn_readfirstlane((tile.rows - wm * C::kWTM + MF - 1) / MF);
+
+    // MFMA of one sub-tile; the weight fragment goes first, so the
+    // accumulator holds the transposed sub-tile (a lane owns one activation
+    // row and runs of four adjacent output columns).
+    auto mfma = [](const bf16x8_t& w, const bf16x8_t& x, const typename C::Acc& c) __attribute__((always_inline)) {
+      if constexpr (MF == 32)
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, x, c, 0, 0, 0);
+      else
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, x, c, 0, 0, 0);
+    };
+    // Fragment coordinates.  An MF x 16*64/MF (k) operand fragment: lane l
+    // holds row / column (l % MF) and the 8 consecutive k values of 16-byte
+    // chunk kc = kk * (64 / MF) + l / MF of the 128-byte LDS row.
+    const int f_rc = lane % MF, f_kc = lane / MF;
+
+    // Operand fragments of one step.  GNK: bf16 weight fragments; MXFP4: the
+    // packed dwords (a lane's 8 k values of sub-step kk are logical dword
+    // kk * (64 / MF) + l / MF of the column's 32-byte record, at
+    // mx_dword_pos; with MF == 32 the four are one 16-byte chunk) and the two
+    // scale bytes.
+    struct Frags {
+      bf16x8_t af[C::kKS][C::kTM];
+      bf16x8_t bf[LAYOUT == kDGNK ? C::kKS : 1][C::kTN];
+      uint32_t bw[C::kKS][C::kTN];
+      uint32_t s2[C::kTN];
+    };
+    auto read_frags = [&](int slot, Frags& f) __attribute__((always_inline)) {
       const uint8_t* as = smem + slot * C::kSlot;
       const uint8_t* bs = as + C::kABytes;
-#pragma unroll
-      for (int ks = 0; ks < kSK / 32; ++ks) {
-        const int kc = ks * 4 + (lane / 16);  // logical 16-byte chunk of this lane
-        bf16x8_t af[C::kTM];
-#pragma unroll
-        for (int i = 0; i < C::kTM; ++i) {
-          const int r = wm * C::kWTM + i * 16 + (lane % 16);
-          af[i] = *reinterpret_cast<const bf16x8_t*>(as + r * 128 + ((kc ^ (r & 7)) * 16));
-        }
-        // B fragments one at a time: read, expand, feed the column of MFMAs
+      if constexpr (LAYOUT == kDMX) {
+        const uint8_t* ss = bs + C::kBBytes;
 #pragma unroll
         for (int j = 0; j < C::kTN; ++j) {
-          const int c = dlds_col<BN, C::kTN, EPI>(wn, j) + (lane % 16);
-          bf16x8_t bfr;
-          if constexpr (LAYOUT == kDGNK) {
-            bfr = *reinterpret_cast<const bf16x8_t*>(bs + c * 128 + ((kc ^ (c & 7)) * 16));
-          } else {
-            const uint32_t w =
-                *reinterpret_cast<const uint32_t*>(bs + c * 32 + ((ks ^ ((c >> 3) & 1)) * 16) + (lane / 16) * 4);
-            const uint32_t sb = (s2[j] >> (8 * ks)) & 0xffu;
-            uint32_t o[4];
-            if constexpr (!kEdge) {
-              const float sc = __uint_as_float(sb << 23);
-              o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
-              o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
-              o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
-              o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
+          const int c = dlds_col<BN, C::kTN, EPI, MF>(wn, j) + f_rc;
+          f.s2[j] = *reinterpret_cast<const uint16_t*>(ss + c * 2);
+        }
+      }
+#pragma unroll
+      for (int kk = 0; kk < C::kKS; ++kk) {
+        const int kc = kk * (64 / MF) + f_kc;
+#pragma unroll
+        for (int j = 0; j < C::kTN; ++j) {
+          const int c = dlds_col<BN, C::kTN, EPI, MF>(wn, j) + f_rc;
+          if constexpr (LAYOUT == kDMX) {
+            if constexpr (MF == 32) {
+              if (kk == 0) {
+                const uint4 w = *reinterpret_cast<const uint4*>(bs + c * 32 + f_kc * 16);
+                f.bw[0][j] = w.x;
+                f.bw[1][j] = w.y;
+                f.bw[2][j] = w.z;
+                f.bw[3][j] = w.w;
+              }
             } else {
-#pragma unroll
-              for (int b = 0; b < 4; ++b) o[b] = dequant_byte((w >> (8 * b)) & 0xffu, sb);
+              f.bw[kk][j] = *reinterpret_cast<const uint32_t*>(bs + c * 32 + mx_dword_pos(kc) * 4);
             }
-            bfr = __builtin_bit_cast(bf16x8_t, uint4{o[0], o[1], o[2], o[3]});
+          } else {
+            f.bf[kk][j] = *reinterpret_cast<const bf16x8_t*>(bs + c * 128 + ((kc ^ swz8(c)) * 16));
           }
+        }
+        // read even for skipped sub-tiles: unconditional reads keep the
+        // compiler's lgkmcnt accounting exact
 #pragma unroll
-          for (int i = 0; i < C::kTM; ++i)
-            // weight fragment first: the accumulator holds the transposed
-            // sub-tile (a lane owns one row and four adjacent columns)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(bfr, af[i], acc[i][j], 0, 0, 0);
+        for (int i = 0; i < C::kTM; ++i) {
+          const int r = wm * C::kWTM + i * MF + f_rc;
+          f.af[kk][i] = *reinterpret_cast<const bf16x8_t*>(as + r * 128 + ((kc ^ swz8(r)) * 16));
         }
       }
     };
-
-    // One pipeline step per iteration; the slot index is a run-time value so
-    // the accumulators keep one register assignment across steps.
-    int cur = 0;  // slot of step kt
-    for (int64_t kt = 0; kt < nk; ++kt) {
-      const int ahead = static_cast<int>(nk - 1 - kt < NS - 2 ? nk - 1 - kt : NS - 2);
-      if (wave == 0)
-        wait_step<NS, C::kOps0>(ahead);
-      else
-        wait_step<NS, C::kOps>(ahead);
-      barrier();
-      issue(kt + NS - 1, cur == 0 ? NS - 1 : cur - 1);
-      uint32_t s2[C::kTN];
+    // Conversions and MFMAs of one step.  All weight fragments of the step are
+    // converted first (straight-line code); the exact per-byte conversion for
+    // scale bytes outside 3..252 then rewrites them behind one wave-uniform
+    // branch, taken when some lane of the wave holds such a byte, and the
+    // MFMAs follow.  kFull: every sub-tile holds valid rows; otherwise the
+    // MFMAs of sub-tiles past the valid rows are skipped (wave-uniform).
+    auto compute = [&](const Frags& f, auto full_tag) __attribute__((always_inline)) {
+      auto mfmas = [&](auto full_tag, auto get_b) __attribute__((always_inline)) {
+        constexpr bool kFull = decltype(full_tag)::value;
+#pragma unroll
+        for (int kk = 0; kk < C::kKS; ++kk)
+#pragma unroll
+          for (int j = 0; j < C::kTN; ++j) {
+            const bf16x8_t bfr = get_b(kk, j);
+#pragma unroll
+            for (int i = 0; i < C::kTM; ++i) {
+              if (!kFull && i >= tm_eff) break;
+              acc[i][j] = mfma(bfr, f.af[kk][i], acc[i][j]);
+            }
+          }
+      };
       if constexpr (LAYOUT == kDMX) {
-        const uint8_t* ss = smem + cur * C::kSlot + C::kABytes + C::kBBytes;
-        bool edge = false;
+        bool edge_lane = false;
 #pragma unroll
-        for (int j = 0; j < C::kTN; ++j) {
-          const int c = dlds_col<BN, C::kTN, EPI>(wn, j) + (lane % 16);
-          s2[j] = *reinterpret_cast<const uint16_t*>(ss + c * 2);
-          edge |= !hw_scale_ok(s2[j] & 0xffu) || !hw_scale_ok(s2[j] >> 8);
+        for (int j = 0; j < C::kTN; ++j) edge_lane |= !hw_scale_ok(f.s2[j] & 0xffu) || !hw_scale_ok(f.s2[j] >> 8);
+        const bool edge = __builtin_amdgcn_ballot_w64(edge_lane) != 0;
+        uint32_t bq[C::kKS][C::kTN][4];
+#pragma unroll
+        for (int kk = 0; kk < C::kKS; ++kk)
+#pragma unroll
+          for (int j = 0; j < C::kTN; ++j) {
+            const uint32_t w = f.bw[kk][j];
+            const uint32_t sb = (f.s2[j] >> (8 * (kk / (C::kKS / 2)))) & 0xffu;  // 32-k scale block of sub-step kk
+            const float sc = __uint_as_float(sb << 23);
+            bq[kk][j][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
+            bq[kk][j][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
+            bq[kk][j][2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
+            bq[kk][j][3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
+          }
+        if (__builtin_expect(edge, false)) {
+#pragma unroll
+          for (int kk = 0; kk < C::kKS; ++kk)
+#pragma unroll
+            for (int j = 0; j < C::kTN; ++j) {
+              const uint32_t w = f.bw[kk][j];
+              const uint32_t sb = (f.s2[j] >> (8 * (kk / (C::kKS / 2)))) & 0xffu;
+#pragma unroll
+              for (int b = 0; b < 4; ++b) bq[kk][j][b] = dequant_byte((w >> (8 * b)) & 0xffu, sb);
+            }
         }
-        if (__builtin_amdgcn_ballot_w64(edge) != 0)
-          compute(cur, s2, std::true_type{});
-        else
-          compute(cur, s2, std::false_type{});
+        auto get_b = [&](int kk, int j) __attribute__((always_inline)) {
+          return __builtin_bit_cast(bf16x8_t, uint4{bq[kk][j][0], bq[kk][j][1], bq[kk][j][2], bq[kk][j][3]});
+        };
+        mfmas(full_tag, get_b);
       } else {
-#pragma unroll
-        for (int j = 0; j < C::kTN; ++j) s2[j] = 0;
-        compute(cur, s2, std::false_type{});
+        auto get_b = [&](int kk, int j) __attribute__((always_inline)) { return f.bf[kk][j]; };
+        mfmas(full_tag, get_b);
       }
-      cur = cur == NS - 1 ? 0 : cur + 1;
-    }
+    };
+    // Wait for step k's DMA with `ahead` younger steps still allowed in
+    // flight, then barrier.
+    auto land = [&](int64_t k) __attribute__((always_inline)) {
+      // youngest step whose DMA has been issued.  Pipelined: the prologue
+      // issues steps 0 .. NS-1, and before land(k), k >= 1, the last issue
+      // was step k+NS-2.  Otherwise: the prologue issues 0 .. NS-2 and step
+      // j issues j+NS-1 after its land.
+      const int64_t youngest = (PIPE && k == 0) ? NS - 1 : k + NS - 2;
+      const int64_t last = nk - 1 < youngest ? nk - 1 : youngest;
+      const int ahead = static_cast<int>(last - k);
+      if (wave == 0)
+        wait_step<NS + 1, C::kOps0>(ahead);
+      else
+        wait_step<NS + 1, C::kOps>(ahead);
+      barrier();
+    };
+    // The K loop, instantiated once for tiles whose sub-tiles all hold valid
+    // rows and once for the last, partial tile of a group (one wave-uniform
+    // test per tile instead of one per MFMA).
+    auto k_loop = [&](auto full_tag) __attribute__((always_inline)) {
+      if constexpr (PIPE) {
+        auto step = [&](int64_t k, const Frags& cur, Frags& nxt) __attribute__((always_inline)) {
+          if (k + 1 < nk) {
+            land(k + 1);
+            issue(k + NS, static_cast<int>(k % NS));
+            read_frags(static_cast<int>((k + 1) % NS), nxt);
+          }
+          compute(cur, full_tag);
+        };
+        Frags fa, fb;
+        land(0);
+        read_frags(0, fa);
+        for (int64_t kt = 0; kt < nk; kt += 2) {
+          step(kt, fa, fb);
+          if (kt + 1 < nk) step(kt + 1, fb, fa);
+        }
+      } else {
+        // land step k, refill the slot of step k-1, read and compute step k
+        int cur = 0;  // slot of step k
+        for (int64_t kt = 0; kt < nk; ++kt) {
+          land(kt);
+          issue(kt + NS - 1, cur == 0 ? NS - 1 : cur - 1);
+          Frags f;
+          read_frags(cur, f);
+          compute(f, full_tag);
+          cur = cur == NS - 1 ? 0 : cur + 1;
+        }
+      }
+    };
+    if (tm_eff >= C::kTM)
+      k_loop(std::true_type{});
+    else
+      k_loop(std::false_type{});
     // every DMA of this tile has been waited for by the last step
   }
 
-  // Epilogue.  A lane holds output row (lane % 16) of row sub-tile i and the
-  // four adjacent columns 4*(lane/16) .. +3 of column sub-tile j: one 8-byte
-  // (bf16) or 16-byte (f32) store per sub-tile.  Column counts are multiples
-  // of 8 (checked on the host), so a group of four is in or out as a whole.
-  const int r_in = lane % 16, c_in = 4 * (lane / 16);
+  // Epilogue.  A lane holds output row (lane % MF) of row sub-tile i and, for
+  // each q < MF / 8 (q < 1 for MF == 16), the four adjacent columns
+  // q*8 + 4*(lane/MF) .. +3 (MF == 32) or 4*(lane/16) .. +3 (MF == 16) of
+  // column sub-tile j, accumulator elements 4q .. 4q+3: one 8-byte (bf16) or
+  // 16-byte (f32) store per run.  Column counts are multiples of 8 (checked
+  // on the host), so a run of four is in or out as a whole.
+  constexpr int kRuns = MF == 32 ? 4 : 1;
+  const int r_in = lane % MF;
+  auto c_run = [&](int q) { return MF == 32 ? q * 8 + 4 * (lane / 32) : 4 * (lane / 16); };
   if constexpr (EPI == kEpiSitu) {
     const int64_t I = N / 2;
     constexpr int half = C::kTN / 2;
     const SituConsts sc = situ_consts(p.beta, p.beta_lin);
 #pragma unroll
     for (int i = 0; i < C::kTM; ++i) {
-      const int row = wm * C::kWTM + i * 16 + r_in;
+      const int row = wm * C::kWTM + i * MF + r_in;
       if (row >= tile.rows) continue;
       uint16_t* orow = static_cast<uint16_t*>(p.out) + (tile.row0 + row) * I;
 #pragma unroll
-      for (int j = 0; j < half; ++j) {
-        const int64_t col = nt * (BN / 2) + wn * half * 16 + j * 16 + c_in;
-        if (col >= I) continue;
-        uint2 packed{0u, 0u};  // padding bucket: zeros (SiTU(0, 0) == 0)
-        if (!tile.zero) {
-          float v[4];
+      for (int j = 0; j < half; ++j)
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            float gv = acc[i][j][r], uv = acc[i][j + half][r];
-            if (p.round_before_act) {
-              gv = static_cast<float>(static_cast<__bf16>(gv));
-              uv = static_cast<float>(static_cast<__bf16>(uv));
+        for (int q = 0; q < kRuns; ++q) {
+          const int64_t col = nt * (BN / 2) + wn * half * MF + j * MF + c_run(q);
+          if (col >= I) continue;
+          uint2 packed{0u, 0u};  // padding bucket: zeros (SiTU(0, 0) == 0)
+          if (!tile.zero) {
+            float v[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float gv = acc[i][j][q * 4 + r], uv = acc[i][j + half][q * 4 + r];
+              if (p.round_before_act) {
+                gv = static_cast<float>(static_cast<__bf16>(gv));
+                uv = static_cast<float>(static_cast<__bf16>(uv));
+              }
+              v[r] = situ_epi(gv, uv, sc);
             }
-            v[r] = situ_epi(gv, uv, sc);
+            packed = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
           }
-          packed = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+          *reinterpret_cast<uint2*>(orow + col) = packed;
         }
-        *reinterpret_cast<uint2*>(orow + col) = packed;
-      }
     }
   } else {
 #pragma unroll
     for (int i = 0; i < C::kTM; ++i) {
-      const int row = wm * C::kWTM + i * 16 + r_in;
+      const int row = wm * C::kWTM + i * MF + r_in;
       if (row >= tile.rows) continue;
       const int64_t obase = (tile.row0 + row) * N;
 #pragma unroll
-      for (int j = 0; j < C::kTN; ++j) {
-        const int64_t col = nt * BN + wn * C::kTN * 16 + j * 16 + c_in;
-        if (col >= N) continue;
-        const floatx4 a = acc[i][j];
-        if (p.out_dtype == LMOE_F32) {
-          *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + col) = float4{a[0], a[1], a[2], a[3]};
-        } else {
-          *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + obase + col) =
-              uint2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+      for (int j = 0; j < C::kTN; ++j)
+#pragma unroll
+        for (int q = 0; q < kRuns; ++q) {
+          const int64_t col = nt * BN + wn * C::kTN * MF + j * MF + c_run(q);
+          if (col >= N) continue;
+          const float a0 = acc[i][j][q * 4], a1 = acc[i][j][q * 4 + 1], a2 = acc[i][j][q * 4 + 2],
+                      a3 = acc[i][j][q * 4 + 3];
+          if (p.out_dtype == LMOE_F32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + col) = float4{a0, a1, a2, a3};
+          } else {
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+                uint2{pack_bf16x2(a0, a1), pack_bf16x2(a2, a3)};
+          }
         }
-      }
     }
   }
   }  // persistent tile loop
@@ -415,9 +554,13 @@ bool xcd_stripe_n() {
   return v;
 }
 
-template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4>
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32, bool PIPE = false>
 int launch_dma(const Params& p, hipStream_t st, const char* name) {
-  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN>;
+  if constexpr (EPI == kEpiSitu && (BN / WN / MF) % 2 != 0) {
+    return fail(LMOE_ERR_UNSUPPORTED, "%s: SiTU tile %dx%d with %dx%d MFMAs has no gate/up pairing", name, BM, BN, MF,
+                MF);
+  } else {
+  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>;
   const int64_t out_cols = EPI == kEpiSitu ? p.N / 2 : p.N;
   const int64_t cols_per_tile = EPI == kEpiSitu ? BN / 2 : BN;
   const int64_t ntiles = ceil_div(out_cols, cols_per_tile);
@@ -436,7 +579,7 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
                        name);
   const size_t lds = static_cast<size_t>(NS) * C::kSlot;
   static const hipError_t attr_rc =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr_rc != hipSuccess)
     return fail(LMOE_ERR_HIP, "%s: LDS size attribute (%zu bytes): %s", name, lds, hipGetErrorString(attr_rc));
@@ -445,15 +588,17 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
     const int64_t resident = kXcds * ((static_cast<int64_t>(cu_count()) * C::kLdsBlocks) / kXcds);
     if (resident >= kXcds && resident < grid) grid = resident;
   }
-  grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN>
+  grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>
       <<<dim3(static_cast<unsigned>(grid)), C::kThreads, lds, st>>>(p, ntiles, gm, blocks);
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;
+  }
 }
 
 // Re-tile MXFP4 weights to k-step-major order: packed (G, N, K/2) ->
-// (G, K/64, N, 32) and E8M0 scales (G, N, K/32) -> (G, K/64, N, 2).  One
-// thread per (group, step, column): two 16-byte copies and one 2-byte copy.
+// (G, K/64, N, 32) with each 32-byte record's dwords in mx_dword_pos order,
+// and E8M0 scales (G, N, K/32) -> (G, K/64, N, 2).  One thread per (group,
+// step, column): two 16-byte copies and one 2-byte copy.
 __global__ __launch_bounds__(256) void tile_mxfp4_kernel(const uint8_t* __restrict__ packed,
                                                          const uint8_t* __restrict__ scale, int64_t G, int64_t N,
                                                          int64_t K, uint8_t* __restrict__ packed_out,
@@ -465,8 +610,9 @@ __global__ __launch_bounds__(256) void tile_mxfp4_kernel(const uint8_t* __restri
     const int64_t n = i % N, s = (i / N) % kb64, g = i / (N * kb64);
     const uint4* src = reinterpret_cast<const uint4*>(packed + (g * N + n) * (K / 2) + 32 * s);
     uint4* dst = reinterpret_cast<uint4*>(packed_out + 32 * i);
-    dst[0] = src[0];
-    dst[1] = src[1];
+    const uint4 a = src[0], b = src[1];  // logical dwords 0..3, 4..7
+    dst[0] = uint4{a.x, a.z, b.x, b.z};  // 0, 2, 4, 6
+    dst[1] = uint4{a.y, a.w, b.y, b.w};  // 1, 3, 5, 7
     const uint8_t* ss = scale + (g * N + n) * (K / 32) + 2 * s;
     scale_out[2 * i] = ss[0];
     scale_out[2 * i + 1] = ss[1];
@@ -474,17 +620,68 @@ __global__ __launch_bounds__(256) void tile_mxfp4_kernel(const uint8_t* __restri
 }
 
 // Tile shape / ring depth of the MXFP4 kernel: LMOE_DMA_CFG = "BMxBNxNS"
-// picks one of the instantiated variants (tuning sweeps).  Defaults, from
-// sweeps on the LatentMoE expert shapes: 64x256x4 with the fused SiTU
-// epilogue (gate/up: each activation tile feeds 128 gate + 128 up columns),
-// 64x128x4 without (down projection: more blocks in flight).
+// picks one of the instantiated variants ("p": fragments read one step
+// ahead), LMOE_MFMA=16 the 16x16x32 MFMA instead of 32x32x16 (tuning
+// sweeps).  Default, from sweeps on the LatentMoE expert shapes: 64x256x3
+// for both epilogues (gate/up: each activation tile feeds 128 gate + 128 up
+// columns; down: 256 latent columns per activation tile).
 int mx_variant() {
   static const int v = [] {
     const char* e = std::getenv("LMOE_DMA_CFG");
     if (!e) return -1;
     const char* names[] = {"64x128x4", "64x128x6", "64x256x4", "64x256x3", "64x128x3", "32x128x4", "32x256x4",
-                           "64x256x5"};
-    for (int i = 0; i < 8; ++i)
+                           "64x256x5", "128x256x3", "128x128x4", "64x256x4p", "128x256x2", "128x128x3"};
+    for (int i = 0; i < 13; ++i)
+      if (std::strcmp(e, names[i]) == 0) return i;
+    return -1;
+  }();
+  return v;
+}
+
+bool mfma16() {
+  static const bool v = [] {
+    const char* e = std::getenv("LMOE_MFMA");
+    return e && std::strcmp(e, "16") == 0;
+  }();
+  return v;
+}
+
+template <int EPI, int MF>
+int run_mx_shape(const Params& p, hipStream_t st, const char* name) {
+  int v = mx_variant();
+  if (v < 0) v = 3;
+  switch (v) {
+    case 1: return launch_dma<64, 128, kDMX, EPI, 6, 1, 4, MF>(p, st, name);
+    case 2: return launch_dma<64, 256, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
+    case 3: return launch_dma<64, 256, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
+    case 4: return launch_dma<64, 128, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
+    case 5: return launch_dma<32, 128, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
+    case 6: return launch_dma<32, 256, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
+    case 7: return launch_dma<64, 256, kDMX, EPI, 5, 1, 4, MF>(p, st, name);
+    case 8: return launch_dma<128, 256, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
+    case 9: return launch_dma<128, 128, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
+    case 10: return launch_dma<64, 256, kDMX, EPI, 4, 1, 4, MF, true>(p, st, name);
+    case 11: return launch_dma<128, 256, kDMX, EPI, 2, 1, 4, MF>(p, st, name);
+    case 12: return launch_dma<128, 128, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
+    default: return launch_dma<64, 128, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
+  }
+}
+
+template <int EPI>
+int run_mx(const Params& p, hipStream_t st, const char* name) {
+  return mfma16() ? run_mx_shape<EPI, 16>(p, st, name) : run_mx_shape<EPI, 32>(p, st, name);
+}
+
+// Tile shape of the bf16 (GNK) kernel: LMOE_GNK_CFG picks a variant
+// "BMxBNxNS_WMxWN_MF" (tuning sweeps); the defaults are the sweep winners on
+// the LatentMoE dense projections and bf16 expert shapes.
+int gnk_variant() {
+  static const int v = [] {
+    const char* e = std::getenv("LMOE_GNK_CFG");
+    if (!e) return -1;
+    const char* names[] = {"64x128x3_1x4_16", "64x128x3_1x4_32", "128x128x2_2x2_32", "128x128x3_2x2_32",
+                           "128x256x2_2x4_32", "64x256x2_1x4_32", "128x128x2_1x4_32"};
+    for (int i = 0; i < 7; ++i)
       if (std::strcmp(e, names[i]) == 0) return i;
     return -1;
   }();
@@ -492,27 +689,26 @@ int mx_variant() {
 }
 
 template <int EPI>
-int run_mx(const Params& p, hipStream_t st, const char* name) {
-  int v = mx_variant();
-  if (v < 0) v = EPI == kEpiSitu ? 2 : 0;
+int run_gnk(const Params& p, hipStream_t st, const char* name) {
+  int v = gnk_variant();
+  // short K (the 1024-deep up-projection): 128x128 tiles of 2x2 waves
+  if (v < 0) v = (EPI == kEpiNone && p.K <= 1024 && p.G == 1) ? 2 : 0;
   switch (v) {
-    case 1: return launch_dma<64, 128, kDMX, EPI, 6>(p, st, name);
-    case 2: return launch_dma<64, 256, kDMX, EPI, 4>(p, st, name);
-    case 3: return launch_dma<64, 256, kDMX, EPI, 3>(p, st, name);
-    case 4: return launch_dma<64, 128, kDMX, EPI, 3>(p, st, name);
-    case 5: return launch_dma<32, 128, kDMX, EPI, 4>(p, st, name);
-    case 6: return launch_dma<32, 256, kDMX, EPI, 4>(p, st, name);
-    case 7: return launch_dma<64, 256, kDMX, EPI, 5>(p, st, name);
-    default: return launch_dma<64, 128, kDMX, EPI, 4>(p, st, name);
+    case 1: return launch_dma<64, 128, kDGNK, EPI, 3, 1, 4, 32>(p, st, name);
+    case 2: return launch_dma<128, 128, kDGNK, EPI, 2, 2, 2, 32>(p, st, name);
+    case 3: return launch_dma<128, 128, kDGNK, EPI, 3, 2, 2, 32>(p, st, name);
+    case 4: return launch_dma<128, 256, kDGNK, EPI, 2, 2, 4, 32>(p, st, name);
+    case 5: return launch_dma<64, 256, kDGNK, EPI, 2, 1, 4, 32>(p, st, name);
+    case 6: return launch_dma<128, 128, kDGNK, EPI, 2, 1, 4, 32>(p, st, name);
+    default: return launch_dma<64, 128, kDGNK, EPI, 3, 1, 4, 16>(p, st, name);
   }
 }
 
 }  // namespace
 
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name) {
-  constexpr int BM = 64, BN = 128;
-  if (layout == kGNK && epi == kEpiNone) return launch_dma<BM, BN, kDGNK, kEpiNone, 3>(p, st, name);
-  if (layout == kGNK && epi == kEpiSitu) return launch_dma<BM, BN, kDGNK, kEpiSitu, 3>(p, st, name);
+  if (layout == kGNK && epi == kEpiNone) return run_gnk<kEpiNone>(p, st, name);
+  if (layout == kGNK && epi == kEpiSitu) return run_gnk<kEpiSitu>(p, st, name);
   if (layout == kMXFP4 && epi == kEpiNone) return run_mx<kEpiNone>(p, st, name);
   if (layout == kMXFP4 && epi == kEpiSitu) return run_mx<kEpiSitu>(p, st, name);
   return fail(LMOE_ERR_UNSUPPORTED, "%s: DMA path layout %d epilogue %d", name, layout, epi);

@@ -196,13 +196,13 @@ void grouped_gemm_mx_kernel(Params p, int64_t n_tiles, int gm) {
     const int64_t nk = K / kXK;
     const uint8_t* lhs = reinterpret_cast<const uint8_t*>(p.lhs);
 
-    // A codes: LDS chunk q = tid + 256 v <- row q/8, logical chunk (q%8) ^ (row&7)
+    // A codes: LDS chunk q = tid + 256 v <- row q/8, logical chunk (q%8) ^ swz8(row)
     const uint8_t* a_base = uniform_ptr(lhs + tile.row0 * K);
     uint32_t a_off[C::kAOps];
 #pragma unroll
     for (int v = 0; v < C::kAOps; ++v) {
       const int q = tid + C::kThreads * v;
-      const int row = q / 8, kc = (q % 8) ^ (row & 7);
+      const int row = q / 8, kc = (q % 8) ^ swz8(row);
       const int rr = row < tile.rows ? row : 0;
       a_off[v] = static_cast<uint32_t>(rr * K + kc * 16);
     }
@@ -211,7 +211,7 @@ void grouped_gemm_mx_kernel(Params p, int64_t n_tiles, int gm) {
     const uint32_t as_off = static_cast<uint32_t>((lane < tile.rows ? lane : 0) * 4);
     const bool as_active = lane < BM;
     // B: chunk q = tid + 256 u of the slot's B region <- record h = q / (2 BN),
-    // column c = (q % 2BN) / 2, logical chunk (q % 2) ^ ((c >> 3) & 1)
+    // column c = (q % 2BN) / 2, chunk q % 2 (tiled records copied as they are)
     const int64_t rec = N * 32;  // one 64-k record of all columns
     const uint8_t* b_base = uniform_ptr(static_cast<const uint8_t*>(p.rhs) + g * (K / 64) * rec);
     uint32_t b_off[C::kBOps];
@@ -219,7 +219,7 @@ void grouped_gemm_mx_kernel(Params p, int64_t n_tiles, int gm) {
     for (int u = 0; u < C::kBOps; ++u) {
       const int q = tid + C::kThreads * u;
       const int h = q / (2 * BN), rem = q % (2 * BN);
-      const int c = rem / 2, ch = (rem % 2) ^ ((c >> 3) & 1);
+      const int c = rem / 2, ch = rem % 2;
       b_off[u] = static_cast<uint32_t>(h * rec + xrhs_col<BN, EPI>(nt, c, N) * 32 + ch * 16);
     }
     // B scales: wave 0 lane sl <- record h = sl / (BN/8), 8 columns from c0
@@ -285,8 +285,8 @@ void grouped_gemm_mx_kernel(Params p, int64_t n_tiles, int gm) {
 #pragma unroll
       for (int i = 0; i < C::kTM; ++i) {
         const int r = i * 16 + r_lane;
-        const uint4 lo = *reinterpret_cast<const uint4*>(as + r * kXK + ((g_lane ^ (r & 7)) * 16));
-        const uint4 hi = *reinterpret_cast<const uint4*>(as + r * kXK + (((4 + g_lane) ^ (r & 7)) * 16));
+        const uint4 lo = *reinterpret_cast<const uint4*>(as + r * kXK + ((g_lane ^ swz8(r)) * 16));
+        const uint4 hi = *reinterpret_cast<const uint4*>(as + r * kXK + (((4 + g_lane) ^ swz8(r)) * 16));
         af[i] = v8i_t{static_cast<int>(lo.x), static_cast<int>(lo.y), static_cast<int>(lo.z), static_cast<int>(lo.w),
                       static_cast<int>(hi.x), static_cast<int>(hi.y), static_cast<int>(hi.z), static_cast<int>(hi.w)};
         sa[i] = asc[r * 4 + g_lane];
@@ -294,10 +294,14 @@ void grouped_gemm_mx_kernel(Params p, int64_t n_tiles, int gm) {
 #pragma unroll
       for (int j = 0; j < C::kTN; ++j) {
         const int c = xlds_col<BN, C::kTN, EPI>(wn, j) + r_lane;
-        const int h = g_lane / 2, ch = (g_lane % 2) ^ ((c >> 3) & 1);
-        const uint4 w = *reinterpret_cast<const uint4*>(bs + (h * BN + c) * 32 + ch * 16);
-        const v8i_t bf = v8i_t{static_cast<int>(w.x), static_cast<int>(w.y), static_cast<int>(w.z),
-                               static_cast<int>(w.w), 0, 0, 0, 0};
+        // logical dwords 4*(g%2) .. +3 of record h = g/2: physical
+        // (mx_dword_pos) 2*(g%2), 4 + 2*(g%2), 2*(g%2) + 1, 4 + 2*(g%2) + 1
+        const int h = g_lane / 2, hb = (g_lane % 2) * 8;
+        const uint8_t* rec0 = bs + (h * BN + c) * 32;
+        const uint2 lo = *reinterpret_cast<const uint2*>(rec0 + hb);
+        const uint2 hi = *reinterpret_cast<const uint2*>(rec0 + 16 + hb);
+        const v8i_t bf = v8i_t{static_cast<int>(lo.x), static_cast<int>(hi.x), static_cast<int>(lo.y),
+                               static_cast<int>(hi.y), 0, 0, 0, 0};
         const int sb = bsc[(h * BN + c) * 2 + (g_lane % 2)];
 #pragma unroll
         for (int i = 0; i < C::kTM; ++i)

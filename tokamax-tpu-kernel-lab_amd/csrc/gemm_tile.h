@@ -25,6 +25,7 @@ namespace gemm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
 constexpr int kBK = 64;
@@ -142,6 +143,20 @@ __device__ TileInfo locate_tile(const int32_t* __restrict__ gs, int64_t G, int64
   }
   return info;
 }
+
+// 16-byte chunk swizzle of 128-byte LDS rows: logical chunk kc of row r sits
+// at physical chunk kc ^ swz8(r).  MFMA fragment reads fetch one chunk from
+// each of 16 consecutive rows per 16-lane group; with 64 four-byte banks the
+// rows r and r + 8 must then land in different chunks too, which plain
+// (r & 7) does not give (a 2-way conflict on every fragment read).
+__device__ __forceinline__ int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+
+// Tiled MXFP4 record: the 32 bytes (64 k) of one column and k step hold the
+// eight 4-byte groups of 8 k values in the order 0, 2, 4, 6, 1, 3, 5, 7, so
+// a lane of a 32x32x16 MFMA fragment (k groups g, g+2, g+4, g+6 of its
+// column) reads its whole k step as one contiguous 16-byte chunk.  Physical
+// dword of logical dword d:
+__device__ __forceinline__ int mx_dword_pos(int d) { return (d & 1) * 4 + (d >> 1); }
 
 constexpr int kXcds = 8;  // MI355X: 8 XCDs; consecutive blocks go to consecutive XCDs
 

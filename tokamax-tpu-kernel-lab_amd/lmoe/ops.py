@@ -211,7 +211,9 @@ def mxfp4_tile_weights(w_packed: torch.Tensor, w_scale: torch.Tensor) -> tuple[t
   ``prefuse_gateup_weights``, rd.py:610-641): checkpoint-layout packed
   (G, N, K/2) and E8M0 scales (G, N, K/32) -> k-step-major (G, K/64, N, 32)
   and (G, K/64, N, 2), as ``ragged_dot_mxfp4(..., weight_layout="tiled")``
-  streams them (one contiguous read per k step and column run)."""
+  streams them (one contiguous read per k step and column run).  Each 32-byte
+  record keeps the checkpoint's eight 4-byte groups in the order
+  0, 2, 4, 6, 1, 3, 5, 7."""
   _dev(w_packed, w_scale)
   if w_packed.dtype != torch.uint8 or w_scale.dtype != torch.uint8 or w_packed.dim() != 3:
     raise ValueError("packed / scale must be uint8 (G, N, K/2) / (G, N, K/32)")
