@@ -162,7 +162,7 @@ def main():
   roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
               "frac": round(achieved / HBM_PEAK_GBS, 4),
               "traffic": traffic.get("bytes_per_launch") if traffic else None,
-              "kernel": "grouped_gemm_kernel<MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
+              "kernel": "grouped_gemm_dma_kernel<64, 256, MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
               "algorithmic_bytes": int(nbytes), "algorithmic_flops": flops,
               "kernel_us": round(gateup_ms * 1000.0, 2)}
   grouped = {"tflops": round(tflops, 2),

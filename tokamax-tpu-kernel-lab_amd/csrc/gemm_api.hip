@@ -52,6 +52,7 @@ int check_common(const void* lhs, const void* rhs, const int32_t* gs, int64_t M,
                  (long long)M, (long long)K, (long long)N, (long long)G);
   LMOE_CHECK_ARG(zero_group >= -1 && zero_group < G, "%s: bad zero_group %d", name, zero_group);
   LMOE_CHECK_ARG(M == 0 || (lhs && rhs && gs && out), "%s: null pointer", name);
+  LMOE_CHECK_SUPPORTED(M < (1ll << 31), "%s: M=%lld rows (the tile scan counts rows in 32 bits)", name, (long long)M);
   return LMOE_OK;
 }
 

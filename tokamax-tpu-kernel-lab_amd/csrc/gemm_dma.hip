@@ -88,9 +88,11 @@ struct DCfg {
   // capped so that the same number of waves fits on each SIMD
   static constexpr int kLdsBlocks = 163840 / (NS * kSlot + 64);
   static constexpr int kWavesPerEuRaw = kLdsBlocks * kWaves / 4;
-  // at most 2 waves per SIMD: the two fragment sets of the software pipeline
-  // plus the accumulators need up to 256 VGPRs
-  static constexpr int kWavesPerEu = kWavesPerEuRaw < 1 ? 1 : (kWavesPerEuRaw > 2 ? 2 : kWavesPerEuRaw);
+  // at most 3 waves per SIMD (at most 2 with the software pipeline, whose two
+  // fragment sets plus the accumulators need up to 256 VGPRs)
+  static constexpr int kWavesCap = PIPE ? 2 : 3;
+  static constexpr int kWavesPerEu =
+      kWavesPerEuRaw < 1 ? 1 : (kWavesPerEuRaw > kWavesCap ? kWavesCap : kWavesPerEuRaw);
 };
 
 // First LDS column of column sub-tile j of wave wn.  With the SiTU epilogue
@@ -129,7 +131,10 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
   __shared__ TileInfo s_tile;
   __shared__ int64_t s_nt;
 
-  const int64_t tm = threadIdx.x < 64 ? total_m_tiles<BM>(p.group_sizes, p.G, p.M) : 0;  // used by wave 0
+  // total m-tiles, used by wave 0 to map virtual tiles when m-tile groups go
+  // round-robin over the XCDs (gm > 0); with n-tiles striped (gm == 0)
+  // locate_tile itself returns "no work" past the last tile
+  const int64_t tm = (gm > 0 && threadIdx.x < 64) ? total_m_tiles<BM>(p.group_sizes, p.G, p.M) : INT64_MAX;
   // Persistent blocks: block b takes virtual tiles b, b + gridDim.x, ... (the
   // grid is a multiple of the XCD count, so a virtual tile keeps its XCD).
   for (int64_t vb = blockIdx.x; vb < n_virtual; vb += gridDim.x) {

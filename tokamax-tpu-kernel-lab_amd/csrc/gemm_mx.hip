@@ -433,6 +433,7 @@ extern "C" int lmoe_ragged_dot_mxfp8_mxfp4(const uint8_t* lhs_q, const uint8_t* 
                                            int out_dtype, void* stream) {
   const char* name = "ragged_dot_mxfp8_mxfp4";
   LMOE_CHECK_ARG(M >= 0 && K > 0 && N > 0 && G > 0, "%s: bad sizes", name);
+  LMOE_CHECK_SUPPORTED(M < (1ll << 31), "%s: M=%lld rows (the tile scan counts rows in 32 bits)", name, (long long)M);
   LMOE_CHECK_ARG(zero_group >= -1 && zero_group < G, "%s: bad zero_group %d", name, zero_group);
   LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
   LMOE_CHECK_ARG(valid_dtype(out_dtype), "%s: bad out dtype", name);

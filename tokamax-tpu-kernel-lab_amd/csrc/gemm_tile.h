@@ -77,41 +77,70 @@ __device__ int64_t total_m_tiles(const int32_t* __restrict__ gs, int64_t G, int6
   return tiles + (tail + BM - 1) / BM;
 }
 
-// Find (group, first row, rows) of m-tile `mt`.  Executed by wave 0.
+// Saturating add of non-negative 32-bit counts (cap <= 2^31).
+__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b, uint32_t cap) {
+  const uint32_t s = a + b;
+  return s < cap ? s : cap;
+}
+
+// Inclusive wave-wide prefix sum (saturating at cap) with DPP row shifts and
+// row broadcasts: six dependent steps, no LDS traffic.
+__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x, uint32_t cap) {
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xf, 0xf, false), cap);  // row_shr:1
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xf, 0xf, false), cap);  // row_shr:2
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xf, 0xf, false), cap);  // row_shr:4
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xf, 0xf, false), cap);  // row_shr:8
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xa, 0xf, false), cap);  // row_bcast:15
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false), cap);  // row_bcast:31
+  return x;
+}
+
+// Find (group, first row, rows) of m-tile `mt`.  Executed by wave 0.  Lane l
+// holds groups l, l + 64, ...: the group sizes of up to kPre chunks of 64 are
+// loaded before any is scanned, so their latencies overlap; group counts are
+// clipped to [0, M] and the running sums saturate at M (row counts) and at
+// 2^31 - 1 (tile counts), so 32-bit scans are exact where it matters.
 template <int BM>
 __device__ TileInfo locate_tile(const int32_t* __restrict__ gs, int64_t G, int64_t M, int zero_group,
                                 int64_t mt) {
+  constexpr int kPre = 4;
+  constexpr uint32_t kTileCap = 0x7fffffffu;
   const int lane = threadIdx.x % 64;
-  int64_t cum_tiles = 0, cum_rows = 0;
+  const uint32_t m32 = static_cast<uint32_t>(M);  // M < 2^31 (checked on the host)
+  uint32_t cum_tiles = 0, cum_rows = 0;
   TileInfo info{-1, 0, 0, false};
-  for (int64_t g0 = 0; g0 < G; g0 += 64) {
-    const int64_t g = g0 + lane;
-    int64_t n = g < G ? gs[g] : 0;
-    n = n < 0 ? 0 : n;
-    // rows past M are never computed
-    int64_t tiles = (n + BM - 1) / BM;
-    int64_t incl_t = tiles, incl_r = n;
+  for (int64_t g0 = 0; g0 < G; g0 += 64 * kPre) {
+    uint32_t n_pre[kPre];
 #pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const int64_t yt = __shfl_up(incl_t, off, 64);
-      const int64_t yr = __shfl_up(incl_r, off, 64);
-      if (lane >= off) {
-        incl_t += yt;
-        incl_r += yr;
+    for (int c = 0; c < kPre; ++c) {
+      const int64_t g = g0 + 64 * c + lane;
+      const int32_t v = g < G ? gs[g] : 0;
+      n_pre[c] = v < 0 ? 0u : (static_cast<uint32_t>(v) < m32 ? static_cast<uint32_t>(v) : m32);
+    }
+#pragma unroll
+    for (int c = 0; c < kPre; ++c) {
+      if (g0 + 64 * c >= G) break;
+      const int64_t g = g0 + 64 * c + lane;
+      const uint32_t n = n_pre[c];
+      const uint32_t tiles = (n + BM - 1) / BM;
+      const uint32_t incl_t = wave_scan_sat(tiles, kTileCap), incl_r = wave_scan_sat(n, m32);
+      // exclusive prefixes: the previous lane's inclusive ones (wave_shr:1);
+      // a saturated prefix stays >= M, so such groups get no rows
+      const uint32_t prev_t = __builtin_amdgcn_update_dpp(0u, incl_t, 0x138, 0xf, 0xf, false);
+      const uint32_t prev_r = __builtin_amdgcn_update_dpp(0u, incl_r, 0x138, 0xf, 0xf, false);
+      const int64_t excl_t = sat_add(cum_tiles, prev_t, kTileCap);
+      const int64_t excl_r = sat_add(cum_rows, prev_r, m32);
+      if (g < G && mt >= excl_t && mt < excl_t + tiles) {
+        const int64_t local = mt - excl_t;
+        info.group = static_cast<int>(g);
+        info.row0 = excl_r + local * BM;
+        const int64_t left = static_cast<int64_t>(n) - local * BM;
+        info.rows = static_cast<int>(left < BM ? left : BM);
+        info.zero = (g == zero_group);
       }
+      cum_tiles = sat_add(cum_tiles, __builtin_amdgcn_readlane(incl_t, 63), kTileCap);
+      cum_rows = sat_add(cum_rows, __builtin_amdgcn_readlane(incl_r, 63), m32);
     }
-    const int64_t excl_t = cum_tiles + incl_t - tiles;
-    const int64_t excl_r = cum_rows + incl_r - n;
-    if (g < G && mt >= excl_t && mt < excl_t + tiles) {
-      const int64_t local = mt - excl_t;
-      info.group = static_cast<int>(g);
-      info.row0 = excl_r + local * BM;
-      const int64_t left = n - local * BM;
-      info.rows = static_cast<int>(left < BM ? left : BM);
-      info.zero = (g == zero_group);
-    }
-    cum_tiles += __shfl(incl_t, 63, 64);
-    cum_rows += __shfl(incl_r, 63, 64);
   }
   // broadcast the (single) hit
   const uint64_t hit = __ballot(info.group >= 0);
@@ -125,7 +154,7 @@ __device__ TileInfo locate_tile(const int32_t* __restrict__ gs, int64_t G, int64
     // tail tiles: zero rows [sum(group_sizes), M)
     const int64_t q = mt - cum_tiles;
     const int64_t r0 = cum_rows + q * BM;
-    if (r0 < M) {
+    if (q >= 0 && r0 < M) {
       info.group = 0;
       info.row0 = r0;
       const int64_t left = M - r0;
@@ -168,21 +197,23 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs; consecutive blocks go to consecutiv
 // of a group on one XCD (the A rows are read by one XCD only).
 template <int BM>
 __device__ TileInfo schedule_tile(const Params& p, int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt) {
-  const int64_t xcd = vb % kXcds, slot = vb / kXcds;
+  // grids and tile counts are < 2^31 (checked on the host): 32-bit index math
+  const uint32_t v32 = static_cast<uint32_t>(vb), nt32 = static_cast<uint32_t>(n_tiles);
+  const uint32_t xcd = v32 % kXcds, slot = v32 / kXcds;
   TileInfo ti{-1, 0, 0, false};
   nt = 0;
   if (gm == 0) {
-    const int64_t per = n_tiles / kXcds;
-    const int64_t mt = slot / per;
+    const uint32_t per = nt32 / kXcds;
+    const uint32_t mt = slot / per;
     nt = xcd + kXcds * (slot % per);
     if (mt < tm) ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, mt);
   } else {
-    const int64_t span = static_cast<int64_t>(gm) * n_tiles;
-    const int64_t m_base = ((slot / span) * kXcds + xcd) * gm;
-    const int64_t r = slot % span;
+    const uint32_t span = static_cast<uint32_t>(gm) * nt32;
+    const int64_t m_base = (static_cast<int64_t>(slot / span) * kXcds + xcd) * gm;
+    const uint32_t r = slot % span;
     if (m_base < tm) {
-      const int64_t gm_eff = tm - m_base < gm ? tm - m_base : gm;
-      if (r < gm_eff * n_tiles) {
+      const uint32_t gm_eff = static_cast<uint32_t>(tm - m_base < gm ? tm - m_base : gm);
+      if (r < gm_eff * nt32) {
         nt = r / gm_eff;
         ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, m_base + r % gm_eff);
       }
