@@ -114,6 +114,17 @@ int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_
                           int zero_group, int mode, int epilogue, float beta, float beta_lin,
                           void* out, void* stream);
 
+/* ---- dense projections on hipBLASLt ------------------------------------------------
+ * out (M, N) = x (M, K) @ w_nk^T, w_nk stored (N, K): the layer's plain dense
+ * projections (x = hidden @ down_proj, ref.py:634-655; out = normed @ up_proj,
+ * ref.py:430) as a library GEMM (ROCm hipBLASLt), f32 accumulation.  x and w
+ * share a dtype (bf16 or f32); out bf16 or f32.  Uses only algorithms that
+ * need no workspace; the first call per device creates a hipBLASLt handle and
+ * the first call per shape a plan, both kept until the process ends.
+ */
+int lmoe_dense_blaslt(const void* x, int x_dtype, const void* w_nk, int w_dtype, int64_t M, int64_t K, int64_t N,
+                      void* out, int out_dtype, void* stream);
+
 /* ---- a18: MXFP4 weight preparation ------------------------------------------------
  * One-time weight preparation, the MXFP4 counterpart of prefuse_gateup_weights
  * (rd.py:610-641): k-step-major re-tiling of checkpoint-layout weights,

@@ -64,7 +64,9 @@ def build(jobs: int | None = None, verbose: bool = False) -> str:
   with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
     objs = list(ex.map(lambda s: _compile(s, verbose), srcs))
   tmp = OUT + ".tmp"
-  cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+  # hipBLASLt: the plain dense projections (gemm_blaslt.hip)
+  cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-L/opt/rocm/lib", "-lhipblaslt",
+         "-Wl,-rpath,/opt/rocm/lib", "-o", tmp]
   r = subprocess.run(cmd, capture_output=True, text=True)
   if r.returncode != 0:
     raise RuntimeError(f"link failed:\n{r.stderr}")

@@ -78,34 +78,51 @@ __device__ __forceinline__ void store_vec(void* p, int64_t i, int dtype, const f
 
 // Adds the rows rows[0..n) (ascending) with weights wts[] into routed_out[t]
 // with the scatter-add rounding: product in promoted(shard, w) dtype, cast to
-// out dtype, each add rounded to out dtype.
+// out dtype, each add rounded to out dtype.  Rows are loaded kBatch at a time
+// before any is added, so their memory latencies overlap; the adds keep the
+// ascending order.
 template <int VEC>
-__device__ void accumulate_token(const void* shard, int sdt, const int32_t* rows, const float* wts,
-                                 int n, int64_t lat, void* out, int odt, int64_t t, int prod_dt,
-                                 int lane) {
+__device__ __forceinline__ void accumulate_token(const void* shard, int sdt, const int32_t* rows, const float* wts,
+                                                 int n, int64_t lat, void* out, int odt, int64_t t, int prod_dt,
+                                                 int lane) {
+  constexpr int kBatch = VEC == 8 ? 8 : 4;
   for (int64_t c0 = static_cast<int64_t>(lane) * VEC; c0 < lat; c0 += kWave * VEC) {
     float acc[VEC];
     load_vec<VEC>(out, t * lat + c0, odt, acc);
-    for (int r = 0; r < n; ++r) {
-      float x[VEC];
-      load_vec<VEC>(shard, static_cast<int64_t>(rows[r]) * lat + c0, sdt, x);
-      const float w = wts[r];
+    for (int r0 = 0; r0 < n; r0 += kBatch) {
+      // unconditional loads (a batch past n re-reads row n-1) keep the loads
+      // of a batch together ahead of the adds
+      float x[kBatch][VEC];
 #pragma unroll
-      for (int j = 0; j < VEC; ++j) {
-        float v = round_to(__fmul_rn(x[j], w), prod_dt);
-        v = round_to(v, odt);
-        acc[j] = round_to(__fadd_rn(acc[j], v), odt);
+      for (int b = 0; b < kBatch; ++b) {
+        const int r = r0 + b < n ? r0 + b : n - 1;
+        load_vec<VEC>(shard, static_cast<int64_t>(rows[r]) * lat + c0, sdt, x[b]);
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        if (r0 + b >= n) break;
+        const float w = wts[r0 + b];
+#pragma unroll
+        for (int j = 0; j < VEC; ++j) {
+          float v = round_to(__fmul_rn(x[b][j], w), prod_dt);
+          v = round_to(v, odt);
+          acc[j] = round_to(__fadd_rn(acc[j], v), odt);
+        }
       }
     }
     store_vec<VEC>(out, t * lat + c0, odt, acc);
   }
 }
 
-template <int VEC>
+// SDT / ODT >= 0 fix the shard / output dtypes at compile time (the layer's
+// bf16 case), which keeps the batched row loads free of dtype branches; -1
+// reads them from the arguments.
+template <int VEC, int SDT = -1, int ODT = -1>
 __global__ __launch_bounds__(256) void combine_slots_kernel(
-    const void* __restrict__ shard, int sdt, const int32_t* __restrict__ slot_pos,
+    const void* __restrict__ shard, int sdt_arg, const int32_t* __restrict__ slot_pos,
     const void* __restrict__ w, int wdt, int T, int k, int64_t lat, int mode, void* __restrict__ out,
-    int odt) {
+    int odt_arg) {
+  const int sdt = SDT >= 0 ? SDT : sdt_arg, odt = ODT >= 0 ? ODT : odt_arg;
   __shared__ int32_t rows_s[kTokensPerBlock][kWave];
   __shared__ float wts_s[kTokensPerBlock][kWave];
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -123,14 +140,24 @@ __global__ __launch_bounds__(256) void combine_slots_kernel(
       float acc[VEC];
 #pragma unroll
       for (int j = 0; j < VEC; ++j) acc[j] = 0.0f;
-      for (int j = 0; j < k; ++j) {
-        const int row = rows_s[wave][j];
-        if (row < 0) continue;
-        float x[VEC];
-        load_vec<VEC>(shard, static_cast<int64_t>(row) * lat + c0, sdt, x);
-        const float wv = wts_s[wave][j];
+      constexpr int kBatch = VEC == 8 ? 8 : 4;  // row loads in flight before the adds
+      for (int j0 = 0; j0 < k; j0 += kBatch) {
+        float x[kBatch][VEC];
 #pragma unroll
-        for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(x[q], wv));
+        for (int b = 0; b < kBatch; ++b) {
+          // unconditional loads (dropped slots re-read row 0) keep the batch's
+          // loads together ahead of the adds
+          const int row = j0 + b < k ? rows_s[wave][j0 + b] : -1;
+          load_vec<VEC>(shard, static_cast<int64_t>(row >= 0 ? row : 0) * lat + c0, sdt, x[b]);
+        }
+#pragma unroll
+        for (int b = 0; b < kBatch; ++b) {
+          const int row = j0 + b < k ? rows_s[wave][j0 + b] : -1;
+          if (row < 0) continue;
+          const float wv = wts_s[wave][j0 + b];
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) acc[q] = __fadd_rn(acc[q], __fmul_rn(x[b][q], wv));
+        }
       }
       store_vec<VEC>(out, static_cast<int64_t>(t) * lat + c0, odt, acc);
     }
@@ -198,8 +225,11 @@ __global__ __launch_bounds__(256) void combine_csr_kernel(
   }
 }
 
+// Many bins (tokens): large chunks keep the scanned (token, chunk) array small.
+constexpr int kCombineChunk = 1024;
+
 int64_t combine_ws_bytes(int64_t m, int64_t T) {
-  const int64_t chunks = csort::num_chunks(m > 0 ? m : 1);
+  const int64_t chunks = csort::num_chunks<kCombineChunk>(m > 0 ? m : 1);
   return (2 * chunks * T + (T + 1) + m + 64) * static_cast<int64_t>(sizeof(int32_t));
 }
 
@@ -228,7 +258,11 @@ extern "C" int lmoe_combine_slots(const void* shard_out, int shard_dtype, const 
   if (T == 0) return LMOE_OK;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned blocks = static_cast<unsigned>(ceil_div(T, kTokensPerBlock));
-  if (vec8_ok(shard_out, routed_out, lat, shard_dtype, out_dtype))
+  if (vec8_ok(shard_out, routed_out, lat, shard_dtype, out_dtype) && shard_dtype == LMOE_BF16 &&
+      out_dtype == LMOE_BF16)
+    combine_slots_kernel<8, LMOE_BF16, LMOE_BF16><<<blocks, 256, 0, st>>>(
+        shard_out, shard_dtype, slot_pos, w, w_dtype, (int)T, (int)k, lat, mode, routed_out, out_dtype);
+  else if (vec8_ok(shard_out, routed_out, lat, shard_dtype, out_dtype))
     combine_slots_kernel<8><<<blocks, 256, 0, st>>>(shard_out, shard_dtype, slot_pos, w, w_dtype,
                                                    (int)T, (int)k, lat, mode, routed_out, out_dtype);
   else
@@ -256,7 +290,7 @@ extern "C" int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype,
     return fail(LMOE_ERR_WORKSPACE, "combine_scatter_add: workspace %lld < %lld",
                 (long long)workspace_size, (long long)need);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const int64_t chunks = csort::num_chunks(m);
+  const int64_t chunks = csort::num_chunks<kCombineChunk>(m);
   int32_t* ws = static_cast<int32_t*>(workspace);
   int32_t* hist = ws;
   int32_t* base = hist + chunks * T;
@@ -265,14 +299,14 @@ extern "C" int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype,
   int32_t* num_kept = order + m;
   const int Ti = static_cast<int>(T);
   TokenKey key{padded_token_idx, Ti};
-  csort::hist_kernel<<<dim3(static_cast<unsigned>(chunks)), 256, (T + 1) * sizeof(int32_t), st>>>(
-      key, m, Ti, hist);
+  csort::hist_kernel<kCombineChunk><<<dim3(static_cast<unsigned>(chunks)), 256, (T + 1) * sizeof(int32_t), st>>>(
+      key, m, Ti, chunks, hist);
   LMOE_CHECK_LAUNCH("combine_hist");
-  csort::scan_kernel<<<1, csort::kScanThreads, 0, st>>>(hist, static_cast<int>(chunks), Ti,
-                                                        (1ll << 40), base, nullptr, offsets, num_kept);
+  if (csort::launch_scan(hist, chunks, Ti, (1ll << 40), base, nullptr, offsets, num_kept, st) != hipSuccess)
+    return fail(LMOE_ERR_HIP, "combine_scan: LDS attribute");
   LMOE_CHECK_LAUNCH("combine_scan");
-  csort::place_kernel<<<dim3(static_cast<unsigned>(chunks)), 64, T * sizeof(int32_t), st>>>(
-      key, m, Ti, csort::key_bits_for(Ti), base, OrderSink{order});
+  csort::place_kernel<kCombineChunk><<<dim3(static_cast<unsigned>(chunks)), 64, T * sizeof(int32_t), st>>>(
+      key, m, Ti, csort::key_bits_for(Ti), chunks, base, OrderSink{order});
   LMOE_CHECK_LAUNCH("combine_place");
   const unsigned blocks = static_cast<unsigned>(ceil_div(T, kTokensPerBlock));
   if (vec8_ok(shard_out, routed_out, lat, shard_dtype, out_dtype))

@@ -3,17 +3,23 @@
 // deterministic combine (rows grouped by token in ascending row order).
 //
 // Three launches, no host synchronisation, no atomics in the ordering:
-//   1. hist  : each chunk of kChunk keys builds an LDS histogram of its keys.
-//   2. scan  : one block turns the per-chunk histograms into per-chunk bases
-//              base[c][b] = offset[b] + sum_{c' < c} hist[c'][b], where
-//              offset[b] is the exclusive prefix of the bin totals, and the
-//              kept count of each bin after truncating positions >= limit.
+//   1. hist  : each chunk of CHUNK keys builds an LDS histogram of its keys
+//              and writes it bin-major: hist[b * chunks + c].
+//   2. scan  : one block computes the exclusive prefix sum of hist in that
+//              (bin, chunk) order, which is exactly the first output position
+//              of bin b's keys from chunk c: base[b][c] = offset[b] +
+//              sum_{c' < c} hist[b][c'], offset[b] being the exclusive prefix
+//              of the bin totals.  It also gives the kept count of each bin
+//              after truncating positions >= limit.
 //   3. place : one 64-lane wavefront walks its chunk in order, 64 keys at a
 //              time.  Lanes holding equal keys are found with one ballot per
 //              key bit (match-any); a lane's position is
 //              running[key] + popcount(peers below it), so equal keys keep
 //              their input order (stability) without any sort network.
 // Keys are in [0, nbins]; nbins itself is the sentinel ("not in any bin").
+// CHUNK trades parallelism in hist/place (more chunks) against the size of
+// the scanned array (nbins x chunks): small for few bins (dispatch), large
+// for many (the token-keyed combine).
 #pragma once
 
 #include "lmoe_common.h"
@@ -22,7 +28,6 @@ namespace lmoe {
 namespace csort {
 namespace {  // kernels are instantiated per translation unit
 
-constexpr int kChunk = 1024;
 constexpr int kScanThreads = 1024;
 
 inline int key_bits_for(int nbins) {
@@ -31,99 +36,126 @@ inline int key_bits_for(int nbins) {
   return b;
 }
 
-inline int64_t num_chunks(int64_t n) { return ceil_div(n, kChunk); }
+template <int CHUNK>
+inline int64_t num_chunks(int64_t n) {
+  return ceil_div(n, CHUNK);
+}
 
-template <class KeyFn>
-__global__ __launch_bounds__(256) void hist_kernel(KeyFn key, int64_t n, int nbins,
+template <int CHUNK, class KeyFn>
+__global__ __launch_bounds__(256) void hist_kernel(KeyFn key, int64_t n, int nbins, int64_t chunks,
                                                    int32_t* __restrict__ hist) {
   extern __shared__ int32_t h[];
   const int nbt = nbins + 1;
   for (int i = threadIdx.x; i < nbt; i += blockDim.x) h[i] = 0;
   __syncthreads();
-  const int64_t base = static_cast<int64_t>(blockIdx.x) * kChunk;
-  for (int i = threadIdx.x; i < kChunk; i += blockDim.x) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * CHUNK;
+  for (int i = threadIdx.x; i < CHUNK; i += blockDim.x) {
     const int64_t s = base + i;
     if (s < n) atomicAdd(&h[key(s)], 1);
   }
   __syncthreads();
-  for (int i = threadIdx.x; i < nbins; i += blockDim.x)
-    hist[static_cast<int64_t>(blockIdx.x) * nbins + i] = h[i];
+  for (int i = threadIdx.x; i < nbins; i += blockDim.x) hist[i * chunks + blockIdx.x] = h[i];
 }
 
-// Exclusive scan of one value per thread over a kScanThreads block.
-__device__ __forceinline__ int64_t block_exclusive_scan(int64_t v, int64_t* total) {
-  __shared__ int64_t wsum[kScanThreads / 64];
+// Exclusive scan of one 32-bit value per thread over a kScanThreads block
+// (totals < 2^31); *total receives the block sum.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* total) {
+  __shared__ uint32_t wsum[kScanThreads / 64];
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-  int64_t x = v;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    int64_t y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+  const uint32_t x = wave_scan_sat(v, 0x7fffffffu);
   if (lane == 63) wsum[wave] = x;
   __syncthreads();
   if (wave == 0) {
-    int64_t w = lane < kScanThreads / 64 ? wsum[lane] : 0;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      int64_t y = __shfl_up(w, off, 64);
-      if (lane >= off) w += y;
-    }
-    if (lane < kScanThreads / 64) wsum[lane] = w;
+    const uint32_t w = lane < kScanThreads / 64 ? wsum[lane] : 0u;
+    const uint32_t ws = wave_scan_sat(w, 0x7fffffffu);
+    if (lane < kScanThreads / 64) wsum[lane] = ws;
   }
   __syncthreads();
-  const int64_t wave_prefix = wave > 0 ? wsum[wave - 1] : 0;
+  const uint32_t wave_prefix = wave > 0 ? wsum[wave - 1] : 0u;
   *total = wsum[kScanThreads / 64 - 1];
   __syncthreads();
   return wave_prefix + x - v;
 }
 
-// One block of kScanThreads.  bin_kept[b] = number of keys of bin b whose
-// position is < limit; offsets[b] = first position of bin b; *num_kept = sum.
+// One block of kScanThreads; dynamic LDS (nbins + 1) ints.  Thread t scans the
+// contiguous segment [t * per, (t + 1) * per) of the (bin, chunk) array; up to
+// kHeld elements per thread are loaded once, all in flight together, and
+// kept in registers for the second pass (one memory round trip for the usual
+// sizes; larger arrays loop).  bin_kept[b] = number of keys of bin b whose
+// position is < limit; offsets[b] = first position of bin b (clipped to
+// limit); *num_kept = sum.
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
-    const int32_t* __restrict__ hist, int chunks, int nbins, int64_t limit,
+    const int32_t* __restrict__ hist, int64_t chunks, int nbins, int64_t limit,
     int32_t* __restrict__ base, int32_t* __restrict__ bin_kept, int32_t* __restrict__ offsets,
     int32_t* __restrict__ num_kept) {
-  const int per = (nbins + kScanThreads - 1) / kScanThreads;
-  const int b0 = threadIdx.x * per;
-  int64_t local = 0;
-  for (int b = b0; b < b0 + per && b < nbins; ++b)
-    for (int c = 0; c < chunks; ++c) local += hist[static_cast<int64_t>(c) * nbins + b];
-  int64_t total_all = 0;
-  int64_t off = block_exclusive_scan(local, &total_all);
-  for (int b = b0; b < b0 + per && b < nbins; ++b) {
-    int64_t run = off;
-    for (int c = 0; c < chunks; ++c) {
-      const int64_t i = static_cast<int64_t>(c) * nbins + b;
-      const int32_t hcount = hist[i];
-      base[i] = static_cast<int32_t>(run);
-      run += hcount;
+  extern __shared__ int32_t bin_start[];
+  constexpr int kHeld = 16;
+  const int64_t total_n = chunks * nbins;
+  const int64_t per = (total_n + kScanThreads - 1) / kScanThreads;
+  const int64_t i0 = threadIdx.x * per;
+  const int64_t i1 = i0 + per < total_n ? i0 + per : total_n;
+  int32_t held[kHeld];
+#pragma unroll
+  for (int q = 0; q < kHeld; ++q) held[q] = i0 + q < i1 ? hist[i0 + q] : 0;
+  uint32_t local = 0;
+#pragma unroll
+  for (int q = 0; q < kHeld; ++q) local += static_cast<uint32_t>(held[q]);
+  for (int64_t i = i0 + kHeld; i < i1; ++i) local += static_cast<uint32_t>(hist[i]);
+  uint32_t total = 0;
+  uint32_t run = block_exclusive_scan(local, &total);
+  int64_t bin = i0 / chunks, chunk = i0 % chunks;  // coordinates of element i
+  auto emit = [&](int64_t i, int32_t v) {
+    base[i] = static_cast<int32_t>(run);
+    if (chunk == 0) bin_start[bin] = static_cast<int32_t>(run);
+    run += static_cast<uint32_t>(v);
+    if (++chunk == chunks) {
+      chunk = 0;
+      ++bin;
     }
-    const int64_t tot = run - off;
+  };
+#pragma unroll
+  for (int q = 0; q < kHeld; ++q)
+    if (i0 + q < i1) emit(i0 + q, held[q]);
+  for (int64_t i = i0 + kHeld; i < i1; ++i) emit(i, hist[i]);
+  if (threadIdx.x == 0) bin_start[nbins] = static_cast<int32_t>(total);
+  __syncthreads();
+  for (int b = threadIdx.x; b < nbins; b += kScanThreads) {
+    const int64_t off = bin_start[b], tot = bin_start[b + 1] - off;
     int64_t kept = limit - off;
     kept = kept < 0 ? 0 : (kept > tot ? tot : kept);
     if (bin_kept) bin_kept[b] = static_cast<int32_t>(kept);
     if (offsets) offsets[b] = static_cast<int32_t>(off < limit ? off : limit);
-    off = run;
   }
   if (threadIdx.x == 0) {
-    const int64_t nk = total_all < limit ? total_all : limit;
+    const int64_t nk = static_cast<int64_t>(total) < limit ? static_cast<int64_t>(total) : limit;
     *num_kept = static_cast<int32_t>(nk);
     if (offsets) offsets[nbins] = static_cast<int32_t>(nk);
   }
 }
 
+// Launch the scan with (nbins + 1) ints of dynamic LDS (up to 64 KB, beyond the
+// default dynamic limit once the static wave totals are added).
+inline hipError_t launch_scan(const int32_t* hist, int64_t chunks, int nbins, int64_t limit, int32_t* base,
+                              int32_t* bin_kept, int32_t* offsets, int32_t* num_kept, hipStream_t st) {
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+  if (attr != hipSuccess) return attr;
+  scan_kernel<<<1, kScanThreads, (nbins + 1) * sizeof(int32_t), st>>>(hist, chunks, nbins, limit, base, bin_kept,
+                                                                      offsets, num_kept);
+  return hipSuccess;
+}
+
 // Sink(s, key, pos, real): called for every s < n; pos is meaningful when real.
-template <class KeyFn, class Sink>
-__global__ __launch_bounds__(64) void place_kernel(KeyFn key, int64_t n, int nbins, int key_bits,
+template <int CHUNK, class KeyFn, class Sink>
+__global__ __launch_bounds__(64) void place_kernel(KeyFn key, int64_t n, int nbins, int key_bits, int64_t chunks,
                                                    const int32_t* __restrict__ base, Sink sink) {
   extern __shared__ int32_t run[];
   const int lane = threadIdx.x;
-  for (int i = lane; i < nbins; i += 64) run[i] = base[static_cast<int64_t>(blockIdx.x) * nbins + i];
+  for (int i = lane; i < nbins; i += 64) run[i] = base[i * chunks + blockIdx.x];
   __syncthreads();
-  const int64_t chunk_base = static_cast<int64_t>(blockIdx.x) * kChunk;
+  const int64_t chunk_base = static_cast<int64_t>(blockIdx.x) * CHUNK;
   const uint64_t below = (1ull << lane) - 1ull;
-  for (int it = 0; it < kChunk / 64; ++it) {
+  for (int it = 0; it < CHUNK / 64; ++it) {
     const int64_t s = chunk_base + it * 64 + lane;
     if (chunk_base + it * 64 >= n) break;  // uniform across the wave
     const bool active = s < n;

@@ -82,6 +82,10 @@ __global__ __launch_bounds__(256) void gather_kernel(
   }
 }
 
+// Few bins (local experts): small chunks, many place waves (and a scanned
+// (expert, chunk) array that stays within a few thousand entries).
+constexpr int kDispatchChunk = 512;
+
 struct Workspace {
   int32_t* hist;
   int32_t* base;
@@ -89,7 +93,7 @@ struct Workspace {
 };
 
 int64_t workspace_bytes(int64_t n, int64_t L) {
-  const int64_t chunks = csort::num_chunks(n > 0 ? n : 1);
+  const int64_t chunks = csort::num_chunks<kDispatchChunk>(n > 0 ? n : 1);
   return (2 * chunks * L + 64) * static_cast<int64_t>(sizeof(int32_t));
 }
 
@@ -124,24 +128,23 @@ extern "C" int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, 
                  "dispatch_local: null output");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t n = T * k;
-  const int64_t chunks = csort::num_chunks(n > 0 ? n : 1);
+  const int64_t chunks = csort::num_chunks<kDispatchChunk>(n > 0 ? n : 1);
   int32_t* ws = static_cast<int32_t*>(workspace);
   Workspace w{ws, ws + chunks * L, ws + 2 * chunks * L};
   const int Li = static_cast<int>(L);
   DispatchKey key{topk_idx, static_cast<int>(local_start), Li};
   // With n == 0 the single chunk still writes an all-zero histogram.
-  csort::hist_kernel<<<dim3(static_cast<unsigned>(chunks)), 256, (L + 1) * sizeof(int32_t), st>>>(
-      key, n, Li, w.hist);
+  csort::hist_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 256, (L + 1) * sizeof(int32_t), st>>>(
+      key, n, Li, chunks, w.hist);
   LMOE_CHECK_LAUNCH("dispatch_hist");
-  csort::scan_kernel<<<1, csort::kScanThreads, 0, st>>>(w.hist, static_cast<int>(chunks), Li,
-                                                        m_padded, w.base, group_sizes, nullptr,
-                                                        w.num_kept);
+  if (csort::launch_scan(w.hist, chunks, Li, m_padded, w.base, group_sizes, nullptr, w.num_kept, st) != hipSuccess)
+    return fail(LMOE_ERR_HIP, "dispatch_scan: LDS attribute");
   LMOE_CHECK_LAUNCH("dispatch_scan");
   if (n > 0) {
     DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
                       padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
-    csort::place_kernel<<<dim3(static_cast<unsigned>(chunks)), 64, L * sizeof(int32_t), st>>>(
-        key, n, Li, csort::key_bits_for(Li), w.base, sink);
+    csort::place_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 64, L * sizeof(int32_t), st>>>(
+        key, n, Li, csort::key_bits_for(Li), chunks, w.base, sink);
     LMOE_CHECK_LAUNCH("dispatch_place");
   }
   // The gather also finalises group_sizes[L] and per_expert_counts (block 0),

@@ -77,24 +77,6 @@ __device__ int64_t total_m_tiles(const int32_t* __restrict__ gs, int64_t G, int6
   return tiles + (tail + BM - 1) / BM;
 }
 
-// Saturating add of non-negative 32-bit counts (cap <= 2^31).
-__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b, uint32_t cap) {
-  const uint32_t s = a + b;
-  return s < cap ? s : cap;
-}
-
-// Inclusive wave-wide prefix sum (saturating at cap) with DPP row shifts and
-// row broadcasts: six dependent steps, no LDS traffic.
-__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x, uint32_t cap) {
-  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xf, 0xf, false), cap);  // row_shr:1
-  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xf, 0xf, false), cap);  // row_shr:2
-  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xf, 0xf, false), cap);  // row_shr:4
-  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xf, 0xf, false), cap);  // row_shr:8
-  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xa, 0xf, false), cap);  // row_bcast:15
-  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false), cap);  // row_bcast:31
-  return x;
-}
-
 // Find (group, first row, rows) of m-tile `mt`.  Executed by wave 0.  Lane l
 // holds groups l, l + 64, ...: the group sizes of up to kPre chunks of 64 are
 // loaded before any is scanned, so their latencies overlap; group counts are

@@ -44,12 +44,10 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even f32 -> bf16 (NaN stays a quiet NaN).
+// Round-to-nearest-even f32 -> bf16 with the hardware conversion
+// (v_cvt_pk_bf16_f32; NaN stays a quiet NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
 __device__ __forceinline__ float round_bf16(float f) { return bf16_to_f32(f32_to_bf16(f)); }
@@ -75,5 +73,48 @@ __device__ __forceinline__ void store_from_f32(void* p, int64_t i, float v, int 
 inline int dtype_size(int dtype) { return dtype == LMOE_BF16 ? 2 : 4; }
 
 inline bool valid_dtype(int dtype) { return dtype == LMOE_BF16 || dtype == LMOE_F32; }
+
+// ---- wave-wide (64-lane) primitives on DPP row shifts / row broadcasts ----
+// Each is six dependent DPP steps (no LDS traffic); lanes whose DPP source
+// falls outside the row take the operation's identity.
+
+// Saturating add of non-negative 32-bit counts (cap <= 2^31).
+__device__ __forceinline__ uint32_t sat_add(uint32_t a, uint32_t b, uint32_t cap) {
+  const uint32_t s = a + b;
+  return s < cap ? s : cap;
+}
+
+// Inclusive prefix sum over the wave, saturating at cap.
+__device__ __forceinline__ uint32_t wave_scan_sat(uint32_t x, uint32_t cap) {
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x111, 0xf, 0xf, false), cap);  // row_shr:1
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x112, 0xf, 0xf, false), cap);  // row_shr:2
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x114, 0xf, 0xf, false), cap);  // row_shr:4
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x118, 0xf, 0xf, false), cap);  // row_shr:8
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x142, 0xa, 0xf, false), cap);  // row_bcast:15
+  x = sat_add(x, __builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false), cap);  // row_bcast:31
+  return x;
+}
+
+// Wave-wide maximum / minimum of unsigned 32-bit values (uniform result):
+// an inclusive max (min) scan whose last lane holds the answer.
+__device__ __forceinline__ uint32_t wave_max_u32(uint32_t x) {
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0u, x, 0x111, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0u, x, 0x112, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0u, x, 0x114, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0u, x, 0x118, 0xf, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0u, x, 0x142, 0xa, 0xf, false)));
+  x = max(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(0u, x, 0x143, 0xc, 0xf, false)));
+  return __builtin_amdgcn_readlane(x, 63);
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t x) {
+  constexpr uint32_t kId = 0xffffffffu;
+  x = min(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(kId, x, 0x111, 0xf, 0xf, false)));
+  x = min(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(kId, x, 0x112, 0xf, 0xf, false)));
+  x = min(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(kId, x, 0x114, 0xf, 0xf, false)));
+  x = min(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(kId, x, 0x118, 0xf, 0xf, false)));
+  x = min(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(kId, x, 0x142, 0xa, 0xf, false)));
+  x = min(x, static_cast<uint32_t>(__builtin_amdgcn_update_dpp(kId, x, 0x143, 0xc, 0xf, false)));
+  return __builtin_amdgcn_readlane(x, 63);
+}
 
 }  // namespace lmoe

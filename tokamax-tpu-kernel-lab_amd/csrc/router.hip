@@ -2,10 +2,12 @@
 // step 1, ref.py:347-361): one 64-wide wavefront per token.
 //
 // Each lane owns the experts e = c*64 + lane (c < EPL), so the logits row is read
-// with fully coalesced loads.  Selection is k rounds of a wavefront arg-max over
-// a 64-bit key (order-preserving float bits << 32 | ~expert), which gives
-// "descending value, ties to the lower expert id" -- jax.lax.top_k's order --
-// in one max.  Only the winning lane rescans its EPL candidates per round.
+// with fully coalesced loads.  Selection is k rounds of a wavefront arg-max:
+// a wave maximum of the order-preserving float bits of every lane's best
+// remaining candidate, then a wave minimum of the expert ids holding that
+// value, which gives "descending value, ties to the lower expert id" --
+// jax.lax.top_k's order.  Both reductions are DPP row shifts / broadcasts (no
+// LDS round trips); only the winning lane rescans its EPL candidates.
 #include <cmath>
 
 #include "lmoe_common.h"
@@ -20,17 +22,6 @@ __device__ __forceinline__ uint32_t ordered_bits(float f) {
   if (f == 0.0f) f = 0.0f;  // -0 and +0 compare equal: canonicalise
   uint32_t u = __float_as_uint(f);
   return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    uint32_t lo = __shfl_xor(static_cast<uint32_t>(v), off, kWave);
-    uint32_t hi = __shfl_xor(static_cast<uint32_t>(v >> 32), off, kWave);
-    uint64_t o = (static_cast<uint64_t>(hi) << 32) | lo;
-    v = o > v ? o : v;
-  }
-  return v;
 }
 
 __device__ __forceinline__ float wave_max_f32(float v) {
@@ -95,38 +86,41 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     }
   }
 
-  auto local_best = [&]() -> uint64_t {
-    uint64_t best = 0;
+  // this lane's best remaining candidate: largest key, ties to the lower c
+  uint32_t best_key = 0;
+  int best_c = -1;
+  auto local_best = [&]() {
+    best_key = 0;
+    best_c = -1;
 #pragma unroll
     for (int c = 0; c < EPL; ++c) {
-      if (!((taken >> c) & 1ull)) {
-        const uint32_t e = static_cast<uint32_t>(c * kWave + lane);
-        const uint64_t cand = (static_cast<uint64_t>(key[c]) << 32) | static_cast<uint32_t>(~e);
-        best = cand > best ? cand : best;
+      if (!((taken >> c) & 1ull) && (best_c < 0 || key[c] > best_key)) {
+        best_key = key[c];
+        best_c = c;
       }
     }
-    return best;
   };
 
-  uint64_t mine = local_best();
+  local_best();
   int my_idx = 0;
   float my_w = 0.0f;
   float sum = 0.0f;
   for (int j = 0; j < k; ++j) {
-    const uint64_t win = wave_max_u64(mine);
-    const int e = static_cast<int>(~static_cast<uint32_t>(win));
-    const int wl = e % kWave;
-    const int wc = e / kWave;
+    const uint32_t m = wave_max_u32(best_c >= 0 ? best_key : 0u);
+    const uint32_t cand = (best_c >= 0 && best_key == m) ? static_cast<uint32_t>(best_c * kWave + lane) : 0xffffffffu;
+    const uint32_t e = wave_min_u32(cand);  // k <= E, so some lane holds a candidate
+    const int wl = static_cast<int>(e % kWave);
+    const int wc = static_cast<int>(e / kWave);
     float v = 0.0f;
 #pragma unroll
     for (int c = 0; c < EPL; ++c) v = (c == wc) ? s[c] : v;
-    const float w = __shfl(v, wl, kWave);
+    const float w = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), wl));
     if (lane == wl) {
       taken |= 1ull << wc;
-      mine = local_best();
+      local_best();
     }
     if (lane == j) {
-      my_idx = e;
+      my_idx = static_cast<int>(e);
       my_w = w;
     }
     sum = __fadd_rn(sum, w);

@@ -13,6 +13,7 @@ stream; nothing falls back to torch or the CPU.
 from __future__ import annotations
 
 import math
+import os
 from typing import NamedTuple
 
 import torch
@@ -367,10 +368,47 @@ def _ones_group(m: int, device) -> torch.Tensor:
   return t
 
 
+_DENSE_BACKENDS = ("auto", "hip", "blaslt")
+
+
+def _dense_backend_default() -> str:
+  b = os.environ.get("LMOE_DENSE", "auto")
+  if b not in _DENSE_BACKENDS:
+    raise ValueError(f"LMOE_DENSE={b!r}: one of {_DENSE_BACKENDS}")
+  return b
+
+
 def dense(x: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None,
-          w_layout: str = "kn") -> torch.Tensor:
-  """x @ w as a one-group grouped GEMM on the same kernels (w (K, N), or
-  (N, K) with w_layout="nk")."""
+          w_layout: str = "kn", backend: str | None = None) -> torch.Tensor:
+  """x @ w (w (K, N), or (N, K) with w_layout="nk").
+
+  ``backend``: "hip" runs it as a one-group grouped GEMM on the hand-written
+  kernels; "blaslt" calls hipBLASLt (the ROCm library GEMM; (N, K) weights
+  only); "auto" (default, or $LMOE_DENSE) uses hipBLASLt for bf16 (N, K)
+  weights -- the layer's router-logits (f32 out), down- and up-projections --
+  and the hand-written kernels otherwise.  Both accumulate the exact bf16
+  products in f32; only the summation order differs."""
+  backend = backend or _dense_backend_default()
+  if backend not in _DENSE_BACKENDS:
+    raise ValueError(f"backend {backend!r}")
+  out_dtype = out_dtype or x.dtype
+  use_blaslt = backend == "blaslt" or (backend == "auto" and w_layout == "nk" and x.dtype == torch.bfloat16
+                                       and w.dtype == torch.bfloat16)
+  if use_blaslt:
+    if w_layout != "nk":
+      raise NotImplementedError("the hipBLASLt backend takes (N, K) weights")
+    _dev(x, w)
+    if x.dim() != 2 or w.dim() != 2 or w.shape[1] != x.shape[1]:
+      raise ValueError(f"dense: x {tuple(x.shape)} / w {tuple(w.shape)}")
+    if w.dtype != x.dtype:
+      raise NotImplementedError(f"mixed x {x.dtype} / w {w.dtype}")
+    x, w = x.contiguous(), w.contiguous()
+    m, k = x.shape
+    n = w.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    check(lib().lmoe_dense_blaslt(_p(x), _dt(x), _p(w), _dt(w), m, k, n, _p(out), _dt(out), _stream()),
+          "dense_blaslt")
+    return out
   rhs = w.unsqueeze(0)
   return ragged_dot(x, rhs, _ones_group(x.shape[0], x.device), preferred_element_type=out_dtype,
                     rhs_layout="gkn" if w_layout == "kn" else "gnk")
