@@ -144,7 +144,7 @@ def main():
   for _ in range(args.warmup):
     layer.forward(hidden)
   torch.cuda.synchronize()
-  events = [{"gateup": (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))}
+  events = [{k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for k in ("gateup", "down")}
             for _ in range(args.steps)]
   t0 = time.perf_counter()
   for i in range(args.steps):
@@ -153,8 +153,9 @@ def main():
   t1 = time.perf_counter()
   ms_per_step = (t1 - t0) * 1000.0 / args.steps
   gateup_ms = statistics.mean(e["gateup"][0].elapsed_time(e["gateup"][1]) for e in events)
+  down_ms = statistics.mean(e["down"][0].elapsed_time(e["down"][1]) for e in events)
   tokens_per_s = c.tokens / (ms_per_step / 1000.0)
-  log(f"{ms_per_step:.3f} ms/step, gate/up kernel {gateup_ms * 1000:.1f} us")
+  log(f"{ms_per_step:.3f} ms/step, gate/up kernel {gateup_ms * 1000:.1f} us, down kernel {down_ms * 1000:.1f} us")
 
   achieved = nbytes / (gateup_ms / 1000.0) / 1e9
   tflops = flops / (gateup_ms / 1000.0) / 1e12

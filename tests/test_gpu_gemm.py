@@ -254,6 +254,38 @@ def test_ragged_dot_mxfp4_tiled_weights(gpu_device, m, k, n, g, situ, zg):
   assert torch.equal(out, chk)
 
 
+@pytest.mark.parametrize("situ", [False, True])
+def test_ragged_dot_mxfp4_tiled_many_tiles(gpu_device, situ):
+  """Several tiles per persistent block (the streamed kernel prefetches each
+  next tile's first K steps during the current one): skewed group sizes with
+  empty and one-row groups, a zero-group padding bucket between real groups'
+  tiles and at the end, and partial last tiles of every size."""
+  from lmoe import ops
+  rng = np.random.default_rng(31 + situ)
+  m, k, n, g = 12000, 256, 2048, 41
+  w = 1.0 / np.arange(1, g + 1) ** 1.1
+  gs = rng.multinomial(m - 3000 - 123, w / w.sum()).astype(np.int32)
+  gs[[3, 17]] = 0
+  gs[5] = 1
+  zg = 20
+  gs[zg] = 3000  # padding bucket in the middle of the groups
+  lhs = O.bf16_round(rng.standard_normal((m, k)))
+  start = int(gs[:zg].sum())
+  lhs[start:start + gs[zg]] = 0.0
+  packed, scale = _mx_weights(rng, g, n, k)
+  epi = (4.0, 25.0) if situ else None
+  banner(f"mxfp4 tiled many tiles situ={situ}")
+  ref = O.ragged_dot_mxfp4(lhs, packed, scale, gs, "bf16", epi)
+  fa = "situ:4.0:25.0" if situ else None
+  tpk, tsc = ops.mxfp4_tile_weights(to_dev(packed), to_dev(scale))
+  out = to_np(ops.ragged_dot_mxfp4(to_dev(lhs, "bf16"), tpk, tsc, to_dev(gs), fuse_gateup_activation=fa,
+                                   zero_group=zg, weight_layout="tiled"))
+  assert out.shape == ref.shape
+  assert max_rel(out, ref) <= BF16_TOL
+  assert np.all(out[start:start + gs[zg]] == 0)
+  assert np.all(out[int(gs.sum()):] == 0)
+
+
 def test_mxfp4_tiled_edge_scales(gpu_device):
   """Scale bytes 0..2 (denormal products) and 253..255 (overflow to inf) take
   the exact per-byte conversion: NaN-aware bit equality with the

@@ -13,6 +13,7 @@
 // on first use and kept until the process ends.
 #include <hipblaslt/hipblaslt.h>
 
+#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -69,19 +70,25 @@ int get_plan(const Key& key, hipblasLtHandle_t* handle, const Plan** plan) {
   const uint64_t no_ws = 0;
   ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_ws,
                                                    sizeof(no_ws)) == HIPBLAS_STATUS_SUCCESS;
-  hipblasLtMatmulHeuristicResult_t res{};
+  // LMOE_BLASLT_ALGO=i takes the i-th of the heuristic's candidates instead
+  // of its first (tuning sweeps); an index past the list falls back to 0.
+  constexpr int kMaxAlgos = 16;
+  hipblasLtMatmulHeuristicResult_t res[kMaxAlgos] = {};
   int found = 0;
-  ok = ok && hipblasLtMatmulAlgoGetHeuristic(*handle, p.desc, p.a, p.b, p.d, p.d, pref, 1, &res, &found) ==
+  ok = ok && hipblasLtMatmulAlgoGetHeuristic(*handle, p.desc, p.a, p.b, p.d, p.d, pref, kMaxAlgos, res, &found) ==
                  HIPBLAS_STATUS_SUCCESS;
   if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-  if (!ok || found < 1 || res.state != HIPBLAS_STATUS_SUCCESS) {
+  int pick = 0;
+  if (const char* e = std::getenv("LMOE_BLASLT_ALGO")) pick = std::atoi(e);
+  if (pick < 0 || pick >= found || res[pick].state != HIPBLAS_STATUS_SUCCESS) pick = 0;
+  if (!ok || found < 1 || res[pick].state != HIPBLAS_STATUS_SUCCESS) {
     if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
     for (auto l : {p.a, p.b, p.d})
       if (l) hipblasLtMatrixLayoutDestroy(l);
     return fail(LMOE_ERR_UNSUPPORTED, "dense_blaslt: no hipBLASLt algorithm for M=%lld N=%lld K=%lld",
                 (long long)M, (long long)N, (long long)K);
   }
-  p.algo = res.algo;
+  p.algo = res[pick].algo;
   *plan = &g_plans.emplace(key, p).first->second;
   return LMOE_OK;
 }

@@ -31,6 +31,7 @@
 // re-tiled once by lmoe_mxfp4_tile into k-step-major order: packed
 // (G, K/64, N, 32) and scales (G, K/64, N, 2), so that one step's weights for
 // a run of columns are one contiguous stretch of memory.  K % 64 == 0.
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -131,10 +132,10 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
   __shared__ TileInfo s_tile;
   __shared__ int64_t s_nt;
 
-  // total m-tiles, used by wave 0 to map virtual tiles when m-tile groups go
-  // round-robin over the XCDs (gm > 0); with n-tiles striped (gm == 0)
-  // locate_tile itself returns "no work" past the last tile
-  const int64_t tm = (gm > 0 && threadIdx.x < 64) ? total_m_tiles<BM>(p.group_sizes, p.G, p.M) : INT64_MAX;
+  // total m-tiles, used by wave 0 to map virtual tiles when m-tiles are
+  // spread over the XCDs by group or range (gm != 0); with n-tiles striped
+  // (gm == 0) locate_tile itself returns "no work" past the last tile
+  const int64_t tm = (gm != 0 && threadIdx.x < 64) ? total_m_tiles<BM>(p.group_sizes, p.G, p.M) : INT64_MAX;
   // Persistent blocks: block b takes virtual tiles b, b + gridDim.x, ... (the
   // grid is a multiple of the XCD count, so a virtual tile keeps its XCD).
   for (int64_t vb = blockIdx.x; vb < n_virtual; vb += gridDim.x) {
@@ -460,68 +461,489 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
   // Epilogue.  A lane holds output row (lane % MF) of row sub-tile i and, for
   // each q < MF / 8 (q < 1 for MF == 16), the four adjacent columns
   // q*8 + 4*(lane/MF) .. +3 (MF == 32) or 4*(lane/16) .. +3 (MF == 16) of
-  // column sub-tile j, accumulator elements 4q .. 4q+3: one 8-byte (bf16) or
-  // 16-byte (f32) store per run.  Column counts are multiples of 8 (checked
-  // on the host), so a run of four is in or out as a whole.
+  // column sub-tile j, accumulator elements 4q .. 4q+3.  Column counts are
+  // multiples of 8 (checked on the host), so a run of four is in or out as a
+  // whole.
+  //
+  // bf16 output (always with SiTU) is staged through LDS: each lane writes
+  // its 8-byte runs into a row-major copy of the output tile (rows padded by
+  // 16 bytes, which spreads the 32 rows of one write over all banks), then the
+  // block writes whole rows with consecutive 16-byte stores.  Written
+  // directly, every store instruction would touch 32 rows with 16 bytes each,
+  // which costs the address unit one cycle per row and HBM a 32-byte write
+  // per 16 bytes.  f32 output (16-byte runs) is stored directly.
   constexpr int kRuns = MF == 32 ? 4 : 1;
+  constexpr int kOutCols = EPI == kEpiSitu ? BN / 2 : BN;  // output columns of a tile
+  constexpr int kOutTN = EPI == kEpiSitu ? C::kTN / 2 : C::kTN;  // output sub-tiles of a wave
+  constexpr int kStageRow = kOutCols * 2 + 16;              // bytes per staged row
+  constexpr bool kCanStage = BM * kStageRow <= NS * C::kSlot;
   const int r_in = lane % MF;
   auto c_run = [&](int q) { return MF == 32 ? q * 8 + 4 * (lane / 32) : 4 * (lane / 16); };
-  if constexpr (EPI == kEpiSitu) {
-    const int64_t I = N / 2;
-    constexpr int half = C::kTN / 2;
-    const SituConsts sc = situ_consts(p.beta, p.beta_lin);
+  const int64_t n_out = EPI == kEpiSitu ? N / 2 : N;
+  const int64_t col0 = nt * kOutCols;  // first output column of the tile
+  // bf16 values of run q of output sub-tile j of row sub-tile i
+  auto bf16_run = [&](int i, int j, int q) __attribute__((always_inline)) {
+    float v[4];
+    if constexpr (EPI == kEpiSitu) {
+      const SituConsts sc = situ_consts(p.beta, p.beta_lin);
 #pragma unroll
-    for (int i = 0; i < C::kTM; ++i) {
-      const int row = wm * C::kWTM + i * MF + r_in;
-      if (row >= tile.rows) continue;
-      uint16_t* orow = static_cast<uint16_t*>(p.out) + (tile.row0 + row) * I;
-#pragma unroll
-      for (int j = 0; j < half; ++j)
-#pragma unroll
-        for (int q = 0; q < kRuns; ++q) {
-          const int64_t col = nt * (BN / 2) + wn * half * MF + j * MF + c_run(q);
-          if (col >= I) continue;
-          uint2 packed{0u, 0u};  // padding bucket: zeros (SiTU(0, 0) == 0)
-          if (!tile.zero) {
-            float v[4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              float gv = acc[i][j][q * 4 + r], uv = acc[i][j + half][q * 4 + r];
-              if (p.round_before_act) {
-                gv = static_cast<float>(static_cast<__bf16>(gv));
-                uv = static_cast<float>(static_cast<__bf16>(uv));
-              }
-              v[r] = situ_epi(gv, uv, sc);
-            }
-            packed = uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-          }
-          *reinterpret_cast<uint2*>(orow + col) = packed;
+      for (int r = 0; r < 4; ++r) {
+        float gv = acc[i][j][q * 4 + r], uv = acc[i][j + kOutTN][q * 4 + r];
+        if (p.round_before_act) {
+          gv = static_cast<float>(static_cast<__bf16>(gv));
+          uv = static_cast<float>(static_cast<__bf16>(uv));
         }
+        v[r] = situ_epi(gv, uv, sc);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = acc[i][j][q * 4 + r];
+    }
+    return uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+  };
+  if (kCanStage && (EPI == kEpiSitu || p.out_dtype != LMOE_F32)) {
+    __syncthreads();  // every wave is done with the K loop's LDS slots
+    if (!tile.zero) {
+#pragma unroll
+      for (int i = 0; i < C::kTM; ++i) {
+        // rows past the tile are staged too (never stored)
+        uint8_t* srow = smem + (wm * C::kWTM + i * MF + r_in) * kStageRow;
+#pragma unroll
+        for (int j = 0; j < kOutTN; ++j)
+#pragma unroll
+          for (int q = 0; q < kRuns; ++q)
+            *reinterpret_cast<uint2*>(srow + (wn * kOutTN * MF + j * MF + c_run(q)) * 2) = bf16_run(i, j, q);
+      }
+    }
+    __syncthreads();
+    constexpr int kChunks = kOutCols / 8;  // 16-byte chunks per output row
+    static_assert(BM * kChunks % C::kThreads == 0, "staged store split");
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+#pragma unroll
+    for (int v = 0; v < BM * kChunks / C::kThreads; ++v) {
+      const int idx = tid + C::kThreads * v;
+      const int row = idx / kChunks, ch = idx % kChunks;
+      if (row >= tile.rows || col0 + ch * 8 >= n_out) continue;
+      // padding bucket: zeros (SiTU(0, 0) == 0)
+      const uint4 val = tile.zero ? uint4{0u, 0u, 0u, 0u}
+                                  : *reinterpret_cast<const uint4*>(smem + row * kStageRow + ch * 16);
+      *reinterpret_cast<uint4*>(out + (tile.row0 + row) * n_out + col0 + ch * 8) = val;
     }
   } else {
 #pragma unroll
     for (int i = 0; i < C::kTM; ++i) {
       const int row = wm * C::kWTM + i * MF + r_in;
       if (row >= tile.rows) continue;
-      const int64_t obase = (tile.row0 + row) * N;
+      const int64_t obase = (tile.row0 + row) * n_out;
 #pragma unroll
-      for (int j = 0; j < C::kTN; ++j)
+      for (int j = 0; j < kOutTN; ++j)
 #pragma unroll
         for (int q = 0; q < kRuns; ++q) {
-          const int64_t col = nt * BN + wn * C::kTN * MF + j * MF + c_run(q);
-          if (col >= N) continue;
-          const float a0 = acc[i][j][q * 4], a1 = acc[i][j][q * 4 + 1], a2 = acc[i][j][q * 4 + 2],
-                      a3 = acc[i][j][q * 4 + 3];
-          if (p.out_dtype == LMOE_F32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + col) = float4{a0, a1, a2, a3};
+          const int64_t col = col0 + wn * kOutTN * MF + j * MF + c_run(q);
+          if (col >= n_out) continue;
+          if (EPI != kEpiSitu && p.out_dtype == LMOE_F32) {
+            *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + col) =
+                float4{acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]};
           } else {
             *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + obase + col) =
-                uint2{pack_bf16x2(a0, a1), pack_bf16x2(a2, a3)};
+                tile.zero ? uint2{0u, 0u} : bf16_run(i, j, q);
           }
         }
     }
   }
   }  // persistent tile loop
+}
+
+// ---------------------------------------------------------------------------
+// Streamed persistent variant (MXFP4 weights, bf16 output).
+//
+// Each block builds the tile table in LDS once and then loops over its tiles
+// (virtual tiles blockIdx.x, + gridDim.x, ...).  Every wave looks its tiles up
+// itself, and the DMA ring runs as one stream across tiles: during the last
+// NS-1 K steps of a tile the refills fetch the first NS-1 steps of the next
+// tile, so the next tile's operands land while this one finishes its MFMAs
+// and its epilogue.  The epilogue stages the output through the ring slot of
+// the tile's last K step (free once every wave has read that step) in rounds
+// of kStageRows rows; the other slots keep receiving the next tile's steps.
+//
+// Wait accounting: at step k of a tile, the vector memory operations issued
+// after step k's DMA are (a) the later DMA steps already issued, NS-2 of them
+// or fewer near the end of a tile with nothing to prefetch, and, in a tile
+// whose first NS-1 steps were prefetched, for k <= NS-2, (b) the previous
+// tile's epilogue stores, issued after those prefetched steps.  Every lane
+// issues the same number of stores per round (out-of-range rows and columns
+// store a valid neighbour's value again), so (b) is a wave-uniform count.
+// Vector memory operations complete in issue order (one vmcnt counter), so
+// s_waitcnt vmcnt(a + b) waits for exactly step k.
+// ---------------------------------------------------------------------------
+template <int BM, int BN, int EPI, int NS, int MF>
+struct SCfg {
+  using C = DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF, false>;
+  static constexpr int kOutCols = EPI == kEpiSitu ? BN / 2 : BN;  // bf16 output columns of a tile
+  static constexpr int kChunks = kOutCols / 8;                     // 16-byte chunks per output row
+  // staged rows: 8 bytes of padding put row r's dword 0 in bank 2r (mod 64),
+  // so the 32 rows of one half-wave's 8-byte writes hit every bank once
+  static constexpr int kStageRow = kOutCols * 2 + 8;
+  static constexpr int kStageRows0 = (C::kSlot / kStageRow) / MF * MF;
+  static constexpr int kStageRows = kStageRows0 < BM ? kStageRows0 : BM;
+  static constexpr int kRounds = BM / kStageRows;
+  static constexpr int kStoresPerRound = kStageRows * kChunks / C::kThreads;  // per wave
+  static_assert(kStageRows >= MF && BM % kStageRows == 0, "staging rounds");
+  static_assert(kStageRows * kChunks % C::kThreads == 0, "staged store split");
+  static_assert((NS - 2) * C::kOps0 + kRounds * kStoresPerRound < 64, "vmcnt range");
+};
+
+// s_waitcnt vmcnt(a * OPS + r * SPR) lgkmcnt(0) for runtime a in [0, NS-2]
+// and r in [0, R] (wave-uniform).
+template <int NS, int OPS, int SPR, int R>
+__device__ __forceinline__ void wait_stream(int a, int r) {
+  static_for<NS - 1>([&](auto ac) __attribute__((always_inline)) {
+    constexpr int A = decltype(ac)::value;
+    if (a == A) {
+      static_for<R + 1>([&](auto rc) __attribute__((always_inline)) {
+        constexpr int Rr = decltype(rc)::value;
+        if (r == Rr) wait_vm_lgkm<A * OPS + Rr * SPR>();
+        return true;
+      });
+    }
+    return true;
+  });
+}
+
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
+
+template <int BM, int BN, int EPI, int NS, int MF>
+__global__ __launch_bounds__((DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF, false>::kThreads))
+__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF, false>::kWavesPerEu)))
+void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtual) {
+  using S = SCfg<BM, BN, EPI, NS, MF>;
+  using C = typename S::C;
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  __shared__ uint32_t s_wsum[2 * C::kWaves];
+  const int G = static_cast<int>(p.G);
+  uint32_t* tt = reinterpret_cast<uint32_t*>(smem + NS * C::kSlot);
+  uint32_t* tr = tt + (G + 1);
+  build_tile_table<BM, C::kThreads>(p.group_sizes, G, static_cast<uint32_t>(p.M), tt, tr, s_wsum);
+  const int64_t K = p.K, N = p.N;
+  const int64_t nk = K / kSK;
+  const int64_t n_out = EPI == kEpiSitu ? N / 2 : N;
+  const int64_t rows_tail = p.M - static_cast<int64_t>(tr[G]);
+  const int64_t tm = static_cast<int64_t>(tt[G]) + (rows_tail + BM - 1) / BM;
+
+  // wave-uniform tile lookup (lane from the per-tile opaque thread index, so
+  // that no lane-dependent LDS address is hoisted out of the tile loop and
+  // held across the K loop)
+  auto sched = [&](int64_t vb, int64_t& nt, int lane) __attribute__((always_inline)) {
+    TileInfo t = schedule_tile_with(n_tiles, gm, vb, tm, nt, [&](int64_t mt) {
+      return locate_tile_lds<BM>(tt, tr, G, p.M, p.zero_group, mt, lane);
+    });
+    t.group = __builtin_amdgcn_readfirstlane(t.group);
+    t.rows = __builtin_amdgcn_readfirstlane(t.rows);
+    t.zero = __builtin_amdgcn_readfirstlane(static_cast<int>(t.zero)) != 0;
+    t.row0 = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t.row0))) |
+             (static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(t.row0 >> 32))) << 32);
+    nt = static_cast<int64_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(nt)));
+    return t;
+  };
+
+  // DMA addressing of one tile: wave-uniform bases, 32-bit per-lane offsets
+  // (the same layout as grouped_gemm_dma_kernel).
+  struct Addr {
+    const uint8_t* a_base;
+    const uint8_t* b_base;
+    const uint8_t* s_base;
+    uint32_t a_off[C::kAOps];
+    uint32_t b_off[C::kBOps];
+    uint32_t s_off;
+  };
+  auto make_addr = [&](const TileInfo& t, int64_t nt, int tid) __attribute__((always_inline)) {
+    Addr d;
+    d.a_base = uniform_ptr(p.lhs + t.row0 * K);
+#pragma unroll
+    for (int v = 0; v < C::kAOps; ++v) {
+      const int q = tid + C::kThreads * v;
+      const int row = q / 8, kc = (q % 8) ^ swz8(row);
+      const int rr = row < t.rows ? row : 0;
+      d.a_off[v] = static_cast<uint32_t>(rr * K * 2 + kc * 16);
+    }
+    d.b_base = uniform_ptr(static_cast<const uint8_t*>(p.rhs) + t.group * N * (K / 2));
+#pragma unroll
+    for (int u = 0; u < C::kBOps; ++u) {
+      const int q = tid + C::kThreads * u;
+      d.b_off[u] = static_cast<uint32_t>(drhs_col<BN, EPI>(nt, q / 2, N) * 32 + (q % 2) * 16);
+    }
+    const int c0 = (tid % 64 % C::kSLanes) * 8;
+    int64_t n0;
+    if constexpr (EPI == kEpiSitu) {
+      const int64_t I = N / 2;
+      int64_t j0 = nt * (BN / 2) + (c0 % (BN / 2));
+      j0 = j0 <= I - 8 ? j0 : I - 8;
+      n0 = c0 < BN / 2 ? j0 : I + j0;
+    } else {
+      n0 = nt * BN + c0;
+      n0 = n0 <= N - 8 ? n0 : N - 8;
+    }
+    d.s_base = uniform_ptr(p.scale + t.group * (K / 64) * N * 2);
+    d.s_off = static_cast<uint32_t>(n0 * 2);
+    return d;
+  };
+
+  int64_t vb = blockIdx.x;
+  int64_t nt = 0;
+  TileInfo cur = vb < n_virtual ? sched(vb, nt, static_cast<int>(threadIdx.x % 64)) : TileInfo{-1, 0, 0, false};
+  bool cur_pf = false;  // cur's first NS-1 steps were issued during the previous tile
+  int prev_rounds = 0;  // store rounds of the previous tile's epilogue
+  int slot0 = 0;        // ring slot of cur's step 0
+  while (vb < n_virtual) {
+    int tid;
+    asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(static_cast<int>(threadIdx.x)));
+    const int lane = tid % 64, wave = tid / 64;
+    const int wn = wave;  // WM == 1
+
+    const int64_t vb_n = vb + gridDim.x;
+    int64_t nt_n = 0;
+    const TileInfo nxt = vb_n < n_virtual ? sched(vb_n, nt_n, lane) : TileInfo{-1, 0, 0, false};
+    const bool pf = cur.group >= 0 && !cur.zero && nxt.group >= 0 && !nxt.zero && nk >= NS - 1;
+    const int rounds = cur.group < 0 || cur.zero ? 0 : (cur.rows + S::kStageRows - 1) / S::kStageRows;
+
+    typename C::Acc acc[C::kTM][C::kTN];
+#pragma unroll
+    for (int i = 0; i < C::kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::kTN; ++j)
+#pragma unroll
+        for (int e = 0; e < C::kAccN; ++e) acc[i][j][e] = 0.f;
+
+    const int r_in = lane % MF;
+    auto c_run = [&](int q) { return MF == 32 ? q * 8 + 4 * (lane / 32) : 4 * (lane / 16); };
+    constexpr int kRuns = MF == 32 ? 4 : 1;
+    constexpr int kOutTN = EPI == kEpiSitu ? C::kTN / 2 : C::kTN;
+    const int64_t col0 = nt * S::kOutCols;
+    uint16_t* out = static_cast<uint16_t*>(p.out);
+
+    if (cur.group < 0) {
+      // no work (virtual tiles past the last m-tile)
+    } else if (!cur.zero) {
+      const Addr ca = make_addr(cur, nt, tid);
+      const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_offset(smem) + wave * 64 * 16);
+      auto issue = [&](const Addr& d, int64_t step, int slot) __attribute__((always_inline)) {
+        const uint32_t base = lds_wave + slot * C::kSlot;
+#pragma unroll
+        for (int v = 0; v < C::kAOps; ++v) dma16s(d.a_off[v], d.a_base + step * (kSK * 2), base + v * C::kThreads * 16);
+#pragma unroll
+        for (int u = 0; u < C::kBOps; ++u)
+          dma16s(d.b_off[u], d.b_base + step * (N * 32), base + C::kABytes + u * C::kThreads * 16);
+        if (wave == 0) {
+          const uint32_t sbase = base + C::kABytes + C::kBBytes;
+          if (lane < C::kSLanes) dma16s(d.s_off, d.s_base + step * (N * 2), sbase);
+        }
+      };
+      if (!cur_pf) {
+        for (int64_t s = 0; s < NS - 1 && s < nk; ++s) issue(ca, s, static_cast<int>((slot0 + s) % NS));
+      }
+      const int tm_eff = __builtin_amdgcn_readfirstlane((cur.rows + MF - 1) / MF);
+      auto mfma = [](const bf16x8_t& w, const bf16x8_t& x, const typename C::Acc& c) __attribute__((always_inline)) {
+        if constexpr (MF == 32)
+          return __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, x, c, 0, 0, 0);
+        else
+          return __builtin_amdgcn_mfma_f32_16x16x32_bf16(w, x, c, 0, 0, 0);
+      };
+      const int f_rc = lane % MF, f_kc = lane / MF;
+      struct Frags {
+        bf16x8_t af[C::kKS][C::kTM];
+        uint32_t bw[C::kKS][C::kTN];
+        uint32_t s2[C::kTN];
+      };
+      auto read_frags = [&](int slot, Frags& f) __attribute__((always_inline)) {
+        const uint8_t* as = smem + slot * C::kSlot;
+        const uint8_t* bs = as + C::kABytes;
+        const uint8_t* ss = bs + C::kBBytes;
+#pragma unroll
+        for (int j = 0; j < C::kTN; ++j) {
+          const int c = dlds_col<BN, C::kTN, EPI, MF>(wn, j) + f_rc;
+          f.s2[j] = *reinterpret_cast<const uint16_t*>(ss + c * 2);
+        }
+#pragma unroll
+        for (int kk = 0; kk < C::kKS; ++kk) {
+          const int kc = kk * (64 / MF) + f_kc;
+#pragma unroll
+          for (int j = 0; j < C::kTN; ++j) {
+            const int c = dlds_col<BN, C::kTN, EPI, MF>(wn, j) + f_rc;
+            if constexpr (MF == 32) {
+              if (kk == 0) {
+                const uint4 w = *reinterpret_cast<const uint4*>(bs + c * 32 + f_kc * 16);
+                f.bw[0][j] = w.x;
+                f.bw[1][j] = w.y;
+                f.bw[2][j] = w.z;
+                f.bw[3][j] = w.w;
+              }
+            } else {
+              f.bw[kk][j] = *reinterpret_cast<const uint32_t*>(bs + c * 32 + mx_dword_pos(kc) * 4);
+            }
+          }
+#pragma unroll
+          for (int i = 0; i < C::kTM; ++i) {
+            const int r = i * MF + f_rc;
+            f.af[kk][i] = *reinterpret_cast<const bf16x8_t*>(as + r * 128 + ((kc ^ swz8(r)) * 16));
+          }
+        }
+      };
+      // Conversions and MFMAs of one step: every weight fragment converted
+      // with v_cvt_scalef32_pk_bf16_fp4, rewritten by the exact per-byte
+      // conversion behind one wave-uniform branch when some lane holds a
+      // scale byte outside 3..252, then the MFMAs.
+      auto compute = [&](const Frags& f, auto full_tag) __attribute__((always_inline)) {
+        constexpr bool kFull = decltype(full_tag)::value;
+        bool edge_lane = false;
+#pragma unroll
+        for (int j = 0; j < C::kTN; ++j) edge_lane |= !hw_scale_ok(f.s2[j] & 0xffu) || !hw_scale_ok(f.s2[j] >> 8);
+        const bool edge = __builtin_amdgcn_ballot_w64(edge_lane) != 0;
+        uint32_t bq[C::kKS][C::kTN][4];
+#pragma unroll
+        for (int kk = 0; kk < C::kKS; ++kk)
+#pragma unroll
+          for (int j = 0; j < C::kTN; ++j) {
+            const uint32_t w = f.bw[kk][j];
+            const uint32_t sb = (f.s2[j] >> (8 * (kk / (C::kKS / 2)))) & 0xffu;  // 32-k scale block of sub-step kk
+            const float sc = __uint_as_float(sb << 23);
+            bq[kk][j][0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
+            bq[kk][j][1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
+            bq[kk][j][2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
+            bq[kk][j][3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
+          }
+        if (__builtin_expect(edge, false)) {
+#pragma unroll
+          for (int kk = 0; kk < C::kKS; ++kk)
+#pragma unroll
+            for (int j = 0; j < C::kTN; ++j) {
+              const uint32_t w = f.bw[kk][j];
+              const uint32_t sb = (f.s2[j] >> (8 * (kk / (C::kKS / 2)))) & 0xffu;
+#pragma unroll
+              for (int b = 0; b < 4; ++b) bq[kk][j][b] = dequant_byte((w >> (8 * b)) & 0xffu, sb);
+            }
+        }
+#pragma unroll
+        for (int kk = 0; kk < C::kKS; ++kk)
+#pragma unroll
+          for (int j = 0; j < C::kTN; ++j) {
+            const bf16x8_t bfr =
+                __builtin_bit_cast(bf16x8_t, uint4{bq[kk][j][0], bq[kk][j][1], bq[kk][j][2], bq[kk][j][3]});
+#pragma unroll
+            for (int i = 0; i < C::kTM; ++i) {
+              if (!kFull && i >= tm_eff) break;
+              acc[i][j] = mfma(bfr, f.af[kk][i], acc[i][j]);
+            }
+          }
+      };
+      auto k_loop = [&](auto full_tag) __attribute__((always_inline)) {
+        int slot = slot0;  // slot of step kt
+        for (int64_t kt = 0; kt < nk; ++kt) {
+          // wait for step kt: (a) later DMA steps issued, (b) prefetched
+          // tiles' first steps are older than the previous epilogue's stores
+          const int64_t left = nk - 1 - kt;
+          const int a = pf || left >= NS - 2 ? NS - 2 : static_cast<int>(left);
+          const int b = (cur_pf && kt <= NS - 2) ? prev_rounds : 0;
+          if (__builtin_expect(a == NS - 2 && b == 0, 1)) {  // steady state: one test
+            if (wave == 0)
+              wait_vm_lgkm<(NS - 2) * C::kOps0>();
+            else
+              wait_vm_lgkm<(NS - 2) * C::kOps>();
+          } else if (wave == 0) {
+            wait_stream<NS, C::kOps0, S::kStoresPerRound, S::kRounds>(a, b);
+          } else {
+            wait_stream<NS, C::kOps, S::kStoresPerRound, S::kRounds>(a, b);
+          }
+          barrier();
+          // refill the slot of step kt-1: this tile's step kt+NS-1, or the
+          // next tile's step kt+NS-1-nk
+          const int wslot = slot == 0 ? NS - 1 : slot - 1;
+          const int64_t s = kt + NS - 1;
+          if (s < nk)
+            issue(ca, s, wslot);
+          else if (pf)
+            issue(make_addr(nxt, nt_n, tid), s - nk, wslot);
+          Frags f;
+          read_frags(slot, f);
+          compute(f, full_tag);
+          slot = slot == NS - 1 ? 0 : slot + 1;
+        }
+      };
+      if (tm_eff >= C::kTM)
+        k_loop(std::true_type{});
+      else
+        k_loop(std::false_type{});
+
+      // Epilogue: stage in the slot of the last step, round by round.
+      const int stage_slot = static_cast<int>((slot0 + nk - 1) % NS);
+      uint8_t* stg = smem + stage_slot * C::kSlot;
+      const int last_ch = static_cast<int>((n_out - col0 < S::kOutCols ? n_out - col0 : S::kOutCols) / 8) - 1;
+      const SituConsts sc = situ_consts(p.beta, p.beta_lin);
+      static_for<S::kRounds>([&](auto rc) __attribute__((always_inline)) {
+        constexpr int R = decltype(rc)::value;
+        if (R > 0 && R >= rounds) return false;  // a tile has >= 1 row: round 0 always runs
+        lds_barrier();  // the slot's previous readers are done
+#pragma unroll
+        for (int i = 0; i < C::kTM; ++i) {
+          if (i * MF / S::kStageRows != R) continue;
+          uint8_t* srow = stg + (i * MF + r_in - R * S::kStageRows) * S::kStageRow;
+#pragma unroll
+          for (int j = 0; j < kOutTN; ++j)
+#pragma unroll
+            for (int q = 0; q < kRuns; ++q) {
+              float v[4];
+#pragma unroll
+              for (int e = 0; e < 4; ++e) {
+                if constexpr (EPI == kEpiSitu) {
+                  float gv = acc[i][j][q * 4 + e], uv = acc[i][j + kOutTN][q * 4 + e];
+                  if (p.round_before_act) {
+                    gv = static_cast<float>(static_cast<__bf16>(gv));
+                    uv = static_cast<float>(static_cast<__bf16>(uv));
+                  }
+                  v[e] = situ_epi(gv, uv, sc);
+                } else {
+                  v[e] = acc[i][j][q * 4 + e];
+                }
+              }
+              *reinterpret_cast<uint2*>(srow + (wn * kOutTN * MF + j * MF + c_run(q)) * 2) =
+                  uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+            }
+        }
+        lds_barrier();
+#pragma unroll
+        for (int v = 0; v < S::kStoresPerRound; ++v) {
+          const int idx = tid + C::kThreads * v;
+          int row = R * S::kStageRows + idx / S::kChunks, ch = idx % S::kChunks;
+          // out-of-range rows / columns store a valid neighbour again, so
+          // every lane issues the same number of stores
+          row = row < cur.rows ? row : cur.rows - 1;
+          ch = ch <= last_ch ? ch : last_ch;
+          const uint4 val =
+              *reinterpret_cast<const uint4*>(stg + (row - R * S::kStageRows) * S::kStageRow + ch * 16);
+          *reinterpret_cast<uint4*>(out + (cur.row0 + row) * n_out + col0 + ch * 8) = val;
+        }
+        return true;
+      });
+      slot0 = static_cast<int>((slot0 + nk) % NS);
+    } else {
+      // padding bucket / tail rows: zeros, stored directly (the zero comes
+      // from an opaque move, so it is not a constant held across the K loop)
+      uint32_t z;
+      asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+      constexpr int kZeroOps = BM * S::kChunks / C::kThreads;
+#pragma unroll
+      for (int v = 0; v < kZeroOps; ++v) {
+        const int idx = tid + C::kThreads * v;
+        const int row = idx / S::kChunks, ch = idx % S::kChunks;
+        if (row < cur.rows && col0 + ch * 8 < n_out)
+          *reinterpret_cast<uint4*>(out + (cur.row0 + row) * n_out + col0 + ch * 8) = uint4{z, z, z, z};
+      }
+    }
+    cur = nxt;
+    nt = nt_n;
+    vb = vb_n;
+    cur_pf = pf;
+    prev_rounds = rounds;
+  }
 }
 
 // Compute units of the current device (cached per device).
@@ -549,12 +971,16 @@ bool persistent_blocks() {
   return v;
 }
 
-// LMOE_XCD_MAP=mtile keeps m-tile groups per XCD for grouped problems (A/B
-// timing); the default stripes n-tiles over the XCDs when they divide evenly.
-bool xcd_stripe_n() {
-  static const bool v = [] {
+// XCD mapping of grouped problems (A/B timing): LMOE_XCD_MAP=mtile deals
+// m-tiles round-robin to the XCDs, =mrange gives each XCD a contiguous m-tile
+// range; the default stripes n-tiles over the XCDs when they divide evenly.
+enum XcdMap { kMapStripeN = 0, kMapMTile = 1, kMapMRange = 2 };
+XcdMap xcd_map() {
+  static const XcdMap v = [] {
     const char* e = std::getenv("LMOE_XCD_MAP");
-    return !(e && std::strcmp(e, "mtile") == 0);
+    if (e && std::strcmp(e, "mtile") == 0) return kMapMTile;
+    if (e && std::strcmp(e, "mrange") == 0) return kMapMRange;
+    return kMapStripeN;
   }();
   return v;
 }
@@ -573,7 +999,10 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
   if (ntiles == 0 || p.M == 0) return LMOE_OK;
   int gm = p.G == 1 ? 4 : 1;
   int64_t blocks = kXcds * ceil_div(ceil_div(mtiles, gm), kXcds) * gm * ntiles;
-  if (p.G > 1 && ntiles % kXcds == 0 && xcd_stripe_n()) {
+  if (p.G > 1 && xcd_map() == kMapMRange) {
+    gm = -1;  // contiguous m-tile ranges per XCD
+    blocks = kXcds * ceil_div(mtiles, kXcds) * ntiles;
+  } else if (p.G > 1 && ntiles % kXcds == 0 && xcd_map() == kMapStripeN) {
     gm = 0;  // n-tiles striped over the XCDs
     blocks = mtiles * ntiles;
   }
@@ -598,6 +1027,75 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;
   }
+}
+
+// LMOE_STREAM=0 keeps the MXFP4 grouped GEMM on the one-block-per-tile
+// kernel (A/B timing); by default the streamed persistent kernel runs
+// wherever it applies.
+bool stream_enabled() {
+  static const bool v = [] {
+    const char* e = std::getenv("LMOE_STREAM");
+    return !(e && std::strcmp(e, "0") == 0);
+  }();
+  return v;
+}
+
+// The streamed persistent kernel: bf16 output, and the LDS tile table
+// (8 (G + 1) bytes) must leave room for the blocks per CU that the ring alone
+// allows.  Returns 1 when it ran (or failed: *rc set), 0 when it does not
+// apply.
+template <int BM, int BN, int EPI, int NS, int MF>
+int try_stream(const Params& p, hipStream_t st, const char* name, int* rc) {
+  using S = SCfg<BM, BN, EPI, NS, MF>;
+  using C = typename S::C;
+  if (!stream_enabled() || p.G < 1 || p.M == 0) return 0;
+  if (EPI != kEpiSitu && p.out_dtype != LMOE_BF16) return 0;
+  const int64_t ring = static_cast<int64_t>(NS) * C::kSlot;
+  const int64_t lds = ring + ((8 * (p.G + 1) + 15) / 16) * 16;
+  const int64_t per_cu = 163840 / (lds + 64);
+  if (per_cu < 1 || per_cu < C::kLdsBlocks) return 0;
+  const int64_t out_cols = EPI == kEpiSitu ? p.N / 2 : p.N;
+  const int64_t ntiles = ceil_div(out_cols, S::kOutCols);
+  const int64_t mtiles = ceil_div(p.M, BM) + p.G + 1;
+  int gm = p.G == 1 ? 4 : 1;
+  int64_t blocks = kXcds * ceil_div(ceil_div(mtiles, gm), kXcds) * gm * ntiles;
+  if (p.G > 1 && xcd_map() == kMapMRange) {
+    gm = -1;
+    blocks = kXcds * ceil_div(mtiles, kXcds) * ntiles;
+  } else if (p.G > 1 && ntiles % kXcds == 0 && xcd_map() == kMapStripeN) {
+    gm = 0;
+    blocks = mtiles * ntiles;
+  }
+  *rc = LMOE_OK;
+  if (blocks >= (1ll << 31)) {
+    *rc = fail(LMOE_ERR_UNSUPPORTED, "%s: grid too large", name);
+    return 1;
+  }
+  const int64_t w_bytes = p.N * (p.K / 2);
+  if (!(w_bytes < (1ll << 32) && BM * p.K * 2 < (1ll << 32))) {
+    *rc = fail(LMOE_ERR_UNSUPPORTED, "%s: group too large for the DMA path", name);
+    return 1;
+  }
+  // raise the kernel's dynamic LDS limit when a larger table needs it
+  static std::atomic<int64_t> lds_set{0};
+  if (lds > lds_set.load()) {
+    const hipError_t attr_rc =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_stream_kernel<BM, BN, EPI, NS, MF>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+    if (attr_rc != hipSuccess) {
+      *rc = fail(LMOE_ERR_HIP, "%s: LDS size attribute (%lld bytes): %s", name, (long long)lds,
+                 hipGetErrorString(attr_rc));
+      return 1;
+    }
+    lds_set.store(lds);
+  }
+  const int64_t resident = kXcds * ((static_cast<int64_t>(cu_count()) * C::kLdsBlocks) / kXcds);
+  const int64_t grid = resident >= kXcds && resident < blocks ? resident : blocks;
+  grouped_gemm_stream_kernel<BM, BN, EPI, NS, MF>
+      <<<dim3(static_cast<unsigned>(grid)), C::kThreads, static_cast<size_t>(lds), st>>>(p, ntiles, gm, blocks);
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) *rc = fail(LMOE_ERR_HIP, "%s: launch failed: %s", name, hipGetErrorString(e));
+  return 1;
 }
 
 // Re-tile MXFP4 weights to k-step-major order: packed (G, N, K/2) ->
@@ -627,9 +1125,7 @@ __global__ __launch_bounds__(256) void tile_mxfp4_kernel(const uint8_t* __restri
 // Tile shape / ring depth of the MXFP4 kernel: LMOE_DMA_CFG = "BMxBNxNS"
 // picks one of the instantiated variants ("p": fragments read one step
 // ahead), LMOE_MFMA=16 the 16x16x32 MFMA instead of 32x32x16 (tuning
-// sweeps).  Default, from sweeps on the LatentMoE expert shapes: 64x256x3
-// for both epilogues (gate/up: each activation tile feeds 128 gate + 128 up
-// columns; down: 256 latent columns per activation tile).
+// sweeps).  The defaults are chosen in run_mx_shape.
 int mx_variant() {
   static const int v = [] {
     const char* e = std::getenv("LMOE_DMA_CFG");
@@ -653,8 +1149,15 @@ bool mfma16() {
 
 template <int EPI, int MF>
 int run_mx_shape(const Params& p, hipStream_t st, const char* name) {
+  // Defaults, from sweeps on the LatentMoE expert shapes: the streamed
+  // kernel with 64x256 tiles and a 3-deep ring (3 blocks per CU) where it
+  // applies, else the one-block-per-tile kernel with 64x256 tiles, ring depth
+  // 3 for the fused gate/up and 4 for the down projection.
   int v = mx_variant();
-  if (v < 0) v = 3;
+  int rc = LMOE_OK;
+  if ((v < 0 || v == 3) && try_stream<64, 256, EPI, 3, MF>(p, st, name, &rc)) return rc;
+  if (v == 2 && try_stream<64, 256, EPI, 4, MF>(p, st, name, &rc)) return rc;
+  if (v < 0) v = EPI == kEpiSitu ? 3 : 2;
   switch (v) {
     case 1: return launch_dma<64, 128, kDMX, EPI, 6, 1, 4, MF>(p, st, name);
     case 2: return launch_dma<64, 256, kDMX, EPI, 4, 1, 4, MF>(p, st, name);

@@ -176,9 +176,14 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs; consecutive blocks go to consecutiv
 // weight column slice is read by one XCD only, and the m-tiles of a group,
 // which share it, follow each other there so its later reads hit that XCD's
 // L2); gm > 0: groups of gm m-tiles round-robin over the XCDs with all n-tiles
-// of a group on one XCD (the A rows are read by one XCD only).
-template <int BM>
-__device__ TileInfo schedule_tile(const Params& p, int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt) {
+// of a group on one XCD (the A rows are read by one XCD only); gm < 0: XCD x
+// takes the contiguous m-tile range [x * ceil(tm/8), (x+1) * ceil(tm/8)), each
+// m-tile with all its n-tiles in a row, so both the A rows and (but for the
+// groups that straddle a range boundary) a group's weights are read by one
+// XCD only.
+template <class Locate>
+__device__ __forceinline__ TileInfo schedule_tile_with(int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt,
+                                                       Locate&& locate) {
   // grids and tile counts are < 2^31 (checked on the host): 32-bit index math
   const uint32_t v32 = static_cast<uint32_t>(vb), nt32 = static_cast<uint32_t>(n_tiles);
   const uint32_t xcd = v32 % kXcds, slot = v32 / kXcds;
@@ -188,7 +193,13 @@ __device__ TileInfo schedule_tile(const Params& p, int64_t n_tiles, int gm, int6
     const uint32_t per = nt32 / kXcds;
     const uint32_t mt = slot / per;
     nt = xcd + kXcds * (slot % per);
-    if (mt < tm) ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, mt);
+    if (mt < tm) ti = locate(mt);
+  } else if (gm < 0) {
+    const uint32_t per = static_cast<uint32_t>((tm + kXcds - 1) / kXcds);
+    const uint32_t ml = slot / nt32;
+    nt = slot % nt32;
+    const int64_t mt = static_cast<int64_t>(xcd) * per + ml;
+    if (ml < per && mt < tm) ti = locate(mt);
   } else {
     const uint32_t span = static_cast<uint32_t>(gm) * nt32;
     const int64_t m_base = (static_cast<int64_t>(slot / span) * kXcds + xcd) * gm;
@@ -197,11 +208,114 @@ __device__ TileInfo schedule_tile(const Params& p, int64_t n_tiles, int gm, int6
       const uint32_t gm_eff = static_cast<uint32_t>(tm - m_base < gm ? tm - m_base : gm);
       if (r < gm_eff * nt32) {
         nt = r / gm_eff;
-        ti = locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, m_base + r % gm_eff);
+        ti = locate(m_base + r % gm_eff);
       }
     }
   }
   return ti;
+}
+
+template <int BM>
+__device__ TileInfo schedule_tile(const Params& p, int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt) {
+  return schedule_tile_with(n_tiles, gm, vb, tm, nt, [&](int64_t mt) {
+    return locate_tile<BM>(p.group_sizes, p.G, p.M, p.zero_group, mt);
+  });
+}
+
+// Tile table in LDS, built once per block by the streamed (persistent)
+// kernels: tt[g] = exclusive prefix of the m-tile counts ceil(n_g / BM)
+// (saturating at 2^31 - 1) and tr[g] = exclusive prefix of the row counts
+// (saturating at M), g = 0 .. G, with n_g = group_sizes[g] clipped to
+// [0, M].  The same clipping and saturation as locate_tile, so both give the
+// same tiles.  Runs on all threads of the block (THREADS, a multiple of 64);
+// `wsum` holds THREADS / 64 scratch words.  Ends with the table visible to
+// every wave.
+template <int BM, int THREADS>
+__device__ __forceinline__ void build_tile_table(const int32_t* __restrict__ gs, int G, uint32_t m32, uint32_t* tt, uint32_t* tr,
+                                 uint32_t* wsum) {
+  constexpr uint32_t kTileCap = 0x7fffffffu;
+  constexpr int kWaves = THREADS / 64;
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  uint32_t carry_t = 0, carry_r = 0;
+  for (int g0 = 0; g0 < G; g0 += THREADS) {
+    const int g = g0 + static_cast<int>(threadIdx.x);
+    const int32_t v = g < G ? gs[g] : 0;
+    const uint32_t n = v < 0 ? 0u : (static_cast<uint32_t>(v) < m32 ? static_cast<uint32_t>(v) : m32);
+    const uint32_t tiles = (n + BM - 1) / BM;
+    const uint32_t it = wave_scan_sat(tiles, kTileCap), ir = wave_scan_sat(n, m32);
+    // wave totals -> exclusive wave offsets (two words per wave)
+    if (lane == 63) {
+      wsum[2 * wave] = it;
+      wsum[2 * wave + 1] = ir;
+    }
+    __syncthreads();
+    uint32_t off_t = carry_t, off_r = carry_r, tot_t = carry_t, tot_r = carry_r;
+    for (int w = 0; w < kWaves; ++w) {
+      if (w < wave) {
+        off_t = sat_add(off_t, wsum[2 * w], kTileCap);
+        off_r = sat_add(off_r, wsum[2 * w + 1], m32);
+      }
+      tot_t = sat_add(tot_t, wsum[2 * w], kTileCap);
+      tot_r = sat_add(tot_r, wsum[2 * w + 1], m32);
+    }
+    if (g < G) {
+      // exclusive = offset + inclusive - own (the own term never saturated
+      // alone: recompute from the previous lane's inclusive value)
+      const uint32_t pt = __builtin_amdgcn_update_dpp(0u, it, 0x138, 0xf, 0xf, false);  // wave_shr:1
+      const uint32_t pr = __builtin_amdgcn_update_dpp(0u, ir, 0x138, 0xf, 0xf, false);
+      tt[g] = sat_add(off_t, lane == 0 ? 0u : pt, kTileCap);
+      tr[g] = sat_add(off_r, lane == 0 ? 0u : pr, m32);
+    }
+    carry_t = tot_t;
+    carry_r = tot_r;
+    __syncthreads();  // wsum is reused by the next chunk
+  }
+  if (threadIdx.x == 0) {
+    tt[G] = carry_t;
+    tr[G] = carry_r;
+  }
+  __syncthreads();
+}
+
+// locate_tile from the LDS tile table; executed by every wave for itself
+// (wave-uniform result; `lane` = this thread's lane).
+template <int BM>
+__device__ __forceinline__ TileInfo locate_tile_lds(const uint32_t* tt, const uint32_t* tr, int G, int64_t M,
+                                                    int zero_group, int64_t mt, int lane) {
+  TileInfo info{-1, 0, 0, false};
+  int hit_g = -1;
+  for (int g0 = 0; g0 < G; g0 += 64) {
+    const int g = g0 + lane;
+    const bool hit = g < G && static_cast<int64_t>(tt[g]) <= mt && mt < static_cast<int64_t>(tt[g + 1]);
+    const uint64_t b = __ballot(hit);
+    if (b) {
+      hit_g = g0 + __ffsll(static_cast<long long>(b)) - 1;
+      break;
+    }
+  }
+  if (hit_g >= 0) {
+    const int64_t local = mt - tt[hit_g];
+    const int64_t n_eff = static_cast<int64_t>(tr[hit_g + 1]) - tr[hit_g];  // rows left before M
+    const int64_t left = n_eff - local * BM;
+    if (left > 0) {
+      info.group = hit_g;
+      info.row0 = tr[hit_g] + local * BM;
+      info.rows = static_cast<int>(left < BM ? left : BM);
+      info.zero = hit_g == zero_group;
+    }
+  } else {
+    // tail tiles: zero rows [sum(group_sizes), M)
+    const int64_t q = mt - tt[G];
+    const int64_t r0 = tr[G] + q * BM;
+    if (q >= 0 && r0 < M) {
+      info.group = 0;
+      info.row0 = r0;
+      const int64_t left = M - r0;
+      info.rows = static_cast<int>(left < BM ? left : BM);
+      info.zero = true;
+    }
+  }
+  return info;
 }
 
 __device__ __forceinline__ float situ(float g, float u, float beta, float beta_lin) {
