@@ -173,6 +173,12 @@ int lmoe_ragged_dot_mxfp8_mxfp4(const uint8_t* lhs_q, const uint8_t* lhs_scale_t
 int lmoe_router_topk(const float* logits, const float* bias, int64_t T, int64_t E, int64_t k,
                      int act, int renorm, float scale, int weight_dtype, int32_t* topk_idx,
                      void* topk_w, float* scores_out, void* stream);
+/* Same with the logits rows ld >= E floats apart (e.g. the router columns of
+ * a GEMM that computes the router logits together with another projection of
+ * the same hidden states). */
+int lmoe_router_topk_ld(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E,
+                        int64_t k, int act, int renorm, float scale, int weight_dtype,
+                        int32_t* topk_idx, void* topk_w, float* scores_out, void* stream);
 
 /* ---- a7: local-shard dispatch ------------------------------------------------------
  * Replaces filter_and_pad_to_shard_jittable (ref.py:754-877), bit-identical to
@@ -228,6 +234,12 @@ int lmoe_rms_norm(const void* x, const void* scale, int64_t rows, int64_t n, flo
 int lmoe_situ_and_mul(const void* gate, const void* up, int64_t count, float beta, float beta_lin,
                       int dtype, void* out, void* stream);
 int lmoe_add(const void* a, const void* b, int64_t count, int dtype, void* out, void* stream);
+/* lmoe_cast_rows: out (rows, cols) contiguous = cast(x), x rows ld >= cols
+ * elements apart; f32 -> bf16 rounds to nearest even (the rounding of a bf16
+ * matmul output).  Used to split the layer's fused router + down-projection
+ * GEMM (f32 out) into the f32 logits and the bf16 latent x (ref.py:358/371). */
+int lmoe_cast_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld, void* out,
+                   int out_dtype, void* stream);
 
 #ifdef __cplusplus
 }

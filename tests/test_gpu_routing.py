@@ -68,6 +68,39 @@ def test_router_topk_matches_oracle(gpu_device, t, e, k, kind, act, wdt):
   assert max_rel(scores, ref.scores) <= 1e-5
 
 
+def test_router_topk_strided_logits(gpu_device):
+  """Logits as the router columns of a wider GEMM output (row stride > E):
+  identical results to the contiguous copy."""
+  from lmoe import ops
+  rng = np.random.default_rng(5)
+  t, e, extra, k = 777, 896, 1024, 16
+  wide = to_dev(rng.standard_normal((t, e + extra)).astype(np.float32))
+  bias = to_dev((0.01 * rng.standard_normal(e)).astype(np.float32))
+  view = wide[:, :e]
+  assert view.stride(0) == e + extra
+  a = ops.router_topk_from_logits(view, bias, k, True, 2.5, "sigmoid", torch.bfloat16, return_scores=True)
+  b = ops.router_topk_from_logits(view.contiguous(), bias, k, True, 2.5, "sigmoid", torch.bfloat16,
+                                  return_scores=True)
+  for x, y in zip(a, b):
+    assert torch.equal(x, y)
+
+
+@pytest.mark.parametrize("rows,cols,ld", [(4096, 1024, 1920), (333, 96, 96), (17, 5, 9)])
+def test_cast_rows_f32_to_bf16(gpu_device, rows, cols, ld):
+  """Strided f32 -> bf16 rows: round-to-nearest-even, bit-identical to
+  torch's conversion (incl. NaN, +-inf, -0, values that round up past the
+  bf16 maximum)."""
+  from lmoe import ops
+  rng = np.random.default_rng(rows)
+  x = (rng.standard_normal((rows, ld)) * 10.0 ** rng.integers(-30, 30, (rows, ld))).astype(np.float32)
+  x.flat[:6] = [np.nan, np.inf, -np.inf, -0.0, 3.3961775e38, 1.0 + 2.0 ** -8]
+  xd = to_dev(x)
+  got = ops.cast_rows(xd[:, :cols], torch.bfloat16)
+  want = xd[:, :cols].to(torch.bfloat16)
+  assert got.is_contiguous() and got.shape == (rows, cols)
+  assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
 def test_router_golden_bias(gpu_device):
   """The golden bundles' uninitialised bias (1.36e5, denormals) through the GPU gate."""
   import _golden

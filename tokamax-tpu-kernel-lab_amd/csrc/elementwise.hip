@@ -79,6 +79,28 @@ __global__ __launch_bounds__(256) void add_kernel(const void* __restrict__ a, co
     store_from_f32(out, i, __fadd_rn(load_as_f32(a, i, dt), load_as_f32(b, i, dt)), dt);
 }
 
+// out (rows, cols) contiguous = cast(x) with x rows ld elements apart.  Fast
+// path f32 -> bf16 with 4 elements per thread (16-byte load, 8-byte store).
+__global__ __launch_bounds__(256) void cast_rows_f32_bf16x4(const float* __restrict__ x, int64_t rows,
+                                                            int64_t cols, int64_t ld, uint16_t* __restrict__ out) {
+  const int64_t q = cols / 4;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows * q;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / q, c = (i % q) * 4;
+    const float4 v = *reinterpret_cast<const float4*>(x + r * ld + c);
+    *reinterpret_cast<uint2*>(out + r * cols + c) = uint2{gemm::pack_bf16x2(v.x, v.y), gemm::pack_bf16x2(v.z, v.w)};
+  }
+}
+
+__global__ __launch_bounds__(256) void cast_rows_kernel(const void* __restrict__ x, int xdt, int64_t rows,
+                                                        int64_t cols, int64_t ld, void* __restrict__ out, int odt) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < rows * cols;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t r = i / cols, c = i % cols;
+    store_from_f32(out, i, load_as_f32(x, r * ld + c, xdt), odt);
+  }
+}
+
 unsigned grid_for(int64_t count) {
   const int64_t b = ceil_div(count, 256);
   return static_cast<unsigned>(b < 262144 ? (b > 0 ? b : 1) : 262144);
@@ -122,5 +144,23 @@ extern "C" int lmoe_add(const void* a, const void* b, int64_t count, int dtype, 
   if (count == 0) return LMOE_OK;
   add_kernel<<<grid_for(count), 256, 0, static_cast<hipStream_t>(stream)>>>(a, b, count, dtype, out);
   LMOE_CHECK_LAUNCH("add");
+  return LMOE_OK;
+}
+
+extern "C" int lmoe_cast_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld, void* out,
+                              int out_dtype, void* stream) {
+  LMOE_CHECK_ARG(rows >= 0 && cols >= 0 && ld >= cols && valid_dtype(x_dtype) && valid_dtype(out_dtype),
+                 "cast_rows: bad arguments");
+  if (rows == 0 || cols == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(x && out, "cast_rows: null pointer");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (x_dtype == LMOE_F32 && out_dtype == LMOE_BF16 && cols % 4 == 0 && ld % 4 == 0 && aligned(x, 16) &&
+      aligned(out, 8)) {
+    cast_rows_f32_bf16x4<<<grid_for(rows * cols / 4), 256, 0, st>>>(static_cast<const float*>(x), rows, cols, ld,
+                                                                      static_cast<uint16_t*>(out));
+  } else {
+    cast_rows_kernel<<<grid_for(rows * cols), 256, 0, st>>>(x, x_dtype, rows, cols, ld, out, out_dtype);
+  }
+  LMOE_CHECK_LAUNCH("cast_rows");
   return LMOE_OK;
 }

@@ -38,13 +38,13 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
 
 template <int EPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(
-    const float* __restrict__ logits, const float* __restrict__ bias, int T, int E, int k, int act,
+    const float* __restrict__ logits, int64_t ld, const float* __restrict__ bias, int T, int E, int k, int act,
     int renorm, float scale, int wdtype, int32_t* __restrict__ idx_out, void* __restrict__ w_out,
     float* __restrict__ scores_out) {
   const int lane = threadIdx.x % kWave;
   const int t = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
   if (t >= T) return;
-  const float* row = logits + static_cast<int64_t>(t) * E;
+  const float* row = logits + static_cast<int64_t>(t) * ld;
 
   float s[EPL];
   uint32_t key[EPL];
@@ -136,22 +136,23 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 }
 
 template <int EPL>
-void launch_router(const float* logits, const float* bias, int T, int E, int k, int act, int renorm,
+void launch_router(const float* logits, int64_t ld, const float* bias, int T, int E, int k, int act, int renorm,
                    float scale, int wdtype, int32_t* idx, void* w, float* scores, hipStream_t st) {
   dim3 grid(static_cast<unsigned>(ceil_div(T, kWavesPerBlock)));
-  router_topk_kernel<EPL><<<grid, 256, 0, st>>>(logits, bias, T, E, k, act, renorm, scale, wdtype,
+  router_topk_kernel<EPL><<<grid, 256, 0, st>>>(logits, ld, bias, T, E, k, act, renorm, scale, wdtype,
                                                  idx, w, scores);
 }
 
 }  // namespace
 }  // namespace lmoe
 
-extern "C" int lmoe_router_topk(const float* logits, const float* bias, int64_t T, int64_t E,
-                                int64_t k, int act, int renorm, float scale, int weight_dtype,
-                                int32_t* topk_idx, void* topk_w, float* scores_out, void* stream) {
+extern "C" int lmoe_router_topk_ld(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E,
+                                   int64_t k, int act, int renorm, float scale, int weight_dtype,
+                                   int32_t* topk_idx, void* topk_w, float* scores_out, void* stream) {
   using namespace lmoe;
   LMOE_CHECK_ARG(T >= 0 && E > 0 && k > 0, "router_topk: bad sizes T=%lld E=%lld k=%lld",
                  (long long)T, (long long)E, (long long)k);
+  LMOE_CHECK_ARG(ld >= E, "router_topk: row stride %lld < E=%lld", (long long)ld, (long long)E);
   LMOE_CHECK_ARG(k <= E, "router_topk: k=%lld > E=%lld", (long long)k, (long long)E);
   LMOE_CHECK_SUPPORTED(k <= 64, "router_topk: k=%lld > 64", (long long)k);
   LMOE_CHECK_SUPPORTED(E <= 4096, "router_topk: E=%lld > 4096", (long long)E);
@@ -165,7 +166,7 @@ extern "C" int lmoe_router_topk(const float* logits, const float* bias, int64_t 
   const int Ti = static_cast<int>(T), Ei = static_cast<int>(E), ki = static_cast<int>(k);
 #define LMOE_ROUTER_CASE(N)                                                                   \
   if (epl <= N) {                                                                             \
-    launch_router<N>(logits, bias, Ti, Ei, ki, act, renorm, scale, weight_dtype, topk_idx,    \
+    launch_router<N>(logits, ld, bias, Ti, Ei, ki, act, renorm, scale, weight_dtype, topk_idx, \
                      topk_w, scores_out, st);                                                 \
     LMOE_CHECK_LAUNCH("router_topk");                                                         \
     return LMOE_OK;                                                                           \
@@ -179,4 +180,11 @@ extern "C" int lmoe_router_topk(const float* logits, const float* bias, int64_t 
   LMOE_ROUTER_CASE(64)
 #undef LMOE_ROUTER_CASE
   return fail(LMOE_ERR_UNSUPPORTED, "router_topk: E=%lld", (long long)E);
+}
+
+extern "C" int lmoe_router_topk(const float* logits, const float* bias, int64_t T, int64_t E, int64_t k, int act,
+                                int renorm, float scale, int weight_dtype, int32_t* topk_idx, void* topk_w,
+                                float* scores_out, void* stream) {
+  return lmoe_router_topk_ld(logits, E, bias, T, E, k, act, renorm, scale, weight_dtype, topk_idx, topk_w,
+                             scores_out, stream);
 }

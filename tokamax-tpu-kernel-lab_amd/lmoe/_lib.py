@@ -54,6 +54,7 @@ SIGNATURES = {
     "lmoe_quantize_mxfp8": ([P, I32, I64, I64, P, P, P], I32),
     "lmoe_ragged_dot_mxfp8_mxfp4": ([P, P, P, P, P, I64, I64, I64, I64, I32, I32, F, F, P, I32, P], I32),
     "lmoe_router_topk": ([P, P, I64, I64, I64, I32, I32, F, I32, P, P, P, P], I32),
+    "lmoe_router_topk_ld": ([P, I64, P, I64, I64, I64, I32, I32, F, I32, P, P, P, P], I32),
     "lmoe_dispatch_workspace_size": ([I64, I64, I64], I64),
     "lmoe_dispatch_local": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P,
                              I64, P], I32),
@@ -64,6 +65,7 @@ SIGNATURES = {
     "lmoe_dense_blaslt": ([P, I32, P, I32, I64, I64, I64, P, I32, P], I32),
     "lmoe_situ_and_mul": ([P, P, I64, F, F, I32, P, P], I32),
     "lmoe_add": ([P, P, I64, I32, P, P], I32),
+    "lmoe_cast_rows": ([P, I32, I64, I64, I64, P, I32, P], I32),
 }
 
 _lock = threading.Lock()

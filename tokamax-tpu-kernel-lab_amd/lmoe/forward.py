@@ -157,6 +157,13 @@ class LocalShardLatentMoE:
     self.router_nk = router_weight.t().contiguous()
     self.bias = e_score_correction_bias.float().contiguous()
     self.down_nk = down_proj.t().contiguous()
+    # router logits and the down-projection read the same hidden states: one
+    # GEMM over the concatenated (E + lat, H) weights (f32 out) replaces two,
+    # reading the activations once; the latent columns are then rounded to
+    # bf16, which is what the separate bf16 GEMM returns
+    self.router_down_nk = None
+    if self.router_nk.dtype == torch.bfloat16 and self.down_nk.dtype == torch.bfloat16:
+      self.router_down_nk = torch.cat([self.router_nk, self.down_nk], 0).contiguous()
     self.up_nk = up_proj.t().contiguous()
     self.norm_scale = norm_scale.contiguous()
     self.experts = dict(experts)
@@ -182,8 +189,14 @@ class LocalShardLatentMoE:
     ev = kernel_events or {}
     t = hidden.shape[0]
     b, bl = c.activation_situ_beta, c.activation_situ_linear_beta
-    logits = self._dense(hidden, self.router_nk, torch.float32)
-    x = self._dense(hidden, self.down_nk)
+    if self.router_down_nk is not None and hidden.dtype == torch.bfloat16:
+      e = self.router_nk.shape[0]
+      rd = self._dense(hidden, self.router_down_nk, torch.float32)
+      logits = rd[:, :e]
+      x = ops.cast_rows(rd[:, e:], hidden.dtype)
+    else:
+      logits = self._dense(hidden, self.router_nk, torch.float32)
+      x = self._dense(hidden, self.down_nk)
     idx, w = ops.router_topk_from_logits(logits, self.bias, c.top_k, c.moe_renormalize,
                                          c.routed_scaling_factor, self.act, hidden.dtype)
     m_padded = ops.compute_m_padded(t, c.top_k, c.num_experts, self.L, self.cf)

@@ -33,6 +33,18 @@ def _dt(t: torch.Tensor) -> int:
     raise NotImplementedError(f"dtype {t.dtype} is not supported (bf16 / f32 only)") from None
 
 
+def _dev_rows(t: torch.Tensor) -> torch.Tensor:
+  """A GPU 2-D tensor whose rows may be strided (unit column stride, row
+  stride >= width); anything else is made contiguous."""
+  if not t.is_cuda:
+    raise ValueError("LatentMoE operators need GPU tensors (no CPU fallback)")
+  if t.dim() != 2:
+    raise ValueError("expected a 2-D tensor")
+  if t.stride(1) != 1 or t.stride(0) < t.shape[1]:
+    t = t.contiguous()
+  return t
+
+
 def _dev(*ts: torch.Tensor) -> None:
   for t in ts:
     if t is None:
@@ -338,8 +350,11 @@ def router_topk_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top
                             renormalize: bool = True, scaling: float = 1.0, act: str = "sigmoid",
                             weight_dtype: torch.dtype = torch.float32, return_scores: bool = False):
   """Gate math of ref.py:347-361 / ref.py:601-631 on given f32 logits (T, E):
-  returns (topk_idx int32 (T, k), topk_weight (T, k) weight_dtype[, scores])."""
-  _dev(logits, bias)
+  returns (topk_idx int32 (T, k), topk_weight (T, k) weight_dtype[, scores]).
+  ``logits`` may be a row-strided view (unit column stride), e.g. the router
+  columns of a wider GEMM output."""
+  logits = _dev_rows(logits)
+  _dev(bias)
   if logits.dtype != torch.float32:
     raise ValueError("router logits must be float32 (the reference's gate runs in f32)")
   if bias is not None and bias.dtype != torch.float32:
@@ -348,9 +363,21 @@ def router_topk_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top
   idx = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
   w = torch.empty((t, top_k), dtype=weight_dtype, device=logits.device)
   scores = torch.empty((t, e), dtype=torch.float32, device=logits.device) if return_scores else None
-  check(lib().lmoe_router_topk(_p(logits), _p(bias), t, e, top_k, _ACTS[act], int(renormalize),
-                               scaling, _dt(w), _p(idx), _p(w), _p(scores), _stream()), "router_topk")
+  check(lib().lmoe_router_topk_ld(_p(logits), max(logits.stride(0), e), _p(bias), t, e, top_k, _ACTS[act],
+                                  int(renormalize), scaling, _dt(w), _p(idx), _p(w), _p(scores), _stream()),
+        "router_topk")
   return (idx, w, scores) if return_scores else (idx, w)
+
+
+def cast_rows(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+  """Contiguous ``x.to(dtype)`` of a 2-D, row-strided view (unit column
+  stride); f32 -> bf16 rounds to nearest even."""
+  x = _dev_rows(x)
+  rows, cols = x.shape
+  out = torch.empty((rows, cols), dtype=dtype, device=x.device)
+  check(lib().lmoe_cast_rows(_p(x), _dt(x), rows, cols, max(x.stride(0), cols), _p(out), _dt(out), _stream()),
+        "cast_rows")
+  return out
 
 
 _GROUP_CACHE: dict = {}
