@@ -68,6 +68,35 @@ def test_router_topk_matches_oracle(gpu_device, t, e, k, kind, act, wdt):
   assert max_rel(scores, ref.scores) <= 1e-5
 
 
+@pytest.mark.parametrize("t,e,k,kind,wdt", [
+    (4096, 896, 16, "skew", "bf16"),     # config 5 router
+    (2048, 896, 16, "normal", "f32"),
+    (300, 64, 16, "ties", "f32"),        # integer logits: more than 64 candidates -> full path
+    (257, 8, 2, "normal", "f32"),        # fewer experts than lanes
+    (64, 4096, 64, "normal", "f32"),     # k = 64
+    (100, 896, 1, "normal", "f32"),
+])
+def test_router_candidate_path_equals_full_path(gpu_device, t, e, k, kind, wdt):
+  """Without a full score output the sigmoid gate selects from approximate-
+  score candidates; ids and weights are bit-identical to the exact full path
+  (which runs when scores are requested) and match the oracle."""
+  from lmoe import ops
+  rng = np.random.default_rng(t + 3 * e + k)
+  logits = _logits(rng, t, e, kind)
+  bias = (0.05 * rng.standard_normal(e)).astype(np.float32)
+  if kind == "ties":
+    bias = np.where(np.arange(e) % 7 == 0, 0.25, 0.0).astype(np.float32)
+  wt = torch.bfloat16 if wdt == "bf16" else torch.float32
+  lg, bs = to_dev(logits), to_dev(bias)
+  i1, w1 = ops.router_topk_from_logits(lg, bs, k, True, 2.5, "sigmoid", wt)
+  i2, w2, _ = ops.router_topk_from_logits(lg, bs, k, True, 2.5, "sigmoid", wt, return_scores=True)
+  assert torch.equal(i1, i2)
+  assert torch.equal(w1, w2)
+  ref = O.router_from_logits(logits, bias, k, True, 2.5, "sigmoid", wdt)
+  skip = _near_tie_tokens(ref.scores_for_choice, k)
+  assert np.array_equal(to_np(i1)[~skip], ref.topk_idx[~skip])
+
+
 def test_router_topk_strided_logits(gpu_device):
   """Logits as the router columns of a wider GEMM output (row stride > E):
   identical results to the contiguous copy."""

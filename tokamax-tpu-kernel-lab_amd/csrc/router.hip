@@ -2,12 +2,26 @@
 // step 1, ref.py:347-361): one 64-wide wavefront per token.
 //
 // Each lane owns the experts e = c*64 + lane (c < EPL), so the logits row is read
-// with fully coalesced loads.  Selection is k rounds of a wavefront arg-max:
-// a wave maximum of the order-preserving float bits of every lane's best
-// remaining candidate, then a wave minimum of the expert ids holding that
-// value, which gives "descending value, ties to the lower expert id" --
-// jax.lax.top_k's order.  Both reductions are DPP row shifts / broadcasts (no
-// LDS round trips); only the winning lane rescans its EPL candidates.
+// with fully coalesced loads.  The order is "descending score + bias, ties to
+// the lower expert id" -- jax.lax.top_k's order.
+//
+// Candidate path (sigmoid gate, k <= 64, no full score output): every score
+// is first computed with the hardware exp / reciprocal (a few f32 ulp), which
+// only serves to find a threshold: the k-th largest of the 64 lane maxima
+// (radix select over ballots) is <= the k-th largest approximate key, so
+// every exact top-k element lies within the approximation error of it or
+// above.  Elements above threshold - 2^-18 (|threshold| + 1) -- a margin far
+// above twice that error -- are compacted to LDS (usually barely more than
+// k), their exact scores recomputed with the same correctly rounded
+// operations as the full path, and the at most 64 candidates bitonic-sorted
+// on (key, -expert).  The result is identical to the full path's.  More than
+// 64 candidates (massive ties) fall back to the full path.
+//
+// Full path: exact scores for all experts, then k rounds of a wavefront
+// arg-max: a wave maximum of the order-preserving float bits of every lane's
+// best remaining candidate, then a wave minimum of the expert ids holding that
+// value.  Both reductions are DPP row shifts / broadcasts; only the winning
+// lane rescans its EPL candidates.
 #include <cmath>
 
 #include "lmoe_common.h"
@@ -36,6 +50,41 @@ __device__ __forceinline__ float wave_sum_f32(float v) {
   return v;
 }
 
+__device__ __forceinline__ float from_ordered(uint32_t u) {
+  return __uint_as_float((u & 0x80000000u) ? (u & 0x7fffffffu) : ~u);
+}
+
+// Largest v with #{lanes : x >= v} >= k (the k-th largest x), by radix
+// select from the top bit: one ballot per bit.
+__device__ __forceinline__ uint32_t wave_kth_largest(uint32_t x, int k) {
+  uint32_t prefix = 0;
+#pragma unroll
+  for (int bit = 31; bit >= 0; --bit) {
+    const uint32_t cand = prefix | (1u << bit);
+    if (__popcll(__ballot(x >= cand)) >= k) prefix = cand;
+  }
+  return prefix;
+}
+
+// Wave-wide bitonic sort, descending on key; `val` travels with its key.
+__device__ __forceinline__ void wave_sort_desc(uint64_t& key, float& val, int lane) {
+#pragma unroll
+  for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+    for (int stride = size / 2; stride > 0; stride >>= 1) {
+      const uint32_t plo = __shfl_xor(static_cast<uint32_t>(key), stride, 64);
+      const uint32_t phi = __shfl_xor(static_cast<uint32_t>(key >> 32), stride, 64);
+      const float pv = __shfl_xor(val, stride, 64);
+      const uint64_t pk = (static_cast<uint64_t>(phi) << 32) | plo;
+      const bool lower = (lane & stride) == 0;
+      const bool keep_max = lower == ((lane & size) == 0 || size == 64);
+      const bool take = keep_max ? pk > key : pk < key;
+      key = take ? pk : key;
+      val = take ? pv : val;
+    }
+  }
+}
+
 template <int EPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, int64_t ld, const float* __restrict__ bias, int T, int E, int k, int act,
@@ -52,6 +101,64 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   for (int c = 0; c < EPL; ++c) {
     const int e = c * kWave + lane;
     s[c] = e < E ? row[e] : -INFINITY;
+  }
+  if (act == LMOE_ACT_SIGMOID && scores_out == nullptr && k <= kWave) {
+    __shared__ float s_logit[kWavesPerBlock][kWave];
+    __shared__ int32_t s_expert[kWavesPerBlock][kWave];
+    const int wv = threadIdx.x / kWave;
+    // approximate selection keys and their lane maximum
+    float ap[EPL];
+    uint32_t lmax = 0;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      const int e = c * kWave + lane;
+      const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s[c] * -1.44269504088896341f));
+      ap[c] = sg + (bias ? bias[e < E ? e : 0] : 0.0f);
+      if (e < E) lmax = max(lmax, ordered_bits(ap[c]));
+    }
+    const float th = from_ordered(wave_kth_largest(lmax, k));
+    const float thr = th - 0x1p-18f * (__builtin_fabsf(th) + 1.0f);
+    uint32_t n = 0;
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) n += (c * kWave + lane < E && ap[c] >= thr) ? 1u : 0u;
+    const uint32_t incl = wave_scan_sat(n, 0xffffffffu);
+    const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
+    if (total >= static_cast<uint32_t>(k) && total <= static_cast<uint32_t>(kWave)) {
+      uint32_t pos = incl - n;
+#pragma unroll
+      for (int c = 0; c < EPL; ++c) {
+        const int e = c * kWave + lane;
+        if (e < E && ap[c] >= thr) {
+          s_logit[wv][pos] = s[c];
+          s_expert[wv][pos] = e;
+          ++pos;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+      uint64_t ck = 0;  // below every real key
+      float cs = 0.0f;
+      if (static_cast<uint32_t>(lane) < total) {
+        const float lg = s_logit[wv][lane];
+        const int e = s_expert[wv][lane];
+        cs = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg)));
+        const float sel = bias ? __fadd_rn(cs, bias[e]) : __fadd_rn(cs, 0.0f);
+        ck = (static_cast<uint64_t>(ordered_bits(sel)) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
+      }
+      wave_sort_desc(ck, cs, lane);
+      float sum = 0.0f;
+      for (int j = 0; j < k; ++j)
+        sum = __fadd_rn(sum, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cs), j)));
+      if (lane < k) {
+        float w = cs;
+        if (renorm && k > 1) w = __fdiv_rn(w, __fadd_rn(sum, 1e-20f));
+        w = __fmul_rn(w, scale);
+        const int64_t o = static_cast<int64_t>(t) * k + lane;
+        idx_out[o] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ck));
+        store_from_f32(w_out, o, w, wdtype);
+      }
+      return;
+    }
   }
   if (act == LMOE_ACT_SOFTMAX) {
     float m = -INFINITY;
