@@ -222,6 +222,16 @@ int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype, const int32
 int lmoe_combine_slots(const void* shard_out, int shard_dtype, const int32_t* slot_pos,
                        const void* w, int w_dtype, int64_t T, int64_t k, int64_t lat, int mode,
                        void* routed_out, int out_dtype, void* stream);
+/* lmoe_combine_slots into a zero routed_out, fused with lmoe_rms_norm of the
+ * routed rows (the layer's combine -> _rms_norm, ref.py:413-427 /
+ * ref.py:1113-1141 + 286-293): normed_out (T, lat) = rms_norm(routed) * scale.
+ * routed_out (T, lat) is also written when not NULL.  Bit-identical to the
+ * two calls.  dtype is the routed / normed / scale dtype; lat % 8 == 0,
+ * lat <= 2048; bf16 buffers 16-byte aligned, f32 32-byte aligned. */
+int lmoe_combine_slots_rms_norm(const void* shard_out, int shard_dtype, const int32_t* slot_pos,
+                                const void* w, int w_dtype, int64_t T, int64_t k, int64_t lat, int mode,
+                                const void* norm_scale, float eps, void* routed_out, void* normed_out,
+                                int dtype, void* stream);
 
 /* ---- a14 / a10: adjacent elementwise stages -----------------------------------------
  * lmoe_rms_norm: _rms_norm (ref.py:286-293): f32 mean square, x*rsqrt(var+eps)

@@ -130,6 +130,38 @@ def test_cast_rows_f32_to_bf16(gpu_device, rows, cols, ld):
   assert torch.equal(got.view(torch.int16), want.view(torch.int16))
 
 
+@pytest.mark.parametrize("mode,t,k,lat,dt", [
+    ("scatter_add", 4096, 16, 1024, "bf16"),   # the layer's shape
+    ("scatter_add", 300, 6, 136, "f32"),       # partial lane pass
+    ("slot_sum", 257, 16, 2048, "bf16"),       # four passes
+    ("slot_sum", 64, 2, 8, "f32"),
+])
+def test_combine_rms_norm_fused_equals_two_kernels(gpu_device, mode, t, k, lat, dt):
+  """The fused combine + RMSNorm is bit-identical to combine_slots on zeros
+  followed by rms_norm, for both combine modes, and writes the same routed
+  rows when asked."""
+  from lmoe import ops
+  rng = np.random.default_rng(t + lat)
+  m = t * k // 2
+  tdt = torch.bfloat16 if dt == "bf16" else torch.float32
+  shard = to_dev(rng.standard_normal((m, lat)).astype(np.float32)).to(tdt)
+  perm = rng.permutation(t * k)  # each row feeds at most one slot, about half the slots dropped
+  slot_pos = to_dev(np.where(perm < m, perm, -1).reshape(t, k).astype(np.int32))
+  if mode == "scatter_add":
+    w = to_dev(rng.random(m).astype(np.float32)).to(tdt)
+  else:
+    w = to_dev(rng.random((t, k)).astype(np.float32))
+  scale = to_dev((1.0 + 0.1 * rng.standard_normal(lat)).astype(np.float32)).to(tdt)
+  routed = ops.combine_slots(shard, slot_pos, w, t, k, mode=mode, out_dtype=tdt)
+  ref = ops._rms_norm(routed, scale, 1e-6)
+  normed, routed2 = ops.combine_slots_rms_norm(shard, slot_pos, w, t, k, scale, 1e-6, mode=mode, out_dtype=tdt,
+                                               return_routed=True)
+  assert torch.equal(routed2, routed)
+  assert torch.equal(normed, ref)
+  assert torch.equal(ops.combine_slots_rms_norm(shard, slot_pos, w, t, k, scale, 1e-6, mode=mode, out_dtype=tdt),
+                     ref)
+
+
 def test_router_golden_bias(gpu_device):
   """The golden bundles' uninitialised bias (1.36e5, denormals) through the GPU gate."""
   import _golden

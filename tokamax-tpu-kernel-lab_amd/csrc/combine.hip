@@ -225,6 +225,115 @@ __global__ __launch_bounds__(256) void combine_csr_kernel(
   }
 }
 
+// Combine into a zero-initialised routed row followed by the RMSNorm of
+// that row (ref.py:413-416 / 1113-1141, then ref.py:286-293 / 427): the wave
+// that builds token t's row keeps it in registers (R passes of VEC elements
+// per lane, lat <= 64 * VEC * R) and normalises it, so the routed row need not
+// be written (routed_out may be NULL) or read back.  Same per-element
+// rounding sequence as lmoe_combine_slots on a zeroed output followed by
+// lmoe_rms_norm, and the same element-to-lane split as lmoe_rms_norm (VEC 8
+// for bf16, 4 for f32), so the sum of squares runs in the same order and the
+// result is bit-identical to the two-kernel path.
+template <int VEC, int R, int SDT = -1, int ODT = -1>
+__global__ __launch_bounds__(256) void combine_norm_kernel(
+    const void* __restrict__ shard, int sdt_arg, const int32_t* __restrict__ slot_pos,
+    const void* __restrict__ w, int wdt, int T, int k, int64_t lat, int mode, const void* __restrict__ norm_scale,
+    float eps, void* __restrict__ routed_out, void* __restrict__ normed_out, int odt_arg) {
+  const int sdt = SDT >= 0 ? SDT : sdt_arg, odt = ODT >= 0 ? ODT : odt_arg;
+  __shared__ int32_t rows_s[kTokensPerBlock][kWave];
+  __shared__ float wts_s[kTokensPerBlock][kWave];
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  const int t = blockIdx.x * kTokensPerBlock + wave;
+  if (t >= T) return;
+  int p = -1;
+  if (lane < k) p = slot_pos[static_cast<int64_t>(t) * k + lane];
+  const bool slot_sum = mode == LMOE_COMBINE_SLOT_SUM;
+  int n;
+  if (slot_sum) {
+    rows_s[wave][lane] = p;
+    wts_s[wave][lane] = lane < k ? load_as_f32(w, static_cast<int64_t>(t) * k + lane, wdt) : 0.0f;
+    n = k;
+  } else {
+    const bool valid = lane < k && p >= 0;
+    int rank = 0;
+    for (int j = 0; j < k; ++j) {
+      const int pj = __shfl(p, j, kWave);
+      rank += (pj >= 0 && pj < p) ? 1 : 0;
+    }
+    n = __popcll(__ballot(valid));
+    if (valid) {
+      rows_s[wave][rank] = p;
+      wts_s[wave][rank] = load_as_f32(w, p, wdt);
+    }
+  }
+  wave_sync();
+  const int prod_dt = (sdt == LMOE_F32 || wdt == LMOE_F32) ? LMOE_F32 : LMOE_BF16;
+  constexpr int kBatch = VEC == 8 ? 8 : 4;
+  float v[R][VEC];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t c0 = static_cast<int64_t>(r) * kWave * VEC + static_cast<int64_t>(lane) * VEC;
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) v[r][q] = 0.0f;
+    if (c0 >= lat) continue;
+    for (int r0 = 0; r0 < n; r0 += kBatch) {
+      float x[kBatch][VEC];
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        // unconditional loads (past the end / dropped slots re-read a valid
+        // row) keep a batch's loads together ahead of its adds
+        int row = rows_s[wave][r0 + b < n ? r0 + b : n - 1];
+        row = row >= 0 ? row : 0;
+        load_vec<VEC>(shard, static_cast<int64_t>(row) * lat + c0, sdt, x[b]);
+      }
+#pragma unroll
+      for (int b = 0; b < kBatch; ++b) {
+        if (r0 + b >= n) break;
+        const float wv = wts_s[wave][r0 + b];
+        if (slot_sum) {
+          if (rows_s[wave][r0 + b] < 0) continue;
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) v[r][q] = __fadd_rn(v[r][q], __fmul_rn(x[b][q], wv));
+        } else {
+#pragma unroll
+          for (int q = 0; q < VEC; ++q) {
+            float a = round_to(__fmul_rn(x[b][q], wv), prod_dt);
+            a = round_to(a, odt);
+            v[r][q] = round_to(__fadd_rn(v[r][q], a), odt);
+          }
+        }
+      }
+    }
+    if (slot_sum) {
+#pragma unroll
+      for (int q = 0; q < VEC; ++q) v[r][q] = round_to(v[r][q], odt);
+    }
+    if (routed_out) store_vec<VEC>(routed_out, static_cast<int64_t>(t) * lat + c0, odt, v[r]);
+  }
+  // RMSNorm of the routed row: the per-lane order of lmoe_rms_norm
+  float ss = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    if (static_cast<int64_t>(r) * kWave * VEC + static_cast<int64_t>(lane) * VEC >= lat) continue;
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) ss = __fadd_rn(ss, __fmul_rn(v[r][q], v[r][q]));
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, off, kWave));
+  const float var = __fdiv_rn(ss, static_cast<float>(lat));
+  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(var, eps)));
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t c0 = static_cast<int64_t>(r) * kWave * VEC + static_cast<int64_t>(lane) * VEC;
+    if (c0 >= lat) continue;
+    float sc[VEC], o[VEC];
+    load_vec<VEC>(norm_scale, c0, odt, sc);
+#pragma unroll
+    for (int q = 0; q < VEC; ++q) o[q] = __fmul_rn(round_to(__fmul_rn(v[r][q], inv), odt), sc[q]);
+    store_vec<VEC>(normed_out, static_cast<int64_t>(t) * lat + c0, odt, o);
+  }
+}
+
 // Many bins (tokens): large chunks keep the scanned (token, chunk) array small.
 constexpr int kCombineChunk = 1024;
 
@@ -316,5 +425,59 @@ extern "C" int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype,
     combine_csr_kernel<1><<<blocks, 256, 0, st>>>(shard_out, shard_dtype, order, offsets, padded_w,
                                                  w_dtype, Ti, lat, routed_out, out_dtype);
   LMOE_CHECK_LAUNCH("combine_csr");
+  return LMOE_OK;
+}
+
+extern "C" int lmoe_combine_slots_rms_norm(const void* shard_out, int shard_dtype, const int32_t* slot_pos,
+                                           const void* w, int w_dtype, int64_t T, int64_t k, int64_t lat, int mode,
+                                           const void* norm_scale, float eps, void* routed_out, void* normed_out,
+                                           int dtype, void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(T >= 0 && k > 0 && lat > 0, "combine_rms_norm: bad sizes");
+  LMOE_CHECK_SUPPORTED(k <= 64, "combine_rms_norm: k=%lld > 64", (long long)k);
+  LMOE_CHECK_ARG(valid_dtype(shard_dtype) && valid_dtype(w_dtype) && valid_dtype(dtype),
+                 "combine_rms_norm: bad dtype");
+  LMOE_CHECK_ARG(mode == LMOE_COMBINE_SCATTER_ADD || mode == LMOE_COMBINE_SLOT_SUM,
+                 "combine_rms_norm: bad mode %d", mode);
+  LMOE_CHECK_SUPPORTED(T < (1ll << 31), "combine_rms_norm: T too large");
+  LMOE_CHECK_SUPPORTED(lat % 8 == 0 && lat <= 2048, "combine_rms_norm: lat=%lld (needs a multiple of 8, <= 2048)",
+                       (long long)lat);
+  if (T == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(shard_out && slot_pos && w && norm_scale && normed_out, "combine_rms_norm: null pointer");
+  const size_t oa = dtype == LMOE_BF16 ? 16 : 32;
+  LMOE_CHECK_SUPPORTED(aligned(shard_out, shard_dtype == LMOE_BF16 ? 16 : 32) && aligned(normed_out, oa) &&
+                           aligned(norm_scale, oa) && (!routed_out || aligned(routed_out, oa)),
+                       "combine_rms_norm: buffers must be 16-byte (bf16) / 32-byte (f32) aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const unsigned blocks = static_cast<unsigned>(ceil_div(T, kTokensPerBlock));
+  const bool bf = shard_dtype == LMOE_BF16 && dtype == LMOE_BF16;
+  // lmoe_rms_norm's split: 8 elements per lane and pass for bf16, 4 for f32
+  const int vec = dtype == LMOE_BF16 ? 8 : 4;
+  const int passes = static_cast<int>(ceil_div(lat, 64 * vec));
+#define LMOE_CN_CASE(V, R)                                                                                    \
+  if (vec == V && passes == R) {                                                                             \
+    if (V == 8 && bf)                                                                                        \
+      combine_norm_kernel<V, R, LMOE_BF16, LMOE_BF16><<<blocks, 256, 0, st>>>(                               \
+          shard_out, shard_dtype, slot_pos, w, w_dtype, (int)T, (int)k, lat, mode, norm_scale, eps, routed_out, \
+          normed_out, dtype);                                                                                \
+    else                                                                                                     \
+      combine_norm_kernel<V, R><<<blocks, 256, 0, st>>>(shard_out, shard_dtype, slot_pos, w, w_dtype, (int)T,  \
+                                                        (int)k, lat, mode, norm_scale, eps, routed_out,        \
+                                                        normed_out, dtype);                                  \
+  }
+  LMOE_CN_CASE(8, 1)
+  LMOE_CN_CASE(8, 2)
+  LMOE_CN_CASE(8, 3)
+  LMOE_CN_CASE(8, 4)
+  LMOE_CN_CASE(4, 1)
+  LMOE_CN_CASE(4, 2)
+  LMOE_CN_CASE(4, 3)
+  LMOE_CN_CASE(4, 4)
+  LMOE_CN_CASE(4, 5)
+  LMOE_CN_CASE(4, 6)
+  LMOE_CN_CASE(4, 7)
+  LMOE_CN_CASE(4, 8)
+#undef LMOE_CN_CASE
+  LMOE_CHECK_LAUNCH("combine_rms_norm");
   return LMOE_OK;
 }

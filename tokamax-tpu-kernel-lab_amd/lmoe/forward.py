@@ -225,9 +225,17 @@ class LocalShardLatentMoE:
       shard_out = ops.ragged_dot(act, E["down_nk"], d.group_sizes, rhs_layout="gnk", zero_group=self.L)
     if "down" in ev:
       ev["down"][1].record()
-    routed = ops.combine_slots(shard_out, d.slot_pos, d.padded_combine_weight, t, c.top_k,
-                               mode="scatter_add", out_dtype=hidden.dtype)
-    normed = ops._rms_norm(routed, self.norm_scale, c.rms_norm_eps)
+    if ops.combine_rms_norm_supported(shard_out.shape[-1]):
+      # combine and RMSNorm in one pass; the routed rows are materialised only
+      # when the stages are returned
+      res = ops.combine_slots_rms_norm(shard_out, d.slot_pos, d.padded_combine_weight, t, c.top_k,
+                                       self.norm_scale, c.rms_norm_eps, mode="scatter_add", out_dtype=hidden.dtype,
+                                       return_routed=return_stages)
+      normed, routed = res if return_stages else (res, None)
+    else:
+      routed = ops.combine_slots(shard_out, d.slot_pos, d.padded_combine_weight, t, c.top_k,
+                                 mode="scatter_add", out_dtype=hidden.dtype)
+      normed = ops._rms_norm(routed, self.norm_scale, c.rms_norm_eps)
     out = self._dense(normed, self.up_nk)
     if self.shared is not None:
       S = self.shared

@@ -601,6 +601,28 @@ def combine_slots(shard_out: torch.Tensor, slot_pos: torch.Tensor, weights: torc
   return out
 
 
+def combine_slots_rms_norm(shard_out: torch.Tensor, slot_pos: torch.Tensor, weights: torch.Tensor,
+                           num_tokens: int, top_k: int, norm_scale: torch.Tensor, eps: float, *, mode: str,
+                           out_dtype: torch.dtype | None = None, return_routed: bool = False):
+  """combine_slots into zeros followed by _rms_norm of the routed rows, in one
+  kernel (bit-identical to the two calls): returns normed (T, lat), or
+  (normed, routed) with ``return_routed``."""
+  _dev(shard_out, slot_pos, weights, norm_scale)
+  lat = shard_out.shape[-1]
+  dt = out_dtype or shard_out.dtype
+  m = {"scatter_add": _lib.COMBINE_SCATTER_ADD, "slot_sum": _lib.COMBINE_SLOT_SUM}[mode]
+  normed = torch.empty((num_tokens, lat), dtype=dt, device=shard_out.device)
+  routed = torch.empty_like(normed) if return_routed else None
+  check(lib().lmoe_combine_slots_rms_norm(_p(shard_out), _dt(shard_out), _p(slot_pos), _p(weights), _dt(weights),
+                                          num_tokens, top_k, lat, m, _p(norm_scale.to(dt).contiguous()), eps,
+                                          _p(routed), _p(normed), _dt(normed), _stream()), "combine_rms_norm")
+  return (normed, routed) if return_routed else normed
+
+
+def combine_rms_norm_supported(lat: int) -> bool:
+  return lat % 8 == 0 and lat <= 2048
+
+
 # ---------------------------------------------------------------------------
 # a10 / a14: elementwise stages
 # ---------------------------------------------------------------------------
