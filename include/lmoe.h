@@ -53,6 +53,11 @@ extern "C" {
 #define LMOE_MXFP4_LDS_DEQUANT 0 /* dequantise weight tiles to bf16 in LDS, bf16 MFMA */
 #define LMOE_MXFP4_SCALED_MFMA 1 /* native scaled MFMA: use lmoe_quantize_mxfp8 + lmoe_ragged_dot_mxfp8_mxfp4 */
 #define LMOE_MXFP4_LDS_DEQUANT_TILED 2 /* as LDS_DEQUANT, weights re-tiled by lmoe_mxfp4_tile */
+/* OR-ed into the mode: the rows of zero_group and the rows past
+ * sum(group_sizes) may be left unwritten instead of zeroed (for callers that
+ * never read them, e.g. the padding bucket of a local-shard layer); honoured
+ * by the tiled path, the others write zeros. */
+#define LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS 0x100
 
 #define LMOE_COMBINE_SCATTER_ADD 0 /* sharded: sequential adds rounded to out dtype (ref.py:1113-1141) */
 #define LMOE_COMBINE_SLOT_SUM 1    /* unsharded: f32 sum over slots, one cast (ref.py:413-416) */

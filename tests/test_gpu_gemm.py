@@ -284,6 +284,13 @@ def test_ragged_dot_mxfp4_tiled_many_tiles(gpu_device, situ):
   assert max_rel(out, ref) <= BF16_TOL
   assert np.all(out[start:start + gs[zg]] == 0)
   assert np.all(out[int(gs.sum()):] == 0)
+  # zero-group and tail rows left unwritten: every other row is unchanged
+  skip = to_np(ops.ragged_dot_mxfp4(to_dev(lhs, "bf16"), tpk, tsc, to_dev(gs), fuse_gateup_activation=fa,
+                                    zero_group=zg, weight_layout="tiled", skip_zero_group_rows=True))
+  rows = np.ones(m, bool)
+  rows[start:start + gs[zg]] = False
+  rows[int(gs.sum()):] = False
+  assert np.array_equal(skip[rows], out[rows])
 
 
 def test_mxfp4_tiled_edge_scales(gpu_device):

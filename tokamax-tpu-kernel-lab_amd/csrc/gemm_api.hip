@@ -105,6 +105,8 @@ extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, c
                                      int64_t G, int zero_group, int mode, int epilogue, float beta,
                                      float beta_lin, void* out, void* stream) {
   const char* name = "ragged_dot_mxfp4";
+  const int skip_zero_rows = (mode & LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS) != 0;
+  mode &= ~LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS;
   int rc = check_common(lhs, w_packed, group_sizes, M, K, N, G, zero_group, out, name);
   if (rc) return rc;
   LMOE_CHECK_ARG(w_scale || M == 0, "%s: null scale", name);
@@ -114,6 +116,7 @@ extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, c
   LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(w_packed, 16), "%s: 16-byte alignment", name);
   Params p{static_cast<const uint16_t*>(lhs), w_packed, w_scale, group_sizes, M, K, N, G, zero_group,
            out, LMOE_BF16, beta, beta_lin, 1};
+  p.skip_zero_rows = skip_zero_rows;
   const int epi = epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone;
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (mode == LMOE_MXFP4_LDS_DEQUANT) return run_bf16(p, kMXFP4, epi, st, name);

@@ -457,6 +457,9 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
       k_loop(std::false_type{});
     // every DMA of this tile has been waited for by the last step
   }
+  // the caller never reads the zero group's rows or those past the groups
+  // (block-uniform)
+  if (tile.zero && p.skip_zero_rows) continue;
 
   // Epilogue.  A lane holds output row (lane % MF) of row sub-tile i and, for
   // each q < MF / 8 (q < 1 for MF == 16), the four adjacent columns
@@ -924,6 +927,9 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
         return true;
       });
       slot0 = static_cast<int>((slot0 + nk) % NS);
+    } else if (p.skip_zero_rows) {
+      // the caller never reads the zero group's rows or those past the
+      // groups: nothing to store
     } else {
       // padding bucket / tail rows: zeros, stored directly (the zero comes
       // from an opaque move, so it is not a constant held across the K loop)

@@ -47,6 +47,7 @@ struct Params {
   float beta, beta_lin;
   int round_before_act;
   const uint8_t* lhs_scale = nullptr;  // MXFP8 path: E8M0 (K/128, roundup(M, 4), 4)
+  int skip_zero_rows = 0;              // zero_group rows may be left unwritten
 };
 
 struct TileInfo {

@@ -33,6 +33,7 @@ EPI_SITU = 1
 MXFP4_LDS_DEQUANT = 0
 MXFP4_SCALED_MFMA = 1
 MXFP4_LDS_DEQUANT_TILED = 2
+MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS = 0x100
 COMBINE_SCATTER_ADD = 0
 COMBINE_SLOT_SUM = 1
 

@@ -205,10 +205,13 @@ class LocalShardLatentMoE:
     if "gateup" in ev:
       ev["gateup"][0].record()
     if self.expert_format == "mxfp4":
+      # padding-bucket rows (zero_group L) are never read downstream: left
+      # unwritten unless the stages are returned
       act = ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed" + self._sfx], E["gu_scale" + self._sfx],
                                  d.group_sizes,
                                  fuse_gateup_activation=f"situ:{b}:{bl}", mode=self.mxfp4_mode,
-                                 zero_group=self.L, weight_layout=self.weight_layout)
+                                 zero_group=self.L, weight_layout=self.weight_layout,
+                                 skip_zero_group_rows=not return_stages)
     else:
       act = ops.ragged_dot_gateup_situ(d.sorted_tokens, E["gu_nk"], d.group_sizes, b, bl,
                                        rhs_layout="gnk", zero_group=self.L)
@@ -220,7 +223,8 @@ class LocalShardLatentMoE:
       shard_out = ops.ragged_dot_mxfp4(act, E["down_packed" + self._sfx], E["down_scale" + self._sfx],
                                        d.group_sizes,
                                        mode=self.mxfp4_mode, zero_group=self.L,
-                                       weight_layout=self.weight_layout)
+                                       weight_layout=self.weight_layout,
+                                       skip_zero_group_rows=not return_stages)
     else:
       shard_out = ops.ragged_dot(act, E["down_nk"], d.group_sizes, rhs_layout="gnk", zero_group=self.L)
     if "down" in ev:

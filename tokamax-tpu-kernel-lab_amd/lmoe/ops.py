@@ -292,13 +292,16 @@ def ragged_dot_mxfp8_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
 def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
                      group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
                      mode: str = "lds_dequant", zero_group: int = -1,
-                     weight_layout: str = "checkpoint") -> torch.Tensor:
+                     weight_layout: str = "checkpoint", skip_zero_group_rows: bool = False) -> torch.Tensor:
   """Grouped lhs @ deq(W_g)^T with W_g in checkpoint (N, K/2) layout
   (orientation of mxfp4_online_dequant_matmul_pallas.py:1-36) and block-32
   E8M0 scales (G, N, K/32), or with ``weight_layout="tiled"`` the
   (G, K/64, N, 32) / (G, K/64, N, 2) pair from ``mxfp4_tile_weights`` (same
   result, faster kernel).  With ``fuse_gateup_activation`` the N axis is
-  [gate | up] and the SiTU-GLU epilogue is applied (output width N/2)."""
+  [gate | up] and the SiTU-GLU epilogue is applied (output width N/2).
+  ``skip_zero_group_rows``: the rows of ``zero_group`` and those past
+  sum(group_sizes) may be left unwritten (uninitialised) instead of zeroed,
+  for callers that never read them."""
   _dev(lhs, w_packed, w_scale, group_sizes)
   if lhs.dtype != torch.bfloat16:
     raise NotImplementedError("MXFP4 GEMM takes bf16 activations")
@@ -332,6 +335,8 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
                                   fuse_gateup_activation=fuse_gateup_activation, zero_group=zero_group)
   if weight_layout == "tiled":
     mode_id = _lib.MXFP4_LDS_DEQUANT_TILED
+  if skip_zero_group_rows:
+    mode_id |= _lib.MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS
   out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
   check(lib().lmoe_ragged_dot_mxfp4(_p(lhs), _p(w_packed), _p(w_scale), _p(group_sizes), m, k, n, g,
                                     zero_group, mode_id, epi, b, bl, _p(out), _stream()),
