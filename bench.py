@@ -103,8 +103,8 @@ def cpu_baseline(layer, hidden, w, c, sample_tokens, reps):
 def main():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
-  ap.add_argument("--steps", type=int, default=20)
-  ap.add_argument("--warmup", type=int, default=5)
+  ap.add_argument("--steps", type=int, default=100)
+  ap.add_argument("--warmup", type=int, default=20)
   ap.add_argument("--mxfp4-mode", default="lds_dequant", choices=["lds_dequant", "scaled_mfma"])
   ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
   ap.add_argument("--cpu-reps", type=int, default=3)
@@ -163,7 +163,7 @@ def main():
   roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
               "frac": round(achieved / HBM_PEAK_GBS, 4),
               "traffic": traffic.get("bytes_per_launch") if traffic else None,
-              "kernel": "grouped_gemm_dma_kernel<64, 256, MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
+              "kernel": "grouped_gemm_stream_kernel<64, 256, MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
               "algorithmic_bytes": int(nbytes), "algorithmic_flops": flops,
               "kernel_us": round(gateup_ms * 1000.0, 2)}
   grouped = {"tflops": round(tflops, 2),
