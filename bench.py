@@ -100,6 +100,34 @@ def cpu_baseline(layer, hidden, w, c, sample_tokens, reps):
                     f"({med:.2f} s each)"}
 
 
+def capture_layer(torch, layer, hidden):
+  """Capture one layer forward as a HIP graph (torch.cuda.CUDAGraph, private
+  memory pool, capture on a side stream of default priority).  Returns
+  (replay, static_output), or None when a replay differs from the eager
+  forward: each of three replays, with eager work in between, must match it
+  bit for bit."""
+  side = torch.cuda.Stream()
+  side.wait_stream(torch.cuda.current_stream())
+  with torch.cuda.stream(side):
+    layer.forward(hidden)
+  torch.cuda.current_stream().wait_stream(side)
+  torch.cuda.synchronize()
+  g = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(g):
+    out = layer.forward(hidden)
+  torch.cuda.synchronize()
+  for _ in range(3):
+    ref = layer.forward(hidden)
+    torch.cuda.synchronize()
+    out.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    if not torch.equal(out, ref):
+      log("graph replay differs from the eager forward: timing eager launches")
+      return None
+  return g.replay, out
+
+
 def main():
   ap = argparse.ArgumentParser()
   ap.add_argument("--gpus", type=int, default=1)
@@ -109,6 +137,8 @@ def main():
   ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
   ap.add_argument("--cpu-reps", type=int, default=3)
   ap.add_argument("--no-cpu-baseline", action="store_true")
+  ap.add_argument("--eager", action="store_true",
+                  help="time eager launches instead of replays of the layer captured as one HIP graph")
   args = ap.parse_args()
   if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
     print("bench.py measures one GPU only: this build has no multi-GPU path "
@@ -144,6 +174,7 @@ def main():
   for _ in range(args.warmup):
     layer.forward(hidden)
   torch.cuda.synchronize()
+  # eager steps with events around the two expert GEMMs (their in-layer times)
   events = [{k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for k in ("gateup", "down")}
             for _ in range(args.steps)]
   t0 = time.perf_counter()
@@ -151,11 +182,29 @@ def main():
     layer.forward(hidden, kernel_events=events[i])
   torch.cuda.synchronize()
   t1 = time.perf_counter()
-  ms_per_step = (t1 - t0) * 1000.0 / args.steps
+  eager_ms = (t1 - t0) * 1000.0 / args.steps
   gateup_ms = statistics.mean(e["gateup"][0].elapsed_time(e["gateup"][1]) for e in events)
   down_ms = statistics.mean(e["down"][0].elapsed_time(e["down"][1]) for e in events)
+  log(f"eager: {eager_ms:.3f} ms/step, gate/up kernel {gateup_ms * 1000:.1f} us, down kernel {down_ms * 1000:.1f} us")
+
+  execution = "eager launches"
+  ms_per_step = eager_ms
+  if not args.eager:
+    graph = capture_layer(torch, layer, hidden)
+    if graph is not None:
+      replay, out = graph
+      for _ in range(args.warmup):
+        replay()
+      torch.cuda.synchronize()
+      t0 = time.perf_counter()
+      for _ in range(args.steps):
+        replay()
+      torch.cuda.synchronize()
+      t1 = time.perf_counter()
+      ms_per_step = (t1 - t0) * 1000.0 / args.steps
+      execution = "HIP-graph replay of the whole layer (captured once; replays checked bit-exact against eager)"
+      log(f"graph replay: {ms_per_step:.3f} ms/step")
   tokens_per_s = c.tokens / (ms_per_step / 1000.0)
-  log(f"{ms_per_step:.3f} ms/step, gate/up kernel {gateup_ms * 1000:.1f} us, down kernel {down_ms * 1000:.1f} us")
 
   achieved = nbytes / (gateup_ms / 1000.0) / 1e9
   tflops = flops / (gateup_ms / 1000.0) / 1e12
@@ -187,7 +236,8 @@ def main():
                  "local_experts": f"{c.local_start}..{c.local_start + c.local_experts - 1}",
                  "expert_weights": "mxfp4 (e2m1, e8m0 block-32)", "capacity_factor": c.capacity_factor,
                  "m_padded": m_padded, "routed_rows": rows, "router_skew": "zipf(1.2) on logits",
-                 "shared_experts": 0, "parallelism": "single GPU (one expert shard)"},
+                 "shared_experts": 0, "parallelism": "single GPU (one expert shard)",
+                 "execution": execution, "eager_ms_per_step": round(eager_ms, 4)},
       "roofline": roofline, "grouped_gemm": grouped, "cpu_baseline": cpu,
   }
   print(json.dumps(line), flush=True)

@@ -137,3 +137,68 @@ def test_local_shard_layer_bf16_matches_oracle(gpu_device):
   if np.array_equal(idx, st["topk_idx"]):
     assert max_rel(to_np(gs["shard_out"]), st["shard_out"]) <= 2e-2
     assert max_rel(to_np(out), ref) <= 2e-2
+
+
+def _mxfp4_layer(dev, tokens=512):
+  """A reduced config-5 layer (MXFP4 experts, skewed router) and its inputs."""
+  from lmoe.forward import LocalShardLatentMoE
+  from lmoe.workloads import Config5, make_config5
+  c = Config5(tokens=tokens, hidden=512, latent=256, intermediate=256, experts=128, top_k=16,
+              local_start=16, local_experts=16)
+  hidden, w, experts = make_config5(dev, c, "mxfp4")
+  layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                              e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
+                              up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,
+                              local_num_experts=c.local_experts, expert_format="mxfp4", experts=experts,
+                              capacity_factor=c.capacity_factor)
+  return c, hidden, w, experts, layer
+
+
+def test_local_shard_layer_mxfp4_matches_oracle(gpu_device):
+  """The benchmarked layer end to end (fused router + down-projection GEMM,
+  candidate-path router, dispatch, streamed MXFP4 expert GEMMs that skip the
+  padding rows, fused combine + RMSNorm, up-projection) against the oracle's
+  single-shard forward on the dequantised experts; the stage-returning run
+  (padding rows written) gives the same output bit for bit."""
+  c, hidden, w, experts, layer = _mxfp4_layer(gpu_device)
+  L = c.local_experts
+  deq = lambda p, s: np.stack([O.dequantize_mxfp4(to_np(p[g]), to_np(s[g])) for g in range(L + 1)])
+  gu = deq(experts["gu_packed"], experts["gu_scale"])            # (L+1, 2I, lat)
+  dn = deq(experts["down_packed"], experts["down_scale"])        # (L+1, lat, I)
+  I = c.intermediate
+  gate, up = gu[:, :I, :].transpose(0, 2, 1), gu[:, I:, :].transpose(0, 2, 1)
+  down = dn.transpose(0, 2, 1)
+  wn = {k: to_np(v) for k, v in w.items()}
+  ref, st = O.single_shard_forward(to_np(hidden), wn, gate, up, down, c.config(), "bf16", c.local_start, L,
+                                   capacity_factor=c.capacity_factor, include_shared=False)
+  out = layer.forward(hidden)
+  out_st, gs = layer.forward(hidden, return_stages=True)
+  assert torch.equal(out, out_st)
+  idx = to_np(gs["topk_idx"])
+  assert np.mean(np.all(idx == st["topk_idx"], axis=1)) >= 0.99
+  if np.array_equal(idx, st["topk_idx"]):
+    assert np.array_equal(to_np(gs["dispatch"].group_sizes), st["dispatch"].group_sizes)
+    assert max_rel(to_np(gs["shard_out"]), st["shard_out"]) <= 2e-2
+    assert max_rel(to_np(out), ref) <= 2e-2
+
+
+def test_local_shard_layer_graph_replay(gpu_device):
+  """The layer captured as one HIP graph: three replays, with eager work in
+  between, each bit-identical to the eager forward (the bench times replays)."""
+  c, hidden, w, experts, layer = _mxfp4_layer(gpu_device, tokens=1024)
+  side = torch.cuda.Stream()
+  side.wait_stream(torch.cuda.current_stream())
+  with torch.cuda.stream(side):
+    layer.forward(hidden)
+  torch.cuda.current_stream().wait_stream(side)
+  torch.cuda.synchronize()
+  g = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(g):
+    out = layer.forward(hidden)
+  for _ in range(3):
+    ref = layer.forward(hidden)
+    torch.cuda.synchronize()
+    out.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
