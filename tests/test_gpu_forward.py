@@ -202,3 +202,39 @@ def test_local_shard_layer_graph_replay(gpu_device):
     g.replay()
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+def test_local_shard_layer_from_safetensors_checkpoint(gpu_device, tmp_path):
+  """Experts written to a safetensors checkpoint under the reference's key
+  table (w1 gate, w3 up, w2 down; fetch_real_mxfp4_expert_weights.py:51-67),
+  read back by lmoe.loader into a second layer: the forward is bit-identical to
+  the layer built from the in-memory weights."""
+  from safetensors.numpy import save_file
+  from lmoe.forward import LocalShardLatentMoE
+  from lmoe.loader import load_mxfp4_experts
+  c, hidden, w, experts, layer = _mxfp4_layer(gpu_device)
+  L, I = c.local_experts, c.intermediate
+  key = "language_model.model.layers.7.block_sparse_moe.experts.{}.{}"
+  tensors = {}
+  for g in range(L):
+    gp, gs = to_np(experts["gu_packed"][g]), to_np(experts["gu_scale"][g])
+    tensors[key.format(c.local_start + g, "w1.weight_packed")] = np.ascontiguousarray(gp[:I])
+    tensors[key.format(c.local_start + g, "w1.weight_scale")] = np.ascontiguousarray(gs[:I])
+    tensors[key.format(c.local_start + g, "w3.weight_packed")] = np.ascontiguousarray(gp[I:])
+    tensors[key.format(c.local_start + g, "w3.weight_scale")] = np.ascontiguousarray(gs[I:])
+    tensors[key.format(c.local_start + g, "w2.weight_packed")] = to_np(experts["down_packed"][g])
+    tensors[key.format(c.local_start + g, "w2.weight_scale")] = to_np(experts["down_scale"][g])
+  path = str(tmp_path / "experts.safetensors")
+  save_file(tensors, path)
+  loaded = load_mxfp4_experts(path, 7, range(c.local_start, c.local_start + L), device=gpu_device)
+  for name in ("gu_packed", "gu_scale", "down_packed", "down_scale"):
+    # the loader's padding expert is all-zero bytes; the synthetic one has zero
+    # codes under a nonzero scale: both dequantise to zeros
+    assert torch.equal(loaded[name][:L], experts[name][:L]), name
+    assert not loaded[name][L].any(), name
+  layer2 = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                               e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
+                               up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,
+                               local_num_experts=L, expert_format="mxfp4", experts=loaded,
+                               capacity_factor=c.capacity_factor)
+  assert torch.equal(layer2.forward(hidden), layer.forward(hidden))

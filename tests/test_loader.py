@@ -1,0 +1,174 @@
+"""MXFP4 checkpoint loader (lmoe.loader) on CPU.
+
+Checkpoints are written by the ``safetensors`` library itself, an independent
+writer of the format the reference's fetcher parses
+(05_ragged_dot_on_tpu/fetch_real_mxfp4_expert_weights.py:51-67): reading its
+files back byte-exact pins the header-length / data-section offset rule and
+the key table (README.md:303-318, w1 = gate, w3 = up, w2 = down).  The
+tensor-by-tensor path (experts split over shards, non-contiguous spans) is
+covered by a sharded checkpoint with an index file.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+from safetensors.numpy import save_file
+
+from lmoe import loader
+
+LAYER, I, LAT = 3, 64, 128
+
+
+def _expert(rng):
+  u8 = lambda *s: rng.integers(0, 256, s, dtype=np.uint8)
+  return {"w1.weight_packed": u8(I, LAT // 2), "w1.weight_scale": u8(I, LAT // 32),
+          "w3.weight_packed": u8(I, LAT // 2), "w3.weight_scale": u8(I, LAT // 32),
+          "w2.weight_packed": u8(LAT, I // 2), "w2.weight_scale": u8(LAT, I // 32)}
+
+
+def _key(e, name, layer=LAYER):
+  return f"language_model.model.layers.{layer}.block_sparse_moe.experts.{e}.{name}"
+
+
+def _checkpoint(rng, n_experts=24):
+  tensors, experts = {}, {}
+  for e in range(n_experts):
+    experts[e] = _expert(rng)
+    tensors.update({_key(e, k): v for k, v in experts[e].items()})
+  # neighbours the loader must skip: another layer's expert, dense weights of
+  # other dtypes that sort before the U8 tensors in the data section
+  tensors.update({_key(0, k, LAYER + 1): v for k, v in _expert(rng).items()})
+  tensors["language_model.model.layers.3.self_attn.q_proj.weight"] = rng.standard_normal((32, 48)).astype(np.float32)
+  tensors["language_model.model.layers.3.block_sparse_moe.gate.weight"] = rng.standard_normal((24, 40)).astype(np.float16)
+  return tensors, experts
+
+
+def _check(got, experts, ids, padding=True):
+  want_gu_p = np.stack([np.concatenate([experts[e]["w1.weight_packed"], experts[e]["w3.weight_packed"]]) for e in ids])
+  want_gu_s = np.stack([np.concatenate([experts[e]["w1.weight_scale"], experts[e]["w3.weight_scale"]]) for e in ids])
+  want_d_p = np.stack([experts[e]["w2.weight_packed"] for e in ids])
+  want_d_s = np.stack([experts[e]["w2.weight_scale"] for e in ids])
+  L = len(ids)
+  for name, want in (("gu_packed", want_gu_p), ("gu_scale", want_gu_s), ("down_packed", want_d_p),
+                     ("down_scale", want_d_s)):
+    t = got[name].numpy()
+    assert t.dtype == np.uint8
+    assert t.shape == ((L + 1,) if padding else (L,)) + want.shape[1:], name
+    assert np.array_equal(t[:L], want), name
+    if padding:
+      assert not t[L].any(), name
+
+
+def test_single_file_local_range(tmp_path):
+  rng = np.random.default_rng(0)
+  tensors, experts = _checkpoint(rng)
+  path = str(tmp_path / "model.safetensors")
+  save_file(tensors, path, metadata={"format": "pt"})
+  ids = list(range(16, 24))  # a local shard: experts [16, 24)
+  got = loader.load_mxfp4_experts(path, LAYER, ids, device="cpu")
+  _check(got, experts, ids)
+  assert got["gu_packed"].shape == (9, 2 * I, LAT // 2)
+  got = loader.load_mxfp4_experts(path, LAYER, [5, 2, 11], device="cpu", padding_expert=False)
+  _check(got, experts, [5, 2, 11], padding=False)
+
+
+def test_header_offsets_are_relative_to_the_data_section(tmp_path):
+  rng = np.random.default_rng(1)
+  tensors, experts = _checkpoint(rng, 4)
+  path = str(tmp_path / "m.safetensors")
+  save_file(tensors, path)
+  header, start = loader.read_header(path)
+  with open(path, "rb") as f:
+    n = int.from_bytes(f.read(8), "little")
+    f.seek(start + header[_key(2, "w2.weight_scale")]["data_offsets"][0])
+    raw = f.read(LAT * I // 32)
+  assert start == 8 + n
+  assert np.array_equal(np.frombuffer(raw, np.uint8).reshape(LAT, I // 32), experts[2]["w2.weight_scale"])
+  # an expert's six tensors lie back to back in this file: one span covers them
+  offs = sorted(header[_key(2, k)]["data_offsets"] for k in experts[2])
+  assert all(a[1] == b[0] for a, b in zip(offs, offs[1:]))
+
+
+def test_sharded_checkpoint_with_index(tmp_path):
+  """gate/up of every expert in one shard, down in another: the six tensors of
+  an expert span two files, so they are read one by one."""
+  rng = np.random.default_rng(2)
+  tensors, experts = _checkpoint(rng, 8)
+  a = {k: v for k, v in tensors.items() if ".w2." not in k}
+  b = {k: v for k, v in tensors.items() if ".w2." in k}
+  save_file(a, str(tmp_path / "model-00001-of-00002.safetensors"))
+  save_file(b, str(tmp_path / "model-00002-of-00002.safetensors"))
+  wm = {k: "model-00001-of-00002.safetensors" for k in a}
+  wm.update({k: "model-00002-of-00002.safetensors" for k in b})
+  with open(tmp_path / "model.safetensors.index.json", "w") as f:
+    json.dump({"metadata": {}, "weight_map": wm}, f)
+  got = loader.load_mxfp4_experts(str(tmp_path), LAYER, range(2, 6), device="cpu")
+  _check(got, experts, [2, 3, 4, 5])
+  os.remove(tmp_path / "model.safetensors.index.json")  # directory without an index
+  got = loader.load_mxfp4_experts(str(tmp_path), LAYER, range(2, 6), device="cpu")
+  _check(got, experts, [2, 3, 4, 5])
+
+
+def test_non_contiguous_expert_in_one_file(tmp_path):
+  """Interleaved experts (a writer that orders keys differently): the single
+  span check fails and the reader falls back to per-tensor reads."""
+  rng = np.random.default_rng(3)
+  _, experts = _checkpoint(rng, 3)
+  # hand-written file, tensors in the order w1(e0) w1(e1) ... so e0 is split
+  order = [(e, k) for k in experts[0] for e in range(3)]
+  header, blobs, off = {}, [], 0
+  for e, k in order:
+    v = experts[e][k]
+    header[_key(e, k)] = {"dtype": "U8", "shape": list(v.shape), "data_offsets": [off, off + v.nbytes]}
+    blobs.append(v.tobytes())
+    off += v.nbytes
+  hb = json.dumps(header).encode()
+  hb += b" " * (-len(hb) % 8)
+  path = tmp_path / "x.safetensors"
+  path.write_bytes(len(hb).to_bytes(8, "little") + hb + b"".join(blobs))
+  got = loader.load_mxfp4_experts(str(path), LAYER, [1, 0, 2], device="cpu")
+  _check(got, experts, [1, 0, 2])
+
+
+def test_errors(tmp_path):
+  rng = np.random.default_rng(4)
+  tensors, experts = _checkpoint(rng, 4)
+  path = str(tmp_path / "m.safetensors")
+  save_file(tensors, path)
+  with pytest.raises(KeyError, match="expert 7"):
+    loader.load_mxfp4_experts(path, LAYER, [1, 7], device="cpu")
+  with pytest.raises(KeyError):
+    loader.load_mxfp4_experts(path, LAYER + 2, [0], device="cpu")
+  with pytest.raises(ValueError, match="no experts"):
+    loader.load_mxfp4_experts(path, LAYER, [], device="cpu")
+  # a shape that differs from the first expert's
+  bad = dict(tensors)
+  bad[_key(2, "w2.weight_scale")] = np.zeros((LAT, I // 16), np.uint8)
+  save_file(bad, str(tmp_path / "bad.safetensors"))
+  with pytest.raises(ValueError, match="expert 2"):
+    loader.load_mxfp4_experts(str(tmp_path / "bad.safetensors"), LAYER, [0, 2], device="cpu")
+  # gate scales inconsistent with the packed K
+  bad = dict(tensors)
+  bad[_key(0, "w1.weight_scale")] = np.zeros((I, LAT // 16), np.uint8)
+  save_file(bad, str(tmp_path / "bad2.safetensors"))
+  with pytest.raises(ValueError, match="gate/up shapes"):
+    loader.load_mxfp4_experts(str(tmp_path / "bad2.safetensors"), LAYER, [0], device="cpu")
+  # not U8
+  bad = dict(tensors)
+  bad[_key(1, "w3.weight_packed")] = experts[1]["w3.weight_packed"].astype(np.int8)
+  save_file(bad, str(tmp_path / "bad3.safetensors"))
+  with pytest.raises(ValueError, match="U8"):
+    loader.load_mxfp4_experts(str(tmp_path / "bad3.safetensors"), LAYER, [1], device="cpu")
+  # truncated file: the header is intact, the data section is short
+  raw = open(path, "rb").read()
+  (tmp_path / "trunc.safetensors").write_bytes(raw[:-100])
+  with pytest.raises(ValueError, match="outside the file"):  # the other layer's expert is stored last
+    loader.load_mxfp4_experts(str(tmp_path / "trunc.safetensors"), LAYER + 1, [0], device="cpu")
+  (tmp_path / "short.safetensors").write_bytes(b"\x05\x00")
+  with pytest.raises(ValueError, match="not a safetensors"):
+    loader.read_header(str(tmp_path / "short.safetensors"))
+  (tmp_path / "huge.safetensors").write_bytes((1 << 40).to_bytes(8, "little") + b"{}")
+  with pytest.raises(ValueError, match="exceeds"):
+    loader.read_header(str(tmp_path / "huge.safetensors"))

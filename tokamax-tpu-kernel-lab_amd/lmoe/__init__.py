@@ -9,7 +9,8 @@ kernels through the C-ABI library ``liblmoe.so`` (declared in
   ops       reference-shaped operators: ragged_dot, _router_gate,
             filter_and_pad_to_shard[_jittable], _combine_shard_contribution, ...
   forward   latent_moe_forward family
-  mx        MXFP4 weight preparation
+  loader    MXFP4 expert weights from safetensors checkpoints
+  kernel_bench  per-kernel timing helpers
   workloads seeded synthetic inputs for the BASELINE configs
 """
 
