@@ -119,6 +119,25 @@ int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_
                           int zero_group, int mode, int epilogue, float beta, float beta_lin,
                           void* out, void* stream);
 
+/* ---- a18, decode regime: skinny-M grouped GEMM on tiled MXFP4 weights -------------
+ * Same result contract as lmoe_ragged_dot_mxfp4 with LMOE_MXFP4_LDS_DEQUANT_TILED
+ * (w_tiled / s_tiled from lmoe_mxfp4_tile, bf16 lhs and out, epilogue
+ * LMOE_EPI_NONE or LMOE_EPI_SITU, flags 0 or LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS),
+ * for the case the reference's decode sweep runs through the same ragged_dot
+ * (rd.py:553-577: num_tokens 1..128, a few rows per local expert) and the
+ * config-4 matmul at small M (odq.py:65-172).  Each weight byte of a group
+ * with rows is read once per pass of 16 * c rows, c in {1, 2, 4} chosen from
+ * min(M, max_group_rows) (max_group_rows <= 0: unknown; a bound that is too
+ * small only costs extra passes).  Partial sums are added in a fixed order
+ * (repeatable bit for bit) but not in the tile kernel's: the two agree within
+ * bf16 rounding, not bit for bit.  K % 128 == 0, N % 16 == 0 (N % 32 with
+ * SiTU), G <= 1024; lhs, w_tiled and out 16-byte aligned.  No workspace.
+ */
+int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_tiled, const uint8_t* s_tiled,
+                                 const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                                 int zero_group, int flags, int epilogue, float beta, float beta_lin,
+                                 int64_t max_group_rows, void* out, void* stream);
+
 /* ---- dense projections on hipBLASLt ------------------------------------------------
  * out (M, N) = x (M, K) @ w_nk^T, w_nk stored (N, K): the layer's plain dense
  * projections (x = hidden @ down_proj, ref.py:634-655; out = normed @ up_proj,

@@ -46,6 +46,16 @@ def test_version_and_error_string(L):
                                        ctypes.c_void_p(16), 16, 96, 16, 1, -1, 0, 0, 0.0, 0.0,
                                        ctypes.c_void_p(16), None), _lib.ERR_UNSUPPORTED),
     (lambda L: L.lmoe_mxfp4_dequant(None, None, 1, 4, 33, 32, None, 0, None), _lib.ERR_INVALID),
+    # skinny MXFP4 GEMM: K % 128, group count, flags
+    (lambda L: L.lmoe_ragged_dot_mxfp4_skinny(ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256),
+                                              ctypes.c_void_p(256), 16, 192, 64, 1, -1, 0, 0, 0.0, 0.0, 0,
+                                              ctypes.c_void_p(256), None), _lib.ERR_UNSUPPORTED),
+    (lambda L: L.lmoe_ragged_dot_mxfp4_skinny(ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256),
+                                              ctypes.c_void_p(256), 16, 128, 64, 1025, -1, 0, 0, 0.0, 0.0, 0,
+                                              ctypes.c_void_p(256), None), _lib.ERR_UNSUPPORTED),
+    (lambda L: L.lmoe_ragged_dot_mxfp4_skinny(ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256),
+                                              ctypes.c_void_p(256), 16, 128, 64, 1, -1, 0x2, 0, 0.0, 0.0, 0,
+                                              ctypes.c_void_p(256), None), _lib.ERR_INVALID),
 ])
 def test_argument_validation(L, call, code):
   assert call(L) == code

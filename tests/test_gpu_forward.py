@@ -238,3 +238,59 @@ def test_local_shard_layer_from_safetensors_checkpoint(gpu_device, tmp_path):
                                local_num_experts=L, expert_format="mxfp4", experts=loaded,
                                capacity_factor=c.capacity_factor)
   assert torch.equal(layer2.forward(hidden), layer.forward(hidden))
+
+
+@pytest.mark.parametrize("tokens", [1, 16, 64])
+def test_local_shard_layer_decode_matches_oracle(gpu_device, tokens):
+  """Decode regime (rd.py:553-577: num_tokens 1..128 through the same layer):
+  the expert GEMMs take the skinny MXFP4 kernel; output vs the oracle's
+  single-shard forward at the bf16 bar, the stage-returning run (padding rows
+  written) bit-identical, and one HIP-graph replay equal to the eager run."""
+  from lmoe import ops
+  c, hidden, w, experts, layer = _mxfp4_layer(gpu_device, tokens=tokens)
+  assert layer._decode_path(tokens)
+  L = c.local_experts
+  deq = lambda p, s: np.stack([O.dequantize_mxfp4(to_np(p[g]), to_np(s[g])) for g in range(L + 1)])
+  gu = deq(experts["gu_packed"], experts["gu_scale"])
+  dn = deq(experts["down_packed"], experts["down_scale"])
+  I = c.intermediate
+  gate, up = gu[:, :I, :].transpose(0, 2, 1), gu[:, I:, :].transpose(0, 2, 1)
+  down = dn.transpose(0, 2, 1)
+  wn = {k: to_np(v) for k, v in w.items()}
+  ref, st = O.single_shard_forward(to_np(hidden), wn, gate, up, down, c.config(), "bf16", c.local_start, L,
+                                   capacity_factor=c.capacity_factor, include_shared=False)
+  out = layer.forward(hidden)
+  out_st, gs = layer.forward(hidden, return_stages=True)
+  assert torch.equal(out, out_st)
+  idx = to_np(gs["topk_idx"])
+  if np.array_equal(idx, st["topk_idx"]):
+    assert np.array_equal(to_np(gs["dispatch"].group_sizes), st["dispatch"].group_sizes)
+    assert max_rel(to_np(gs["shard_out"]), st["shard_out"]) <= 2e-2
+    assert max_rel(to_np(out), ref) <= 2e-2
+  else:
+    assert np.mean(np.all(idx == st["topk_idx"], axis=1)) >= 0.9
+  # the skinny gate/up GEMM against the tile kernel on this layer's own
+  # dispatch (valid rows; the padding rows are written as zeros by both)
+  cfg = c.config()
+  d = gs["dispatch"]
+  tile = ops.ragged_dot_mxfp4(d.sorted_tokens, layer.experts["gu_packed_tiled"], layer.experts["gu_scale_tiled"],
+                              d.group_sizes, zero_group=L, weight_layout="tiled",
+                              fuse_gateup_activation=f"situ:{cfg.activation_situ_beta}:{cfg.activation_situ_linear_beta}")
+  assert max_rel(to_np(gs["act"]), to_np(tile)) <= 2e-2
+  if tokens == 1:
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+      layer.forward(hidden)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+      gout = layer.forward(hidden)
+    for _ in range(2):
+      eager = layer.forward(hidden)
+      torch.cuda.synchronize()
+      gout.zero_()
+      g.replay()
+      torch.cuda.synchronize()
+      assert torch.equal(gout, eager)

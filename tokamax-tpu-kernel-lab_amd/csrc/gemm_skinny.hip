@@ -1,0 +1,400 @@
+// Skinny-M grouped MXFP4 GEMM for the decode regime: the ragged_dot of the
+// local-shard expert FFN when each group holds a handful of rows
+// (rd.py:553-577 sweeps num_tokens 1..128 through the same ragged_dot; at
+// T=1, k=16 about three local experts receive one row each), and the config-4
+// MXFP4 matmul at small M.  Math: lhs @ deq(W_g)^T as in odq.py:65-172.
+//
+// Here the weight read is the whole cost (a few rows per 2 MB expert) and
+// the time is set by memory latency, so the kernel is built to put each
+// weight byte in flight once, early, from as many waves as possible:
+//   * work item = (hit group, 16 output columns); the block's waves (4, or 8
+//     when there are few items) split the item's K axis and reduce their
+//     accumulators in LDS in a fixed wave order -- deterministic, no atomics,
+//     no workspace;
+//   * the hit groups (nonzero rows, not the padding group) are compacted in
+//     LDS first, so padding and empty experts cost no work, and the grid is
+//     the number of blocks resident at once, each walking items with a grid
+//     stride;
+//   * a wave issues the loads of up to four k-step pairs (weights and the
+//     activations of every row chunk) before their MFMAs;
+//   * weights come from the k-step-major tiled layout (lmoe_mxfp4_tile): the
+//     16 columns x 2 k-steps a wave reads per load are two contiguous 512 B
+//     runs, expanded in registers with v_cvt_scalef32_pk_bf16_fp4 and fed to
+//     v_mfma_f32_16x16x32_bf16 as the A operand (rows of the MFMA = weight
+//     columns), the activations as the B operand, so each lane ends with four
+//     consecutive output columns of one row (8-byte stores).
+// A group's rows are taken 16, 32 or 64 at a time (template NC, from the
+// caller's bound on group rows); larger groups take further passes over the
+// same weights (correct for any group size, fast for small ones).
+#include "lmoe_common.h"
+#include "gemm_tile.h"
+
+#include <algorithm>
+#include <atomic>
+
+namespace lmoe {
+namespace gemm {
+namespace {
+
+constexpr int kSkMaxChunks = 4;    // 16-row chunks per pass: 1, 2 or 4 (template NC)
+constexpr int kSkMaxGroups = 1024;
+
+struct SkinnyParams {
+  const uint16_t* x;     // (M, K) bf16, rows sorted by group
+  const uint8_t* w;      // (G, K/64, N, 32) tiled e2m1 pairs
+  const uint8_t* s;      // (G, K/64, N, 2) tiled E8M0 scales
+  const int32_t* gs;     // (G,)
+  int64_t M, K, N, G;
+  int zero_group;
+  int skip_zero_rows;
+  float beta, beta_lin;
+  uint16_t* out;         // (M, N) bf16, or (M, N/2) with the SiTU epilogue
+  int n_ct;              // 16-column output tiles
+};
+
+// One packed dword (8 e2m1 values, low nibble first) with its scale byte ->
+// 8 bf16, exactly as dequant32 does it.
+__device__ __forceinline__ bf16x8_t dq8(uint32_t w, uint32_t sb) {
+  uint4 o;
+  if (hw_scale_ok(sb)) {
+    const float sc = __uint_as_float(sb << 23);
+    o.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 0));
+    o.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 1));
+    o.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 2));
+    o.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, sc, 3));
+  } else {
+    const float sc = e8m0_to_float(sb);
+    uint32_t r[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const uint32_t byte = (w >> (8 * b)) & 0xffu;
+      r[b] = fp4_to_bf16_bits(byte & 15u, sc) | (fp4_to_bf16_bits(byte >> 4, sc) << 16);
+    }
+    o = uint4{r[0], r[1], r[2], r[3]};
+  }
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : i == 1 ? v.y : i == 2 ? v.z : v.w;
+}
+
+template <int EPI>
+__device__ __forceinline__ void store_out(const SkinnyParams& p, int64_t row, int64_t col, int64_t nout,
+                                          const floatx4 (&v)[EPI == kEpiSitu ? 2 : 1]) {
+  float o[4];
+  if constexpr (EPI == kEpiSitu) {
+    const SituConsts sc = situ_consts(p.beta, p.beta_lin);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // the reference rounds both GEMM outputs to bf16 before the activation
+      const float g = static_cast<float>(static_cast<__bf16>(v[0][e]));
+      const float u = static_cast<float>(static_cast<__bf16>(v[1][e]));
+      o[e] = situ_epi(g, u, sc);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = v[0][e];
+  }
+  *reinterpret_cast<uint2*>(p.out + row * nout + col) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+}
+
+template <int EPI, int NC, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void skinny_mx_kernel(SkinnyParams p) {
+  constexpr int kThreads = WAVES * 64;
+  constexpr int GPT = kSkMaxGroups / kThreads;       // groups per thread in the table scan
+  constexpr int NB = EPI == kEpiSitu ? 2 : 1;        // gate and up tiles
+  // k-step pairs in flight per wave (fewer with two weight tiles: registers)
+  constexpr int D = (NC == 1 ? 4 : NC == 2 ? 2 : 1) / (NB == 2 && NC < 4 ? 2 : 1);
+  __shared__ int32_t s_hit_g[kSkMaxGroups];
+  __shared__ int32_t s_hit_n[kSkMaxGroups];
+  __shared__ int64_t s_hit_r0[kSkMaxGroups];
+  __shared__ uint64_t s_wsum[WAVES];
+  __shared__ int64_t s_misc[4];  // zero-group first row, zero-group rows, sum of rows (<= M), hit groups
+  __shared__ floatx4 s_red[WAVES - 1][NB][64];
+
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int64_t M = p.M, K = p.K, N = p.N, G = p.G;
+  const int64_t nout = N / NB;
+
+  // ---- hit-group table: exclusive scan of (rows << 16 | hit) over <= 1024 groups
+  if (t == 0) {
+    s_misc[0] = 0;
+    s_misc[1] = 0;
+  }
+  int64_t sz[GPT];
+  uint64_t v = 0;
+#pragma unroll
+  for (int i = 0; i < GPT; ++i) {
+    const int64_t g = GPT * t + i;
+    const int32_t n = g < G ? p.gs[g] : 0;
+    sz[i] = n > 0 ? n : 0;
+    v += (static_cast<uint64_t>(sz[i]) << 16) + ((sz[i] > 0 && g != p.zero_group) ? 1u : 0u);
+  }
+  uint64_t incl = v;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const uint64_t o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl += o;
+  }
+  if (lane == 63) s_wsum[wv] = incl;
+  __syncthreads();
+  uint64_t excl = incl - v;
+  for (int w = 0; w < wv; ++w) excl += s_wsum[w];
+  {
+    int64_t r = static_cast<int64_t>(excl >> 16);
+    int h = static_cast<int>(excl & 0xffffu);
+#pragma unroll
+    for (int i = 0; i < GPT; ++i) {
+      const int64_t g = GPT * t + i;
+      if (g < G) {
+        const int64_t n = sz[i];
+        const int64_t rows = std::max<int64_t>(0, std::min<int64_t>(n, M - r));  // rows past M are dropped
+        if (n > 0 && g != p.zero_group) {
+          s_hit_g[h] = static_cast<int32_t>(g);
+          s_hit_r0[h] = r;
+          s_hit_n[h] = static_cast<int32_t>(rows);
+          ++h;
+        }
+        if (g == p.zero_group) {
+          s_misc[0] = r;
+          s_misc[1] = rows;
+        }
+        r += n;
+      }
+    }
+    if (t == kThreads - 1) {
+      s_misc[2] = std::min<int64_t>(r, M);
+      s_misc[3] = h;
+    }
+  }
+  __syncthreads();
+
+  // ---- zero rows: the padding group and rows past sum(group_sizes)
+  if (!p.skip_zero_rows) {
+    const int64_t z0 = s_misc[0], zn = s_misc[1], S = s_misc[2];
+    const int64_t per_row = nout / 8;
+    const int64_t total = (zn + (M - S)) * per_row;
+    for (int64_t c = static_cast<int64_t>(blockIdx.x) * kThreads + t; c < total;
+         c += static_cast<int64_t>(gridDim.x) * kThreads) {
+      const int64_t rr = c / per_row, cc = c % per_row;
+      const int64_t row = rr < zn ? z0 + rr : S + (rr - zn);
+      reinterpret_cast<uint4*>(p.out + row * nout)[cc] = uint4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  // ---- items: (hit group, 16-column tile), K split over the block's waves
+  const int64_t nhit = s_misc[3];
+  const int nct = p.n_ct;
+  const int64_t items = nhit * nct;
+  const int64_t K64 = K / 64;
+  const int P = static_cast<int>(K / 128);  // k-step pairs
+  const int q = lane >> 4, ks_off = q >> 1, hh = q & 1, l16 = lane & 15;
+
+  for (int64_t it = blockIdx.x; it < items; it += gridDim.x) {
+    const int ct = static_cast<int>(it % nct);
+    const int64_t hi = it / nct;
+    const int64_t g = s_hit_g[hi], r0 = s_hit_r0[hi];
+    const int rows = s_hit_n[hi];
+    const int64_t colw = static_cast<int64_t>(ct) * 16 + l16;  // this lane's weight column (gate half)
+    const uint8_t* wb = p.w + g * K64 * N * 32 + hh * 16;
+    const uint8_t* sb = p.s + g * K64 * N * 2;
+    auto ldw = [&](int pr, uint4 (&w)[NB], uint32_t (&sc)[NB]) {
+      const int64_t kst = 2 * static_cast<int64_t>(pr) + ks_off;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int64_t col = colw + nb * nout;
+        w[nb] = *reinterpret_cast<const uint4*>(wb + (kst * N + col) * 32);
+        sc[nb] = *reinterpret_cast<const uint16_t*>(sb + (kst * N + col) * 2);
+      }
+    };
+    const int64_t oc = static_cast<int64_t>(ct) * 16 + 4 * q;  // this lane's first output column
+
+    for (int rb = 0; rb < rows; rb += 16 * NC) {
+      const int nrc = std::min(NC, (rows - rb + 15) / 16);
+      auto ldx = [&](int pr, int rc, uint4 (&x)[4]) {
+        const int lr = rb + rc * 16 + l16;
+        if (lr < rows) {
+          const uint16_t* xp = p.x + (r0 + lr) * K + (2 * static_cast<int64_t>(pr) + ks_off) * 64 + hh * 8;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) x[s] = *reinterpret_cast<const uint4*>(xp + 16 * s);
+        } else {
+#pragma unroll
+          for (int s = 0; s < 4; ++s) x[s] = uint4{0u, 0u, 0u, 0u};
+        }
+      };
+
+      floatx4 acc[NC][NB];
+#pragma unroll
+      for (int rc = 0; rc < NC; ++rc)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[rc][nb] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+      // this wave's k-step pairs wv, wv + WAVES, ...: D of them in flight at
+      // once (weights and every row chunk's activations), then their MFMAs
+      for (int j0 = wv; j0 < P; j0 += WAVES * D) {
+        uint4 w[D][NB], x[D][NC][4];
+        uint32_t sc[D][NB];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+          const int pr = j0 + WAVES * d;
+          if (pr < P) {
+            ldw(pr, w[d], sc[d]);
+#pragma unroll
+            for (int rc = 0; rc < NC; ++rc)
+              if (rc < nrc) ldx(pr, rc, x[d][rc]);
+          }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+          if (j0 + WAVES * d < P) {
+            bf16x8_t a[NB][4];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+              for (int s = 0; s < 4; ++s)
+                a[nb][s] = dq8(word(w[d][nb], s), s < 2 ? (sc[d][nb] & 0xffu) : (sc[d][nb] >> 8));
+#pragma unroll
+            for (int rc = 0; rc < NC; ++rc) {
+              if (rc < nrc) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s) {
+                  const bf16x8_t bx = __builtin_bit_cast(bf16x8_t, x[d][rc][s]);
+#pragma unroll
+                  for (int nb = 0; nb < NB; ++nb)
+                    acc[rc][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[nb][s], bx, acc[rc][nb], 0, 0, 0);
+                }
+              }
+            }
+          }
+        }
+      }
+
+      // block reduction in wave order 0, 1, ..., WAVES-1, then the epilogue
+#pragma unroll
+      for (int rc = 0; rc < NC; ++rc) {
+        if (rc < nrc) {
+          __syncthreads();
+          if (wv > 0) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) s_red[wv - 1][nb][lane] = acc[rc][nb];
+          }
+          __syncthreads();
+          if (wv == 0) {
+            floatx4 sum[NB];
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              sum[nb] = acc[rc][nb];
+#pragma unroll
+              for (int w = 0; w < WAVES - 1; ++w) sum[nb] += s_red[w][nb][lane];
+            }
+            const int lr = rb + rc * 16 + l16;
+            if (lr < rows) store_out<EPI>(p, r0 + lr, oc, nout, sum);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Rows per pass: the smallest of 16, 32, 64 covering the largest group
+// (bounded by M and by the caller's hint); larger groups take more passes.
+int skinny_chunks(int64_t M, int64_t max_group_rows) {
+  const int64_t bound = max_group_rows > 0 ? std::min(M, max_group_rows) : M;
+  int nc = 1;
+  while (nc < kSkMaxChunks && 16 * nc < bound) nc *= 2;
+  return nc;
+}
+
+// Blocks of one instance resident at once on the device: the grid size (each
+// block walks items with a grid stride, so no block sits idle past the first
+// wave of blocks).
+template <int EPI, int NC, int WAVES>
+unsigned resident_blocks() {
+  static std::atomic<unsigned> cached{0};
+  unsigned v = cached.load(std::memory_order_relaxed);
+  if (v == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, skinny_mx_kernel<EPI, NC, WAVES>, WAVES * 64, 0) !=
+            hipSuccess ||
+        cus <= 0 || per_cu <= 0) {
+      cus = 256;
+      per_cu = 1;
+    }
+    v = static_cast<unsigned>(cus * per_cu);
+    cached.store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
+
+template <int EPI, int NC, int WAVES>
+void launch_one(const SkinnyParams& p, int64_t upper, hipStream_t st) {
+  const unsigned grid =
+      static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(upper, resident_blocks<EPI, NC, WAVES>())));
+  skinny_mx_kernel<EPI, NC, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+}
+
+template <int EPI, int WAVES>
+void launch_nc(const SkinnyParams& p, int nc, int64_t upper, hipStream_t st) {
+  switch (nc) {
+    case 1: launch_one<EPI, 1, WAVES>(p, upper, st); break;
+    case 2: launch_one<EPI, 2, WAVES>(p, upper, st); break;
+    default: launch_one<EPI, 4, WAVES>(p, upper, st); break;
+  }
+}
+
+}  // namespace
+}  // namespace gemm
+}  // namespace lmoe
+
+using namespace lmoe;
+using namespace lmoe::gemm;
+
+extern "C" int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_tiled, const uint8_t* s_tiled,
+                                            const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                                            int zero_group, int flags, int epilogue, float beta, float beta_lin,
+                                            int64_t max_group_rows, void* out, void* stream) {
+  const char* name = "ragged_dot_mxfp4_skinny";
+  LMOE_CHECK_ARG(M >= 0 && K > 0 && N > 0 && G > 0, "%s: bad sizes M=%lld K=%lld N=%lld G=%lld", name,
+                 (long long)M, (long long)K, (long long)N, (long long)G);
+  LMOE_CHECK_ARG(zero_group >= -1 && zero_group < G, "%s: bad zero_group %d", name, zero_group);
+  LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
+  LMOE_CHECK_ARG((flags & ~LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS) == 0, "%s: unknown flags 0x%x", name, flags);
+  const int epi = epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone;
+  LMOE_CHECK_SUPPORTED(K % 128 == 0, "%s: needs K %% 128 == 0 (K=%lld)", name, (long long)K);
+  LMOE_CHECK_SUPPORTED(N % (epi == kEpiSitu ? 32 : 16) == 0, "%s: needs 16-column output tiles (N=%lld)", name,
+                       (long long)N);
+  LMOE_CHECK_SUPPORTED(G <= kSkMaxGroups, "%s: at most %d groups (G=%lld)", name, kSkMaxGroups, (long long)G);
+  LMOE_CHECK_SUPPORTED(M < (1ll << 31), "%s: M=%lld", name, (long long)M);
+  if (M == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(lhs && w_tiled && s_tiled && group_sizes && out, "%s: null pointer", name);
+  LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(w_tiled, 16) && aligned(out, 16) && aligned(s_tiled, 2),
+                       "%s: lhs, weights and out must be 16-byte aligned", name);
+  const int nc = skinny_chunks(M, max_group_rows);
+  const int64_t nout = epi == kEpiSitu ? N / 2 : N;
+  const int64_t nct = nout / 16;
+  SkinnyParams p{static_cast<const uint16_t*>(lhs), w_tiled, s_tiled, group_sizes, M, K, N, G, zero_group,
+                 (flags & LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS) != 0, beta, beta_lin, static_cast<uint16_t*>(out),
+                 static_cast<int>(nct)};
+  // at most min(G, M) groups have rows: with fewer items than one per CU,
+  // eight waves per item (more of the K axis in flight), else four
+  const int64_t items_bound = std::min<int64_t>(G, M) * nct;
+  const int64_t upper = std::max(items_bound, ceil_div(M * nout / 8, 256));
+  const bool wide = items_bound < 256;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (epi == kEpiSitu) {
+    if (wide)
+      launch_nc<kEpiSitu, 8>(p, nc, upper, st);
+    else
+      launch_nc<kEpiSitu, 4>(p, nc, upper, st);
+  } else {
+    if (wide)
+      launch_nc<kEpiNone, 8>(p, nc, upper, st);
+    else
+      launch_nc<kEpiNone, 4>(p, nc, upper, st);
+  }
+  LMOE_CHECK_LAUNCH(name);
+  return LMOE_OK;
+}

@@ -146,7 +146,8 @@ class LocalShardLatentMoE:
   def __init__(self, config: LatentMoEConfig, *, router_weight, e_score_correction_bias, down_proj,
                up_proj, norm_scale, local_expert_start: int, local_num_experts: int,
                expert_format: str, experts: dict, shared: dict | None = None,
-               capacity_factor: float = 2.0, act: str = "sigmoid", mxfp4_mode: str = "lds_dequant"):
+               capacity_factor: float = 2.0, act: str = "sigmoid", mxfp4_mode: str = "lds_dequant",
+               decode_tokens: int = 64):
     self.config = config
     self.L = local_num_experts
     self.start = local_expert_start
@@ -154,6 +155,10 @@ class LocalShardLatentMoE:
     self.act = act
     self.expert_format = expert_format
     self.mxfp4_mode = mxfp4_mode
+    # up to this many tokens the expert GEMMs run the skinny (decode) MXFP4
+    # kernel: no local expert receives more than T rows (a token picks an
+    # expert at most once), so a pass of up to T rows covers every group
+    self.decode_tokens = decode_tokens
     self.router_nk = router_weight.t().contiguous()
     self.bias = e_score_correction_bias.float().contiguous()
     self.down_nk = down_proj.t().contiguous()
@@ -177,6 +182,15 @@ class LocalShardLatentMoE:
         pk, sc = ops.mxfp4_tile_weights(experts[f"{w}_packed"], experts[f"{w}_scale"])
         self.experts[f"{w}_packed_tiled"], self.experts[f"{w}_scale_tiled"] = pk, sc
       self.weight_layout, self._sfx = "tiled", "_tiled"
+
+  def _decode_path(self, t: int) -> bool:
+    """Decode regime: few tokens, lds_dequant mode on tiled weights, shapes
+    the skinny kernel takes (both expert GEMMs)."""
+    if t > self.decode_tokens or self.mxfp4_mode != "lds_dequant" or self.weight_layout != "tiled":
+      return False
+    c = self.config
+    return (ops.skinny_supported(c.latent_size, 2 * c.intermediate_size, self.L + 1, True)
+            and ops.skinny_supported(c.intermediate_size, c.latent_size, self.L + 1, False))
 
   def _dense(self, x, w_nk, out_dtype=None):
     return ops.dense(x, w_nk, out_dtype=out_dtype, w_layout="nk")
@@ -202,6 +216,9 @@ class LocalShardLatentMoE:
     m_padded = ops.compute_m_padded(t, c.top_k, c.num_experts, self.L, self.cf)
     d = ops.dispatch_local(idx, w, x, self.start, self.L, m_padded)
     E = self.experts
+    mx_mode, mx_kw = self.mxfp4_mode, {}
+    if self.expert_format == "mxfp4" and self._decode_path(t):
+      mx_mode, mx_kw = "skinny", {"max_group_rows": t}
     if "gateup" in ev:
       ev["gateup"][0].record()
     if self.expert_format == "mxfp4":
@@ -209,9 +226,9 @@ class LocalShardLatentMoE:
       # unwritten unless the stages are returned
       act = ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed" + self._sfx], E["gu_scale" + self._sfx],
                                  d.group_sizes,
-                                 fuse_gateup_activation=f"situ:{b}:{bl}", mode=self.mxfp4_mode,
+                                 fuse_gateup_activation=f"situ:{b}:{bl}", mode=mx_mode,
                                  zero_group=self.L, weight_layout=self.weight_layout,
-                                 skip_zero_group_rows=not return_stages)
+                                 skip_zero_group_rows=not return_stages, **mx_kw)
     else:
       act = ops.ragged_dot_gateup_situ(d.sorted_tokens, E["gu_nk"], d.group_sizes, b, bl,
                                        rhs_layout="gnk", zero_group=self.L)
@@ -222,9 +239,9 @@ class LocalShardLatentMoE:
     if self.expert_format == "mxfp4":
       shard_out = ops.ragged_dot_mxfp4(act, E["down_packed" + self._sfx], E["down_scale" + self._sfx],
                                        d.group_sizes,
-                                       mode=self.mxfp4_mode, zero_group=self.L,
+                                       mode=mx_mode, zero_group=self.L,
                                        weight_layout=self.weight_layout,
-                                       skip_zero_group_rows=not return_stages)
+                                       skip_zero_group_rows=not return_stages, **mx_kw)
     else:
       shard_out = ops.ragged_dot(act, E["down_nk"], d.group_sizes, rhs_layout="gnk", zero_group=self.L)
     if "down" in ev:

@@ -134,6 +134,10 @@ def bench_cfg4(dev, rounds, calls):
     ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled"), rounds, calls,
                  name=f"cfg4 mxfp4 matmul tiled weights M={m}")
     report(f"cfg4 mxfp4 matmul tiled weights M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
+    if m <= 128:
+      ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled", mode="skinny"), rounds,
+                   calls, name=f"cfg4 mxfp4 matmul skinny M={m}")
+      report(f"cfg4 mxfp4 matmul skinny M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
     ms = time_fn(lambda: ops.quantize_mxfp8(a), rounds, calls, name=f"cfg4 mxfp8 quantise M={m}")
     report(f"cfg4 mxfp8 quantise M={m}", ms, 0, m * k_ * (2 + 1 + 1 / 32), m=m)
     q, qs = ops.quantize_mxfp8(a)

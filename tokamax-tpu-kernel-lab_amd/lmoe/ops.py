@@ -216,7 +216,13 @@ def dequantize_mxfp4(weight_packed: torch.Tensor, weight_scale: torch.Tensor,
   return out
 
 
-_MX_MODES = {"lds_dequant": _lib.MXFP4_LDS_DEQUANT, "scaled_mfma": _lib.MXFP4_SCALED_MFMA}
+_MX_MODES = {"lds_dequant": _lib.MXFP4_LDS_DEQUANT, "scaled_mfma": _lib.MXFP4_SCALED_MFMA, "skinny": -1}
+
+
+def skinny_supported(k: int, n: int, g: int, situ: bool) -> bool:
+  """Shapes the skinny (decode) MXFP4 kernel takes: K % 128 == 0, 16-column
+  output tiles, at most 1024 groups."""
+  return k % 128 == 0 and n % (32 if situ else 16) == 0 and g <= 1024
 
 
 def mxfp4_tile_weights(w_packed: torch.Tensor, w_scale: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
@@ -292,7 +298,8 @@ def ragged_dot_mxfp8_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
 def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
                      group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
                      mode: str = "lds_dequant", zero_group: int = -1,
-                     weight_layout: str = "checkpoint", skip_zero_group_rows: bool = False) -> torch.Tensor:
+                     weight_layout: str = "checkpoint", skip_zero_group_rows: bool = False,
+                     max_group_rows: int = 0) -> torch.Tensor:
   """Grouped lhs @ deq(W_g)^T with W_g in checkpoint (N, K/2) layout
   (orientation of mxfp4_online_dequant_matmul_pallas.py:1-36) and block-32
   E8M0 scales (G, N, K/32), or with ``weight_layout="tiled"`` the
@@ -301,7 +308,13 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   [gate | up] and the SiTU-GLU epilogue is applied (output width N/2).
   ``skip_zero_group_rows``: the rows of ``zero_group`` and those past
   sum(group_sizes) may be left unwritten (uninitialised) instead of zeroed,
-  for callers that never read them."""
+  for callers that never read them.
+
+  ``mode="skinny"`` (tiled weights, K % 128 == 0): the decode-regime kernel
+  for groups of a few rows -- each weight byte of a group with rows read once
+  per pass of up to 16, 32, 64 or 128 rows, sized from min(M,
+  ``max_group_rows``) (0: unknown).  Equal to the other modes within bf16
+  rounding (another f32 summation order), not bit for bit."""
   _dev(lhs, w_packed, w_scale, group_sizes)
   if lhs.dtype != torch.bfloat16:
     raise NotImplementedError("MXFP4 GEMM takes bf16 activations")
@@ -333,6 +346,15 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
     q, qs = quantize_mxfp8(lhs)
     return ragged_dot_mxfp8_mxfp4(q, qs, w_packed, w_scale, group_sizes,
                                   fuse_gateup_activation=fuse_gateup_activation, zero_group=zero_group)
+  if mode == "skinny":
+    if weight_layout != "tiled":
+      raise NotImplementedError("the skinny kernel reads mxfp4_tile_weights output (weight_layout='tiled')")
+    flags = _lib.MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS if skip_zero_group_rows else 0
+    out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
+    check(lib().lmoe_ragged_dot_mxfp4_skinny(_p(lhs), _p(w_packed), _p(w_scale), _p(group_sizes), m, k, n, g,
+                                             zero_group, flags, epi, b, bl, max_group_rows, _p(out), _stream()),
+          "ragged_dot_mxfp4_skinny")
+    return out
   if weight_layout == "tiled":
     mode_id = _lib.MXFP4_LDS_DEQUANT_TILED
   if skip_zero_group_rows:
