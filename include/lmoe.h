@@ -224,6 +224,23 @@ int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, int w_dtype
                         void* padded_w, int32_t* slot_pos, void* workspace,
                         int64_t workspace_size, void* stream);
 
+/* The same dispatch in one launch for decode-sized batches (T*k <= 8192,
+ * m_padded <= 8192, L < 1024): every output as lmoe_dispatch_local, bit for
+ * bit, except that x may be a row-strided (row stride x_ld elements) bf16 or
+ * f32 array and sorted_tokens is bf16 (f32 rounded to nearest even, the same
+ * rounding as lmoe_cast_rows).  lat % 8 == 0, x rows and sorted_tokens
+ * 16-byte aligned.  With LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS the padding rows
+ * of sorted_tokens (from sum(group_sizes[:L]) on) are left unwritten, for
+ * callers that never read them.  No workspace.
+ */
+#define LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS 0x1
+int lmoe_dispatch_local_small(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
+                              int x_dtype, int64_t x_ld, int64_t T, int64_t k, int64_t lat,
+                              int64_t local_start, int64_t L, int64_t m_padded, uint16_t* sorted_tokens,
+                              int32_t* group_sizes, uint8_t* valid, int32_t* per_expert_counts,
+                              int32_t* padded_token_idx, void* padded_w, int32_t* slot_pos, int flags,
+                              void* stream);
+
 /* ---- a13: combine -----------------------------------------------------------------
  * lmoe_combine_scatter_add replaces _combine_shard_contribution (ref.py:1113-1141):
  * routed_out.at[idx].add((shard_out * w[:, None]).astype(routed_out.dtype)),

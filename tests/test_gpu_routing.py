@@ -185,14 +185,21 @@ DISPATCH_CASES = [
 ]
 
 
-def _run_dispatch(topk_idx, topk_w, x, wdt, start, L, m_padded):
+def _run_dispatch(topk_idx, topk_w, x, wdt, start, L, m_padded, path="sort"):
   from lmoe import ops
-  return ops.dispatch_local(to_dev(topk_idx), to_dev(topk_w, wdt), to_dev(x, "bf16"), start, L, m_padded)
+  t, k = topk_idx.shape
+  if path == "small" and not ops.small_dispatch_supported(t, k, x.shape[1], L, m_padded):
+    pytest.skip("beyond the one-launch dispatch's sizes")
+  return ops.dispatch_local(to_dev(topk_idx), to_dev(topk_w, wdt), to_dev(x, "bf16"), start, L, m_padded,
+                            path=path)
 
 
+@pytest.mark.parametrize("path", ["sort", "small"])
 @pytest.mark.parametrize("name,t,k,e,start,L,cf,tile,wdt", DISPATCH_CASES)
-def test_dispatch_matches_oracle_bit_exact(gpu_device, name, t, k, e, start, L, cf, tile, wdt):
-  banner(f"dispatch {name}")
+def test_dispatch_matches_oracle_bit_exact(gpu_device, name, t, k, e, start, L, cf, tile, wdt, path):
+  """Both dispatch paths (multi-block counting sort; one launch for
+  decode-sized batches) against the oracle, all six outputs and slot_pos."""
+  banner(f"dispatch {name} {path}")
   rng = np.random.default_rng(len(name) * 31 + t)
   topk_idx = np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32)
   topk_w = O.cast(rng.uniform(size=(t, k)), wdt)
@@ -200,7 +207,7 @@ def test_dispatch_matches_oracle_bit_exact(gpu_device, name, t, k, e, start, L, 
   m_padded = O.compute_m_padded(t, k, e, L, cf, tile)
   ref, slot_pos = O.filter_and_pad_to_shard_jittable(topk_idx, topk_w, x, k, e, start, L, cf, tile,
                                                      return_slot_pos=True)
-  got = _run_dispatch(topk_idx, topk_w, x, wdt, start, L, m_padded)
+  got = _run_dispatch(topk_idx, topk_w, x, wdt, start, L, m_padded, path)
   for field in ("sorted_tokens", "group_sizes", "valid_mask", "per_expert_counts", "padded_token_idx",
                 "padded_combine_weight"):
     a, b = to_np(getattr(got, field)), getattr(ref, field)
@@ -209,8 +216,9 @@ def test_dispatch_matches_oracle_bit_exact(gpu_device, name, t, k, e, start, L, 
   assert np.array_equal(to_np(got.slot_pos), slot_pos)
 
 
+@pytest.mark.parametrize("path", ["sort", "small"])
 @pytest.mark.parametrize("case", ["empty_shard", "extreme_skew", "boundary"])
-def test_dispatch_literal_kats(gpu_device, case):
+def test_dispatch_literal_kats(gpu_device, case, path):
   """test_sharded_routing_local.py literal inputs (62-99, 102-125, 232-266)."""
   if case == "empty_shard":
     ti = np.array([[0, 1], [1, 2], [6, 7], [7, 0], [2, 3]], np.int32)
@@ -224,9 +232,33 @@ def test_dispatch_literal_kats(gpu_device, case):
   x = O.bf16_round(np.random.default_rng(5).standard_normal((t, 32)))
   m_padded = O.compute_m_padded(t, k, e, L, 4.0, 1)
   ref = O.filter_and_pad_to_shard(ti, tw, x, k, e, start, L, 4.0, 1)
-  got = _run_dispatch(ti, tw, x, "f32", start, L, m_padded)
+  got = _run_dispatch(ti, tw, x, "f32", start, L, m_padded, path)
   for a, b in zip(got[:6], ref):
     assert np.array_equal(to_np(a), b)
+
+
+@pytest.mark.parametrize("t", [1, 37, 512])
+def test_dispatch_small_from_strided_f32(gpu_device, t):
+  """The one-launch dispatch reading the latent columns of the fused f32
+  router + down-projection output (row stride E + lat) equals cast-to-bf16
+  then the sort path; with the padding rows skipped every other output and
+  the kept rows are unchanged."""
+  from lmoe import ops
+  rng = np.random.default_rng(40 + t)
+  k, e, L, lat = 16, 896, 112, 256
+  topk_idx = torch.tensor(np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32), device="cuda")
+  topk_w = torch.tensor(rng.uniform(size=(t, k)).astype(np.float32), device="cuda")
+  rd = torch.tensor(rng.standard_normal((t, e + lat)).astype(np.float32), device="cuda")
+  m_padded = O.compute_m_padded(t, k, e, L, 2.0, 128)
+  ref = ops.dispatch_local(topk_idx, topk_w, ops.cast_rows(rd[:, e:], torch.bfloat16), 0, L, m_padded, path="sort")
+  got = ops.dispatch_local(topk_idx, topk_w, rd[:, e:], 0, L, m_padded, path="small")
+  for a, b in zip(got, ref):
+    assert torch.equal(a, b)
+  skip = ops.dispatch_local(topk_idx, topk_w, rd[:, e:], 0, L, m_padded, path="small", skip_padding_rows=True)
+  nk = int(ref.group_sizes[:L].sum())
+  assert torch.equal(skip.sorted_tokens[:nk], ref.sorted_tokens[:nk])
+  for a, b in zip(skip[1:], ref[1:]):
+    assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("odt", ["bf16", "f32"])

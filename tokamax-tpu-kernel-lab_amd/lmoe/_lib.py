@@ -34,6 +34,7 @@ MXFP4_LDS_DEQUANT = 0
 MXFP4_SCALED_MFMA = 1
 MXFP4_LDS_DEQUANT_TILED = 2
 MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS = 0x100
+DISPATCH_FLAG_SKIP_PADDING_ROWS = 0x1
 COMBINE_SCATTER_ADD = 0
 COMBINE_SLOT_SUM = 1
 
@@ -60,6 +61,7 @@ SIGNATURES = {
     "lmoe_dispatch_workspace_size": ([I64, I64, I64], I64),
     "lmoe_dispatch_local": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P,
                              I64, P], I32),
+    "lmoe_dispatch_local_small": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, I32, P], I32),
     "lmoe_combine_workspace_size": ([I64, I64], I64),
     "lmoe_combine_scatter_add": ([P, I32, P, P, I32, I64, I64, I64, P, I32, P, I64, P], I32),
     "lmoe_combine_slots": ([P, I32, P, P, I32, I64, I64, I64, I32, P, I32, P], I32),

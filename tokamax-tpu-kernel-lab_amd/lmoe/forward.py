@@ -203,18 +203,31 @@ class LocalShardLatentMoE:
     ev = kernel_events or {}
     t = hidden.shape[0]
     b, bl = c.activation_situ_beta, c.activation_situ_linear_beta
+    m_padded = ops.compute_m_padded(t, c.top_k, c.num_experts, self.L, self.cf)
+    decode = (self._decode_path(t) and hidden.dtype == torch.bfloat16
+              and ops.small_dispatch_supported(t, c.top_k, c.latent_size, self.L, m_padded))
+    x_src = None
     if self.router_down_nk is not None and hidden.dtype == torch.bfloat16:
       e = self.router_nk.shape[0]
       rd = self._dense(hidden, self.router_down_nk, torch.float32)
       logits = rd[:, :e]
-      x = ops.cast_rows(rd[:, e:], hidden.dtype)
+      if decode:
+        # the one-launch dispatch rounds the f32 latent rows to bf16 as it
+        # gathers them: no separate cast
+        x_src = rd[:, e:]
+        x = ops.cast_rows(x_src, hidden.dtype) if return_stages else None
+      else:
+        x = ops.cast_rows(rd[:, e:], hidden.dtype)
     else:
       logits = self._dense(hidden, self.router_nk, torch.float32)
       x = self._dense(hidden, self.down_nk)
     idx, w = ops.router_topk_from_logits(logits, self.bias, c.top_k, c.moe_renormalize,
                                          c.routed_scaling_factor, self.act, hidden.dtype)
-    m_padded = ops.compute_m_padded(t, c.top_k, c.num_experts, self.L, self.cf)
-    d = ops.dispatch_local(idx, w, x, self.start, self.L, m_padded)
+    if decode:
+      d = ops.dispatch_local(idx, w, x_src if x_src is not None else x, self.start, self.L, m_padded, path="small",
+                             skip_padding_rows=not return_stages)
+    else:
+      d = ops.dispatch_local(idx, w, x, self.start, self.L, m_padded, path="sort")
     E = self.experts
     mx_mode, mx_kw = self.mxfp4_mode, {}
     if self.expert_format == "mxfp4" and self._decode_path(t):

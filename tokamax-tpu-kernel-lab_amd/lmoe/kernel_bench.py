@@ -5,7 +5,7 @@ warm-up, then rounds of back-to-back calls timed with device events, median
 over rounds) and its metrics (bf16 TFLOP/s, GB/s, fraction of the binding
 roofline: valid rows only, each weight byte counted once).
 
-  python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5,copy] [--rounds 10] [--calls 20]
+  python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5,decode,copy] [--rounds 10] [--calls 20]
 
 Prints one JSON object per measured kernel.
 """
@@ -28,6 +28,9 @@ PEAK = {"bf16": 2500.0, "fp8": 5000.0, "mxfp4": 10100.0}
 
 _FILTER = None  # substring: only kernels whose name contains it are run
 _PROFILE = False  # run each selected kernel a few times, no timing
+
+
+_DECODE_TOKENS = (1, 2, 4, 8, 16, 32, 64, 128)
 
 
 def time_fn(fn, rounds=10, calls=20, name=""):
@@ -203,6 +206,51 @@ def bench_cfg5(dev, rounds, calls):
   report("cfg5 up-proj GEMM 4096x1024x7168", ms, 2.0 * T * lat * H, T * lat * 2 + lat * H * 2 + T * H * 2)
 
 
+def _capture(layer, hidden):
+  """The layer forward as one HIP graph (warm-up on a side stream of default
+  priority, then capture); returns (replay, static output)."""
+  side = torch.cuda.Stream()
+  side.wait_stream(torch.cuda.current_stream())
+  with torch.cuda.stream(side):
+    layer.forward(hidden)
+  torch.cuda.current_stream().wait_stream(side)
+  torch.cuda.synchronize()
+  g = torch.cuda.CUDAGraph()
+  with torch.cuda.graph(g):
+    out = layer.forward(hidden)
+  torch.cuda.synchronize()
+  return g.replay, out
+
+
+def bench_decode(dev, rounds, calls):
+  """The config-5 layer in the decode regime (rd.py:553-577 sweeps
+  num_tokens 1..128): T tokens through the full local-shard forward, timed as
+  HIP-graph replays (the serving loop's launch mode).  Bytes per step = the
+  dense projection weights (router, down, up) + the MXFP4 weights of the
+  local experts that receive rows; the roofline is those bytes at 8 TB/s."""
+  from .forward import LocalShardLatentMoE
+  c = Config5()
+  hidden, w, experts = make_config5(dev, c, "mxfp4")
+  layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                              e_score_correction_bias=w["e_score_correction_bias"],
+                              down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                              local_expert_start=c.local_start, local_num_experts=c.local_experts,
+                              expert_format="mxfp4", experts=experts, capacity_factor=c.capacity_factor)
+  L, lat, inter, H = c.local_experts, c.latent, c.intermediate, c.hidden
+  dense_bytes = 2 * H * (c.experts + 2 * lat)
+  expert_bytes = (2 * inter * lat + lat * inter) * (0.5 + 1 / 32)
+  for t in _DECODE_TOKENS:
+    h = hidden[:t].contiguous()
+    _, st = layer.forward(h, return_stages=True)
+    gs = st["dispatch"].group_sizes.cpu().numpy()
+    hit = int((gs[:L] > 0).sum())
+    replay, _ = _capture(layer, h)
+    nm = f"decode layer T={t}"
+    ms = time_fn(replay, rounds, calls, name=nm)
+    report(nm, ms, 0, dense_bytes + hit * expert_bytes + t * H * 4, tokens=t, experts_hit=hit,
+           skinny_expert_gemms=layer._decode_path(t), tokens_per_s=round(t / (ms / 1000)) if ms else None)
+
+
 def bench_copy(dev, rounds, calls):
   """Plain 256 MiB device copy: the calibration kernel for the HBM traffic
   counters (FETCH_SIZE / WRITE_SIZE should read 256 MiB each)."""
@@ -220,9 +268,11 @@ def main():
   ap.add_argument("--calls", type=int, default=20)
   ap.add_argument("--kernel", default=None, help="only kernels whose name contains this")
   ap.add_argument("--profile", action="store_true", help="run the selected kernels 5x, untimed")
+  ap.add_argument("--tokens", default="1,2,4,8,16,32,64,128", help="decode: token counts")
   a = ap.parse_args()
-  global _FILTER, _PROFILE
+  global _FILTER, _PROFILE, _DECODE_TOKENS
   _FILTER, _PROFILE = a.kernel, a.profile
+  _DECODE_TOKENS = tuple(int(x) for x in a.tokens.split(","))
   dev = torch.device("cuda:0")
   for name in a.only.split(","):
     globals()[f"bench_{name}"](dev, a.rounds, a.calls)

@@ -519,16 +519,57 @@ class Dispatch(NamedTuple):
   slot_pos: torch.Tensor
 
 
+SMALL_DISPATCH_SLOTS = 8192
+
+
+def small_dispatch_supported(t: int, k: int, lat: int, L: int, m_padded: int) -> bool:
+  """Sizes the one-launch dispatch takes (decode-sized batches)."""
+  return t * k <= SMALL_DISPATCH_SLOTS and m_padded <= 8192 and L + 1 <= 1024 and lat % 8 == 0
+
+
 def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.Tensor,
-                   local_expert_start: int, local_num_experts: int, m_padded: int) -> Dispatch:
-  """The GPU dispatch with an explicit m_padded; also returns slot_pos (T*k,)."""
-  _dev(topk_idx, topk_weight, x)
+                   local_expert_start: int, local_num_experts: int, m_padded: int, *, path: str = "auto",
+                   skip_padding_rows: bool = False) -> Dispatch:
+  """The GPU dispatch with an explicit m_padded; also returns slot_pos (T*k,).
+
+  ``path``: "sort" (the multi-block counting sort + gather), "small" (one
+  launch for decode-sized batches, ``small_dispatch_supported``) or "auto"
+  (small when supported and x is bf16).  Both give the same outputs bit for
+  bit.  The small path also takes x as a row-strided view (unit column
+  stride) of bf16 or f32 values and writes bf16 sorted tokens (f32 rounded to
+  nearest even); ``skip_padding_rows`` then leaves the padding rows of
+  sorted_tokens unwritten."""
   if topk_idx.dtype != torch.int32:
     raise ValueError("topk_idx must be int32")
   t, k = topk_idx.shape
   lat = x.shape[-1]
-  dev = x.device
   L = local_num_experts
+  small_ok = small_dispatch_supported(t, k, lat, L, m_padded)
+  if path == "auto":
+    path = "small" if small_ok and x.dtype == torch.bfloat16 and x.is_contiguous() else "sort"
+  if path == "small":
+    if not small_ok:
+      raise NotImplementedError(f"one-launch dispatch: T*k={t * k}, m_padded={m_padded}, L={L}, lat={lat}")
+    x = _dev_rows(x)
+    _dev(topk_idx, topk_weight)
+    dev = x.device
+    sorted_tokens = torch.empty((m_padded, lat), dtype=torch.bfloat16, device=dev)
+    group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
+    valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
+    counts = torch.empty((L,), dtype=torch.int32, device=dev)
+    tok = torch.empty((m_padded,), dtype=torch.int32, device=dev)
+    w = torch.empty((m_padded,), dtype=topk_weight.dtype, device=dev)
+    slot_pos = torch.empty((t * k,), dtype=torch.int32, device=dev)
+    flags = _lib.DISPATCH_FLAG_SKIP_PADDING_ROWS if skip_padding_rows else 0
+    check(lib().lmoe_dispatch_local_small(_p(topk_idx), _p(topk_weight), _dt(topk_weight), _p(x), _dt(x),
+                                          x.stride(0) if t > 0 else lat, t, k, lat, local_expert_start, L,
+                                          m_padded, _p(sorted_tokens), _p(group_sizes), _p(valid), _p(counts),
+                                          _p(tok), _p(w), _p(slot_pos), flags, _stream()), "dispatch_local_small")
+    return Dispatch(sorted_tokens, group_sizes, valid, counts, tok, w, slot_pos)
+  if path != "sort":
+    raise ValueError(f"path {path!r}")
+  _dev(topk_idx, topk_weight, x)
+  dev = x.device
   sorted_tokens = torch.empty((m_padded, lat), dtype=x.dtype, device=dev)
   group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
   valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
