@@ -148,6 +148,15 @@ int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_tiled, const 
  */
 int lmoe_dense_blaslt(const void* x, int x_dtype, const void* w_nk, int w_dtype, int64_t M, int64_t K, int64_t N,
                       void* out, int out_dtype, void* stream);
+/* The same dense projection for a few rows (a decode step's M = T tokens),
+ * on a hand-written skinny kernel: x (M, K) bf16 @ w_nk^T with bf16 w_nk
+ * (N, K), f32 accumulation, out bf16 or f32.  Each weight byte is read once
+ * per 16/32/64 rows; the K axis is split over a block's waves and summed in a
+ * fixed order (repeatable bit for bit, another order than hipBLASLt's).
+ * K % 128 == 0, N % 16 == 0, pointers 16-byte aligned.  No workspace.
+ */
+int lmoe_dense_skinny(const void* x, const void* w_nk, int64_t M, int64_t K, int64_t N, void* out, int out_dtype,
+                      void* stream);
 
 /* ---- a18: MXFP4 weight preparation ------------------------------------------------
  * One-time weight preparation, the MXFP4 counterpart of prefuse_gateup_weights

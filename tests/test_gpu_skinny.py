@@ -167,3 +167,26 @@ def test_skinny_alternating_layouts_repeatable(gpu_device):
       assert max_rel(to_np(act)[:4], ref[:4]) <= BF16_TOL  # rows of the three hit groups
     else:
       assert torch.equal(act, first[0]) and torch.equal(out, first[1])
+
+
+@pytest.mark.parametrize("m,k,n,odt", [(1, 7168, 1920, "f32"), (5, 7168, 1920, "f32"), (16, 1024, 7168, "bf16"),
+                                       (40, 512, 384, "f32"), (100, 256, 96, "bf16")])
+def test_dense_skinny_matches_fp32_reference(gpu_device, m, k, n, odt):
+  """The few-row dense projection (decode step: fused router + down
+  projection with f32 out, up-projection with bf16 out; 40 and 100 rows take
+  several passes) against an fp32 torch matmul of the same bf16 operands
+  (f32 out within 1e-5 relative, bf16 out within 2e-2) and against hipBLASLt;
+  repeatable bit for bit."""
+  from lmoe import ops
+  g = torch.Generator(device="cuda").manual_seed(m * 7 + n)
+  x = torch.randn((m, k), device="cuda", generator=g).to(torch.bfloat16)
+  w = (torch.randn((n, k), device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+  dt = torch.float32 if odt == "f32" else torch.bfloat16
+  ref = x.float() @ w.float().t()
+  a = ops.dense(x, w, out_dtype=dt, w_layout="nk", backend="skinny")
+  b = ops.dense(x, w, out_dtype=dt, w_layout="nk", backend="skinny")
+  lib = ops.dense(x, w, out_dtype=dt, w_layout="nk", backend="blaslt")
+  assert torch.equal(a, b)
+  tol = 1e-5 if odt == "f32" else 2e-2
+  assert max_rel(to_np(a), to_np(ref)) <= tol
+  assert max_rel(to_np(a), to_np(lib)) <= tol

@@ -297,6 +297,122 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_mx_kernel(SkinnyParams p) {
   }
 }
 
+// Dense x (M, K) @ W^T with bf16 W stored (N, K), for a few rows (the dense
+// projections of a decode step, M = T): the same work split as above with one
+// group -- item = 16 output columns, K over the block's waves, LDS reduction
+// in wave order -- and the weights loaded straight into the MFMA A operand:
+// within a 128-deep k-step pair lane (column c, q) holds k = 32q .. 32q+31 of
+// column c (64 contiguous bytes), the activations the same k of its row.
+template <int NC, int WAVES, bool OUT_F32>
+__global__ __launch_bounds__(WAVES * 64) void skinny_dense_kernel(const uint16_t* __restrict__ x,
+                                                                   const uint16_t* __restrict__ w, int64_t M,
+                                                                   int64_t K, int64_t N, void* __restrict__ out) {
+  constexpr int D = NC == 1 ? 4 : NC == 2 ? 2 : 1;  // k-step pairs in flight per wave
+  __shared__ floatx4 s_red[WAVES - 1][64];
+  const int t = threadIdx.x, lane = t & 63, wv = t >> 6;
+  const int q = lane >> 4, l16 = lane & 15;
+  const int P = static_cast<int>(K / 128);
+  const int64_t nct = N / 16;
+  for (int64_t ct = blockIdx.x; ct < nct; ct += gridDim.x) {
+    const uint16_t* wr = w + (ct * 16 + l16) * K + 32 * q;
+    for (int64_t rb = 0; rb < M; rb += 16 * NC) {
+      const int nrc = static_cast<int>(std::min<int64_t>(NC, (M - rb + 15) / 16));
+      floatx4 acc[NC];
+#pragma unroll
+      for (int rc = 0; rc < NC; ++rc) acc[rc] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int j0 = wv; j0 < P; j0 += WAVES * D) {
+        uint4 a[D][4], b[D][NC][4];
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+          const int pr = j0 + WAVES * d;
+          if (pr < P) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) a[d][s] = *reinterpret_cast<const uint4*>(wr + 128 * static_cast<int64_t>(pr) + 8 * s);
+#pragma unroll
+            for (int rc = 0; rc < NC; ++rc) {
+              if (rc < nrc) {
+                const int64_t row = rb + rc * 16 + l16;
+                const uint16_t* xr = x + row * K + 128 * static_cast<int64_t>(pr) + 32 * q;
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                  b[d][rc][s] = row < M ? *reinterpret_cast<const uint4*>(xr + 8 * s) : uint4{0u, 0u, 0u, 0u};
+              }
+            }
+          }
+        }
+#pragma unroll
+        for (int d = 0; d < D; ++d) {
+          if (j0 + WAVES * d < P) {
+#pragma unroll
+            for (int rc = 0; rc < NC; ++rc) {
+              if (rc < nrc) {
+#pragma unroll
+                for (int s = 0; s < 4; ++s)
+                  acc[rc] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a[d][s]),
+                                                                    __builtin_bit_cast(bf16x8_t, b[d][rc][s]), acc[rc],
+                                                                    0, 0, 0);
+              }
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int rc = 0; rc < NC; ++rc) {
+        if (rc < nrc) {
+          __syncthreads();
+          if (wv > 0) s_red[wv - 1][lane] = acc[rc];
+          __syncthreads();
+          if (wv == 0) {
+            floatx4 sum = acc[rc];
+#pragma unroll
+            for (int v = 0; v < WAVES - 1; ++v) sum += s_red[v][lane];
+            const int64_t row = rb + rc * 16 + l16;
+            if (row < M) {
+              const int64_t o = row * N + ct * 16 + 4 * q;
+              if constexpr (OUT_F32)
+                *reinterpret_cast<floatx4*>(static_cast<float*>(out) + o) = sum;
+              else
+                *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + o) =
+                    uint2{pack_bf16x2(sum[0], sum[1]), pack_bf16x2(sum[2], sum[3])};
+            }
+          }
+        }
+      }
+    }
+  }
+}
+
+template <int NC, int WAVES, bool F32>
+void launch_dense(const uint16_t* x, const uint16_t* w, int64_t M, int64_t K, int64_t N, void* out, hipStream_t st) {
+  static std::atomic<unsigned> cached{0};
+  unsigned res = cached.load(std::memory_order_relaxed);
+  if (res == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, skinny_dense_kernel<NC, WAVES, F32>, WAVES * 64, 0) !=
+            hipSuccess ||
+        cus <= 0 || per_cu <= 0) {
+      cus = 256;
+      per_cu = 1;
+    }
+    res = static_cast<unsigned>(cus * per_cu);
+    cached.store(res, std::memory_order_relaxed);
+  }
+  const unsigned grid = static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(N / 16, res)));
+  skinny_dense_kernel<NC, WAVES, F32><<<grid, WAVES * 64, 0, st>>>(x, w, M, K, N, out);
+}
+
+template <int WAVES, bool F32>
+void dense_nc(int nc, const uint16_t* x, const uint16_t* w, int64_t M, int64_t K, int64_t N, void* out,
+              hipStream_t st) {
+  switch (nc) {
+    case 1: launch_dense<1, WAVES, F32>(x, w, M, K, N, out, st); break;
+    case 2: launch_dense<2, WAVES, F32>(x, w, M, K, N, out, st); break;
+    default: launch_dense<4, WAVES, F32>(x, w, M, K, N, out, st); break;
+  }
+}
+
 // Rows per pass: the smallest of 16, 32, 64 covering the largest group
 // (bounded by M and by the caller's hint); larger groups take more passes.
 int skinny_chunks(int64_t M, int64_t max_group_rows) {
@@ -394,6 +510,38 @@ extern "C" int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_ti
       launch_nc<kEpiNone, 8>(p, nc, upper, st);
     else
       launch_nc<kEpiNone, 4>(p, nc, upper, st);
+  }
+  LMOE_CHECK_LAUNCH(name);
+  return LMOE_OK;
+}
+
+extern "C" int lmoe_dense_skinny(const void* x, const void* w_nk, int64_t M, int64_t K, int64_t N, void* out,
+                                 int out_dtype, void* stream) {
+  const char* name = "dense_skinny";
+  LMOE_CHECK_ARG(M >= 0 && K > 0 && N > 0, "%s: bad sizes M=%lld K=%lld N=%lld", name, (long long)M, (long long)K,
+                 (long long)N);
+  LMOE_CHECK_ARG(out_dtype == LMOE_BF16 || out_dtype == LMOE_F32, "%s: bad out dtype", name);
+  LMOE_CHECK_SUPPORTED(K % 128 == 0 && N % 16 == 0, "%s: needs K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
+                       name, (long long)K, (long long)N);
+  if (M == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(x && w_nk && out, "%s: null pointer", name);
+  LMOE_CHECK_SUPPORTED(aligned(x, 16) && aligned(w_nk, 16) && aligned(out, 16), "%s: 16-byte alignment", name);
+  const int nc = skinny_chunks(M, 0);
+  const auto* xp = static_cast<const uint16_t*>(x);
+  const auto* wp = static_cast<const uint16_t*>(w_nk);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  // fewer 16-column items than CUs: eight waves per item, else four
+  const bool wide = N / 16 < 256;
+  if (out_dtype == LMOE_F32) {
+    if (wide)
+      dense_nc<8, true>(nc, xp, wp, M, K, N, out, st);
+    else
+      dense_nc<4, true>(nc, xp, wp, M, K, N, out, st);
+  } else {
+    if (wide)
+      dense_nc<8, false>(nc, xp, wp, M, K, N, out, st);
+    else
+      dense_nc<4, false>(nc, xp, wp, M, K, N, out, st);
   }
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;

@@ -422,7 +422,7 @@ def _ones_group(m: int, device) -> torch.Tensor:
   return t
 
 
-_DENSE_BACKENDS = ("auto", "hip", "blaslt")
+_DENSE_BACKENDS = ("auto", "hip", "blaslt", "skinny")
 
 
 def _dense_backend_default() -> str:
@@ -432,22 +432,48 @@ def _dense_backend_default() -> str:
   return b
 
 
+# The skinny dense kernel's parallelism is one block per 16 output columns:
+# measured against hipBLASLt at M = 1..16 it wins from N = 4096 on (the
+# decode up-projection, 7168 columns: 5.4 vs 6.4 us) and loses below (the
+# 1920-column router + down projection: 11.4 vs 10.4 us, half the CUs idle).
+SKINNY_DENSE_ROWS = 16
+SKINNY_DENSE_MIN_N = 4096
+
+
 def dense(x: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None,
           w_layout: str = "kn", backend: str | None = None) -> torch.Tensor:
   """x @ w (w (K, N), or (N, K) with w_layout="nk").
 
   ``backend``: "hip" runs it as a one-group grouped GEMM on the hand-written
   kernels; "blaslt" calls hipBLASLt (the ROCm library GEMM; (N, K) weights
-  only); "auto" (default, or $LMOE_DENSE) uses hipBLASLt for bf16 (N, K)
-  weights -- the layer's router-logits (f32 out), down- and up-projections --
-  and the hand-written kernels otherwise.  Both accumulate the exact bf16
-  products in f32; only the summation order differs."""
+  only); "skinny" the hand-written few-row kernel (bf16 (N, K) weights,
+  K % 128 == 0, N % 16 == 0).  "auto" (default, or $LMOE_DENSE), for bf16
+  (N, K) weights -- the layer's router logits (f32 out), down- and
+  up-projections: the skinny kernel for at most SKINNY_DENSE_ROWS rows and
+  N >= SKINNY_DENSE_MIN_N, else hipBLASLt; for other weights the hand-written
+  grouped kernels.  All accumulate the exact bf16 products in f32; only the
+  summation order differs."""
   backend = backend or _dense_backend_default()
   if backend not in _DENSE_BACKENDS:
     raise ValueError(f"backend {backend!r}")
   out_dtype = out_dtype or x.dtype
-  use_blaslt = backend == "blaslt" or (backend == "auto" and w_layout == "nk" and x.dtype == torch.bfloat16
-                                       and w.dtype == torch.bfloat16)
+  nk_bf16 = w_layout == "nk" and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
+  if backend == "auto" and nk_bf16 and x.dim() == 2 and x.shape[0] <= SKINNY_DENSE_ROWS \
+     and x.shape[1] % 128 == 0 and w.shape[0] % 16 == 0 and w.shape[0] >= SKINNY_DENSE_MIN_N:
+    backend = "skinny"
+  if backend == "skinny":
+    if not nk_bf16:
+      raise NotImplementedError("the skinny dense kernel takes bf16 x and bf16 (N, K) weights")
+    _dev(x, w)
+    if x.dim() != 2 or w.dim() != 2 or w.shape[1] != x.shape[1]:
+      raise ValueError(f"dense: x {tuple(x.shape)} / w {tuple(w.shape)}")
+    x, w = x.contiguous(), w.contiguous()
+    m, k = x.shape
+    n = w.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    check(lib().lmoe_dense_skinny(_p(x), _p(w), m, k, n, _p(out), _dt(out), _stream()), "dense_skinny")
+    return out
+  use_blaslt = backend == "blaslt" or (backend == "auto" and nk_bf16)
   if use_blaslt:
     if w_layout != "nk":
       raise NotImplementedError("the hipBLASLt backend takes (N, K) weights")
