@@ -249,6 +249,17 @@ int lmoe_dispatch_local_small(const int32_t* topk_idx, const void* topk_w, int w
                               int32_t* group_sizes, uint8_t* valid, int32_t* per_expert_counts,
                               int32_t* padded_token_idx, void* padded_w, int32_t* slot_pos, int flags,
                               void* stream);
+/* The same contract as lmoe_dispatch_local_small (row-strided bf16 or f32 x,
+ * bf16 sorted_tokens, optional skip of the padding rows) at any size: the
+ * one-launch kernel when T*k, m_padded and L fit it, else the counting sort of
+ * lmoe_dispatch_local and a gather that rounds f32 rows to bf16.  Workspace:
+ * lmoe_dispatch_workspace_size(T, k, L) bytes (unused on the one-launch path).
+ */
+int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x, int x_dtype,
+                             int64_t x_ld, int64_t T, int64_t k, int64_t lat, int64_t local_start, int64_t L,
+                             int64_t m_padded, uint16_t* sorted_tokens, int32_t* group_sizes, uint8_t* valid,
+                             int32_t* per_expert_counts, int32_t* padded_token_idx, void* padded_w,
+                             int32_t* slot_pos, int flags, void* workspace, int64_t workspace_size, void* stream);
 
 /* ---- a13: combine -----------------------------------------------------------------
  * lmoe_combine_scatter_add replaces _combine_shard_contribution (ref.py:1113-1141):

@@ -337,3 +337,27 @@ def test_dispatch_deterministic_rerun(gpu_device):
   b = _run_dispatch(ti, tw, x, "bf16", 0, L, m)
   for u, v in zip(a, b):
     assert torch.equal(u, v)
+
+
+def test_dispatch_rows_sort_path_from_strided_f32(gpu_device):
+  """Prefill-sized dispatch (T*k = 32768 slots, past the one-launch kernel)
+  from the f32 latent columns of the fused projection output: the counting
+  sort with the converting gather equals cast-to-bf16 then the bf16 sort path
+  bit for bit; with the padding rows skipped every other output and the kept
+  rows are unchanged."""
+  from lmoe import ops
+  rng = np.random.default_rng(77)
+  t, k, e, L, lat = 2048, 16, 896, 112, 128
+  topk_idx = torch.tensor(np.stack([rng.permutation(e)[:k] for _ in range(t)]).astype(np.int32), device="cuda")
+  topk_w = torch.tensor(rng.uniform(size=(t, k)).astype(np.float32), device="cuda")
+  rd = torch.tensor(rng.standard_normal((t, e + lat)).astype(np.float32), device="cuda")
+  m_padded = O.compute_m_padded(t, k, e, L, 2.0, 128)
+  ref = ops.dispatch_local(topk_idx, topk_w, ops.cast_rows(rd[:, e:], torch.bfloat16), 0, L, m_padded, path="sort")
+  got = ops.dispatch_local(topk_idx, topk_w, rd[:, e:], 0, L, m_padded, path="sort")
+  for a, b in zip(got, ref):
+    assert torch.equal(a, b)
+  skip = ops.dispatch_local(topk_idx, topk_w, rd[:, e:], 0, L, m_padded, path="sort", skip_padding_rows=True)
+  nk = int(ref.group_sizes[:L].sum())
+  assert torch.equal(skip.sorted_tokens[:nk], ref.sorted_tokens[:nk])
+  for a, b in zip(skip[1:], ref[1:]):
+    assert torch.equal(a, b)

@@ -9,6 +9,7 @@
 // the padding bucket.  Then one gather pass copies x rows into sorted_tokens
 // and fills the padding rows (zero row, token -1, weight 0, valid 0).
 #include "csort.h"
+#include "gemm_tile.h"
 
 namespace lmoe {
 namespace {
@@ -79,6 +80,52 @@ __global__ __launch_bounds__(256) void gather_kernel(
       val = x[static_cast<int64_t>(t) * row_vecs + v];
     }
     out[p * row_vecs + v] = val;
+  }
+}
+
+// The gather for a row-strided bf16 or f32 x written as bf16 (f32 rounded to
+// nearest even), optionally leaving the padding rows of out unwritten; the
+// metadata of every row as gather_kernel writes it.
+template <bool F32>
+__global__ __launch_bounds__(256) void gather_rows_kernel(
+    const void* __restrict__ x, int64_t x_ld, int64_t lat, const int32_t* __restrict__ num_kept_p,
+    int64_t m_padded, uint16_t* __restrict__ out, int skip_padding, uint8_t* __restrict__ valid,
+    int32_t* __restrict__ tok, uint8_t* __restrict__ w_out, int wsize, int32_t* __restrict__ group_sizes,
+    int32_t* __restrict__ per_expert, int L) {
+  const int nk = *num_kept_p;
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < L; i += blockDim.x) per_expert[i] = group_sizes[i];
+    if (threadIdx.x == 0) group_sizes[L] = static_cast<int32_t>(m_padded - nk);
+  }
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * kGatherRows;
+  const int64_t r1 = r0 + kGatherRows < m_padded ? r0 + kGatherRows : m_padded;
+  for (int64_t p = r0 + threadIdx.x; p < r1; p += blockDim.x) {
+    valid[p] = p < nk ? 1 : 0;
+    if (p >= nk) {
+      tok[p] = -1;
+      if (wsize == 4)
+        reinterpret_cast<uint32_t*>(w_out)[p] = 0;
+      else
+        reinterpret_cast<uint16_t*>(w_out)[p] = 0;
+    }
+  }
+  const int64_t vecs = lat / 8;
+  const int64_t re = skip_padding ? (r1 < nk ? r1 : (r0 > nk ? r0 : nk)) : r1;
+  for (int64_t i = threadIdx.x; i < (re - r0) * vecs; i += blockDim.x) {
+    const int64_t p = r0 + i / vecs, v = i % vecs;
+    uint4 o{0u, 0u, 0u, 0u};
+    if (p < nk) {
+      const int64_t src = static_cast<int64_t>(tok[p]) * x_ld + v * 8;
+      if constexpr (F32) {
+        const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + src);
+        const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(x) + src + 4);
+        o = uint4{gemm::pack_bf16x2(a.x, a.y), gemm::pack_bf16x2(a.z, a.w), gemm::pack_bf16x2(b.x, b.y),
+                  gemm::pack_bf16x2(b.z, b.w)};
+      } else {
+        o = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(x) + src);
+      }
+    }
+    reinterpret_cast<uint4*>(out + p * lat)[v] = o;
   }
 }
 
@@ -162,6 +209,70 @@ extern "C" int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, 
         static_cast<uint16_t*>(sorted_tokens), valid, padded_token_idx,
         static_cast<uint8_t*>(padded_w), dtype_size(w_dtype), group_sizes, per_expert_counts, Li);
   }
+  LMOE_CHECK_LAUNCH("dispatch_gather");
+  return LMOE_OK;
+}
+
+extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
+                                        int x_dtype, int64_t x_ld, int64_t T, int64_t k, int64_t lat,
+                                        int64_t local_start, int64_t L, int64_t m_padded, uint16_t* sorted_tokens,
+                                        int32_t* group_sizes, uint8_t* valid, int32_t* per_expert_counts,
+                                        int32_t* padded_token_idx, void* padded_w, int32_t* slot_pos, int flags,
+                                        void* workspace, int64_t workspace_size, void* stream) {
+  using namespace lmoe;
+  const char* name = "dispatch_local_rows";
+  LMOE_CHECK_ARG(T >= 0 && k > 0 && lat > 0 && L > 0 && m_padded >= 0 && local_start >= 0 && x_ld >= lat,
+                 "%s: bad sizes", name);
+  LMOE_CHECK_ARG(valid_dtype(w_dtype) && valid_dtype(x_dtype), "%s: bad dtype", name);
+  LMOE_CHECK_ARG((flags & ~LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS) == 0, "%s: unknown flags 0x%x", name, flags);
+  // decode-sized batches: one launch
+  if (T * k <= 8192 && m_padded <= 8192 && L + 1 <= 1024)
+    return lmoe_dispatch_local_small(topk_idx, topk_w, w_dtype, x, x_dtype, x_ld, T, k, lat, local_start, L,
+                                     m_padded, sorted_tokens, group_sizes, valid, per_expert_counts,
+                                     padded_token_idx, padded_w, slot_pos, flags, stream);
+  LMOE_CHECK_SUPPORTED(T * k < (1ll << 31) && m_padded < (1ll << 31) && L < (1 << 20),
+                       "%s: sizes exceed int32 indexing", name);
+  LMOE_CHECK_SUPPORTED(L + 1 <= 12288, "%s: L=%lld exceeds the LDS histogram", name, (long long)L);
+  LMOE_CHECK_SUPPORTED(lat % 8 == 0 && x_ld % (x_dtype == LMOE_F32 ? 4 : 8) == 0 && aligned(x, 16) &&
+                           aligned(sorted_tokens, 16),
+                       "%s: lat %% 8 == 0 and 16-byte aligned rows", name);
+  const int64_t need = workspace_bytes(T * k, L);
+  if (!workspace || workspace_size < need)
+    return fail(LMOE_ERR_WORKSPACE, "%s: workspace %lld bytes < %lld", name, (long long)workspace_size,
+                (long long)need);
+  LMOE_CHECK_ARG(group_sizes && valid && per_expert_counts && padded_token_idx && padded_w && topk_idx && topk_w &&
+                     (sorted_tokens || m_padded == 0),
+                 "%s: null output", name);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t n = T * k;
+  const int64_t chunks = csort::num_chunks<kDispatchChunk>(n > 0 ? n : 1);
+  int32_t* ws = static_cast<int32_t*>(workspace);
+  Workspace w{ws, ws + chunks * L, ws + 2 * chunks * L};
+  const int Li = static_cast<int>(L);
+  DispatchKey key{topk_idx, static_cast<int>(local_start), Li};
+  csort::hist_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 256, (L + 1) * sizeof(int32_t), st>>>(
+      key, n, Li, chunks, w.hist);
+  LMOE_CHECK_LAUNCH("dispatch_hist");
+  if (csort::launch_scan(w.hist, chunks, Li, m_padded, w.base, group_sizes, nullptr, w.num_kept, st) != hipSuccess)
+    return fail(LMOE_ERR_HIP, "dispatch_scan: LDS attribute");
+  LMOE_CHECK_LAUNCH("dispatch_scan");
+  if (n > 0) {
+    DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
+                      padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
+    csort::place_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 64, L * sizeof(int32_t), st>>>(
+        key, n, Li, csort::key_bits_for(Li), chunks, w.base, sink);
+    LMOE_CHECK_LAUNCH("dispatch_place");
+  }
+  const unsigned blocks = static_cast<unsigned>(m_padded > 0 ? ceil_div(m_padded, kGatherRows) : 1);
+  const int skip = (flags & LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS) != 0;
+  if (x_dtype == LMOE_F32)
+    gather_rows_kernel<true><<<blocks, 256, 0, st>>>(x, x_ld, lat, w.num_kept, m_padded, sorted_tokens, skip, valid,
+                                                    padded_token_idx, static_cast<uint8_t*>(padded_w),
+                                                    dtype_size(w_dtype), group_sizes, per_expert_counts, Li);
+  else
+    gather_rows_kernel<false><<<blocks, 256, 0, st>>>(x, x_ld, lat, w.num_kept, m_padded, sorted_tokens, skip, valid,
+                                                     padded_token_idx, static_cast<uint8_t*>(padded_w),
+                                                     dtype_size(w_dtype), group_sizes, per_expert_counts, Li);
   LMOE_CHECK_LAUNCH("dispatch_gather");
   return LMOE_OK;
 }

@@ -62,6 +62,7 @@ SIGNATURES = {
     "lmoe_dispatch_local": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P,
                              I64, P], I32),
     "lmoe_dispatch_local_small": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, I32, P], I32),
+    "lmoe_dispatch_local_rows": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, I32, P, I64, P], I32),
     "lmoe_combine_workspace_size": ([I64, I64], I64),
     "lmoe_combine_scatter_add": ([P, I32, P, P, I32, I64, I64, I64, P, I32, P, I64, P], I32),
     "lmoe_combine_slots": ([P, I32, P, P, I32, I64, I64, I64, I32, P, I32, P], I32),

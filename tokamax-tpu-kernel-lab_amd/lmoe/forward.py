@@ -211,23 +211,20 @@ class LocalShardLatentMoE:
       e = self.router_nk.shape[0]
       rd = self._dense(hidden, self.router_down_nk, torch.float32)
       logits = rd[:, :e]
-      if decode:
-        # the one-launch dispatch rounds the f32 latent rows to bf16 as it
-        # gathers them: no separate cast
-        x_src = rd[:, e:]
-        x = ops.cast_rows(x_src, hidden.dtype) if return_stages else None
-      else:
-        x = ops.cast_rows(rd[:, e:], hidden.dtype)
+      # the dispatch rounds the f32 latent rows to bf16 as it gathers them:
+      # no separate cast (x itself is materialised only for the stages)
+      x_src = rd[:, e:]
+      x = ops.cast_rows(x_src, hidden.dtype) if return_stages else None
     else:
       logits = self._dense(hidden, self.router_nk, torch.float32)
       x = self._dense(hidden, self.down_nk)
     idx, w = ops.router_topk_from_logits(logits, self.bias, c.top_k, c.moe_renormalize,
                                          c.routed_scaling_factor, self.act, hidden.dtype)
-    if decode:
-      d = ops.dispatch_local(idx, w, x_src if x_src is not None else x, self.start, self.L, m_padded, path="small",
-                             skip_padding_rows=not return_stages)
-    else:
-      d = ops.dispatch_local(idx, w, x, self.start, self.L, m_padded, path="sort")
+    # padding rows of the sorted tokens are read by no later stage (the MXFP4
+    # expert GEMMs skip the padding bucket) unless the stages are returned
+    skip = self.expert_format == "mxfp4" and not return_stages
+    d = ops.dispatch_local(idx, w, x_src if x_src is not None else x, self.start, self.L, m_padded,
+                           path="small" if decode else "sort", skip_padding_rows=skip)
     E = self.experts
     mx_mode, mx_kw = self.mxfp4_mode, {}
     if self.expert_format == "mxfp4" and self._decode_path(t):

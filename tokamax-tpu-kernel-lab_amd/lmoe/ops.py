@@ -561,10 +561,10 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
   ``path``: "sort" (the multi-block counting sort + gather), "small" (one
   launch for decode-sized batches, ``small_dispatch_supported``) or "auto"
   (small when supported and x is bf16).  Both give the same outputs bit for
-  bit.  The small path also takes x as a row-strided view (unit column
-  stride) of bf16 or f32 values and writes bf16 sorted tokens (f32 rounded to
-  nearest even); ``skip_padding_rows`` then leaves the padding rows of
-  sorted_tokens unwritten."""
+  bit.  A contiguous x keeps its dtype in sorted_tokens; a row-strided view
+  (unit column stride) of bf16 or f32 values, or ``skip_padding_rows``, gives
+  bf16 sorted tokens (f32 rounded to nearest even), and ``skip_padding_rows``
+  leaves their padding rows unwritten."""
   if topk_idx.dtype != torch.int32:
     raise ValueError("topk_idx must be int32")
   t, k = topk_idx.shape
@@ -594,6 +594,26 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
     return Dispatch(sorted_tokens, group_sizes, valid, counts, tok, w, slot_pos)
   if path != "sort":
     raise ValueError(f"path {path!r}")
+  if skip_padding_rows or not x.is_contiguous():
+    # row-strided bf16 / f32 rows, written as bf16: the counting sort with a
+    # converting gather (the one-launch kernel when the sizes fit it)
+    x = _dev_rows(x)
+    _dev(topk_idx, topk_weight)
+    dev = x.device
+    sorted_tokens = torch.empty((m_padded, lat), dtype=torch.bfloat16, device=dev)
+    group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
+    valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
+    counts = torch.empty((L,), dtype=torch.int32, device=dev)
+    tok = torch.empty((m_padded,), dtype=torch.int32, device=dev)
+    w = torch.empty((m_padded,), dtype=topk_weight.dtype, device=dev)
+    slot_pos = torch.empty((t * k,), dtype=torch.int32, device=dev)
+    ws = _workspace(lib().lmoe_dispatch_workspace_size(t, k, L), dev)
+    flags = _lib.DISPATCH_FLAG_SKIP_PADDING_ROWS if skip_padding_rows else 0
+    check(lib().lmoe_dispatch_local_rows(_p(topk_idx), _p(topk_weight), _dt(topk_weight), _p(x), _dt(x),
+                                         x.stride(0) if t > 0 else lat, t, k, lat, local_expert_start, L, m_padded,
+                                         _p(sorted_tokens), _p(group_sizes), _p(valid), _p(counts), _p(tok), _p(w),
+                                         _p(slot_pos), flags, _p(ws), ws.numel(), _stream()), "dispatch_local_rows")
+    return Dispatch(sorted_tokens, group_sizes, valid, counts, tok, w, slot_pos)
   _dev(topk_idx, topk_weight, x)
   dev = x.device
   sorted_tokens = torch.empty((m_padded, lat), dtype=x.dtype, device=dev)
