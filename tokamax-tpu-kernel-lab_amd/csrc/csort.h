@@ -145,21 +145,34 @@ inline hipError_t launch_scan(const int32_t* hist, int64_t chunks, int nbins, in
   return hipSuccess;
 }
 
-// Sink(s, key, pos, real): called for every s < n; pos is meaningful when real.
+// sink.load(s) -> u32 is read for every s < n before any rank is computed;
+// sink(s, key, pos, real, loaded): called for every s < n; pos is meaningful
+// when real.  All the chunk's keys and loads are issued up front (one memory
+// round trip per chunk, not one per 64 slots).
 template <int CHUNK, class KeyFn, class Sink>
 __global__ __launch_bounds__(64) void place_kernel(KeyFn key, int64_t n, int nbins, int key_bits, int64_t chunks,
                                                    const int32_t* __restrict__ base, Sink sink) {
+  constexpr int IT = CHUNK / 64;
   extern __shared__ int32_t run[];
   const int lane = threadIdx.x;
+  const int64_t chunk_base = static_cast<int64_t>(blockIdx.x) * CHUNK;
+  int keys[IT];
+  uint32_t loaded[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t s = chunk_base + it * 64 + lane;
+    keys[it] = s < n ? key(s) : nbins;
+    loaded[it] = s < n ? sink.load(s) : 0u;
+  }
   for (int i = lane; i < nbins; i += 64) run[i] = base[i * chunks + blockIdx.x];
   __syncthreads();
-  const int64_t chunk_base = static_cast<int64_t>(blockIdx.x) * CHUNK;
   const uint64_t below = (1ull << lane) - 1ull;
-  for (int it = 0; it < CHUNK / 64; ++it) {
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
     const int64_t s = chunk_base + it * 64 + lane;
     if (chunk_base + it * 64 >= n) break;  // uniform across the wave
     const bool active = s < n;
-    const int kk = active ? key(s) : nbins;
+    const int kk = keys[it];
     const bool real = active && kk < nbins;
     uint64_t peers = __ballot(real);
     for (int b = 0; b < key_bits; ++b) {
@@ -173,7 +186,7 @@ __global__ __launch_bounds__(64) void place_kernel(KeyFn key, int64_t n, int nbi
     __syncthreads();
     if (real && (peers & below) == 0) run[kk] = pos + __popcll(peers);
     __syncthreads();
-    if (active) sink(s, kk, pos, real);
+    if (active) sink(s, kk, pos, real, loaded[it]);
   }
 }
 

@@ -32,14 +32,18 @@ struct DispatchSink {
   uint8_t* w_out;
   int32_t* slot_pos;
   int64_t limit;
-  __device__ __forceinline__ void operator()(int64_t s, int key, int pos, bool real) const {
+  // the slot's combine weight bits, read before the ranks are known
+  __device__ __forceinline__ uint32_t load(int64_t s) const {
+    return wsize == 4 ? reinterpret_cast<const uint32_t*>(w)[s] : reinterpret_cast<const uint16_t*>(w)[s];
+  }
+  __device__ __forceinline__ void operator()(int64_t s, int key, int pos, bool real, uint32_t wbits) const {
     const bool kept = real && pos < limit;
     if (kept) {
       tok_out[pos] = static_cast<int32_t>(s / k);
       if (wsize == 4)
-        reinterpret_cast<uint32_t*>(w_out)[pos] = reinterpret_cast<const uint32_t*>(w)[s];
+        reinterpret_cast<uint32_t*>(w_out)[pos] = wbits;
       else
-        reinterpret_cast<uint16_t*>(w_out)[pos] = reinterpret_cast<const uint16_t*>(w)[s];
+        reinterpret_cast<uint16_t*>(w_out)[pos] = static_cast<uint16_t>(wbits);
     }
     if (slot_pos) slot_pos[s] = kept ? pos : -1;
   }
