@@ -361,3 +361,18 @@ def test_dispatch_rows_sort_path_from_strided_f32(gpu_device):
   assert torch.equal(skip.sorted_tokens[:nk], ref.sorted_tokens[:nk])
   for a, b in zip(skip[1:], ref[1:]):
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("path", ["sort", "small"])
+def test_dispatch_empty_batch(gpu_device, path):
+  """T = 0 tokens: every row is padding (zero row, token -1, weight 0), the
+  group sizes are all padding, on both dispatch paths."""
+  from lmoe import ops
+  L, lat, m_padded = 16, 64, 128
+  idx = torch.empty((0, 4), dtype=torch.int32, device="cuda")
+  w = torch.empty((0, 4), dtype=torch.float32, device="cuda")
+  x = torch.empty((0, lat), dtype=torch.bfloat16, device="cuda")
+  d = ops.dispatch_local(idx, w, x, 0, L, m_padded, path=path)
+  assert d.sorted_tokens.shape == (m_padded, lat) and not d.sorted_tokens.any()
+  assert d.group_sizes[:L].sum().item() == 0 and d.group_sizes[L].item() == m_padded
+  assert not d.valid_mask.any() and bool((d.padded_token_idx == -1).all()) and not d.padded_combine_weight.any()

@@ -190,3 +190,20 @@ def test_dense_skinny_matches_fp32_reference(gpu_device, m, k, n, odt):
   tol = 1e-5 if odt == "f32" else 2e-2
   assert max_rel(to_np(a), to_np(ref)) <= tol
   assert max_rel(to_np(a), to_np(lib)) <= tol
+
+
+def test_skinny_empty_and_all_padding(gpu_device):
+  """M = 0 returns an empty result; groups that are all padding (only the
+  zero group has rows) give all-zero rows, with nothing computed."""
+  from lmoe import ops
+  rng = np.random.default_rng(13)
+  k, n, g = 256, 64, 3
+  packed, scale = _mx_weights(rng, g, n, k)
+  tpk, tsc = ops.mxfp4_tile_weights(to_dev(packed), to_dev(scale))
+  empty = ops.ragged_dot_mxfp4(torch.empty((0, k), dtype=torch.bfloat16, device="cuda"), tpk, tsc,
+                               to_dev(np.zeros(g, np.int32)), weight_layout="tiled", mode="skinny")
+  assert empty.shape == (0, n)
+  x = to_dev(O.bf16_round(rng.standard_normal((40, k))), "bf16")
+  out = ops.ragged_dot_mxfp4(x, tpk, tsc, to_dev(np.array([0, 0, 40], np.int32)), zero_group=2,
+                             weight_layout="tiled", mode="skinny")
+  assert out.shape == (40, n) and not out.any()
