@@ -311,6 +311,11 @@ int lmoe_add(const void* a, const void* b, int64_t count, int dtype, void* out, 
  * GEMM (f32 out) into the f32 logits and the bf16 latent x (ref.py:358/371). */
 int lmoe_cast_rows(const void* x, int x_dtype, int64_t rows, int64_t cols, int64_t ld, void* out,
                    int out_dtype, void* stream);
+/* lmoe_transpose: out (G, C, R) = in (G, R, C) transposed per batch, 2- or
+ * 4-byte elements, out not aliasing in.  Turns the reference's (G, K, N)
+ * ragged_dot weights (rd.py:358-369) into the k-contiguous (G, N, K) layout
+ * the fast grouped GEMM kernels read. */
+int lmoe_transpose(const void* in, int64_t G, int64_t R, int64_t C, int elem_bytes, void* out, void* stream);
 
 #ifdef __cplusplus
 }

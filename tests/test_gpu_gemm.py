@@ -354,3 +354,16 @@ def test_dense_blaslt_matches_oracle(gpu_device, m, k, n, odt):
   assert max_rel(got, ref) <= tol
   hip = to_np(ops.dense(to_dev(x, "bf16"), to_dev(w, "bf16"), out_dtype=out_dt, w_layout="nk", backend="hip"))
   assert max_rel(hip, ref) <= tol
+
+
+@pytest.mark.parametrize("elem,r,c", [(2, 130, 77), (4, 130, 77), (2, 132, 200), (2, 2048, 1024)])
+def test_transpose_batched(gpu_device, elem, r, c):
+  """lmoe_transpose: (G, R, C) -> (G, C, R) bit for bit; ragged edges (the
+  element-wise kernel) and R, C multiples of 4 (the 8-byte bf16 kernel)."""
+  from lmoe import _lib
+  dt = torch.bfloat16 if elem == 2 else torch.float32
+  x = torch.randn((3, r, c), device="cuda").to(dt)
+  out = torch.empty((3, c, r), dtype=dt, device="cuda")
+  _lib.check(_lib.lib().lmoe_transpose(x.data_ptr(), 3, r, c, elem, out.data_ptr(),
+                                       torch.cuda.current_stream().cuda_stream), "transpose")
+  assert torch.equal(out, x.transpose(1, 2))

@@ -164,3 +164,83 @@ extern "C" int lmoe_cast_rows(const void* x, int x_dtype, int64_t rows, int64_t 
   LMOE_CHECK_LAUNCH("cast_rows");
   return LMOE_OK;
 }
+
+namespace lmoe {
+namespace {
+
+// Batched transpose out[g][c][r] = in[g][r][c] through a 64x64 LDS tile
+// (one padding element per row: the column reads hit distinct banks).
+template <typename T>
+__global__ __launch_bounds__(256) void transpose_kernel(const T* __restrict__ in, int64_t R, int64_t C,
+                                                        T* __restrict__ out) {
+  __shared__ T tile[64][65];
+  const int64_t g = blockIdx.z;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const T* src = in + g * R * C;
+  T* dst = out + g * R * C;
+  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    if (r < R && c < C) tile[i][tx] = src[r * C + c];
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (r < R && c < C) dst[c * R + r] = tile[tx][i];
+  }
+}
+
+// The same for 2-byte elements with R % 4 == 0 and C % 4 == 0: 8-byte loads
+// of 4 consecutive columns and 8-byte stores of 4 consecutive rows.
+__global__ __launch_bounds__(256) void transpose16x4_kernel(const uint16_t* __restrict__ in, int64_t R, int64_t C,
+                                                            uint16_t* __restrict__ out) {
+  __shared__ uint16_t tile[64][68];
+  const int64_t g = blockIdx.z;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const uint16_t* src = in + g * R * C;
+  uint16_t* dst = out + g * R * C;
+  const int tq = threadIdx.x % 16, ty = threadIdx.x / 16;
+  for (int i = ty; i < 64; i += 16) {
+    const int64_t r = r0 + i, c = c0 + 4 * tq;
+    if (r < R && c < C) {
+      const uint2 v = *reinterpret_cast<const uint2*>(src + r * C + c);
+      tile[i][4 * tq] = static_cast<uint16_t>(v.x);
+      tile[i][4 * tq + 1] = static_cast<uint16_t>(v.x >> 16);
+      tile[i][4 * tq + 2] = static_cast<uint16_t>(v.y);
+      tile[i][4 * tq + 3] = static_cast<uint16_t>(v.y >> 16);
+    }
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 16) {
+    const int64_t c = c0 + i, r = r0 + 4 * tq;
+    if (c < C && r < R) {
+      const uint32_t lo = tile[4 * tq][i] | (static_cast<uint32_t>(tile[4 * tq + 1][i]) << 16);
+      const uint32_t hi = tile[4 * tq + 2][i] | (static_cast<uint32_t>(tile[4 * tq + 3][i]) << 16);
+      *reinterpret_cast<uint2*>(dst + c * R + r) = uint2{lo, hi};
+    }
+  }
+}
+
+}  // namespace
+}  // namespace lmoe
+
+extern "C" int lmoe_transpose(const void* in, int64_t G, int64_t R, int64_t C, int elem_bytes, void* out,
+                              void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(G >= 0 && R >= 0 && C >= 0, "transpose: bad sizes");
+  LMOE_CHECK_ARG(elem_bytes == 2 || elem_bytes == 4, "transpose: elem_bytes %d", elem_bytes);
+  LMOE_CHECK_SUPPORTED(G < 65536, "transpose: G=%lld batches", (long long)G);
+  if (G * R * C == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(in && out && in != out, "transpose: null or aliased pointer");
+  const dim3 grid(static_cast<unsigned>(ceil_div(C, 64)), static_cast<unsigned>(ceil_div(R, 64)),
+                  static_cast<unsigned>(G));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (elem_bytes == 2 && R % 4 == 0 && C % 4 == 0 && aligned(in, 8) && aligned(out, 8))
+    transpose16x4_kernel<<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(in), R, C, static_cast<uint16_t*>(out));
+  else if (elem_bytes == 2)
+    transpose_kernel<uint16_t><<<grid, 256, 0, st>>>(static_cast<const uint16_t*>(in), R, C, static_cast<uint16_t*>(out));
+  else
+    transpose_kernel<uint32_t><<<grid, 256, 0, st>>>(static_cast<const uint32_t*>(in), R, C, static_cast<uint32_t*>(out));
+  LMOE_CHECK_LAUNCH("transpose");
+  return LMOE_OK;
+}

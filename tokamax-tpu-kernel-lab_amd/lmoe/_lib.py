@@ -73,6 +73,7 @@ SIGNATURES = {
     "lmoe_situ_and_mul": ([P, P, I64, F, F, I32, P, P], I32),
     "lmoe_add": ([P, P, I64, I32, P, P], I32),
     "lmoe_cast_rows": ([P, I32, I64, I64, I64, P, I32, P], I32),
+    "lmoe_transpose": ([P, I64, I64, I64, I32, P, P], I32),
 }
 
 _lock = threading.Lock()

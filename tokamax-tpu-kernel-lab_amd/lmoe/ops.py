@@ -109,6 +109,13 @@ def ragged_dot(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor, 
   if rhs.dtype != lhs.dtype:
     raise NotImplementedError(f"mixed lhs {lhs.dtype} / rhs {rhs.dtype}")
   out_dtype = preferred_element_type or lhs.dtype
+  if layout == _lib.RHS_GKN and lhs.dtype == torch.bfloat16 and k % 64 == 0 and n % 8 == 0:
+    # reference-layout bf16 weights: one transpose into the k-contiguous
+    # layout (lmoe_transpose), then the DMA-pipelined kernel for (G, N, K)
+    # -- faster than the transpose-on-store kernel for the (G, K, N) layout
+    rhs_t = torch.empty((g, n, k), dtype=rhs.dtype, device=rhs.device)
+    check(lib().lmoe_transpose(_p(rhs), g, k, n, 2, _p(rhs_t), _stream()), "transpose")
+    rhs, layout = rhs_t, _lib.RHS_GNK
   out = torch.empty((m, n), dtype=out_dtype, device=lhs.device)
   check(lib().lmoe_ragged_dot(_p(lhs), _dt(lhs), _p(rhs), layout, _p(group_sizes), m, k, n, g,
                               zero_group, _p(out), _dt(out), _stream()), "ragged_dot")
