@@ -33,8 +33,10 @@ _PROFILE = False  # run each selected kernel a few times, no timing
 _DECODE_TOKENS = (1, 2, 4, 8, 16, 32, 64, 128)
 
 
-def time_fn(fn, rounds=10, calls=20, name=""):
-  """Median per-call ms over `rounds` rounds of `calls` pipelined calls."""
+def time_fn(fn, rounds=10, calls=20, name="", graph=True):
+  """Median per-call ms over `rounds` rounds of `calls` back-to-back calls,
+  each round one replay of the calls captured as a HIP graph (``graph=False``:
+  eager launches, for a ``fn`` that already replays a graph)."""
   if _FILTER and _FILTER not in name:
     return None
   if _PROFILE:
@@ -44,12 +46,36 @@ def time_fn(fn, rounds=10, calls=20, name=""):
     return None
   fn()
   torch.cuda.synchronize()
+  # the calls of one round captured as one HIP graph (no host launch cost in
+  # the timing, as in the layer's graph replay); eager launches if a call
+  # cannot be captured
+  run = None
+  try:
+    if not graph:
+      raise RuntimeError("eager launches requested")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+      fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+      for _ in range(calls):
+        fn()
+    torch.cuda.synchronize()
+    run = g.replay
+  except Exception:  # noqa: BLE001 -- fall back to eager launches
+    torch.cuda.synchronize()
   per = []
   for _ in range(rounds):
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
-    for _ in range(calls):
-      fn()
+    if run is not None:
+      run()
+    else:
+      for _ in range(calls):
+        fn()
     b.record()
     b.synchronize()
     per.append(a.elapsed_time(b) / calls)
@@ -246,7 +272,7 @@ def bench_decode(dev, rounds, calls):
     hit = int((gs[:L] > 0).sum())
     replay, _ = _capture(layer, h)
     nm = f"decode layer T={t}"
-    ms = time_fn(replay, rounds, calls, name=nm)
+    ms = time_fn(replay, rounds, calls, name=nm, graph=False)
     report(nm, ms, 0, dense_bytes + hit * expert_bytes + t * H * 4, tokens=t, experts_hit=hit,
            skinny_expert_gemms=layer._decode_path(t), tokens_per_s=round(t / (ms / 1000)) if ms else None)
 
