@@ -208,13 +208,28 @@ def main():
 
   achieved = nbytes / (gateup_ms / 1000.0) / 1e9
   tflops = flops / (gateup_ms / 1000.0) / 1e12
+  # the HBM rate a plain 256 MiB device copy reaches on this GPU (read +
+  # write bytes / time): the practical ceiling beside the published peak
+  src = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+  dst = torch.empty_like(src)
+  for _ in range(3):
+    dst.copy_(src)
+  ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+  ev0.record()
+  for _ in range(10):
+    dst.copy_(src)
+  ev1.record()
+  ev1.synchronize()
+  copy_gbs = 2 * (256 << 20) * 10 / (ev0.elapsed_time(ev1) / 1000.0) / 1e9
+  del src, dst
   traffic = load_traffic("traffic_cfg5_gateup_mxfp4.json")
   roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
               "frac": round(achieved / HBM_PEAK_GBS, 4),
               "traffic": traffic.get("bytes_per_launch") if traffic else None,
               "kernel": "grouped_gemm_stream_kernel<64, 256, MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
               "algorithmic_bytes": int(nbytes), "algorithmic_flops": flops,
-              "kernel_us": round(gateup_ms * 1000.0, 2)}
+              "kernel_us": round(gateup_ms * 1000.0, 2),
+              "copy_GBps": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4)}
   grouped = {"tflops": round(tflops, 2),
              "pct_mxfp4_peak": round(100 * tflops / PEAK_TFLOPS["mxfp4"], 2),
              "pct_bf16_peak": round(100 * tflops / PEAK_TFLOPS["bf16"], 2),
