@@ -29,6 +29,7 @@ namespace csort {
 namespace {  // kernels are instantiated per translation unit
 
 constexpr int kScanThreads = 1024;
+constexpr int64_t kScanDynLds = 65536;  // dynamic LDS of the scan (bin starts + staged histogram)
 
 inline int key_bits_for(int nbins) {
   int b = 0;
@@ -87,25 +88,47 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* t
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const int32_t* __restrict__ hist, int64_t chunks, int nbins, int64_t limit,
     int32_t* __restrict__ base, int32_t* __restrict__ bin_kept, int32_t* __restrict__ offsets,
-    int32_t* __restrict__ num_kept) {
-  extern __shared__ int32_t bin_start[];
+    int32_t* __restrict__ num_kept, int staged) {
+  extern __shared__ int32_t bin_start[];  // nbins + 1, then (staged) the histogram
   constexpr int kHeld = 16;
+  static_assert(kScanDynLds / 4 <= kHeld * kScanThreads, "a staged histogram is copied in one pass");
   const int64_t total_n = chunks * nbins;
   const int64_t per = (total_n + kScanThreads - 1) / kScanThreads;
   const int64_t i0 = threadIdx.x * per;
   const int64_t i1 = i0 + per < total_n ? i0 + per : total_n;
+  // Staged: the histogram is copied into LDS with coalesced loads, each thread
+  // scans its contiguous run there (an odd run length hits distinct banks) and
+  // the bases go back out coalesced.  Unstaged, the runs are read and written
+  // in global memory directly (lanes 4*per bytes apart).
+  int32_t* stage = bin_start + ((nbins + 4) & ~3);
+  if (staged) {  // total_n <= kHeld * kScanThreads: every load in flight at once
+    int32_t v[kHeld];
+#pragma unroll
+    for (int q = 0; q < kHeld; ++q) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(q) * kScanThreads;
+      v[q] = i < total_n ? hist[i] : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < kHeld; ++q) {
+      const int64_t i = threadIdx.x + static_cast<int64_t>(q) * kScanThreads;
+      if (i < total_n) stage[i] = v[q];
+    }
+    __syncthreads();
+  }
+  const int32_t* src = staged ? stage : hist;
+  int32_t* dst = staged ? stage : base;
   int32_t held[kHeld];
 #pragma unroll
-  for (int q = 0; q < kHeld; ++q) held[q] = i0 + q < i1 ? hist[i0 + q] : 0;
+  for (int q = 0; q < kHeld; ++q) held[q] = i0 + q < i1 ? src[i0 + q] : 0;
   uint32_t local = 0;
 #pragma unroll
   for (int q = 0; q < kHeld; ++q) local += static_cast<uint32_t>(held[q]);
-  for (int64_t i = i0 + kHeld; i < i1; ++i) local += static_cast<uint32_t>(hist[i]);
+  for (int64_t i = i0 + kHeld; i < i1; ++i) local += static_cast<uint32_t>(src[i]);
   uint32_t total = 0;
   uint32_t run = block_exclusive_scan(local, &total);
   int64_t bin = i0 / chunks, chunk = i0 % chunks;  // coordinates of element i
   auto emit = [&](int64_t i, int32_t v) {
-    base[i] = static_cast<int32_t>(run);
+    dst[i] = static_cast<int32_t>(run);
     if (chunk == 0) bin_start[bin] = static_cast<int32_t>(run);
     run += static_cast<uint32_t>(v);
     if (++chunk == chunks) {
@@ -116,9 +139,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 #pragma unroll
   for (int q = 0; q < kHeld; ++q)
     if (i0 + q < i1) emit(i0 + q, held[q]);
-  for (int64_t i = i0 + kHeld; i < i1; ++i) emit(i, hist[i]);
+  for (int64_t i = i0 + kHeld; i < i1; ++i) emit(i, src[i]);
   if (threadIdx.x == 0) bin_start[nbins] = static_cast<int32_t>(total);
   __syncthreads();
+  if (staged)
+    for (int64_t i = threadIdx.x; i < total_n; i += kScanThreads) base[i] = stage[i];
   for (int b = threadIdx.x; b < nbins; b += kScanThreads) {
     const int64_t off = bin_start[b], tot = bin_start[b + 1] - off;
     int64_t kept = limit - off;
@@ -133,15 +158,20 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   }
 }
 
-// Launch the scan with (nbins + 1) ints of dynamic LDS (up to 64 KB, beyond the
-// default dynamic limit once the static wave totals are added).
+// Launch the scan with (nbins + 1) ints of dynamic LDS, plus the whole
+// histogram when that still fits in kScanDynLds (64 KB, beyond the default
+// dynamic limit once the static wave totals are added).
 inline hipError_t launch_scan(const int32_t* hist, int64_t chunks, int nbins, int64_t limit, int32_t* base,
                               int32_t* bin_kept, int32_t* offsets, int32_t* num_kept, hipStream_t st) {
   static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_kernel),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, 65536);
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, kScanDynLds);
   if (attr != hipSuccess) return attr;
-  scan_kernel<<<1, kScanThreads, (nbins + 1) * sizeof(int32_t), st>>>(hist, chunks, nbins, limit, base, bin_kept,
-                                                                      offsets, num_kept);
+  const int64_t head = (nbins + 4) & ~3;  // bin_start ints, the stage 16-byte aligned after them
+  const int64_t staged_bytes = (head + chunks * nbins) * static_cast<int64_t>(sizeof(int32_t));
+  const bool staged = staged_bytes <= kScanDynLds;
+  const size_t lds = staged ? static_cast<size_t>(staged_bytes) : (nbins + 1) * sizeof(int32_t);
+  scan_kernel<<<1, kScanThreads, lds, st>>>(hist, chunks, nbins, limit, base, bin_kept, offsets, num_kept,
+                                            staged ? 1 : 0);
   return hipSuccess;
 }
 
