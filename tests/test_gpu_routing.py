@@ -182,6 +182,11 @@ DISPATCH_CASES = [
     ("all_local", 100, 4, 16, 0, 16, 1.0, 1, "f32"),
     ("last_shard", 64, 2, 24, 18, 6, 4.0, 128, "f32"),
     ("big_chunks", 4096, 16, 896, 448, 112, 2.0, 128, "bf16"),
+    # the sort's one-block scan stages its histogram in 64 KB of LDS: 128 chunks
+    # x 127 experts plus the bin starts fill it exactly; one more expert per
+    # chunk no longer fits and is scanned in place
+    ("scan_lds_full", 4096, 16, 896, 0, 127, 2.0, 128, "bf16"),
+    ("scan_in_place", 4096, 16, 896, 0, 128, 2.0, 128, "f32"),
 ]
 
 
