@@ -57,47 +57,103 @@ def load_traffic(name):
     return json.load(f)
 
 
-def cpu_baseline(layer, hidden, w, c, sample_tokens, reps):
-  """Oracle restatement of the reference single-shard forward on the host:
-  the same weights (MXFP4 experts dequantised to bf16, as the reference does
-  offline), ``sample_tokens`` of the 4096 tokens, median of ``reps`` runs."""
-  import numpy as np
+def cpu_model() -> str:
+  try:
+    with open("/proc/cpuinfo") as f:
+      for line in f:
+        if line.startswith("model name"):
+          return line.split(":", 1)[1].strip()
+  except OSError:
+    pass
+  return "unknown"
+
+
+def oracle_inputs(layer, hidden, w, c):
+  """The layer's weights as the oracle takes them: MXFP4 experts dequantised
+  (bit-exact, as the reference does offline) to (L+1, in, out) f32 arrays,
+  dense weights and the hidden states as f32 numpy arrays."""
   import torch
 
   from lmoe import ops
+  E = layer.experts
+  I = c.intermediate
+  gu = ops.dequantize_mxfp4(E["gu_packed"], E["gu_scale"], out_dtype=torch.bfloat16)  # (L+1, 2I, lat)
+  dn = ops.dequantize_mxfp4(E["down_packed"], E["down_scale"], out_dtype=torch.bfloat16)  # (L+1, lat, I)
+  f = lambda t: t.float().cpu().numpy()
+  gu_h, dn_h = f(gu), f(dn)
+  del gu, dn
+  wd = {k: f(v) for k, v in w.items()}
+  return (f(hidden), wd, gu_h[:, :I, :].transpose(0, 2, 1), gu_h[:, I:, :].transpose(0, 2, 1),
+          dn_h.transpose(0, 2, 1))
+
+
+def cpu_baseline(inputs, c, sample_tokens, reps):
+  """Oracle restatement of the reference single-shard forward on the host:
+  the same weights, ``sample_tokens`` of the 4096 tokens, median of ``reps``
+  runs.  Returns (baseline dict, the last run's (output, stages))."""
   from oracle import lmoe_oracle as O
   try:
     from threadpoolctl import threadpool_info
     threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
   except Exception:  # noqa: BLE001
     threads = len(os.sched_getaffinity(0))
-  E = layer.experts
-  L, I = c.local_experts, c.intermediate
-  gu = ops.dequantize_mxfp4(E["gu_packed"], E["gu_scale"], out_dtype=torch.bfloat16)  # (L+1, 2I, lat)
-  dn = ops.dequantize_mxfp4(E["down_packed"], E["down_scale"], out_dtype=torch.bfloat16)  # (L+1, lat, I)
-  f = lambda t: t.float().cpu().numpy()
-  gu_h, dn_h = f(gu), f(dn)
-  del gu, dn
-  gate = gu_h[:, :I, :].transpose(0, 2, 1)
-  up = gu_h[:, I:, :].transpose(0, 2, 1)
-  down = dn_h.transpose(0, 2, 1)
-  wd = {k: f(v) for k, v in w.items()}
+  h, wd, gate, up, down = inputs
+  h = h[:sample_tokens]
   cfg = c.config()
-  h = f(hidden[:sample_tokens])
-  run = lambda: O.single_shard_forward(h, wd, gate, up, down, cfg, "bf16", c.local_start, L,
+  run = lambda: O.single_shard_forward(h, wd, gate, up, down, cfg, "bf16", c.local_start, c.local_experts,
                                        c.capacity_factor, include_shared=False)
-  run()
+  res = run()
   times = []
   for _ in range(reps):
     t0 = time.perf_counter()
-    run()
+    res = run()
     times.append(time.perf_counter() - t0)
   med = statistics.median(times)
   return {"value": round(sample_tokens / med, 2), "unit": "tokens/s", "cores": int(threads),
-          "kind": "port",
+          "cpu_model": cpu_model(), "kind": "port",
           "sample": f"{sample_tokens} of {c.tokens} tokens through the numpy oracle's single-shard "
                     f"forward (all stages, bf16 rounding emulated), median of {reps} runs "
-                    f"({med:.2f} s each)"}
+                    f"({med:.2f} s each)"}, res
+
+
+def parity(inputs, c, out, st, own):
+  """The benchmarked forward's output against the oracle on the same tokens:
+  routing on the oracle's own logits (agreement), then the oracle run on the
+  device's logits and latent projection -- routing and dispatch bit-exact,
+  final output max-relative error (bf16 bar 2e-2)."""
+  import numpy as np
+  import torch
+
+  from oracle import lmoe_oracle as O
+
+  def np32(t):
+    t = t.detach()
+    if t.dtype == torch.bfloat16:
+      return t.float().cpu().numpy()
+    return t.cpu().numpy()
+
+  h, wd, gate, up, down = inputs
+  cfg = c.config()
+  lg, x = np32(st["router_logits"]), np32(st["x"])
+  ref, rs = O.single_shard_forward(h, wd, gate, up, down, cfg, "bf16", c.local_start, c.local_experts,
+                                   c.capacity_factor, include_shared=False, logits=lg, x=x)
+  idx = np32(st["topk_idx"])
+  out_np = np32(out)
+  mr = lambda a, b: float(np.max(np.abs(a.astype(np.float64) - b)) / max(float(np.max(np.abs(b))), 1e-30))
+  res = {"tolerance": 2e-2,
+         "routing_bit_exact_on_device_logits": bool(np.array_equal(idx, rs["topk_idx"])
+                                                    and np.array_equal(np32(st["topk_weight"]), rs["topk_weight"])),
+         "dispatch_bit_exact": bool(all(np.array_equal(np32(a), b) for a, b in zip(st["dispatch"][:6], rs["dispatch"]))),
+         "shard_out_max_rel": round(mr(np32(st["shard_out"]), rs["shard_out"]), 6),
+         "final_max_rel": round(mr(out_np, ref), 6),
+         "logits_max_rel_vs_oracle_gemm": None, "routing_identical_tokens": None}
+  if own is not None:
+    own_out, own_st = own
+    agree = np.all(idx == own_st["topk_idx"], axis=1)
+    res["logits_max_rel_vs_oracle_gemm"] = float(f"{mr(lg, own_st['router_logits']):.3e}")
+    res["routing_identical_tokens"] = f"{int(agree.sum())}/{agree.size}"
+    res["final_max_rel_vs_oracle_own_routing"] = round(mr(out_np[agree], own_out[agree]), 6)
+  return res
 
 
 def capture_layer(torch, layer, hidden):
@@ -164,7 +220,7 @@ def main():
                               expert_format="mxfp4", experts=experts, capacity_factor=c.capacity_factor,
                               mxfp4_mode=args.mxfp4_mode)
   torch.cuda.synchronize()
-  _, st = layer.forward(hidden, return_stages=True)
+  out_stages, st = layer.forward(hidden, return_stages=True)
   gs = st["dispatch"].group_sizes.cpu().numpy()
   rows, hit, flops, nbytes = gateup_algorithmic(c, gs)
   m_padded = int(gs.sum())
@@ -222,11 +278,22 @@ def main():
   ev1.synchronize()
   copy_gbs = 2 * (256 << 20) * 10 / (ev0.elapsed_time(ev1) / 1000.0) / 1e9
   del src, dst
-  traffic = load_traffic("traffic_cfg5_gateup_mxfp4.json")
+  # the kernel the gate/up launch ran, and the committed counter profile of
+  # that kernel at this workload (HBM bytes per launch), when there is one
+  if args.mxfp4_mode == "scaled_mfma":
+    kernel, traffic_file = "grouped_gemm_mx_kernel (MXFP8 x MXFP4 scaled MFMA, SiTU)", None
+  elif os.environ.get("LMOE_STREAM", "1") == "0":
+    kernel, traffic_file = "grouped_gemm_dma_kernel<MXFP4 tiled, SiTU> (one block per tile)", None
+  else:
+    kernel, traffic_file = ("grouped_gemm_stream_kernel<64, 256, MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
+                            "traffic_cfg5_gateup_mxfp4.json")
+  traffic = load_traffic(traffic_file) if traffic_file else None
   roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
               "frac": round(achieved / HBM_PEAK_GBS, 4),
               "traffic": traffic.get("bytes_per_launch") if traffic else None,
-              "kernel": "grouped_gemm_stream_kernel<64, 256, MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
+              "traffic_source": f"profiles/{traffic_file} (rocprofv3 FETCH_SIZE + WRITE_SIZE, committed)"
+                                if traffic else None,
+              "kernel": kernel,
               "algorithmic_bytes": int(nbytes), "algorithmic_flops": flops,
               "kernel_us": round(gateup_ms * 1000.0, 2),
               "copy_GBps": round(copy_gbs, 1), "frac_of_copy": round(achieved / copy_gbs, 4)}
@@ -235,10 +302,14 @@ def main():
              "pct_bf16_peak": round(100 * tflops / PEAK_TFLOPS["bf16"], 2),
              "mfma_path": args.mxfp4_mode}
 
-  cpu = None
+  cpu, par = None, None
   if not args.no_cpu_baseline:
+    inputs = oracle_inputs(layer, hidden, w, c)
     log(f"cpu baseline on {args.cpu_sample_tokens} tokens")
-    cpu = cpu_baseline(layer, hidden, w, c, args.cpu_sample_tokens, args.cpu_reps)
+    cpu, own = cpu_baseline(inputs, c, args.cpu_sample_tokens, args.cpu_reps)
+    log("parity of the benchmarked forward against the oracle")
+    par = parity(inputs, c, out_stages, st, own if args.cpu_sample_tokens == c.tokens else None)
+    log(f"parity: {par}")
 
   line = {
       "metric": METRIC, "value": round(tokens_per_s, 1), "unit": "tokens/s", "n_gpus": 1,
@@ -253,7 +324,7 @@ def main():
                  "m_padded": m_padded, "routed_rows": rows, "router_skew": "zipf(1.2) on logits",
                  "shared_experts": 0, "parallelism": "single GPU (one expert shard)",
                  "execution": execution, "eager_ms_per_step": round(eager_ms, 4)},
-      "roofline": roofline, "grouped_gemm": grouped, "cpu_baseline": cpu,
+      "roofline": roofline, "grouped_gemm": grouped, "cpu_baseline": cpu, "parity": par,
   }
   print(json.dumps(line), flush=True)
 

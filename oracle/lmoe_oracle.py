@@ -130,6 +130,68 @@ def rms_norm(x, scale, eps: float, dtype: str) -> np.ndarray:
 # ---------------------------------------------------------------------------
 
 
+# Gate scores: a fully specified binary64 evaluation (the router kernel runs
+# the same operation sequence, so the device scores can be compared bit for
+# bit).  exp(t): Cody & Waite argument reduction (W. J. Cody and W. Waite,
+# "Software Manual for the Elementary Functions", 1980) with fdlibm's ln2
+# split (e_exp.c: ln2_hi has 21 trailing zero bits, so n*ln2_hi is exact),
+# then the degree-13 Taylor polynomial of e^r on |r| <= ln2/2 in Horner form,
+# scaled by 2^n.  Only correctly rounded add/sub/mul/div, floor and ldexp are
+# used (numpy evaluates each separately: no fused multiply-add).
+GATE_INV_LN2 = float.fromhex("0x1.71547652b82fep+0")
+GATE_LN2_HI = float.fromhex("0x1.62e42fee00000p-1")
+GATE_LN2_LO = float.fromhex("0x1.a39ef35793c76p-33")
+GATE_INV_FACT = tuple(1.0 / math.factorial(j) for j in range(14))  # each correctly rounded
+
+
+def gate_exp64(t) -> np.ndarray:
+  """binary64 e^t by the fixed sequence above; t > 709 -> inf, t < -708 -> 0."""
+  t = np.asarray(t, np.float64)
+  tc = np.clip(np.where(np.isnan(t), 0.0, t), -708.0, 709.0)
+  n = np.floor(tc * GATE_INV_LN2 + 0.5)
+  r = (tc - n * GATE_LN2_HI) - n * GATE_LN2_LO
+  p = np.full(r.shape, GATE_INV_FACT[13])
+  for j in range(12, -1, -1):
+    p = p * r + GATE_INV_FACT[j]
+  e = np.ldexp(p, n.astype(np.int32))
+  e = np.where(t > 709.0, np.inf, np.where(t < -708.0, 0.0, e))
+  return np.where(np.isnan(t), np.nan, e)
+
+
+def gate_sigmoid(x) -> np.ndarray:
+  """Router sigmoid (``jax.nn.sigmoid`` of ref.py:349 / ref.py:622) as
+  f32(1 / (1 + exp(-x))) evaluated in binary64: the correctly rounded f32
+  sigmoid except within ~2^-50 relative of an f32 rounding boundary."""
+  x = np.asarray(x, F32)
+  with np.errstate(over="ignore", invalid="ignore"):
+    return (1.0 / (1.0 + gate_exp64(-x.astype(np.float64)))).astype(F32)
+
+
+def gate_softmax(x) -> np.ndarray:
+  """Row softmax of the official gate's softmax branch
+  (06_kimi_k3_golden_validation/generate_pytorch_golden.py:151-156):
+  d = f32(x - max), e = exp(d) in binary64, p = f32(e / sum e).  The sum runs
+  in a fixed order: 64 partial sums, partial l adding experts l, l+64,
+  l+128, ... in turn, then an xor butterfly over distances 32, 16, ..., 1."""
+  x = np.asarray(x, F32)
+  lead, e_n = x.shape[:-1], x.shape[-1]
+  x2 = x.reshape(-1, e_n)
+  d = (x2 - np.max(x2, axis=-1, keepdims=True)).astype(F32)
+  with np.errstate(over="ignore", invalid="ignore"):
+    ex = gate_exp64(d.astype(np.float64))
+  chunks = -(-e_n // 64)
+  pad = np.zeros((x2.shape[0], chunks * 64), np.float64)
+  pad[:, :e_n] = ex
+  acc = np.zeros((x2.shape[0], 64), np.float64)
+  for c in range(chunks):
+    acc = acc + pad[:, c * 64:(c + 1) * 64]
+  lanes = np.arange(64)
+  for off in (32, 16, 8, 4, 2, 1):
+    acc = acc + acc[:, lanes ^ off]
+  with np.errstate(invalid="ignore", divide="ignore"):
+    return (ex / acc[:, :1]).astype(F32).reshape(*lead, e_n)
+
+
 def top_k(values, k: int) -> np.ndarray:
   """``jax.lax.top_k`` index semantics: descending by value, equal values ordered
   by ascending index (stable).  Returns int32 (T, k)."""
@@ -150,16 +212,17 @@ def router_from_logits(logits, bias, top_k_: int, renormalize: bool, scaling: fl
   """Gate math of ref.py:347-361 (unsharded, weights stay f32) and
   ref.py:601-631 (``_router_gate``: weights cast to the compute dtype at 630).
 
-  scores = act(logits); choice = scores + bias; idx = top_k(choice);
+  scores = act(logits) (``gate_sigmoid`` / ``gate_softmax``); choice =
+  scores + bias; idx = top_k(choice);
   w = scores[idx]; if k>1 and renorm: w /= sum(w)+1e-20; w *= scaling.
   The softmax branch follows the official gate
   (06_kimi_k3_golden_validation/generate_pytorch_golden.py:151-156).
   """
   logits = np.asarray(logits, F32)
   if act == "sigmoid":
-    scores = sigmoid(logits)
+    scores = gate_sigmoid(logits)
   elif act == "softmax":
-    scores = softmax(logits, axis=-1)
+    scores = gate_softmax(logits)
   else:
     raise NotImplementedError(act)
   bias = np.zeros(logits.shape[-1], F32) if bias is None else np.asarray(bias, F32)
@@ -167,8 +230,12 @@ def router_from_logits(logits, bias, top_k_: int, renormalize: bool, scaling: fl
   idx = top_k(choice, top_k_)
   w = np.take_along_axis(scores, idx.astype(np.int64), axis=-1).astype(F32)
   if top_k_ > 1 and renormalize:
-    denom = np.sum(w, axis=-1, keepdims=True, dtype=F32) + F32(1e-20)
-    w = (w / denom).astype(F32)
+    # f32 sum in top-k order (XLA's reduction order is unspecified; this one
+    # is fixed so the device result can be compared bit for bit)
+    denom = np.zeros(w.shape[:-1] + (1,), F32)
+    for j in range(top_k_):
+      denom = (denom + w[..., j:j + 1]).astype(F32)
+    w = (w / (denom + F32(1e-20))).astype(F32)
   w = (w * F32(scaling)).astype(F32)
   return RouterOut(idx, cast(w, weight_dtype), scores, choice)
 
@@ -442,27 +509,36 @@ def unsharded_combine(outs, order, topk_weight, num_tokens: int, top_k_: int,
 # ---------------------------------------------------------------------------
 
 
-def latent_moe_forward(hidden, w: dict, config, dtype: str, act: str = "sigmoid"):
+def latent_moe_forward(hidden, w: dict, config, dtype: str, act: str = "sigmoid", logits=None,
+                       x=None):
   """``latent_moe_forward``, ref.py:330-435, with the 18 intermediates of
   06_kimi_k3_golden_validation/test_jax_reference_against_pytorch_golden.py:173-275.
 
   ``w`` holds reference-layout (in, out) arrays with keys router_weight,
   e_score_correction_bias, down_proj, up_proj, expert_gate, expert_up,
   expert_down, norm_scale, shared_gate, shared_up, shared_down.
+  ``logits`` / ``x``, when given, replace the router logits GEMM and the
+  down-projection (a checker passes the device's own values, so every later
+  stage is compared on identical routing and identical gathered rows).
   Returns (final_output, intermediates).
   """
   hidden = cast(hidden, dtype)
   inter: dict[str, np.ndarray] = {}
   t = hidden.shape[0]
   k = config.top_k
-  r, logits = router_gate(hidden, w["router_weight"], w["e_score_correction_bias"], config,
-                          act=act, weight_dtype="f32")
+  if logits is None:
+    r, logits = router_gate(hidden, w["router_weight"], w["e_score_correction_bias"], config,
+                            act=act, weight_dtype="f32")
+  else:
+    logits = np.asarray(logits, F32)
+    r = router_from_logits(logits, w["e_score_correction_bias"], config.top_k, config.moe_renormalize,
+                           config.routed_scaling_factor, act, "f32")
   inter["router_logits"] = logits
   inter["router_scores_before_bias"] = r.scores
   inter["router_scores_for_choice"] = r.scores_for_choice
   inter["topk_indices"] = r.topk_idx
   inter["topk_weights"] = r.topk_weight
-  x = matmul(hidden, w["down_proj"], dtype)
+  x = matmul(hidden, w["down_proj"], dtype) if x is None else cast(x, dtype)
   inter["latent_projection"] = x
   order, sorted_tokens, group_sizes = unsharded_dispatch(r.topk_idx, x, config.num_experts)
   inter["sorted_token_indices"] = order
@@ -507,16 +583,23 @@ def latent_moe_forward(hidden, w: dict, config, dtype: str, act: str = "sigmoid"
 def single_shard_forward(hidden, w: dict, shard_gate, shard_up, shard_down, config, dtype: str,
                          local_expert_start: int, local_num_experts: int,
                          capacity_factor: float = 2.0, act: str = "sigmoid",
-                         include_shared: bool = True):
+                         include_shared: bool = True, logits=None, x=None):
   """``latent_moe_forward_ragged_dot_single_shard_jittable``, rd.py:1035-1137,
   with the naive per-expert FFN as the ragged_dot oracle.  ``shard_*`` have
-  L+1 experts (the last is the padding bucket).  Returns (final, stages)."""
+  L+1 experts (the last is the padding bucket).  ``logits`` / ``x``, when
+  given, replace the router logits GEMM and the down-projection (see
+  ``latent_moe_forward``).  Returns (final, stages)."""
   hidden = cast(hidden, dtype)
   stages: dict[str, np.ndarray] = {}
-  x = matmul(hidden, w["down_proj"], dtype)
+  x = matmul(hidden, w["down_proj"], dtype) if x is None else cast(x, dtype)
   stages["x"] = x
-  r, logits = router_gate(hidden, w["router_weight"], w["e_score_correction_bias"], config,
-                          act=act, weight_dtype=dtype)
+  if logits is None:
+    r, logits = router_gate(hidden, w["router_weight"], w["e_score_correction_bias"], config,
+                            act=act, weight_dtype=dtype)
+  else:
+    logits = np.asarray(logits, F32)
+    r = router_from_logits(logits, w["e_score_correction_bias"], config.top_k, config.moe_renormalize,
+                           config.routed_scaling_factor, act, dtype)
   stages["router_logits"] = logits
   stages["topk_idx"] = r.topk_idx
   stages["topk_weight"] = r.topk_weight
@@ -567,19 +650,26 @@ def fp4_e2m1_to_f32(nibble) -> np.ndarray:
   return (mag * np.where((n & 8) != 0, F32(-1.0), F32(1.0))).astype(F32)
 
 
+_BYTES = np.arange(256)
+_MXFP4_PAIR_LUT = np.stack([fp4_e2m1_to_f32(_BYTES & 0x0F), fp4_e2m1_to_f32(_BYTES >> 4)], axis=-1)
+_E8M0_LUT = e8m0_to_f32(_BYTES)
+
+
 def dequantize_mxfp4(weight_packed, weight_scale) -> np.ndarray:
-  """``dequantize_mxfp4``, deq.py:29-67.  packed (N, K/2) u8 (low nibble =
-  element 2j, high = 2j+1), scale (N, K/gs) u8 -> (N, K) float32."""
+  """``dequantize_mxfp4``, deq.py:29-67.  packed (..., N, K/2) u8 (low nibble =
+  element 2j, high = 2j+1), scale (..., N, K/gs) u8 -> (..., N, K) float32."""
   p = np.asarray(weight_packed, np.uint8)
-  n_out, kh = p.shape
+  *lead, n_out, kh = p.shape
   k = kh * 2
   s = np.asarray(weight_scale, np.uint8)
-  gs = k // s.shape[1]
-  combined = np.stack([p & 0x0F, p >> 4], axis=-1).reshape(n_out, k)
-  values = fp4_e2m1_to_f32(combined)
-  scale = np.repeat(e8m0_to_f32(s), gs, axis=1)
+  ng = s.shape[-1]
+  gs = k // ng
+  # byte -> (element 2j, element 2j+1) values, then one multiply by the
+  # block's scale (the same products as decoding each nibble separately)
+  values = _MXFP4_PAIR_LUT[p].reshape(*lead, n_out, ng, gs)
+  scale = _E8M0_LUT[s][..., None]
   with np.errstate(invalid="ignore", over="ignore"):
-    return (values * scale).astype(F32)
+    return (values * scale).astype(F32).reshape(*lead, n_out, k)
 
 
 def mxfp4_matmul(x, weight_packed, weight_scale, dtype: str = "bf16") -> np.ndarray:

@@ -52,6 +52,86 @@ def test_softmax_and_sigmoid_closed_form():
   assert np.max(np.abs(O.sigmoid(x) - 1 / (1 + np.exp(-x64)))) < 1e-6
 
 
+def test_gate_exp64_against_libm():
+  """The router's binary64 exp (Cody-Waite reduction + degree-13 Taylor) is
+  within 1 ulp of the C library's exp over the whole clamped range, exact at
+  0 and 1 ulp-close at integers; outside the range it saturates to inf / 0."""
+  t = np.concatenate([np.linspace(-708.0, 709.0, 400001), np.linspace(-1.0, 1.0, 200001),
+                      np.arange(-708.0, 710.0)])
+  e = O.gate_exp64(t)
+  ulp = np.abs(e - np.exp(t)) / np.spacing(np.exp(t))
+  assert ulp.max() <= 1.0, ulp.max()
+  assert O.gate_exp64(0.0) == 1.0
+  assert abs(O.gate_exp64(1.0) - math.e) <= 2 * np.spacing(math.e)
+  edge = O.gate_exp64(np.array([709.5, 1e300, np.inf, -708.5, -1e300, -np.inf, np.nan]))
+  assert np.array_equal(edge[:6], [np.inf] * 3 + [0.0] * 3) and np.isnan(edge[6])
+
+
+def test_gate_exp64_planted_mistakes_fail():
+  """Dropping the low part of ln2 or the two highest Taylor terms breaks the
+  1-ulp bound."""
+  t = np.linspace(-700.0, 700.0, 100001)
+  good = np.abs(O.gate_exp64(t) - np.exp(t)) / np.spacing(np.exp(t))
+  assert good.max() <= 1.0
+  saved = (O.GATE_LN2_LO, O.GATE_INV_FACT)
+  try:
+    O.GATE_LN2_LO = 0.0
+    assert (np.abs(O.gate_exp64(t) - np.exp(t)) / np.spacing(np.exp(t))).max() > 100
+    O.GATE_LN2_LO = saved[0]
+    O.GATE_INV_FACT = saved[1][:12] + (0.0, 0.0)
+    assert (np.abs(O.gate_exp64(t) - np.exp(t)) / np.spacing(np.exp(t))).max() > 4
+  finally:
+    O.GATE_LN2_LO, O.GATE_INV_FACT = saved
+
+
+def test_gate_sigmoid_is_correctly_rounded():
+  """f32 sigmoid within half an f32 ulp of the extended-precision value (so
+  correctly rounded) on a wide sample, including subnormal results, +-0,
+  +-inf and saturation."""
+  rng = np.random.default_rng(4)
+  x = np.concatenate([rng.standard_normal(400000) * 6, rng.uniform(-110, 40, 100000),
+                      [0.0, -0.0, 88.7, -87.3, -100.0, -103.97, -200.0, 1e30, -1e30, np.inf, -np.inf]])
+  x = x.astype(np.float32)
+  s = O.gate_sigmoid(x)
+  with np.errstate(over="ignore"):
+    ld = 1 / (1 + np.exp(-x.astype(np.longdouble)))
+  half = np.spacing(np.abs(s)).astype(np.longdouble) / 2
+  tiny = np.longdouble(2.0) ** -149  # subnormal spacing
+  assert np.all(np.abs(s.astype(np.longdouble) - ld) <= np.maximum(half, tiny / 2) * (1 + 1e-6))
+  assert O.gate_sigmoid(np.float32(0)) == 0.5 and O.gate_sigmoid(np.float32(np.inf)) == 1.0
+  assert O.gate_sigmoid(np.float32(-np.inf)) == 0.0 and O.gate_sigmoid(np.float32(-100)) > 0
+
+
+def test_gate_softmax_closed_form():
+  """Within one f32 ulp of the extended-precision softmax of the f32
+  differences x - max (the gate subtracts in f32), rows sum to 1, and E not a
+  multiple of 64 (padding partials) works."""
+  rng = np.random.default_rng(5)
+  for e_n in (8, 64, 100, 896, 4096):
+    x = (rng.standard_normal((32, e_n)) * 4).astype(np.float32)
+    p = O.gate_softmax(x)
+    d = (x - x.max(-1, keepdims=True)).astype(np.float32).astype(np.longdouble)
+    ref = np.exp(d)
+    ref /= ref.sum(-1, keepdims=True)
+    assert np.all(np.abs(p - ref) <= np.spacing(p).astype(np.longdouble)), e_n
+    assert np.allclose(p.astype(np.float64).sum(-1), 1.0, atol=1e-6)
+
+
+def test_router_renorm_sums_in_topk_order():
+  """The renormalisation divides by the f32 sum of the chosen scores taken in
+  top-k order (j = 0, 1, ...): checked on values where that order and a
+  pairwise sum round differently."""
+  logits = np.zeros((1, 4), np.float32)
+  scores = np.array([0.5, 2.0 ** -25, 2.0 ** -25, 0.25], np.float32)
+  logits[0] = -np.log(1 / scores.astype(np.float64) - 1)
+  r = O.router_from_logits(logits, np.array([0, 0, 0, 0], np.float32), 4, True, 1.0)
+  s = O.gate_sigmoid(logits)[0][r.topk_idx[0]]
+  seq = np.float32(0)
+  for v in s:
+    seq = np.float32(seq + v)
+  assert np.array_equal(r.topk_weight[0], (s / (seq + np.float32(1e-20))).astype(np.float32))
+
+
 def test_situ_closed_form():
   g = np.linspace(-30, 30, 2001).astype(np.float32)
   u = np.linspace(40, -40, 2001).astype(np.float32)

@@ -1,5 +1,6 @@
 """Host-side workload generation: the OCP MX quantiser and the Zipf group sizes."""
 import numpy as np
+import pytest
 import torch
 
 from lmoe import workloads as W
@@ -36,3 +37,50 @@ def test_zipf_group_sizes():
   gs = W.zipf_group_sizes(8192, 32, seed=2)
   assert gs.sum() == 8192 and (gs == 0).sum() >= 3 and gs.dtype == np.int32
   assert gs.max() > 4 * 8192 / 32  # skewed
+
+
+def test_global_picks_uniform_without_replacement():
+  """Every token's picks are distinct, and over many tokens each expert is
+  picked T*k/E times within a chi-square bound (uniform draw)."""
+  rng = np.random.default_rng(3)
+  t, e, k = 20000, 96, 8
+  picks = W._draw_global_picks(rng, t, e, k)
+  assert picks.shape == (t, k) and picks.min() >= 0 and picks.max() < e
+  assert all(len(set(row)) == k for row in picks[:2000])
+  assert np.all(np.sort(picks, 1)[:, 1:] != np.sort(picks, 1)[:, :-1])
+  counts = np.bincount(picks.reshape(-1), minlength=e)
+  expect = t * k / e
+  chi2 = float(((counts - expect) ** 2 / expect).sum())
+  assert chi2 < e + 6 * np.sqrt(2 * e), chi2  # ~6 sigma above the mean of chi2(e-1)
+  # each position is uniform too (the order within a token is random)
+  first = np.bincount(picks[:, 0], minlength=e)
+  assert float(((first - t / e) ** 2 / (t / e)).sum()) < e + 6 * np.sqrt(2 * e)
+
+
+@pytest.mark.parametrize("t,e,k,L,cf", [(4096, 896, 16, 112, 2.0), (300, 64, 6, 16, 1.5), (1, 896, 16, 112, 2.0),
+                                        (512, 64, 8, 32, 1.0)])
+def test_generate_local_shard_workload_invariants(t, e, k, L, cf):
+  """ref.py:474-598: fixed m_padded = round_up(ceil(T*k*L/E*cf), 128) (the
+  oracle's m_padded formula), per-expert counts as drawn (truncated from the
+  tail on overflow), one padding bucket, zero padding rows, valid mask on the
+  kept rows."""
+  lat = 64
+  st, gs, valid, counts = W.generate_local_shard_workload(t, e, k, L, lat, capacity_factor=cf, seed=t, device="cpu")
+  m_padded = O.compute_m_padded(t, k, e, L, cf)
+  assert st.shape == (m_padded, lat) and st.dtype == torch.bfloat16
+  gs, counts, valid = gs.numpy(), counts.numpy(), valid.numpy()
+  assert gs.shape == (L + 1,) and gs.dtype == np.int32 and gs.sum() == m_padded
+  assert np.array_equal(gs[:L], counts)
+  keep = int(counts.sum())
+  assert valid.sum() == keep and valid[:keep].all() and not valid[keep:].any()
+  assert not st[keep:].float().abs().sum() and (st[:keep].float().abs().sum(1) > 0).all()
+  # the draw itself: the same seeded picks, kept below L, sorted, truncated
+  picks = W._draw_global_picks(np.random.default_rng(t), t, e, k).reshape(-1)
+  raw = np.sort(picks[picks < L])
+  assert np.array_equal(counts, np.bincount(raw[:m_padded], minlength=L))
+  if raw.size > m_padded:
+    # overflow drops the tail: the highest expert ids lose picks first
+    full = np.bincount(raw, minlength=L)
+    lost = np.nonzero(full != counts)[0]
+    assert lost.size and np.array_equal(full[:lost[0]], counts[:lost[0]])
+    assert not counts[lost[0] + 1:].any()

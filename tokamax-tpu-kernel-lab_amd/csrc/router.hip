@@ -5,6 +5,13 @@
 // with fully coalesced loads.  The order is "descending score + bias, ties to
 // the lower expert id" -- jax.lax.top_k's order.
 //
+// Exact scores are the gate functions of gate_math.h (binary64 evaluation with
+// a fixed operation sequence, one rounding to f32), so the host-side checker
+// can reproduce them bit for bit; the softmax denominator is summed in
+// binary64 in a fixed order (each lane over its experts c = 0, 1, ..., then an
+// xor butterfly over lane distances 32, 16, ..., 1).  The renormalisation sum
+// of the k chosen weights runs in f32 in top-k order.
+//
 // Candidate path (sigmoid gate, k <= 64, no full score output): every score
 // is first computed with the hardware exp / reciprocal (a few f32 ulp), which
 // only serves to find a threshold: the k-th largest of the 64 lane maxima
@@ -24,6 +31,7 @@
 // lane rescans its EPL candidates.
 #include <cmath>
 
+#include "gate_math.h"
 #include "lmoe_common.h"
 
 namespace lmoe {
@@ -44,9 +52,11 @@ __device__ __forceinline__ float wave_max_f32(float v) {
   return v;
 }
 
-__device__ __forceinline__ float wave_sum_f32(float v) {
+// Sum over the wave by an xor butterfly (distances 32, 16, ..., 1); every
+// lane ends with the same bits (each step adds the same two values).
+__device__ __forceinline__ double wave_sum_f64(double v) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v = __fadd_rn(v, __shfl_xor(v, off, kWave));
+  for (int off = 32; off > 0; off >>= 1) v = __dadd_rn(v, __shfl_xor(v, off, kWave));
   return v;
 }
 
@@ -141,7 +151,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
       if (static_cast<uint32_t>(lane) < total) {
         const float lg = s_logit[wv][lane];
         const int e = s_expert[wv][lane];
-        cs = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-lg)));
+        cs = gate_sigmoid(lg);
         const float sel = bias ? __fadd_rn(cs, bias[e]) : __fadd_rn(cs, 0.0f);
         ck = (static_cast<uint64_t>(ordered_bits(sel)) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
       }
@@ -165,19 +175,20 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
 #pragma unroll
     for (int c = 0; c < EPL; ++c) m = fmaxf(m, s[c]);
     m = wave_max_f32(m);
-    float sum = 0.0f;
+    double ex[EPL];
+    double sum = 0.0;
 #pragma unroll
     for (int c = 0; c < EPL; ++c) {
       const int e = c * kWave + lane;
-      s[c] = e < E ? expf(__fsub_rn(s[c], m)) : 0.0f;
-      sum = __fadd_rn(sum, s[c]);
+      ex[c] = e < E ? gate_exp64(static_cast<double>(__fsub_rn(s[c], m))) : 0.0;
+      sum = __dadd_rn(sum, ex[c]);
     }
-    sum = wave_sum_f32(sum);
+    sum = wave_sum_f64(sum);
 #pragma unroll
-    for (int c = 0; c < EPL; ++c) s[c] = __fdiv_rn(s[c], sum);
+    for (int c = 0; c < EPL; ++c) s[c] = __double2float_rn(__ddiv_rn(ex[c], sum));
   } else {
 #pragma unroll
-    for (int c = 0; c < EPL; ++c) s[c] = __fdiv_rn(1.0f, __fadd_rn(1.0f, expf(-s[c])));
+    for (int c = 0; c < EPL; ++c) s[c] = gate_sigmoid(s[c]);
   }
   uint64_t taken = 0;
 #pragma unroll

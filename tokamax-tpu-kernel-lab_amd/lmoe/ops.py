@@ -325,6 +325,11 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   _dev(lhs, w_packed, w_scale, group_sizes)
   if lhs.dtype != torch.bfloat16:
     raise NotImplementedError("MXFP4 GEMM takes bf16 activations")
+  if w_packed.dtype != torch.uint8 or w_scale.dtype != torch.uint8:
+    raise ValueError(f"MXFP4 weights must be uint8 packed codes and E8M0 scale bytes, got "
+                     f"{w_packed.dtype} / {w_scale.dtype}")
+  if group_sizes.dtype != torch.int32:
+    raise ValueError("group_sizes must be int32")
   m, k = lhs.shape
   if weight_layout == "tiled":
     if w_packed.dim() != 4 or w_packed.shape[3] != 32:

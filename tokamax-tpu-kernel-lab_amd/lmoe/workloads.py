@@ -167,3 +167,135 @@ def _quantize_chunked(w: torch.Tensor, chunk: int = 8):
 def routed_rows(topk_idx: torch.Tensor, start: int, L: int) -> int:
   """Number of (token, slot) assignments that land in [start, start+L)."""
   return int(((topk_idx >= start) & (topk_idx < start + L)).sum().item())
+
+
+# ---------------------------------------------------------------------------
+# BASELINE configs 1 and 3
+# ---------------------------------------------------------------------------
+
+
+def make_config1(seed: int = 0):
+  """the reduced-scale fp32 layer the reference's naive CPU
+  forward runs (ref.py:330-435): 128 tokens, d_model 256 -> latent 128, 8
+  experts, top-2, expert FFN 128 -> 256 -> 128, one shared expert (the
+  reference's small configs carry one, ref.py:174-188), activations N(0, 1),
+  weights N(0, 0.02^2) from ``seed``, bias 0, norm scale 1.  Returns
+  (config, hidden (128, 256) f32, weights dict of f32 numpy arrays in the
+  reference (in, out) layout)."""
+  cfg = LatentMoEConfig(hidden_size=256, latent_size=128, intermediate_size=256, num_experts=8, top_k=2,
+                        num_shared_experts=1)
+  rng = np.random.default_rng(seed)
+  n = lambda *s: (rng.standard_normal(s) * 0.02).astype(np.float32)
+  h, lat, inter, e = cfg.hidden_size, cfg.latent_size, cfg.intermediate_size, cfg.num_experts
+  w = {
+      "router_weight": n(h, e), "e_score_correction_bias": np.zeros(e, np.float32),
+      "down_proj": n(h, lat), "up_proj": n(lat, h),
+      "expert_gate": n(e, lat, inter), "expert_up": n(e, lat, inter), "expert_down": n(e, inter, lat),
+      "norm_scale": np.ones(lat, np.float32),
+      "shared_gate": n(h, inter), "shared_up": n(h, inter), "shared_down": n(inter, h),
+  }
+  hidden = rng.standard_normal((128, h)).astype(np.float32)
+  return cfg, hidden, w
+
+
+@dataclasses.dataclass
+class Config3:
+  """fused gate/up + SiTU-GLU + down on one GPU's shard."""
+  tokens: int = 2048
+  latent: int = 1024
+  intermediate: int = 2048
+  experts: int = 896
+  top_k: int = 16
+  local_start: int = 0
+  local_experts: int = 112
+  capacity_factor: float = 2.0
+  seed: int = 0
+
+  def config(self) -> LatentMoEConfig:
+    return LatentMoEConfig(hidden_size=self.latent, latent_size=self.latent,
+                           intermediate_size=self.intermediate, num_experts=self.experts,
+                           top_k=self.top_k, num_shared_experts=0)
+
+
+def make_config3(device, c: Config3 | None = None):
+  """Inputs of config 3: router logits N(0, 1) f32 (T, E) *given* (seeded
+  numpy), x N(0, 1) bf16 (T, lat), and the shard's expert weights in the
+  reference (G, K, N) layout, N(0, 0.02^2) bf16, L + 1 groups (the trailing
+  padding bucket is zero).  Returns (logits, x, gate, up, down)."""
+  c = c or Config3()
+  rng = np.random.default_rng(c.seed)
+  logits = torch.from_numpy(rng.standard_normal((c.tokens, c.experts)).astype(np.float32)).to(device)
+  gen = torch.Generator(device=device).manual_seed(c.seed + 1)
+  x = torch.randn((c.tokens, c.latent), generator=gen, device=device).to(torch.bfloat16)
+  L = c.local_experts
+
+  def stack(k, n):
+    w = _normal((L + 1, k, n), 0.02, gen, device)
+    w[L] = 0
+    return w
+
+  gate = stack(c.latent, c.intermediate)
+  up = stack(c.latent, c.intermediate)
+  down = stack(c.intermediate, c.latent)
+  return logits, x, gate, up, down
+
+
+# ---------------------------------------------------------------------------
+# a20: generate_local_shard_workload (ref.py:474-598)
+# ---------------------------------------------------------------------------
+
+
+def _draw_global_picks(rng: np.random.Generator, num_tokens: int, global_num_experts: int,
+                       top_k: int) -> np.ndarray:
+  """(num_tokens, top_k) expert ids, each row top_k distinct ids drawn
+  uniformly without replacement (the first top_k positions of a uniformly
+  random permutation, from the ranks of i.i.d. uniforms)."""
+  keys = rng.random((num_tokens, global_num_experts))
+  return np.argsort(keys, axis=1, kind="stable")[:, :top_k].astype(np.int32)
+
+
+def generate_local_shard_workload(num_tokens: int, global_num_experts: int, top_k: int,
+                                  local_num_experts: int, latent_size: int,
+                                  dtype: torch.dtype = torch.bfloat16, capacity_factor: float = 2.0,
+                                  tile_size: int = 128, *, seed: int = 0, device="cuda"):
+  """``generate_local_shard_workload`` (ref.py:474-598): a synthetic expert
+  shard input under a uniform, untrained top-k-of-E router.
+
+  Each token draws ``top_k`` distinct experts uniformly from
+  ``global_num_experts``; only picks below ``local_num_experts`` are kept (by
+  symmetry, any block of ``local_num_experts`` ids would do).  Kept picks are
+  stable-sorted by expert id.  ``m_padded`` = round_up(ceil(T*k*L/E * cf),
+  tile), the ceil taken on the f32 value as ``jnp.ceil`` does (ref.py:568);
+  picks past ``m_padded`` (aggregate overflow) are dropped from the tail of
+  the sorted order with a warning printed, as in the reference.  The real
+  per-expert counts are left as drawn; one trailing padding bucket brings
+  the total to ``m_padded``.
+
+  Returns (sorted_tokens (m_padded, latent) ``dtype`` with N(0, 1) rows for
+  kept picks and zero padding rows, group_sizes (L+1,) int32, valid_mask
+  (m_padded,) bool, per_expert_counts (L,) int32), all on ``device``.  The
+  draw is seeded (numpy PCG64 for the routing, torch's generator on
+  ``device`` for the token rows), so it is reproducible but not the JAX
+  PRNG stream of the reference."""
+  rng = np.random.default_rng(seed)
+  picks = _draw_global_picks(rng, num_tokens, global_num_experts, top_k).reshape(-1)
+  local_ids = np.sort(picks[picks < local_num_experts], kind="stable")
+  num_raw = local_ids.shape[0]
+  expected_total = num_tokens * top_k * local_num_experts / global_num_experts
+  m_padded = -(-int(np.ceil(np.float32(expected_total * capacity_factor))) // tile_size) * tile_size
+  if num_raw > m_padded:
+    print(f"[shard-workload] WARNING: m_padded={m_padded} overflowed by the total draw -- dropping "
+          f"{num_raw - m_padded} of {num_raw} raw assignments from the tail of the expert-sorted order "
+          "(raise capacity_factor if this matters for the benchmark)")
+    local_ids = local_ids[:m_padded]
+  keep = local_ids.shape[0]
+  counts = np.bincount(local_ids, minlength=local_num_experts).astype(np.int32)
+  group_sizes = np.concatenate([counts, np.array([m_padded - keep], np.int32)])
+  gen = torch.Generator(device=device).manual_seed(seed + 1)
+  sorted_tokens = torch.zeros((m_padded, latent_size), dtype=dtype, device=device)
+  if keep:
+    sorted_tokens[:keep] = torch.randn((keep, latent_size), generator=gen, device=device).to(dtype)
+  valid = torch.zeros(m_padded, dtype=torch.bool, device=device)
+  valid[:keep] = True
+  return (sorted_tokens, torch.from_numpy(group_sizes).to(device), valid,
+          torch.from_numpy(counts).to(device))
