@@ -7,7 +7,9 @@
  * stream), allocates nothing, and returns an int status: LMOE_OK (0) or a
  * negative LMOE_ERR_* code, with a message retrievable from lmoe_last_error()
  * (thread-local).  Calls hold no global state and are safe to issue from
- * several host threads on different streams.
+ * several host threads on different streams, with two exceptions stated at
+ * their declarations: lmoe_dense_blaslt keeps library handles and plans, and
+ * lmoe_dispatch_local_noalloc uses one static scratch array per GPU.
  *
  * Data types: bf16 is stored as its 16-bit pattern (torch.bfloat16 layout),
  * f32 as IEEE float.  Index arrays are int32.  Booleans are one byte.
@@ -232,6 +234,23 @@ int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, int w_dtype
                         uint8_t* valid, int32_t* per_expert_counts, int32_t* padded_token_idx,
                         void* padded_w, int32_t* slot_pos, void* workspace,
                         int64_t workspace_size, void* stream);
+
+/* lmoe_dispatch_local without a workspace argument: no counterpart in the
+ * reference; for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * counting sort's workspace is a 4 MiB static device array (one per GPU, held
+ * until the process ends), so lmoe_dispatch_workspace_size(T, k, L) must not
+ * exceed 4 MiB (e.g. T*k = 65536 slots with L <= 4095): larger sizes return
+ * LMOE_ERR_WORKSPACE without launching anything.  Outputs and semantics are
+ * those of lmoe_dispatch_local, bit for bit.  Every call on one GPU uses the
+ * same array: calls that overlap on one GPU (concurrent streams, host
+ * threads) race; calls ordered on one stream do not.  Allocates nothing.
+ */
+int lmoe_dispatch_local_noalloc(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
+                                int x_dtype, int64_t T, int64_t k, int64_t lat, int64_t local_start,
+                                int64_t L, int64_t m_padded, void* sorted_tokens, int32_t* group_sizes,
+                                uint8_t* valid, int32_t* per_expert_counts, int32_t* padded_token_idx,
+                                void* padded_w, int32_t* slot_pos, void* stream);
 
 /* The same dispatch in one launch for decode-sized batches (T*k <= 8192,
  * m_padded <= 8192, L < 1024): every output as lmoe_dispatch_local, bit for

@@ -46,6 +46,9 @@ def test_version_and_error_string(L):
                                        ctypes.c_void_p(16), 16, 96, 16, 1, -1, 0, 0, 0.0, 0.0,
                                        ctypes.c_void_p(16), None), _lib.ERR_UNSUPPORTED),
     (lambda L: L.lmoe_mxfp4_dequant(None, None, 1, 4, 33, 32, None, 0, None), _lib.ERR_INVALID),
+    # allocation-free dispatch: sizes beyond its static scratch are refused first
+    (lambda L: L.lmoe_dispatch_local_noalloc(None, None, 0, None, 1, 1 << 20, 1, 8, 0, 4096, 128, None, None,
+                                             None, None, None, None, None, None), _lib.ERR_WORKSPACE),
     # skinny MXFP4 GEMM: K % 128, group count, flags
     (lambda L: L.lmoe_ragged_dot_mxfp4_skinny(ctypes.c_void_p(256), ctypes.c_void_p(256), ctypes.c_void_p(256),
                                               ctypes.c_void_p(256), 16, 192, 64, 1, -1, 0, 0, 0.0, 0.0, 0,

@@ -8,6 +8,8 @@
 // >= m_padded are dropped (tail truncation), and rows past the kept count are
 // the padding bucket.  Then one gather pass copies x rows into sorted_tokens
 // and fills the padding rows (zero row, token -1, weight 0, valid 0).
+#include <mutex>
+
 #include "csort.h"
 #include "gemm_tile.h"
 
@@ -148,6 +150,38 @@ int64_t workspace_bytes(int64_t n, int64_t L) {
   return (2 * chunks * L + 64) * static_cast<int64_t>(sizeof(int32_t));
 }
 
+// Allocation-free dispatch: the counting sort's workspace (per-chunk
+// histograms, bin bases, kept count; every byte is written before it is
+// read, so nothing needs clearing) in a file-scope device array.  Each GPU
+// holds its own copy until the process ends.  In host code `scratch` names a
+// host-side stand-in, so its device address is looked up once per device
+// (hipGetSymbolAddress, with that device current) and only that address is
+// passed to kernels.
+constexpr int64_t kNoAllocScratchBytes = int64_t{4} << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(LMOE_ERR_HIP, "dispatch_local_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(LMOE_ERR_UNSUPPORTED, "dispatch_local_noalloc: device %d >= %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(LMOE_ERR_HIP, "dispatch_local_noalloc: hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return LMOE_OK;
+}
+
 }  // namespace
 }  // namespace lmoe
 
@@ -215,6 +249,30 @@ extern "C" int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, 
   }
   LMOE_CHECK_LAUNCH("dispatch_gather");
   return LMOE_OK;
+}
+
+extern "C" int lmoe_dispatch_local_noalloc(const int32_t* topk_idx, const void* topk_w, int w_dtype,
+                                           const void* x, int x_dtype, int64_t T, int64_t k, int64_t lat,
+                                           int64_t local_start, int64_t L, int64_t m_padded,
+                                           void* sorted_tokens, int32_t* group_sizes, uint8_t* valid,
+                                           int32_t* per_expert_counts, int32_t* padded_token_idx,
+                                           void* padded_w, int32_t* slot_pos, void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(T >= 0 && k > 0 && L > 0 && T * k < (1ll << 31) && L < (1 << 20),
+                 "dispatch_local_noalloc: bad sizes T=%lld k=%lld L=%lld", (long long)T, (long long)k,
+                 (long long)L);
+  const int64_t need = workspace_bytes(T * k, L);
+  if (need > kNoAllocScratchBytes)
+    return fail(LMOE_ERR_WORKSPACE,
+                "dispatch_local_noalloc: T*k=%lld, L=%lld need %lld bytes of scratch, more than the %lld-byte "
+                "static array; call lmoe_dispatch_local with a workspace",
+                (long long)(T * k), (long long)L, (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int rc = scratch_on_current_device(&ws);
+  if (rc != LMOE_OK) return rc;
+  return lmoe_dispatch_local(topk_idx, topk_w, w_dtype, x, x_dtype, T, k, lat, local_start, L, m_padded,
+                             sorted_tokens, group_sizes, valid, per_expert_counts, padded_token_idx, padded_w,
+                             slot_pos, ws, kNoAllocScratchBytes, stream);
 }
 
 extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,

@@ -61,6 +61,8 @@ SIGNATURES = {
     "lmoe_dispatch_workspace_size": ([I64, I64, I64], I64),
     "lmoe_dispatch_local": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P,
                              I64, P], I32),
+    "lmoe_dispatch_local_noalloc": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P],
+                                    I32),
     "lmoe_dispatch_local_small": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, I32, P], I32),
     "lmoe_dispatch_local_rows": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, I32, P, I64, P], I32),
     "lmoe_combine_workspace_size": ([I64, I64], I64),
