@@ -97,6 +97,24 @@ int lmoe_ragged_dot_gateup_situ(const void* lhs, const void* rhs_gu, int rhs_lay
                                 int64_t G, int zero_group, float beta, float beta_lin,
                                 int round_before_act, void* out, void* stream);
 
+/* ---- a19: block-scaled fp8 weights ---------------------------------------------
+ * Replaces PallasMosaicTpuV2RaggedDot()(lhs, rhs_q, group_sizes=...,
+ * rhs_scale=..., maybe_quantize_lhs=False) on fp8 weights (rd.py:2789-2811:
+ * one scale per (group, column), rhs_scale (G, 1, 1, N); rd.py:2836-2953: one
+ * per 32 rows of K, (G, K/32, 1, N)).  rhs_q (G, K, N) OCP E4M3 ("fn") codes,
+ * rhs_scale (G, K/block_size, 1, N) f32; every weight is used as
+ * bf16(f32(code) * scale) -- the reference's own check dequantises
+ * (rhs_q.astype(f32) * scale).astype(bf16) and runs ragged_dot -- and the
+ * products are accumulated in f32.  lhs (M, K) bf16, out (M, N) bf16, or
+ * (M, N/2) with LMOE_EPI_SITU ([gate | up] on N, rounded to bf16 before the
+ * activation).  block_size divides K and is a multiple of 4 (the reference
+ * uses K and 32).  K % 8 == 0, N % 8 == 0 (N % 16 with SiTU); lhs 16-byte,
+ * rhs_q 8-byte, rhs_scale 16-byte aligned.  Rows past sum(group_sizes) are zero.
+ */
+int lmoe_ragged_dot_fp8_scaled(const void* lhs, const uint8_t* rhs_q, const float* rhs_scale, int64_t block_size,
+                               const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                               int zero_group, int epilogue, float beta, float beta_lin, void* out, void* stream);
+
 /* ---- a17: MXFP4 dequantisation ---------------------------------------------------
  * Replaces dequantize_mxfp4(weight_packed, weight_scale) (deq.py:29-67):
  * packed (N, K/2) u8 (low nibble = element 2j), scale (N, K/gs) u8 E8M0 ->

@@ -798,6 +798,37 @@ def ragged_dot_mxfp8_mxfp4(lhs_codes, lhs_scales, w_packed, w_scale, group_sizes
   return situ_and_mul(g_, u_, situ[0], situ[1], "bf16")
 
 
+# ---------------------------------------------------------------------------
+# Block-scaled fp8 weights (a19)
+# ---------------------------------------------------------------------------
+
+
+def dequantize_fp8_blockscaled(rhs_q, rhs_scale) -> np.ndarray:
+  """The reference's dequantisation of fp8 weights with f32 block scales,
+  rd.py:2815 (one block per column) and rd.py:2934-2935 (32-row blocks):
+  (rhs_q.astype(f32) * scale).astype(bf16), with rhs_q (G, K, N) E4M3 codes
+  and rhs_scale (G, K/bs, 1, N).  Returns bf16-valued float32 (G, K, N)."""
+  q = fp8_e4m3_to_f32(np.asarray(rhs_q, np.uint8))
+  g, k, n = q.shape
+  sc = np.asarray(rhs_scale, F32)
+  bs = k // sc.shape[1]
+  with np.errstate(over="ignore", invalid="ignore"):
+    deq = (q.reshape(g, k // bs, bs, n) * sc.reshape(g, k // bs, 1, n)).astype(F32)
+  return bf16_round(deq.reshape(g, k, n))
+
+
+def ragged_dot_fp8_scaled(lhs, rhs_q, rhs_scale, group_sizes, dtype: str = "bf16",
+                          situ: tuple[float, float] | None = None) -> np.ndarray:
+  """``PallasMosaicTpuV2RaggedDot()(lhs, rhs_q, rhs_scale=...)`` as the
+  reference checks it (rd.py:2815-2821, rd.py:2934-2941): ragged_dot of lhs
+  with the dequantised bf16 weights, f32 accumulation, one rounding to
+  ``dtype`` (``situ``: the fused SiTU-GLU epilogue on [gate | up])."""
+  w = dequantize_fp8_blockscaled(rhs_q, rhs_scale)
+  if situ is None:
+    return ragged_dot(lhs, w, group_sizes, dtype)
+  return ragged_dot_gateup_situ(lhs, w, group_sizes, situ[0], situ[1], dtype)
+
+
 PINNING = {
     "bf16_round": "closed form: exhaustive bf16 neighbours, torch.bfloat16 cast (tests/test_oracle_basics.py)",
     "router_from_logits / router_gate": "golden bundles router_* / topk_* (6 stages), softmax closed form",
@@ -810,4 +841,6 @@ PINNING = {
     "fp8_e4m3_to_f32 / f32_to_fp8_e4m3": "all 256 codes and a dense sweep incl. ties and subnormals vs torch.float8_e4m3fn",
     "quantize_mxfp8": "OCP MX closed form (exponent choice, saturation, zero block), grid values round-trip exactly",
     "ragged_dot_mxfp8_mxfp4": "brute-force triple loop on small inputs; equals the bf16 oracle when the activations are on the E4M3 grid",
+    "gate_exp64 / gate_sigmoid / gate_softmax": "libm exp within 1 ulp (planted ln2/Taylor mistakes fail), sigmoid correctly rounded vs extended precision, softmax within 1 ulp",
+    "dequantize_fp8_blockscaled / ragged_dot_fp8_scaled": "torch float8_e4m3fn -> f32 * scale -> bf16 casts, all 256 codes x block sizes K and 32",
 }

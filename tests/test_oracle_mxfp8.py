@@ -125,3 +125,43 @@ def test_mxfp8_path_equals_bf16_path_on_the_e4m3_grid():
   x = O.ragged_dot_mxfp8_mxfp4(codes, scales, packed, wsc, gs, "f32")
   y = O.ragged_dot_mxfp4(a, packed, wsc, gs, "f32")
   assert np.max(np.abs(x - y)) <= 1e-5 * np.max(np.abs(y))
+
+
+@pytest.mark.parametrize("bs", [None, 32])
+def test_fp8_blockscaled_dequant_matches_torch(bs):
+  """(rhs_q.astype(f32) * scale).astype(bf16) (rd.py:2815, rd.py:2934-2935)
+  through torch's own float8_e4m3fn -> f32 -> bf16 casts: all 256 codes in
+  every column, per-column (bs = K) and 32-row block scales, including
+  subnormal products and negative / zero scales."""
+  rng = np.random.default_rng(8)
+  g, k, n = 2, 256, 64
+  codes = ((np.arange(k)[:, None] + 7 * np.arange(n)[None, :]) % 256).astype(np.uint8)
+  codes = np.broadcast_to(codes, (g, k, n)).copy()
+  nb = 1 if bs is None else k // bs
+  scale = (rng.standard_normal((g, nb, 1, n)) * 10.0 ** rng.integers(-40, 30, (g, nb, 1, n))).astype(np.float32)
+  scale[0, 0, 0, :4] = [0.0, -1.0, 1e-38, 2.0 ** -140]
+  ours = O.dequantize_fp8_blockscaled(codes, scale)
+  tq = torch.from_numpy(codes).view(torch.float8_e4m3fn).float()
+  ts = torch.from_numpy(scale).repeat_interleave(k // nb, dim=1).reshape(g, k, n)
+  theirs = (tq * ts).to(torch.bfloat16).float().numpy()
+  nan = np.isnan(theirs)
+  assert np.array_equal(np.isnan(ours), nan)
+  assert np.array_equal(ours[~nan].view(np.uint32), theirs[~nan].view(np.uint32))
+
+
+def test_fp8_scaled_ragged_dot_is_dequant_then_matmul():
+  """The fp8 op equals ragged_dot on the dequantised bf16 weights (the
+  reference's own comparison), checked against a per-row float64 brute force."""
+  rng = np.random.default_rng(9)
+  g, k, n = 3, 64, 24
+  codes = rng.integers(0, 256, (g, k, n), dtype=np.uint8)
+  codes[(codes & 0x7F) == 0x7F] = 0  # no NaN codes
+  scale = (rng.uniform(0.5, 2.0, (g, 2, 1, n)) * 0.01).astype(np.float32)
+  gs = np.array([5, 0, 7], np.int32)
+  lhs = O.bf16_round(rng.standard_normal((14, k)))
+  out = O.ragged_dot_fp8_scaled(lhs, codes, scale, gs, "f32")
+  w = O.dequantize_fp8_blockscaled(codes, scale).astype(np.float64)
+  rows = np.repeat(np.arange(g), gs)
+  for r, grp in enumerate(rows):
+    assert np.allclose(out[r], lhs[r].astype(np.float64) @ w[grp], rtol=1e-5, atol=1e-6)
+  assert not out[len(rows):].any()

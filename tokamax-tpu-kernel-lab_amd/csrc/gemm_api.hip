@@ -100,6 +100,31 @@ extern "C" int lmoe_ragged_dot_gateup_situ(const void* lhs, const void* rhs_gu, 
                   static_cast<hipStream_t>(stream), name);
 }
 
+extern "C" int lmoe_ragged_dot_fp8_scaled(const void* lhs, const uint8_t* rhs_q, const float* rhs_scale,
+                                          int64_t block_size, const int32_t* group_sizes, int64_t M, int64_t K,
+                                          int64_t N, int64_t G, int zero_group, int epilogue, float beta,
+                                          float beta_lin, void* out, void* stream) {
+  const char* name = "ragged_dot_fp8_scaled";
+  int rc = check_common(lhs, rhs_q, group_sizes, M, K, N, G, zero_group, out, name);
+  if (rc) return rc;
+  LMOE_CHECK_ARG(rhs_scale || M == 0, "%s: null scale", name);
+  LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
+  LMOE_CHECK_ARG(block_size > 0 && K % block_size == 0, "%s: block_size %lld must divide K=%lld", name,
+                 (long long)block_size, (long long)K);
+  LMOE_CHECK_SUPPORTED(block_size % 4 == 0, "%s: block_size %% 4 == 0 (got %lld)", name, (long long)block_size);
+  LMOE_CHECK_SUPPORTED(K % 8 == 0 && N % (epilogue == LMOE_EPI_SITU ? 16 : 8) == 0,
+                       "%s: needs K %% 8 == 0 and N %% %d == 0 (K=%lld N=%lld)", name,
+                       epilogue == LMOE_EPI_SITU ? 16 : 8, (long long)K, (long long)N);
+  LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(rhs_q, 8) && aligned(rhs_scale, 16) && aligned(out, 4),
+                       "%s: lhs 16-, rhs 8-, scale 16-byte aligned", name);
+  Params p{static_cast<const uint16_t*>(lhs), rhs_q, nullptr, group_sizes, M, K, N, G, zero_group,
+           out, LMOE_BF16, beta, beta_lin, 1};
+  p.scale_f32 = rhs_scale;
+  p.scale_block = block_size;
+  return run_bf16(p, kFP8GKN, epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone, static_cast<hipStream_t>(stream),
+                  name);
+}
+
 extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_t* w_scale,
                                      const int32_t* group_sizes, int64_t M, int64_t K, int64_t N,
                                      int64_t G, int zero_group, int mode, int epilogue, float beta,

@@ -2,8 +2,11 @@
 //
 // Entry points: lmoe_ragged_dot (tokamax.ragged_dot, rd.py:358-369),
 // lmoe_ragged_dot_gateup_situ (fused gate/up + SiTU-GLU, rd.py:644-723 with
-// the epilogue convention of gk.py:114-125) and the LDS-dequant mode of
-// lmoe_ragged_dot_mxfp4 (odq.py:94-99 semantics on the checkpoint layout).
+// the epilogue convention of gk.py:114-125), the LDS-dequant mode of
+// lmoe_ragged_dot_mxfp4 (odq.py:94-99 semantics on the checkpoint layout) and
+// lmoe_ragged_dot_fp8_scaled (fp8 E4M3 weights with f32 block scales,
+// rd.py:2789-2811 / rd.py:2836-2953: each weight is bf16(f32(code) * scale)
+// when its tile is written to LDS, then the bf16 MFMA).
 //
 // Block = 256 threads = WM x WN wavefronts; each wave owns a
 // (BM/WM) x (BN/WN) sub-tile of 16x16 MFMA tiles.  K advances 64 at a time
@@ -46,11 +49,14 @@ struct Cfg {
   static constexpr int kTM = kWTM / 16;
   static constexpr int kTN = kWTN / 16;
   static constexpr int kAVec = BM * kBK / 8 / kThreads;  // 16-byte A loads per thread
-  static constexpr int kBUnits = LAYOUT == kGKN   ? (kBK / 4) * (BN / 8)
-                                 : LAYOUT == kGNK ? BN * (kBK / 8)
-                                                  : BN * (kBK / 32);
+  // B staging unit: GKN / FP8GKN 4 k-rows x 8 columns (transposed on the LDS
+  // store), GNK 8 k values of one column, MXFP4 32 k values of one column
+  static constexpr int kBUnits = (LAYOUT == kGKN || LAYOUT == kFP8GKN) ? (kBK / 4) * (BN / 8)
+                                 : LAYOUT == kGNK                    ? BN * (kBK / 8)
+                                                                     : BN * (kBK / 32);
   static constexpr int kBPer = kBUnits / kThreads;
-  static constexpr int kBRegs = LAYOUT == kGKN ? 4 : 1;
+  static constexpr int kBRegs = (LAYOUT == kGKN || LAYOUT == kFP8GKN) ? 4 : 1;
+  static constexpr int kBScales = LAYOUT == kFP8GKN ? 2 : 1;  // float4s of f32 scales per unit
   static_assert(WM * WN * 64 == kThreads, "4 waves");
   static_assert(kWTM % 16 == 0 && kWTN % 16 == 0, "16x16 MFMA tiles");
   static_assert(BM * kBK / 8 % kThreads == 0, "A tile split");
@@ -145,11 +151,13 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
     uint4 ra_s[S][C::kAVec];
     uint4 rb_s[S][C::kBPer][C::kBRegs];
     uint32_t rs_s[S][C::kBPer];  // MXFP4 scale bytes
+    float4 rf_s[S][C::kBPer][C::kBScales];  // FP8GKN: the unit's 8 column scales
     uint32_t mk_s[S];            // bit v: A vector v valid; bit 16+u: B unit u valid
 
     const int64_t k_last8 = K - 8;  // K % 8 == 0 (K % 64 == 0 for MXFP4)
     auto load_tiles = [&](int64_t k0, uint4 (&ra)[C::kAVec], uint4 (&rb)[C::kBPer][C::kBRegs],
-                          uint32_t (&rs)[C::kBPer], uint32_t& mk) __attribute__((always_inline)) {
+                          uint32_t (&rs)[C::kBPer], float4 (&rf)[C::kBPer][C::kBScales],
+                          uint32_t& mk) __attribute__((always_inline)) {
       uint32_t m = 0;
 #pragma unroll
       for (int v = 0; v < C::kAVec; ++v) {
@@ -178,6 +186,25 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
             const int64_t k = kq + q < K ? kq + q : K - 1;
             rb[u][q] = *reinterpret_cast<const uint4*>(base + k * N);
           }
+        } else if constexpr (LAYOUT == kFP8GKN) {
+          const int kb = idx / (BN / 8), nb = idx % (BN / 8);
+          bool ok;
+          int64_t n = rhs_col<BN, EPI>(nt, nb * 8, N, &ok);
+          n = ok ? n : 0;
+          const uint8_t* base = static_cast<const uint8_t*>(p.rhs) + g * K * N + n;
+          const int64_t kq = k0 + kb * 4;
+          m |= static_cast<uint32_t>(ok && kq < K) << (16 + u);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            const int64_t k = kq + q < K ? kq + q : K - 1;
+            const uint2 v = *reinterpret_cast<const uint2*>(base + k * N);
+            rb[u][q] = uint4{v.x, v.y, 0u, 0u};
+          }
+          // the 4 rows lie in one scale block (scale_block % 4 == 0)
+          const int64_t kc = kq < K ? kq : K - 1;
+          const float* sp = p.scale_f32 + (g * (K / p.scale_block) + kc / p.scale_block) * N + n;
+          rf[u][0] = *reinterpret_cast<const float4*>(sp);
+          rf[u][1] = *reinterpret_cast<const float4*>(sp + 4);
         } else if constexpr (LAYOUT == kGNK) {
           const int c = idx / (kBK / 8), kv = idx % (kBK / 8);
           bool ok;
@@ -210,7 +237,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
     };
 
     auto store_tiles = [&](int buf, const uint4 (&ra)[C::kAVec], const uint4 (&rb)[C::kBPer][C::kBRegs],
-                           const uint32_t (&rs)[C::kBPer], uint32_t mk) __attribute__((always_inline)) {
+                           const uint32_t (&rs)[C::kBPer], const float4 (&rf)[C::kBPer][C::kBScales],
+                           uint32_t mk) __attribute__((always_inline)) {
       uint16_t* as = As[buf];
       uint16_t* bs = Bs[buf];
 #pragma unroll
@@ -241,6 +269,31 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
             hi.y = (w2[d] >> 16) | (w3[d] & 0xffff0000u);
             *reinterpret_cast<uint2*>(&bs[(nb * 8 + 2 * d) * kLdsRow + kb * 4]) = lo;
             *reinterpret_cast<uint2*>(&bs[(nb * 8 + 2 * d + 1) * kLdsRow + kb * 4]) = hi;
+          }
+        } else if constexpr (LAYOUT == kFP8GKN) {
+          const int kb = idx / (BN / 8), nb = idx % (BN / 8);
+          // row q holds k = 4kb + q, columns 0..3 in .x and 4..7 in .y; a
+          // masked unit becomes zero codes under a zero scale
+          const uint32_t lo[4] = {rb[u][0].x & okm, rb[u][1].x & okm, rb[u][2].x & okm, rb[u][3].x & okm};
+          const uint32_t hi[4] = {rb[u][0].y & okm, rb[u][1].y & okm, rb[u][2].y & okm, rb[u][3].y & okm};
+          const float sc[8] = {rf[u][0].x, rf[u][0].y, rf[u][0].z, rf[u][0].w,
+                               rf[u][1].x, rf[u][1].y, rf[u][1].z, rf[u][1].w};
+#pragma unroll
+          for (int c = 0; c < 8; ++c) {
+            const uint32_t* w = c < 4 ? lo : hi;
+            const int sh = 8 * (c % 4);
+            // the column's four codes, k = 4kb .. 4kb+3 in bytes 0..3
+            const uint32_t col = ((w[0] >> sh) & 0xffu) | (((w[1] >> sh) & 0xffu) << 8) |
+                                 (((w[2] >> sh) & 0xffu) << 16) | (((w[3] >> sh) & 0xffu) << 24);
+            const float s = okm ? sc[c] : 0.0f;
+            const floatx2_t f01 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(col), false);
+            const floatx2_t f23 = __builtin_amdgcn_cvt_pk_f32_fp8(static_cast<int>(col), true);
+            uint2 o;
+            o.x = static_cast<uint32_t>(f32_to_bf16(__fmul_rn(f01[0], s))) |
+                  (static_cast<uint32_t>(f32_to_bf16(__fmul_rn(f01[1], s))) << 16);
+            o.y = static_cast<uint32_t>(f32_to_bf16(__fmul_rn(f23[0], s))) |
+                  (static_cast<uint32_t>(f32_to_bf16(__fmul_rn(f23[1], s))) << 16);
+            *reinterpret_cast<uint2*>(&bs[(nb * 8 + c) * kLdsRow + kb * 4]) = o;
           }
         } else if constexpr (LAYOUT == kGNK) {
           const int c = idx / (kBK / 8), kv = idx % (kBK / 8);
@@ -285,10 +338,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
     const int64_t nk = (K + kBK - 1) / kBK;
     static_for<S>([&](auto st_c) __attribute__((always_inline)) {
       constexpr int st = decltype(st_c)::value;
-      if (st < nk) load_tiles(st * kBK, ra_s[st], rb_s[st], rs_s[st], mk_s[st]);
+      if (st < nk) load_tiles(st * kBK, ra_s[st], rb_s[st], rs_s[st], rf_s[st], mk_s[st]);
       return true;
     });
-    store_tiles(0, ra_s[0], rb_s[0], rs_s[0], mk_s[0]);
+    store_tiles(0, ra_s[0], rb_s[0], rs_s[0], rf_s[0], mk_s[0]);
     __syncthreads();
     for (int64_t kt0 = 0; kt0 < nk; kt0 += S) {
       static_for<S>([&](auto st_c) __attribute__((always_inline)) {
@@ -297,10 +350,10 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
         const int64_t kt = kt0 + st;
         if (kt >= nk) return false;
         // slot st held step kt, already in LDS: refill it with step kt + S
-        if (kt + S < nk) load_tiles((kt + S) * kBK, ra_s[st], rb_s[st], rs_s[st], mk_s[st]);
+        if (kt + S < nk) load_tiles((kt + S) * kBK, ra_s[st], rb_s[st], rs_s[st], rf_s[st], mk_s[st]);
         compute(static_cast<int>(kt & 1));
         if (kt + 1 < nk)
-          store_tiles(static_cast<int>((kt + 1) & 1), ra_s[nxt], rb_s[nxt], rs_s[nxt], mk_s[nxt]);
+          store_tiles(static_cast<int>((kt + 1) & 1), ra_s[nxt], rb_s[nxt], rs_s[nxt], rf_s[nxt], mk_s[nxt]);
         __syncthreads();
         return true;
       });
@@ -412,6 +465,8 @@ int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* n
   if (layout == kGNK && epi == kEpiSitu) return dispatch_shape<kGNK, kEpiSitu>(p, st, name);
   if (layout == kMXFP4 && epi == kEpiNone) return dispatch_shape<kMXFP4, kEpiNone>(p, st, name);
   if (layout == kMXFP4 && epi == kEpiSitu) return dispatch_shape<kMXFP4, kEpiSitu>(p, st, name);
+  if (layout == kFP8GKN && epi == kEpiNone) return dispatch_shape<kFP8GKN, kEpiNone>(p, st, name);
+  if (layout == kFP8GKN && epi == kEpiSitu) return dispatch_shape<kFP8GKN, kEpiSitu>(p, st, name);
   return fail(LMOE_ERR_UNSUPPORTED, "%s: layout %d epilogue %d", name, layout, epi);
 }
 

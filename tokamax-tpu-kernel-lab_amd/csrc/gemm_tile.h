@@ -25,6 +25,7 @@ namespace gemm {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef float floatx2_t __attribute__((ext_vector_type(2)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
@@ -32,7 +33,9 @@ constexpr int kBK = 64;
 constexpr int kPad = 8;             // bf16 elements of padding per LDS row
 constexpr int kLdsRow = kBK + kPad;  // LDS row stride (elements)
 
-enum BLayout { kGKN = 0, kGNK = 1, kMXFP4 = 2 };
+// kFP8GKN: (G, K, N) OCP E4M3 codes with f32 scales (G, K/scale_block, N),
+// each weight used as bf16(f32(code) * scale).
+enum BLayout { kGKN = 0, kGNK = 1, kMXFP4 = 2, kFP8GKN = 3 };
 enum Epilogue { kEpiNone = 0, kEpiSitu = 1 };
 
 struct Params {
@@ -48,6 +51,8 @@ struct Params {
   int round_before_act;
   const uint8_t* lhs_scale = nullptr;  // MXFP8 path: E8M0 (K/128, roundup(M, 4), 4)
   int skip_zero_rows = 0;              // zero_group rows may be left unwritten
+  const float* scale_f32 = nullptr;    // kFP8GKN: (G, K/scale_block, N) f32
+  int64_t scale_block = 0;             // kFP8GKN: rows of K per scale
 };
 
 struct TileInfo {

@@ -49,6 +49,7 @@ SIGNATURES = {
     "lmoe_device_arch_ok": ([], I32),
     "lmoe_ragged_dot": ([P, I32, P, I32, P, I64, I64, I64, I64, I32, P, I32, P], I32),
     "lmoe_ragged_dot_gateup_situ": ([P, P, I32, P, I64, I64, I64, I64, I32, F, F, I32, P, P], I32),
+    "lmoe_ragged_dot_fp8_scaled": ([P, P, P, I64, P, I64, I64, I64, I64, I32, I32, F, F, P, P], I32),
     "lmoe_mxfp4_dequant": ([P, P, I64, I64, I64, I64, P, I32, P], I32),
     "lmoe_ragged_dot_mxfp4": ([P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, P, P], I32),
     "lmoe_ragged_dot_mxfp4_skinny": ([P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, I64, P, P], I32),

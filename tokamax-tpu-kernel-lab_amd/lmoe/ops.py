@@ -157,25 +157,84 @@ def ragged_dot_gateup_situ(lhs: torch.Tensor, rhs_gu: torch.Tensor, group_sizes:
   return out
 
 
+def ragged_dot_fp8_scaled(lhs: torch.Tensor, rhs_q: torch.Tensor, rhs_scale: torch.Tensor,
+                          group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
+                          zero_group: int = -1) -> torch.Tensor:
+  """The reference's block-scaled fp8 weight path (rd.py:2789-2811, one scale
+  per column: rhs_scale (G, 1, 1, N); rd.py:2836-2953, one per 32 rows of K:
+  (G, K/32, 1, N)): rhs_q (G, K, N) float8_e4m3fn (or its uint8 codes),
+  rhs_scale (G, K/bs, 1, N) float32.  Each weight is used as
+  bf16(f32(q) * scale), the reference's dequantisation, then a bf16 ragged_dot
+  with f32 accumulation; output (M, N) bf16, or (M, N/2) with the SiTU-GLU
+  epilogue."""
+  _dev(lhs, rhs_q, rhs_scale, group_sizes)
+  if lhs.dtype != torch.bfloat16:
+    raise NotImplementedError("the fp8-weight ragged_dot takes bf16 activations")
+  if rhs_q.dtype not in (torch.float8_e4m3fn, torch.uint8):
+    raise ValueError(f"rhs must be float8_e4m3fn (or its uint8 codes), got {rhs_q.dtype}")
+  if rhs_scale.dtype != torch.float32:
+    raise ValueError(f"rhs_scale must be float32, got {rhs_scale.dtype}")
+  if group_sizes.dtype != torch.int32:
+    raise ValueError("group_sizes must be int32")
+  m, k = lhs.shape
+  if rhs_q.dim() != 3 or rhs_q.shape[1] != k:
+    raise ValueError(f"rhs {tuple(rhs_q.shape)} vs lhs {tuple(lhs.shape)}: want (G, K, N)")
+  g, _, n = rhs_q.shape
+  if (rhs_scale.dim() != 4 or rhs_scale.shape[0] != g or rhs_scale.shape[2] != 1 or rhs_scale.shape[3] != n
+      or rhs_scale.shape[1] == 0 or k % rhs_scale.shape[1]):
+    raise ValueError(f"rhs_scale {tuple(rhs_scale.shape)}: want (G, K/block_size, 1, N) for rhs {tuple(rhs_q.shape)}")
+  if group_sizes.shape != (g,):
+    raise ValueError(f"group_sizes {tuple(group_sizes.shape)} for {g} groups")
+  bs = k // rhs_scale.shape[1]
+  epi, b, bl, width = _lib.EPI_NONE, 0.0, 0.0, n
+  if fuse_gateup_activation is not None:
+    b, bl = parse_fused_activation(fuse_gateup_activation)
+    epi, width = _lib.EPI_SITU, n // 2
+  out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
+  check(lib().lmoe_ragged_dot_fp8_scaled(_p(lhs), _p(rhs_q), _p(rhs_scale), bs, _p(group_sizes), m, k, n, g,
+                                         zero_group, epi, b, bl, _p(out), _stream()), "ragged_dot_fp8_scaled")
+  return out
+
+
 class HipRaggedDot:
   """Op-class form of the grouped GEMM, mirroring how the reference reaches
   the fused and scaled paths through ``PallasMosaicTpuV2RaggedDot()(...)``
   (rd.py:713-720, rd.py:2804-2811): ``op(lhs, rhs, group_sizes=...,
-  fuse_gateup_activation="situ:b:bl", rhs_scale=...)``.  With ``rhs_scale``
-  the rhs is MXFP4 in checkpoint layout (G, N, K/2) u8 and rhs_scale is
-  (G, N, K/32) u8 E8M0."""
+  fuse_gateup_activation="situ:b:bl", rhs_scale=..., maybe_quantize_lhs=...)``.
+
+  ``rhs_scale`` follows the reference's contract when it is float32: rhs is
+  (G, K, N) float8_e4m3fn and rhs_scale (G, K/bs, 1, N)
+  (``ragged_dot_fp8_scaled``).  A uint8 ``rhs_scale`` selects this build's
+  MXFP4 weights instead: rhs (G, N, K/2) packed E2M1 codes, rhs_scale
+  (G, N, K/32) E8M0 bytes (``ragged_dot_mxfp4``).  ``maybe_quantize_lhs=True``
+  quantises the activations to MXFP8 on the MXFP4 path (the native scaled
+  MFMA, tiled weights from ``mxfp4_tile_weights``); the fp8 path has no
+  activation quantisation and raises NotImplementedError for it."""
 
   def __init__(self, mxfp4_mode: str = "lds_dequant"):
     self.mxfp4_mode = mxfp4_mode
 
   def __call__(self, lhs, rhs, *, group_sizes, rhs_scale=None, fuse_gateup_activation=None,
                maybe_quantize_lhs=False, rhs_layout="gkn", zero_group=-1):
-    if maybe_quantize_lhs:
-      raise NotImplementedError("maybe_quantize_lhs")
+    if rhs_scale is not None and rhs_scale.dtype == torch.float32:
+      if maybe_quantize_lhs:
+        raise NotImplementedError("maybe_quantize_lhs with fp8 (E4M3 + f32 scale) weights")
+      return ragged_dot_fp8_scaled(lhs, rhs, rhs_scale, group_sizes,
+                                   fuse_gateup_activation=fuse_gateup_activation, zero_group=zero_group)
     if rhs_scale is not None:
+      if rhs_scale.dtype != torch.uint8:
+        raise ValueError(f"rhs_scale dtype {rhs_scale.dtype}: float32 (fp8 weights) or uint8 (MXFP4 E8M0)")
+      if maybe_quantize_lhs:
+        tiled = rhs.dim() == 4
+        if not tiled:
+          rhs, rhs_scale = mxfp4_tile_weights(rhs, rhs_scale)
+        return ragged_dot_mxfp4(lhs, rhs, rhs_scale, group_sizes, fuse_gateup_activation=fuse_gateup_activation,
+                                mode="scaled_mfma", zero_group=zero_group, weight_layout="tiled")
       return ragged_dot_mxfp4(lhs, rhs, rhs_scale, group_sizes,
                               fuse_gateup_activation=fuse_gateup_activation, mode=self.mxfp4_mode,
-                              zero_group=zero_group)
+                              zero_group=zero_group, weight_layout="tiled" if rhs.dim() == 4 else "checkpoint")
+    if maybe_quantize_lhs:
+      raise NotImplementedError("maybe_quantize_lhs without quantised weights (rhs_scale)")
     if fuse_gateup_activation is not None:
       b, bl = parse_fused_activation(fuse_gateup_activation)
       return ragged_dot_gateup_situ(lhs, rhs, group_sizes, b, bl, rhs_layout=rhs_layout,
