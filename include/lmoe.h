@@ -168,6 +168,15 @@ int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_tiled, const 
  */
 int lmoe_dense_blaslt(const void* x, int x_dtype, const void* w_nk, int w_dtype, int64_t M, int64_t K, int64_t N,
                       void* out, int out_dtype, void* stream);
+/* The same dense projection on this library's own kernel: out (M, N) = x (M, K)
+ * @ w_nk^T with bf16 x and bf16 w_nk (N, K), f32 accumulation, out bf16 or f32
+ * (the layer's router logits + down-projection, ref.py:620 / ref.py:634-655,
+ * and up-projection, ref.py:430).  256 x 128 output tiles on the bf16 MFMA
+ * with a direct-to-LDS DMA pipeline; summation order differs from hipBLASLt's.
+ * K % 64 == 0, N % 8 == 0, buffers 16-byte aligned.  No workspace.
+ */
+int lmoe_dense(const void* x, const void* w_nk, int64_t M, int64_t K, int64_t N, void* out, int out_dtype,
+               void* stream);
 /* The same dense projection for a few rows (a decode step's M = T tokens),
  * on a hand-written skinny kernel: x (M, K) bf16 @ w_nk^T with bf16 w_nk
  * (N, K), f32 accumulation, out bf16 or f32.  Each weight byte is read once

@@ -1004,6 +1004,14 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
   const int64_t mtiles = ceil_div(p.M, BM) + p.G + 1;
   if (ntiles == 0 || p.M == 0) return LMOE_OK;
   int gm = p.G == 1 ? 4 : 1;
+  if (p.G == 1) {
+    // dense: groups of gm m-tiles go round-robin over the XCDs; keep every
+    // XCD busy (at least one group each) with tall tiles
+    const int64_t real_m = ceil_div(p.M, BM);
+    while (gm > 1 && ceil_div(real_m, gm) < kXcds) gm /= 2;
+    const char* e = std::getenv("LMOE_DENSE_GM");
+    if (e && std::atoi(e) > 0) gm = std::atoi(e);
+  }
   int64_t blocks = kXcds * ceil_div(ceil_div(mtiles, gm), kXcds) * gm * ntiles;
   if (p.G > 1 && xcd_map() == kMapMRange) {
     gm = -1;  // contiguous m-tile ranges per XCD

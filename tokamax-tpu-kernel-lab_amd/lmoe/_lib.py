@@ -72,6 +72,7 @@ SIGNATURES = {
     "lmoe_combine_slots_rms_norm": ([P, I32, P, P, I32, I64, I64, I64, I32, P, F, P, P, I32, P], I32),
     "lmoe_rms_norm": ([P, P, I64, I64, F, I32, P, P], I32),
     "lmoe_dense_blaslt": ([P, I32, P, I32, I64, I64, I64, P, I32, P], I32),
+    "lmoe_dense": ([P, P, I64, I64, I64, P, I32, P], I32),
     "lmoe_dense_skinny": ([P, P, I64, I64, I64, P, I32, P], I32),
     "lmoe_situ_and_mul": ([P, P, I64, F, F, I32, P, P], I32),
     "lmoe_add": ([P, P, I64, I32, P, P], I32),

@@ -277,6 +277,23 @@ def bench_decode(dev, rounds, calls):
            skinny_expert_gemms=layer._decode_path(t), tokens_per_s=round(t / (ms / 1000)) if ms else None)
 
 
+def bench_dense(dev, rounds, calls):
+  """The layer's two dense projections at config 5 on each backend: the
+  fused router + down-projection (4096 x 7168 -> 896 + 1024, f32 out) and the
+  up-projection (4096 x 1024 -> 7168, bf16 out)."""
+  gen = torch.Generator(device=dev).manual_seed(6)
+  T, H, E, lat = 4096, 7168, 896, 1024
+  for nm, m, k, n, odt in (("router+down", T, H, E + lat, torch.float32), ("up-proj", T, lat, H, torch.bfloat16)):
+    x = torch.randn((m, k), generator=gen, device=dev).to(torch.bfloat16)
+    w = (torch.randn((n, k), generator=gen, device=dev) * 0.02).to(torch.bfloat16)
+    flops = 2.0 * m * n * k
+    nbytes = m * k * 2 + n * k * 2 + m * n * (4 if odt == torch.float32 else 2)
+    for backend in ("blaslt", "dense", "hip"):
+      name = f"dense {nm} {m}x{k}x{n} [{backend}]"
+      ms = time_fn(lambda: ops.dense(x, w, odt, w_layout="nk", backend=backend), rounds, calls, name=name)
+      report(name, ms, flops, nbytes)
+
+
 def bench_copy(dev, rounds, calls):
   """Plain 256 MiB device copy: the calibration kernel for the HBM traffic
   counters (FETCH_SIZE / WRITE_SIZE should read 256 MiB each)."""

@@ -493,7 +493,7 @@ def _ones_group(m: int, device) -> torch.Tensor:
   return t
 
 
-_DENSE_BACKENDS = ("auto", "hip", "blaslt", "skinny")
+_DENSE_BACKENDS = ("auto", "hip", "dense", "blaslt", "skinny")
 
 
 def _dense_backend_default() -> str:
@@ -543,6 +543,18 @@ def dense(x: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None
     n = w.shape[0]
     out = torch.empty((m, n), dtype=out_dtype, device=x.device)
     check(lib().lmoe_dense_skinny(_p(x), _p(w), m, k, n, _p(out), _dt(out), _stream()), "dense_skinny")
+    return out
+  if backend == "dense":
+    if not nk_bf16:
+      raise NotImplementedError("the dense kernel takes bf16 x and bf16 (N, K) weights")
+    _dev(x, w)
+    if x.dim() != 2 or w.dim() != 2 or w.shape[1] != x.shape[1]:
+      raise ValueError(f"dense: x {tuple(x.shape)} / w {tuple(w.shape)}")
+    x, w = x.contiguous(), w.contiguous()
+    m, k = x.shape
+    n = w.shape[0]
+    out = torch.empty((m, n), dtype=out_dtype, device=x.device)
+    check(lib().lmoe_dense(_p(x), _p(w), m, k, n, _p(out), _dt(out), _stream()), "dense")
     return out
   use_blaslt = backend == "blaslt" or (backend == "auto" and nk_bf16)
   if use_blaslt:
