@@ -365,6 +365,7 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
   if constexpr (EPI == kEpiSitu) {
     const int64_t I = N / 2;
     constexpr int half = C::kTN / 2;
+    const SituConsts sc = situ_consts(p.beta, p.beta_lin);
 #pragma unroll
     for (int i = 0; i < C::kTM; ++i) {
 #pragma unroll
@@ -376,11 +377,8 @@ __global__ __launch_bounds__(kThreads) void grouped_gemm_kernel(Params p, int64_
           const int row = wm * C::kWTM + i * 16 + 4 * (lane / 16) + r;
           if (row >= tile.rows) continue;
           float gv = acc[i][j][r], uv = acc[i][j + half][r];
-          if (p.round_before_act) {
-            gv = round_bf16(gv);
-            uv = round_bf16(uv);
-          }
-          const float v = tile.zero ? 0.0f : situ_fast(gv, uv, p.beta, p.beta_lin);
+          if (p.round_before_act) round_pair_bf16(gv, uv);
+          const float v = tile.zero ? 0.0f : situ_epi(gv, uv, sc);
           static_cast<uint16_t*>(p.out)[(tile.row0 + row) * I + col] = f32_to_bf16(v);
         }
       }

@@ -330,8 +330,7 @@ void grouped_gemm_mx_kernel(Params p, int64_t n_tiles, int gm) {
           if (!tile.zero) {
             float gv = acc[i][j][r], uv = acc[i][j + half][r];
             if (p.round_before_act) {
-              gv = static_cast<float>(static_cast<__bf16>(gv));
-              uv = static_cast<float>(static_cast<__bf16>(uv));
+              round_pair_bf16(gv, uv);
             }
             v = situ_epi(gv, uv, sc);
           }

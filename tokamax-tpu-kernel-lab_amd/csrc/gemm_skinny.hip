@@ -88,8 +88,8 @@ __device__ __forceinline__ void store_out(const SkinnyParams& p, int64_t row, in
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       // the reference rounds both GEMM outputs to bf16 before the activation
-      const float g = static_cast<float>(static_cast<__bf16>(v[0][e]));
-      const float u = static_cast<float>(static_cast<__bf16>(v[1][e]));
+      float g = v[0][e], u = v[1][e];
+      round_pair_bf16(g, u);
       o[e] = situ_epi(g, u, sc);
     }
   } else {

@@ -187,9 +187,16 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs; consecutive blocks go to consecutiv
 // m-tile with all its n-tiles in a row, so both the A rows and (but for the
 // groups that straddle a range boundary) a group's weights are read by one
 // XCD only.
+//
+// gm < 0: XCD x takes the contiguous m-tile range [x per, (x + 1) per),
+// per = ceil(tm_work / 8), of the first tm_work m-tiles (the groups before a
+// trailing zero group, so the ranges hold equal real work), each m-tile's
+// n-tiles in turn; the m-tiles from tm_work on (zero group, tail rows) follow,
+// dealt round-robin.  An XCD then reads an expert's weights and a tile's
+// activation rows from its own L2.
 template <class Locate>
 __device__ __forceinline__ TileInfo schedule_tile_with(int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt,
-                                                       Locate&& locate) {
+                                                       Locate&& locate, int64_t tm_work = -1) {
   // grids and tile counts are < 2^31 (checked on the host): 32-bit index math
   const uint32_t v32 = static_cast<uint32_t>(vb), nt32 = static_cast<uint32_t>(n_tiles);
   const uint32_t xcd = v32 % kXcds, slot = v32 / kXcds;
@@ -201,11 +208,13 @@ __device__ __forceinline__ TileInfo schedule_tile_with(int64_t n_tiles, int gm, 
     nt = xcd + kXcds * (slot % per);
     if (mt < tm) ti = locate(mt);
   } else if (gm < 0) {
-    const uint32_t per = static_cast<uint32_t>((tm + kXcds - 1) / kXcds);
+    const int64_t work = tm_work < 0 || tm_work > tm ? tm : tm_work;
+    const uint32_t per = static_cast<uint32_t>((work + kXcds - 1) / kXcds);
     const uint32_t ml = slot / nt32;
     nt = slot % nt32;
-    const int64_t mt = static_cast<int64_t>(xcd) * per + ml;
-    if (ml < per && mt < tm) ti = locate(mt);
+    const int64_t mt = ml < per ? static_cast<int64_t>(xcd) * per + ml
+                                : work + static_cast<int64_t>(ml - per) * kXcds + xcd;
+    if (ml < per ? mt < work : mt < tm) ti = locate(mt);
   } else {
     const uint32_t span = static_cast<uint32_t>(gm) * nt32;
     const int64_t m_base = (static_cast<int64_t>(slot / span) * kXcds + xcd) * gm;
@@ -332,27 +341,6 @@ __device__ __forceinline__ float situ(float g, float u, float beta, float beta_l
   return __fmul_rn(sg, bu);
 }
 
-// tanh for the fused epilogue: odd Taylor polynomial below |x| = 1/8
-// (relative error < 1e-8), (1 - e^-2|x|) / (1 + e^-2|x|) above, with the
-// hardware exp / reciprocal (a few f32 ulp, below bf16 output resolution).
-__device__ __forceinline__ float tanh_fast(float x) {
-  const float ax = fabsf(x);
-  const float x2 = x * x;
-  const float poly = x * (1.0f - x2 * (0.333333333f - x2 * (0.133333333f - x2 * 0.053968254f)));
-  const float e = __expf(-2.0f * ax);
-  const float t = copysignf((1.0f - e) * __builtin_amdgcn_rcpf(1.0f + e), x);
-  return ax < 0.125f ? poly : t;
-}
-
-// SiTU-GLU with hardware transcendentals, used where the result is rounded to
-// bf16 right away (the fused gate/up epilogue).
-__device__ __forceinline__ float situ_fast(float g, float u, float beta, float beta_lin) {
-  const float sig = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
-  const float sg = beta * tanh_fast(g * __builtin_amdgcn_rcpf(beta)) * sig;
-  const float bu = beta_lin * tanh_fast(u * __builtin_amdgcn_rcpf(beta_lin));
-  return sg * bu;
-}
-
 // Two f32 -> packed bf16 pair (round to nearest even, hardware conversion).
 typedef __bf16 bf16x2_pack_t __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
@@ -362,42 +350,42 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 
 // SiTU-GLU for the fused epilogue (ref.py:305-310):
 //   beta*tanh(g/beta)*sigmoid(g) * beta_lin*tanh(u/beta_lin)
-// with two reciprocals: tanh(x) = (e^2x - 1) / (e^2x + 1) and
-// sigmoid(g) = 1 / (1 + e^-g), so
-//   SiTU = beta*beta_lin * (e1 - 1)(e2 - 1) / ((e1 + 1)(e2 + 1)) / (1 + e0).
-// tanh arguments are clamped to |x| <= 9 (tanh(9) = 1 - 3e-8) so that the
-// tanh product cannot overflow (the sigmoid factor keeps its own reciprocal
-// and goes to 0 only where e^-g overflows); below |x| = 2^-6 the numerator
-// is replaced by
-// (e + 1) * x(1 - x^2/3 + 2x^4/15) (relative error < 1e-10), avoiding the
-// cancellation in e - 1.  Hardware exp2 / reciprocal: a few f32 ulp, far below
-// the bf16 rounding of the result.  NaN inputs give NaN.
+// with three hardware exp2, two reciprocals and no branches:
+// tanh(x) = (a - 1) / (a + 1) with a = e^(2x) and sigmoid(g) = 1 / (1 + e^-g),
+//   SiTU = beta*beta_lin * (a - 1)(c - 1) / ((a + 1)(c + 1)) / (1 + e),
+//   a = 2^(2 log2(e) g / beta), c = 2^(2 log2(e) u / beta_lin), e = 2^(-log2(e) g).
+// The tanh exponents are clamped to [-26, 26] (|x| <= 9: tanh(9) = 1 - 3e-8,
+// saturated in f32), so the tanh quotient cannot overflow; the sigmoid keeps
+// its own reciprocal and goes to 0 only where e^-g overflows (g < -88).  Near
+// g = 0 (u = 0) a - 1 (c - 1) cancels: the absolute error of the result stays
+// below beta*beta_lin*2^-23, far below the bf16 rounding of results of
+// ordinary size.  Hardware exp2 / reciprocal: a few f32 ulp.  A NaN gate or
+// up value gives NaN.  Every GEMM epilogue uses this one function, so the
+// kernels agree bit for bit on equal accumulators.
 struct SituConsts {
-  float ib2, ibl2;   // 2*log2(e)/beta, 2*log2(e)/beta_lin
-  float ib, ibl;     // 1/beta, 1/beta_lin
-  float bbl;         // beta*beta_lin
+  float kg, ku;  // 2*log2(e)/beta, 2*log2(e)/beta_lin
+  float bbl;     // beta*beta_lin
 };
 __device__ __forceinline__ SituConsts situ_consts(float beta, float beta_lin) {
-  const float ib = 1.0f / beta, ibl = 1.0f / beta_lin;
-  return SituConsts{2.0f * 1.44269504088896341f * ib, 2.0f * 1.44269504088896341f * ibl, ib, ibl, beta * beta_lin};
-}
-__device__ __forceinline__ void tanh_frac(float x, float e, float& num, float& den) {
-  den = e + 1.0f;
-  const float t = x * x;
-  const float poly = __builtin_fmaf(t * x, __builtin_fmaf(t, 0.133333333f, -0.333333333f), x);
-  num = __builtin_fabsf(x) < 0.015625f ? den * poly : e - 1.0f;
+  constexpr float kL2e = 1.44269504088896341f;
+  return SituConsts{2.0f * kL2e / beta, 2.0f * kL2e / beta_lin, beta * beta_lin};
 }
 __device__ __forceinline__ float situ_epi(float g, float u, const SituConsts& c) {
-  const float x1 = __builtin_amdgcn_fmed3f(g * c.ib, -9.0f, 9.0f);
-  const float x2 = __builtin_amdgcn_fmed3f(u * c.ibl, -9.0f, 9.0f);
-  const float e1 = __builtin_amdgcn_exp2f(x1 * 2.88539008177792682f);
-  const float e2 = __builtin_amdgcn_exp2f(x2 * 2.88539008177792682f);
-  const float e0 = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
-  float n1, d1, n2, d2;
-  tanh_frac(x1, e1, n1, d1);
-  tanh_frac(x2, e2, n2, d2);
-  const float r = c.bbl * n1 * n2 * __builtin_amdgcn_rcpf(d1 * d2) * __builtin_amdgcn_rcpf(1.0f + e0);
-  return (g != g || u != u) ? __builtin_nanf("") : r;
+  const float a = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(g * c.kg, -26.0f, 26.0f));
+  const float b = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(u * c.ku, -26.0f, 26.0f));
+  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+  const float q = (a - 1.0f) * (b - 1.0f) * __builtin_amdgcn_rcpf((a + 1.0f) * (b + 1.0f));
+  const float r = c.bbl * q * __builtin_amdgcn_rcpf(1.0f + e);
+  return __builtin_isunordered(g, u) ? __builtin_nanf("") : r;
+}
+
+// gate / up accumulators rounded to bf16 (nearest even) with one packed
+// conversion (the epilogue convention of gk.py:114-125).
+__device__ __forceinline__ void round_pair_bf16(float& g, float& u) {
+  const bf16x2_pack_t v = {static_cast<__bf16>(g), static_cast<__bf16>(u)};
+  const uint32_t p = __builtin_bit_cast(uint32_t, v);
+  g = __uint_as_float(p << 16);
+  u = __uint_as_float(p & 0xffff0000u);
 }
 
 // E2M1 nibble with E8M0 scale byte s -> bf16 bits, exact (value has <= 2
