@@ -139,6 +139,24 @@ int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_
                           int zero_group, int mode, int epilogue, float beta, float beta_lin,
                           void* out, void* stream);
 
+/* ---- a18, few long-K tiles: split-K grouped GEMM on tiled MXFP4 weights ---------
+ * Same operation as lmoe_ragged_dot_mxfp4 with LMOE_MXFP4_LDS_DEQUANT_TILED
+ * (the config-4 matmul of odq.py:65-172 / mxfp4_online_dequant_matmul_pallas.py:94-157
+ * at M <= ~1024, where the tile grid alone fills a fraction of the chip): the
+ * K steps of every tile are dealt into k_split contiguous ranges (1 <= k_split
+ * <= K/64; ranges of ceil(K/64 / k_split) steps, fewer ranges when that
+ * leaves one empty), each range's f32 partial sums go to `workspace`
+ * (k_split * M * N * 4 bytes, 16-byte aligned, caller-owned), and a second
+ * kernel adds the ranges in order and applies the epilogue.  Repeatable bit
+ * for bit; agrees with the unsplit kernel within bf16 rounding (another f32
+ * summation order).  Rows of zero_group and past sum(group_sizes) are zero.
+ * k_split == 1 runs the unsplit kernel (workspace unused).
+ */
+int lmoe_ragged_dot_mxfp4_splitk(const void* lhs, const uint8_t* w_packed, const uint8_t* w_scale,
+                                 const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                                 int zero_group, int64_t k_split, float* workspace, int64_t workspace_bytes,
+                                 int epilogue, float beta, float beta_lin, void* out, void* stream);
+
 /* ---- a18, decode regime: skinny-M grouped GEMM on tiled MXFP4 weights -------------
  * Same result contract as lmoe_ragged_dot_mxfp4 with LMOE_MXFP4_LDS_DEQUANT_TILED
  * (w_tiled / s_tiled from lmoe_mxfp4_tile, bf16 lhs and out, epilogue

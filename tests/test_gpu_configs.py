@@ -109,8 +109,9 @@ def config4_weights(gpu_device):
 @pytest.mark.parametrize("m", CONFIG4_M)
 def test_config4_mxfp4_matmul_full_size(gpu_device, config4_weights, m):
   """Every MXFP4 kernel at config 4: LDS dequant on checkpoint-layout and on
-  tiled weights, the skinny kernel (M <= 128), and the native scaled MFMA
-  (MXFP8 activations) against its own exact oracle."""
+  tiled weights (split-K where the default picks it, M <= 1024, and
+  unsplit), the skinny kernel (M <= 128), and the native scaled MFMA (MXFP8
+  activations) against its own exact oracle."""
   from lmoe import ops
   packed, scale, tpk, tsc, pk, sc, wd = config4_weights
   rng = np.random.default_rng(40 + m)
@@ -122,6 +123,8 @@ def test_config4_mxfp4_matmul_full_size(gpu_device, config4_weights, m):
   errs = {}
   errs["checkpoint"] = max_rel(to_np(ops.ragged_dot_mxfp4(ad, packed, scale, gd)), ref)
   errs["tiled"] = max_rel(to_np(ops.ragged_dot_mxfp4(ad, tpk, tsc, gd, weight_layout="tiled")), ref)
+  errs["tiled unsplit"] = max_rel(to_np(ops.ragged_dot_mxfp4(ad, tpk, tsc, gd, weight_layout="tiled", k_split=1)),
+                                  ref)
   if m <= 128:
     errs["skinny"] = max_rel(to_np(ops.ragged_dot_mxfp4(ad, tpk, tsc, gd, weight_layout="tiled", mode="skinny",
                                                         max_group_rows=m)), ref)

@@ -245,7 +245,7 @@ def test_ragged_dot_mxfp4_tiled_weights(gpu_device, m, k, n, g, situ, zg):
   lhs_d, pk_d, gs_d = to_dev(lhs, "bf16"), to_dev(packed), to_dev(gs)
   tpk, tsc = ops.mxfp4_tile_weights(pk_d, to_dev(scale))
   out = ops.ragged_dot_mxfp4(lhs_d, tpk, tsc, gs_d, fuse_gateup_activation=fa, zero_group=zg,
-                             weight_layout="tiled")
+                             weight_layout="tiled", k_split=1)
   chk = ops.ragged_dot_mxfp4(lhs_d, pk_d, to_dev(scale), gs_d, fuse_gateup_activation=fa, zero_group=zg)
   o = to_np(out)
   assert o.shape == ref.shape

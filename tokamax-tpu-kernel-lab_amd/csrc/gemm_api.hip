@@ -6,6 +6,8 @@ namespace gemm {
 int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* name);
 int run_f32(const Params& p, int layout, hipStream_t st, const char* name);
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name);
+int run_dma_splitk(const Params& p, int layout, int epi, int64_t k_split, float* ws, hipStream_t st,
+                   const char* name);
 int tile_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t G, int64_t N, int64_t K, uint8_t* packed_out,
                uint8_t* scale_out, hipStream_t st);
 
@@ -155,6 +157,36 @@ extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, c
                 "%s: the scaled-MFMA path takes MXFP8 activations: lmoe_quantize_mxfp8 + lmoe_ragged_dot_mxfp8_mxfp4",
                 name);
   return fail(LMOE_ERR_INVALID, "%s: bad mode %d", name, mode);
+}
+
+extern "C" int lmoe_ragged_dot_mxfp4_splitk(const void* lhs, const uint8_t* w_packed, const uint8_t* w_scale,
+                                            const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                                            int zero_group, int64_t k_split, float* workspace,
+                                            int64_t workspace_bytes, int epilogue, float beta, float beta_lin,
+                                            void* out, void* stream) {
+  const char* name = "ragged_dot_mxfp4_splitk";
+  int rc = check_common(lhs, w_packed, group_sizes, M, K, N, G, zero_group, out, name);
+  if (rc) return rc;
+  LMOE_CHECK_ARG(w_scale || M == 0, "%s: null scale", name);
+  LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
+  LMOE_CHECK_SUPPORTED(K % 64 == 0, "%s: needs K %% 64 == 0 (K=%lld)", name, (long long)K);
+  LMOE_CHECK_SUPPORTED(N % (epilogue == LMOE_EPI_SITU ? 16 : 8) == 0, "%s: N=%lld", name, (long long)N);
+  LMOE_CHECK_ARG(k_split >= 1 && k_split <= K / 64, "%s: k_split=%lld outside [1, K/64=%lld]", name,
+                 (long long)k_split, (long long)(K / 64));
+  if (M == 0) return LMOE_OK;
+  LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(w_packed, 16) && aligned(w_scale, 16),
+                       "%s: 16-byte alignment", name);
+  // no empty K range: k_split ranges of ceil(steps / k_split) steps
+  const int64_t steps = K / 64, per = ceil_div(steps, k_split), splits = ceil_div(steps, per);
+  Params p{static_cast<const uint16_t*>(lhs), w_packed, w_scale, group_sizes, M, K, N, G, zero_group,
+           out, LMOE_BF16, beta, beta_lin, 1};
+  const int epi = epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (splits == 1) return run_dma(p, kMXFP4, epi, st, name);
+  LMOE_CHECK_ARG(workspace && aligned(workspace, 16), "%s: workspace must be non-null and 16-byte aligned", name);
+  LMOE_CHECK_ARG(workspace_bytes >= splits * M * N * 4, "%s: workspace %lld bytes < %lld (k_split * M * N * 4)",
+                 name, (long long)workspace_bytes, (long long)(splits * M * N * 4));
+  return run_dma_splitk(p, kMXFP4, epi, splits, workspace, st, name);
 }
 
 extern "C" int lmoe_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, int64_t batch,

@@ -146,10 +146,15 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
   asm volatile("v_mov_b32 %0, %1" : "=v"(tid) : "v"(static_cast<int>(threadIdx.x)));
   const int lane = tid % 64, wave = tid / 64;
   const int wm = wave / C::kWN, wn = wave % C::kWN;
+  // split-K: virtual block vb is K range ks of the tile of virtual block tvb
+  // (n_virtual is k_split times the tile grid, a multiple of the XCD count,
+  // so both keep the same XCD)
+  const int64_t nv_tile = n_virtual / p.k_split;
+  const int64_t ks = vb / nv_tile, tvb = vb - ks * nv_tile;
   __syncthreads();  // the previous tile's LDS slots and s_tile are no longer read
   if (wave == 0) {
     int64_t nt = 0;
-    const TileInfo ti = schedule_tile<BM>(p, n_tiles, gm, vb, tm, nt);
+    const TileInfo ti = schedule_tile<BM>(p, n_tiles, gm, tvb, tm, nt);
     if (lane == 0) {
       s_tile = ti;
       s_nt = nt;
@@ -172,13 +177,17 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
 
   if (!tile.zero) {
     const uint32_t smem0 = lds_offset(smem);
-    const int64_t nk = K / kSK;
+    // this block's K steps: [k0, k0 + nk) (all of them without split-K; the
+    // host keeps every range non-empty)
+    const int64_t nk_all = K / kSK, per = (nk_all + p.k_split - 1) / p.k_split;
+    const int64_t k0 = ks * per;
+    const int64_t nk = nk_all - k0 < per ? nk_all - k0 : per;
 
     // DMA addressing: a wave-uniform (SGPR) base per operand that advances by
     // one k step per step, plus a loop-invariant 32-bit per-lane offset.
     // A: LDS chunk position q = tid + kThreads * v of the slot <- row q/8,
     // logical chunk (q%8) ^ swz8(row).  Rows past the tile read row 0 of the tile.
-    const uint8_t* a_base = uniform_ptr(p.lhs + tile.row0 * K);
+    const uint8_t* a_base = uniform_ptr(p.lhs + tile.row0 * K + k0 * kSK);
     uint32_t a_off[C::kAOps];
 #pragma unroll
     for (int v = 0; v < C::kAOps; ++v) {
@@ -190,7 +199,10 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
     // GNK: row n of group g at (g*N + n) * 2K bytes; MXFP4 (k-step-major):
     // column n of step s of group g at ((g*K/64 + s)*N + n) * 32 bytes
     const int64_t b_row = LAYOUT == kDGNK ? K * 2 : 32;
-    const uint8_t* b_base = uniform_ptr(static_cast<const uint8_t*>(p.rhs) + g * N * (LAYOUT == kDGNK ? K * 2 : K / 2));
+    const int64_t b_step = LAYOUT == kDGNK ? kSK * 2 : N * 32;
+    const int64_t s_step = N * 2;
+    const uint8_t* b_base =
+        uniform_ptr(static_cast<const uint8_t*>(p.rhs) + g * N * (LAYOUT == kDGNK ? K * 2 : K / 2) + k0 * b_step);
     uint32_t b_off[C::kBOps];
 #pragma unroll
     for (int u = 0; u < C::kBOps; ++u) {
@@ -226,11 +238,9 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
         n0 = nt * BN + c0;
         n0 = n0 <= N - 8 ? n0 : N - 8;
       }
-      s_base = uniform_ptr(p.scale + g * (K / 64) * N * 2);
+      s_base = uniform_ptr(p.scale + g * (K / 64) * N * 2 + k0 * s_step);
       s_off = static_cast<uint32_t>(n0 * 2);
     }
-    const int64_t b_step = LAYOUT == kDGNK ? kSK * 2 : N * 32;
-    const int64_t s_step = N * 2;
     // LDS destination of this wave's chunk 0 (M0 must be wave-uniform)
     const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(smem0 + wave * 64 * 16);
 
@@ -484,6 +494,8 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
   auto c_run = [&](int q) { return MF == 32 ? q * 8 + 4 * (lane / 32) : 4 * (lane / 16); };
   const int64_t n_out = EPI == kEpiSitu ? N / 2 : N;
   const int64_t col0 = nt * kOutCols;  // first output column of the tile
+  // split-K: this range's f32 partial plane
+  void* const out_base = p.k_split > 1 ? static_cast<void*>(static_cast<float*>(p.out) + ks * p.split_stride) : p.out;
   // bf16 values of run q of output sub-tile j of row sub-tile i
   auto bf16_run = [&](int i, int j, int q) __attribute__((always_inline)) {
     float v[4];
@@ -520,7 +532,7 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
     __syncthreads();
     constexpr int kChunks = kOutCols / 8;  // 16-byte chunks per output row
     static_assert(BM * kChunks % C::kThreads == 0, "staged store split");
-    uint16_t* out = static_cast<uint16_t*>(p.out);
+    uint16_t* out = static_cast<uint16_t*>(out_base);
 #pragma unroll
     for (int v = 0; v < BM * kChunks / C::kThreads; ++v) {
       const int idx = tid + C::kThreads * v;
@@ -544,10 +556,10 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
           const int64_t col = col0 + wn * kOutTN * MF + j * MF + c_run(q);
           if (col >= n_out) continue;
           if (EPI != kEpiSitu && p.out_dtype == LMOE_F32) {
-            *reinterpret_cast<float4*>(static_cast<float*>(p.out) + obase + col) =
+            *reinterpret_cast<float4*>(static_cast<float*>(out_base) + obase + col) =
                 float4{acc[i][j][q * 4], acc[i][j][q * 4 + 1], acc[i][j][q * 4 + 2], acc[i][j][q * 4 + 3]};
           } else {
-            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.out) + obase + col) =
+            *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out_base) + obase + col) =
                 tile.zero ? uint2{0u, 0u} : bf16_run(i, j, q);
           }
         }
@@ -1017,10 +1029,14 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
   if (p.G > 1 && xcd_map() == kMapMRange) {
     gm = -1;  // contiguous m-tile ranges per XCD
     blocks = kXcds * (ceil_div(mtiles, kXcds) + 1) * ntiles;
-  } else if (p.G > 1 && ntiles % kXcds == 0 && (xcd_map() == kMapStripeN || xcd_map() == kMapDefault)) {
-    gm = 0;  // n-tiles striped over the XCDs
+  } else if ((p.G > 1 || p.k_split > 1) && ntiles % kXcds == 0 &&
+             (xcd_map() == kMapStripeN || xcd_map() == kMapDefault)) {
+    // n-tiles striped over the XCDs (split-K too: with few m-tiles the
+    // m-tile groups would leave most XCDs without work)
+    gm = 0;
     blocks = mtiles * ntiles;
   }
+  blocks *= p.k_split;  // one virtual block per (tile, K range)
   LMOE_CHECK_SUPPORTED(blocks < (1ll << 31), "%s: grid too large", name);
   // per-lane DMA offsets are 32-bit: one group's weights and one tile's rows
   const int64_t w_bytes = p.N * (LAYOUT == kDGNK ? p.K * 2 : p.K / 2);
@@ -1232,7 +1248,88 @@ int run_gnk(const Params& p, hipStream_t st, const char* name) {
   }
 }
 
+// Split-K reduction: out = epilogue(plane 0 + plane 1 + ... + plane S-1),
+// the planes added in that order in f32.  The SiTU epilogue pairs columns j
+// and N/2 + j of the summed planes as the fused kernels do (both rounded to
+// bf16 first).  One thread per run of four output columns.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ ws, int64_t S, int64_t stride,
+                                                            int64_t M, int64_t N, int epi, float beta, float beta_lin,
+                                                            int out_dtype, void* __restrict__ out) {
+  const int64_t n_out = epi == kEpiSitu ? N / 2 : N;
+  const int64_t runs = n_out / 4;
+  const int64_t total = M * runs;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total;
+       i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t r = i / runs, c = (i - r * runs) * 4;
+    if (epi == kEpiSitu) {
+      const float* pg = ws + r * N + c;
+      float4 g = *reinterpret_cast<const float4*>(pg);
+      float4 u = *reinterpret_cast<const float4*>(pg + N / 2);
+      for (int64_t sp = 1; sp < S; ++sp) {
+        const float4 dg = *reinterpret_cast<const float4*>(pg + sp * stride);
+        const float4 du = *reinterpret_cast<const float4*>(pg + sp * stride + N / 2);
+        g.x += dg.x; g.y += dg.y; g.z += dg.z; g.w += dg.w;
+        u.x += du.x; u.y += du.y; u.z += du.z; u.w += du.w;
+      }
+      const SituConsts sc = situ_consts(beta, beta_lin);
+      const float gv[4] = {g.x, g.y, g.z, g.w}, uv[4] = {u.x, u.y, u.z, u.w};
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float a = gv[e], b = uv[e];
+        round_pair_bf16(a, b);
+        v[e] = situ_epi(a, b, sc);
+      }
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + r * n_out + c) =
+          uint2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+    } else {
+      const float* pa = ws + r * N + c;
+      float4 a = *reinterpret_cast<const float4*>(pa);
+      for (int64_t sp = 1; sp < S; ++sp) {
+        const float4 d = *reinterpret_cast<const float4*>(pa + sp * stride);
+        a.x += d.x; a.y += d.y; a.z += d.z; a.w += d.w;
+      }
+      if (out_dtype == LMOE_F32)
+        *reinterpret_cast<float4*>(static_cast<float*>(out) + r * n_out + c) = a;
+      else
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + r * n_out + c) =
+            uint2{pack_bf16x2(a.x, a.y), pack_bf16x2(a.z, a.w)};
+    }
+  }
+}
+
 }  // namespace
+
+// Split-K: the DMA kernel with 64x128 tiles computes k_split K ranges of
+// every tile as f32 partial planes in `ws` (k_split * M * N floats), then
+// splitk_reduce_kernel sums them in order and applies the epilogue.  For a
+// few long-K tiles (one group, M <= ~1024) the tile grid alone leaves most of
+// the chip idle and each tile's K loop is latency-bound.
+int run_dma_splitk(const Params& p, int layout, int epi, int64_t k_split, float* ws, hipStream_t st,
+                   const char* name) {
+  Params q = p;
+  q.k_split = k_split;
+  q.split_stride = p.M * p.N;
+  q.out = ws;
+  q.out_dtype = LMOE_F32;
+  q.skip_zero_rows = 0;
+  int rc;
+  if (layout == kMXFP4)
+    rc = launch_dma<64, 128, kDMX, kEpiNone, 4, 1, 4, 32>(q, st, name);
+  else if (layout == kGNK)
+    rc = launch_dma<64, 128, kDGNK, kEpiNone, 3, 1, 4, 16>(q, st, name);
+  else
+    rc = fail(LMOE_ERR_UNSUPPORTED, "%s: split-K layout %d", name, layout);
+  if (rc != LMOE_OK) return rc;
+  const int64_t n_out = epi == kEpiSitu ? p.N / 2 : p.N;
+  const int64_t total = p.M * (n_out / 4);
+  if (total == 0) return LMOE_OK;
+  const int64_t b = ceil_div(total, 256);
+  splitk_reduce_kernel<<<static_cast<unsigned>(b < 65536 ? b : 65536), 256, 0, st>>>(
+      ws, k_split, q.split_stride, p.M, p.N, epi, p.beta, p.beta_lin, p.out_dtype, p.out);
+  LMOE_CHECK_LAUNCH(name);
+  return LMOE_OK;
+}
 
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name) {
   if (layout == kGNK && epi == kEpiNone) return run_gnk<kEpiNone>(p, st, name);

@@ -53,6 +53,11 @@ struct Params {
   int skip_zero_rows = 0;              // zero_group rows may be left unwritten
   const float* scale_f32 = nullptr;    // kFP8GKN: (G, K/scale_block, N) f32
   int64_t scale_block = 0;             // kFP8GKN: rows of K per scale
+  // split-K (DMA kernel, no epilogue): the K steps of every tile are dealt
+  // into k_split contiguous ranges; range r writes its f32 partial sums to
+  // plane r of out, split_stride elements apart
+  int64_t k_split = 1;
+  int64_t split_stride = 0;
 };
 
 struct TileInfo {

@@ -52,6 +52,7 @@ SIGNATURES = {
     "lmoe_ragged_dot_fp8_scaled": ([P, P, P, I64, P, I64, I64, I64, I64, I32, I32, F, F, P, P], I32),
     "lmoe_mxfp4_dequant": ([P, P, I64, I64, I64, I64, P, I32, P], I32),
     "lmoe_ragged_dot_mxfp4": ([P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, P, P], I32),
+    "lmoe_ragged_dot_mxfp4_splitk": ([P, P, P, P, I64, I64, I64, I64, I32, I64, P, I64, I32, F, F, P, P], I32),
     "lmoe_ragged_dot_mxfp4_skinny": ([P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, I64, P, P], I32),
     "lmoe_mxfp4_tile": ([P, P, I64, I64, I64, P, P, P], I32),
     "lmoe_mxfp8_scale_bytes": ([I64, I64], I64),

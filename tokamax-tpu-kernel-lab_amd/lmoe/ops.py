@@ -361,11 +361,26 @@ def ragged_dot_mxfp8_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
   return out
 
 
+def mxfp4_k_split(m: int, n: int, k: int, g: int) -> int:
+  """K ranges for the split-K MXFP4 kernel (1: no split).  One group only
+  (the tile count of a grouped problem depends on device-side group sizes):
+  split until the 64x128 tiles times the ranges reach two per CU, keeping at
+  least 16 K steps (1024 of K) per range (measured at config 4, K = 7168,
+  N = 2048: M = 128 in 7 ranges 21 us against 80 unsplit, M = 1024 in 2
+  ranges 48 us against 84)."""
+  if g != 1 or k % 64 != 0:
+    return 1
+  tiles = -(-m // 64) * -(-n // 128)
+  steps = k // 64
+  want = -(-512 // max(tiles, 1))
+  return max(1, min(want, steps // 16))
+
+
 def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
                      group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
                      mode: str = "lds_dequant", zero_group: int = -1,
                      weight_layout: str = "checkpoint", skip_zero_group_rows: bool = False,
-                     max_group_rows: int = 0) -> torch.Tensor:
+                     max_group_rows: int = 0, k_split: int | None = None) -> torch.Tensor:
   """Grouped lhs @ deq(W_g)^T with W_g in checkpoint (N, K/2) layout
   (orientation of mxfp4_online_dequant_matmul_pallas.py:1-36) and block-32
   E8M0 scales (G, N, K/32), or with ``weight_layout="tiled"`` the
@@ -375,6 +390,12 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   ``skip_zero_group_rows``: the rows of ``zero_group`` and those past
   sum(group_sizes) may be left unwritten (uninitialised) instead of zeroed,
   for callers that never read them.
+
+  ``k_split`` (tiled weights, ``mode="lds_dequant"``): K ranges computed
+  in parallel as f32 partial planes and summed in order by a second kernel;
+  None picks ``mxfp4_k_split`` (a split only for one group with few tiles,
+  e.g. the config-4 matmul at M <= 1024), 1 never splits.  A split result
+  equals the unsplit one within bf16 rounding (another f32 summation order).
 
   ``mode="skinny"`` (tiled weights, K % 128 == 0): the decode-regime kernel
   for groups of a few rows -- each weight byte of a group with rows read once
@@ -428,6 +449,17 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
     return out
   if weight_layout == "tiled":
     mode_id = _lib.MXFP4_LDS_DEQUANT_TILED
+    splits = mxfp4_k_split(m, n, k, g) if k_split is None else int(k_split)
+    if splits > 1:
+      steps = k // 64
+      splits = -(-steps // -(-steps // splits)) if 1 <= splits <= steps else splits  # no empty range
+      ws = torch.empty((splits * m * n,), dtype=torch.float32, device=lhs.device)
+      out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
+      check(lib().lmoe_ragged_dot_mxfp4_splitk(_p(lhs), _p(w_packed), _p(w_scale), _p(group_sizes), m, k, n, g,
+                                               zero_group, splits, _p(ws), ws.numel() * 4, epi, b, bl, _p(out),
+                                               _stream()),
+            "ragged_dot_mxfp4_splitk")
+      return out
   if skip_zero_group_rows:
     mode_id |= _lib.MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS
   out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
