@@ -456,7 +456,7 @@ static bool use_dma_path() {
 }
 
 int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* name) {
-  if (layout == kGNK && p.K % 64 == 0 && use_dma_path()) return run_dma(p, layout, epi, st, name);
+  if ((layout == kGNK || layout == kGKN) && p.K % 64 == 0 && use_dma_path()) return run_dma(p, layout, epi, st, name);
   if (layout == kGKN && epi == kEpiNone) return dispatch_shape<kGKN, kEpiNone>(p, st, name);
   if (layout == kGKN && epi == kEpiSitu) return dispatch_shape<kGKN, kEpiSitu>(p, st, name);
   if (layout == kGNK && epi == kEpiNone) return dispatch_shape<kGNK, kEpiNone>(p, st, name);

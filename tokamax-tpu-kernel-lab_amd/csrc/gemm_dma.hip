@@ -48,7 +48,19 @@ using namespace lmoe::dma;
 
 constexpr int kSK = 64;  // K per pipeline step
 
-enum DmaLayout { kDGNK = 0, kDMX = 1 };
+// kDGKN: bf16 weights in the reference's (G, K, N) layout.  A k step's B
+// tile is 64 k-rows of BN columns, DMA'd as it lies (16-byte chunks of a row
+// XOR-swizzled by swzk(row)), and each MFMA B fragment (8 consecutive k of
+// one column) is read with two gfx950 transposing LDS reads
+// (ds_read_b64_tr_b16): within each 16-lane group, lane c supplies the
+// address of the 4-column run (k0 + c/4, n0 + 4 (c%4)) and lane i receives
+// column n0 + i at rows k0 .. k0+3.
+enum DmaLayout { kDGNK = 0, kDMX = 1, kDGKN = 2 };
+
+// 16-byte chunk swizzle of the kDGKN B tile: the 8 k-rows one transposing
+// read touches (k0..k0+3, k0+8..k0+11) x 4 chunks land on 32 distinct chunk
+// positions mod 256 bytes, so the read runs at the full LDS rate.
+__device__ __forceinline__ int swzk(int row) { return 4 * (row % 4); }
 
 // WM x WN waves; wave (wm, wn) owns rows [wm*BM/WM, ...) and columns
 // [wn*BN/WN, ...) of the tile.  With WM == 1 every weight fragment is expanded
@@ -66,12 +78,12 @@ struct DCfg {
   static constexpr int kAccN = MF == 32 ? 16 : 4;         // accumulator floats per lane per sub-tile
   using Acc = std::conditional_t<MF == 32, floatx16, floatx4>;
   static constexpr int kABytes = BM * 128;                       // A slot
-  static constexpr int kBBytes = LAYOUT == kDGNK ? BN * 128 : BN * 32;  // B slot
+  static constexpr int kBBytes = LAYOUT != kDMX ? BN * 128 : BN * 32;  // B slot
   static constexpr int kSBytes = LAYOUT == kDMX ? BN * 2 : 0;    // scale slot
   static constexpr int kSlot = kABytes + kBBytes + ((kSBytes + 15) / 16) * 16;
   // DMA instructions per wave per step
   static constexpr int kAOps = BM * 8 / kThreads;  // 16-byte chunks per thread
-  static constexpr int kBOps = LAYOUT == kDGNK ? BN * 8 / kThreads : BN * 2 / kThreads;
+  static constexpr int kBOps = LAYOUT != kDMX ? BN * 8 / kThreads : BN * 2 / kThreads;
   // scales: BN columns x 2 bytes per step, fetched by wave 0 alone (kSLanes
   // lanes x 16 B) -- one instruction instead of one per wave
   static constexpr int kSOps = LAYOUT == kDMX ? 1 : 0;
@@ -79,7 +91,8 @@ struct DCfg {
   static constexpr int kOps = kAOps + kBOps;       // per step, every wave
   static constexpr int kOps0 = kAOps + kBOps + kSOps;  // per step, wave 0
   static_assert(kAOps >= 1 && BM * 8 % kThreads == 0, "A DMA split");
-  static_assert(kBOps >= 1 && (LAYOUT == kDGNK ? BN * 8 : BN * 2) % kThreads == 0, "B DMA split");
+  static_assert(kBOps >= 1 && (LAYOUT != kDMX ? BN * 8 : BN * 2) % kThreads == 0, "B DMA split");
+  static_assert(LAYOUT != kDGKN || (MF == 32 && BN % 128 == 0), "(G, K, N) tiles: 32x32 MFMAs, BN % 128 == 0");
   static_assert(LAYOUT != kDMX || (BN % 8 == 0 && kSLanes <= 64), "scale DMA split");
   static_assert(MF == 16 || MF == 32, "MFMA shape");
   static_assert(kTM >= 1 && kTN >= 1 && kWTM % MF == 0 && kWTN % MF == 0, "wave tile");
@@ -121,6 +134,32 @@ __device__ __forceinline__ int64_t drhs_col(int64_t nt, int c, int64_t N) {
     const int64_t n = nt * BN + c;
     return n < N ? n : N - 1;
   }
+}
+
+// First global column of the run of 8 LDS columns c .. c+7 (c % 8 == 0) of
+// n-tile nt: runs past the matrix edge read the last in-bounds run instead
+// (their values are never stored).  N % 8 == 0 (I % 8 == 0 with SiTU).
+template <int BN, int EPI>
+__device__ __forceinline__ int64_t drhs_col8(int64_t nt, int c, int64_t N) {
+  if constexpr (EPI == kEpiSitu) {
+    const int64_t I = N / 2;
+    int64_t j = nt * (BN / 2) + (c < BN / 2 ? c : c - BN / 2);
+    j = j <= I - 8 ? j : I - 8;
+    return c < BN / 2 ? j : I + j;
+  } else {
+    const int64_t n = nt * BN + c;
+    return n <= N - 8 ? n : N - 8;
+  }
+}
+
+typedef short lds_v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) lds_v4i16 lds_v4i16_as3;
+
+// Transposing LDS read (ds_read_b64_tr_b16) at a byte offset into dynamic LDS.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* base, int byte) {
+  const lds_v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_v4i16_as3*)((__attribute__((address_space(3))) uint8_t*)base + byte));
+  return __builtin_bit_cast(uint2, v);
 }
 
 template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM, int WN, int MF, bool PIPE>
@@ -196,13 +235,14 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
       const int rr = row < tile.rows ? row : 0;
       a_off[v] = static_cast<uint32_t>(rr * K * 2 + kc * 16);
     }
-    // GNK: row n of group g at (g*N + n) * 2K bytes; MXFP4 (k-step-major):
-    // column n of step s of group g at ((g*K/64 + s)*N + n) * 32 bytes
+    // GNK: row n of group g at (g*N + n) * 2K bytes; GKN: row k of group g at
+    // (g*K + k) * 2N bytes; MXFP4 (k-step-major): column n of step s of group
+    // g at ((g*K/64 + s)*N + n) * 32 bytes
     const int64_t b_row = LAYOUT == kDGNK ? K * 2 : 32;
-    const int64_t b_step = LAYOUT == kDGNK ? kSK * 2 : N * 32;
+    const int64_t b_step = LAYOUT == kDGNK ? kSK * 2 : LAYOUT == kDGKN ? kSK * N * 2 : N * 32;
     const int64_t s_step = N * 2;
     const uint8_t* b_base =
-        uniform_ptr(static_cast<const uint8_t*>(p.rhs) + g * N * (LAYOUT == kDGNK ? K * 2 : K / 2) + k0 * b_step);
+        uniform_ptr(static_cast<const uint8_t*>(p.rhs) + g * N * (LAYOUT != kDMX ? K * 2 : K / 2) + k0 * b_step);
     uint32_t b_off[C::kBOps];
 #pragma unroll
     for (int u = 0; u < C::kBOps; ++u) {
@@ -210,6 +250,11 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
       if constexpr (LAYOUT == kDGNK) {
         const int c = q / 8, kc = (q % 8) ^ swz8(c);
         b_off[u] = static_cast<uint32_t>(drhs_col<BN, EPI>(nt, c, N) * b_row + kc * 16);
+      } else if constexpr (LAYOUT == kDGKN) {
+        // LDS chunk q: k-row q / (BN/8), position q % (BN/8) <- logical chunk
+        // position ^ swzk(row), i.e. LDS columns 8 ch .. 8 ch + 7
+        const int row = q / (BN / 8), ch = (q % (BN / 8)) ^ swzk(row);
+        b_off[u] = static_cast<uint32_t>(row * N * 2 + drhs_col8<BN, EPI>(nt, ch * 8, N) * 2);
       } else {
         const int c = q / 2, ch = q % 2;
         b_off[u] = static_cast<uint32_t>(drhs_col<BN, EPI>(nt, c, N) * b_row + ch * 16);
@@ -307,7 +352,7 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
     // scale bytes.
     struct Frags {
       bf16x8_t af[C::kKS][C::kTM];
-      bf16x8_t bf[LAYOUT == kDGNK ? C::kKS : 1][C::kTN];
+      bf16x8_t bf[LAYOUT != kDMX ? C::kKS : 1][C::kTN];
       uint32_t bw[C::kKS][C::kTN];
       uint32_t s2[C::kTN];
     };
@@ -340,6 +385,20 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
             } else {
               f.bw[kk][j] = *reinterpret_cast<const uint32_t*>(bs + c * 32 + mx_dword_pos(kc) * 4);
             }
+          } else if constexpr (LAYOUT == kDGKN) {
+            // this lane supplies the address of the run (k-row kc*8 + 4r +
+            // l16/4, columns n0 + 4 (l16%4) ..) and receives column n0 + l16,
+            // k-rows kc*8 + 4r .. +3; n0 = the sub-tile's first column + 16
+            // for lanes 16..31 and 48..63
+            const int l16 = lane % 16;
+            const int col = dlds_col<BN, C::kTN, EPI, MF>(wn, j) + 16 * ((lane / 16) % 2) + 4 * (l16 % 4);
+            uint2 h[2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const int row = kc * 8 + 4 * r + l16 / 4;
+              h[r] = lds_read_tr16(bs, row * (BN * 2) + (((col / 8) ^ swzk(row)) * 16) + (col % 8) * 2);
+            }
+            f.bf[kk][j] = __builtin_bit_cast(bf16x8_t, uint4{h[0].x, h[0].y, h[1].x, h[1].y});
           } else {
             f.bf[kk][j] = *reinterpret_cast<const bf16x8_t*>(bs + c * 128 + ((kc ^ swz8(c)) * 16));
           }
@@ -1039,7 +1098,7 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
   blocks *= p.k_split;  // one virtual block per (tile, K range)
   LMOE_CHECK_SUPPORTED(blocks < (1ll << 31), "%s: grid too large", name);
   // per-lane DMA offsets are 32-bit: one group's weights and one tile's rows
-  const int64_t w_bytes = p.N * (LAYOUT == kDGNK ? p.K * 2 : p.K / 2);
+  const int64_t w_bytes = p.N * (LAYOUT != kDMX ? p.K * 2 : p.K / 2);
   LMOE_CHECK_SUPPORTED(w_bytes < (1ll << 32) && BM * p.K * 2 < (1ll << 32), "%s: group too large for the DMA path",
                        name);
   const size_t lds = static_cast<size_t>(NS) * C::kSlot;
@@ -1298,6 +1357,36 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
+// Tile shape of the bf16 (G, K, N) kernel: LMOE_GKN_CFG picks a variant
+// "BMxBNxNS_WMxWN" (tuning sweeps); 32x32 MFMAs throughout.
+int gkn_variant() {
+  static const int v = [] {
+    const char* e = std::getenv("LMOE_GKN_CFG");
+    if (!e) return -1;
+    const char* names[] = {"64x128x3_1x4", "128x128x2_2x2", "128x128x3_2x2", "64x256x2_1x4", "128x256x2_2x4"};
+    for (int i = 0; i < 5; ++i)
+      if (std::strcmp(e, names[i]) == 0) return i;
+    return -1;
+  }();
+  return v;
+}
+
+template <int EPI>
+int run_gkn(const Params& p, hipStream_t st, const char* name) {
+  // default: 128x256 tiles of 2x4 waves (config 2, the reference-layout
+  // ragged_dot: 71.8 us, the speed of the prepared (G, N, K) layout; 64x128
+  // tiles 77.2 us; transpose + (G, N, K) kernel 118.2 us)
+  int v = gkn_variant();
+  if (v < 0) v = 4;
+  switch (v) {
+    case 1: return launch_dma<128, 128, kDGKN, EPI, 2, 2, 2, 32>(p, st, name);
+    case 2: return launch_dma<128, 128, kDGKN, EPI, 3, 2, 2, 32>(p, st, name);
+    case 3: return launch_dma<64, 256, kDGKN, EPI, 2, 1, 4, 32>(p, st, name);
+    case 4: return launch_dma<128, 256, kDGKN, EPI, 2, 2, 4, 32>(p, st, name);
+    default: return launch_dma<64, 128, kDGKN, EPI, 3, 1, 4, 32>(p, st, name);
+  }
+}
+
 }  // namespace
 
 // Split-K: the DMA kernel with 64x128 tiles computes k_split K ranges of
@@ -1332,6 +1421,8 @@ int run_dma_splitk(const Params& p, int layout, int epi, int64_t k_split, float*
 }
 
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name) {
+  if (layout == kGKN && epi == kEpiNone) return run_gkn<kEpiNone>(p, st, name);
+  if (layout == kGKN && epi == kEpiSitu) return run_gkn<kEpiSitu>(p, st, name);
   if (layout == kGNK && epi == kEpiNone) return run_gnk<kEpiNone>(p, st, name);
   if (layout == kGNK && epi == kEpiSitu) return run_gnk<kEpiSitu>(p, st, name);
   if (layout == kMXFP4 && epi == kEpiNone) return run_mx<kEpiNone>(p, st, name);

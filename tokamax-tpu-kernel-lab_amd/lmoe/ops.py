@@ -109,10 +109,12 @@ def ragged_dot(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor, 
   if rhs.dtype != lhs.dtype:
     raise NotImplementedError(f"mixed lhs {lhs.dtype} / rhs {rhs.dtype}")
   out_dtype = preferred_element_type or lhs.dtype
-  if layout == _lib.RHS_GKN and lhs.dtype == torch.bfloat16 and k % 64 == 0 and n % 8 == 0:
-    # reference-layout bf16 weights: one transpose into the k-contiguous
-    # layout (lmoe_transpose), then the DMA-pipelined kernel for (G, N, K)
-    # -- faster than the transpose-on-store kernel for the (G, K, N) layout
+  if (_GKN_VIA_TRANSPOSE and layout == _lib.RHS_GKN and lhs.dtype == torch.bfloat16 and k % 64 == 0
+      and n % 8 == 0):
+    # A/B timing only: transpose the reference-layout weights into the
+    # k-contiguous layout first (lmoe_transpose), then the (G, N, K) kernel.
+    # The default reads (G, K, N) tiles as they lie and transposes them in
+    # LDS (ds_read_b64_tr_b16).
     rhs_t = torch.empty((g, n, k), dtype=rhs.dtype, device=rhs.device)
     check(lib().lmoe_transpose(_p(rhs), g, k, n, 2, _p(rhs_t), _stream()), "transpose")
     rhs, layout = rhs_t, _lib.RHS_GNK
@@ -120,6 +122,9 @@ def ragged_dot(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor, 
   check(lib().lmoe_ragged_dot(_p(lhs), _dt(lhs), _p(rhs), layout, _p(group_sizes), m, k, n, g,
                               zero_group, _p(out), _dt(out), _stream()), "ragged_dot")
   return out
+
+
+_GKN_VIA_TRANSPOSE = os.environ.get("LMOE_GKN_TRANSPOSE") == "1"
 
 
 def parse_fused_activation(spec: str) -> tuple[float, float]:
