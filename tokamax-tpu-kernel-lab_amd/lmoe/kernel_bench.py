@@ -160,9 +160,15 @@ def bench_cfg4(dev, rounds, calls):
     nbytes = n_ * k_ * (0.5 + 1 / 32) + m * k_ * 2 + m * n_ * 2
     ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, packed, scale, g), rounds, calls, name=f"cfg4 mxfp4 matmul checkpoint scales M={m}")
     report(f"cfg4 mxfp4 matmul checkpoint scales M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
-    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled"), rounds, calls,
-                 name=f"cfg4 mxfp4 matmul tiled weights M={m}")
-    report(f"cfg4 mxfp4 matmul tiled weights M={m}", ms, flops, nbytes, peak_key="bf16", m=m)
+    ks = ops.mxfp4_k_split(m, n_, k_, 1)
+    nm = f"cfg4 mxfp4 matmul tiled weights M={m}" + (f" (split-K {ks})" if ks > 1 else "")
+    ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled"), rounds, calls, name=nm)
+    report(nm, ms, flops, nbytes, peak_key="bf16", m=m, k_split=ks)
+    if ks > 1:
+      nm = f"cfg4 mxfp4 matmul tiled weights M={m} (unsplit)"
+      ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled", k_split=1), rounds, calls,
+                   name=nm)
+      report(nm, ms, flops, nbytes, peak_key="bf16", m=m)
     if m <= 128:
       ms = time_fn(lambda: ops.ragged_dot_mxfp4(a, tpk, tsc, g, weight_layout="tiled", mode="skinny"), rounds,
                    calls, name=f"cfg4 mxfp4 matmul skinny M={m}")
