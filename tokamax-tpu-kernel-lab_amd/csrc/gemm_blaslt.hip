@@ -70,17 +70,16 @@ int get_plan(const Key& key, hipblasLtHandle_t* handle, const Plan** plan) {
   const uint64_t no_ws = 0;
   ok = ok && hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &no_ws,
                                                    sizeof(no_ws)) == HIPBLAS_STATUS_SUCCESS;
-  // LMOE_BLASLT_ALGO=i takes the i-th of the heuristic's candidates instead
-  // of its first (tuning sweeps); an index past the list falls back to 0.
+  // Always the heuristic's first candidate: it measured fastest among the
+  // first nine at the layer's shapes, and a later candidate at those shapes
+  // faulted the GPU, so no override is offered.
   constexpr int kMaxAlgos = 16;
   hipblasLtMatmulHeuristicResult_t res[kMaxAlgos] = {};
   int found = 0;
   ok = ok && hipblasLtMatmulAlgoGetHeuristic(*handle, p.desc, p.a, p.b, p.d, p.d, pref, kMaxAlgos, res, &found) ==
                  HIPBLAS_STATUS_SUCCESS;
   if (pref) hipblasLtMatmulPreferenceDestroy(pref);
-  int pick = 0;
-  if (const char* e = std::getenv("LMOE_BLASLT_ALGO")) pick = std::atoi(e);
-  if (pick < 0 || pick >= found || res[pick].state != HIPBLAS_STATUS_SUCCESS) pick = 0;
+  const int pick = 0;
   if (!ok || found < 1 || res[pick].state != HIPBLAS_STATUS_SUCCESS) {
     if (p.desc) hipblasLtMatmulDescDestroy(p.desc);
     for (auto l : {p.a, p.b, p.d})
