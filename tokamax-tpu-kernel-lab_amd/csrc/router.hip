@@ -20,9 +20,11 @@
 // above.  Elements above threshold - 2^-18 (|threshold| + 1) -- a margin far
 // above twice that error -- are compacted to LDS (usually barely more than
 // k), their exact scores recomputed with the same correctly rounded
-// operations as the full path, and the at most 64 candidates bitonic-sorted
-// on (key, -expert).  The result is identical to the full path's.  More than
-// 64 candidates (massive ties) fall back to the full path.
+// operations as the full path, and each of the at most 64 candidates ranked
+// on (key, -expert) by counting the larger keys, broadcast from LDS (one
+// dependent step instead of a 21-stage sort network).  The result is
+// identical to the full path's.  More than 64 candidates (massive ties) fall
+// back to the full path.
 //
 // Full path: exact scores for all experts, then k rounds of a wavefront
 // arg-max: a wave maximum of the order-preserving float bits of every lane's
@@ -76,25 +78,6 @@ __device__ __forceinline__ uint32_t wave_kth_largest(uint32_t x, int k) {
   return prefix;
 }
 
-// Wave-wide bitonic sort, descending on key; `val` travels with its key.
-__device__ __forceinline__ void wave_sort_desc(uint64_t& key, float& val, int lane) {
-#pragma unroll
-  for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-    for (int stride = size / 2; stride > 0; stride >>= 1) {
-      const uint32_t plo = __shfl_xor(static_cast<uint32_t>(key), stride, 64);
-      const uint32_t phi = __shfl_xor(static_cast<uint32_t>(key >> 32), stride, 64);
-      const float pv = __shfl_xor(val, stride, 64);
-      const uint64_t pk = (static_cast<uint64_t>(phi) << 32) | plo;
-      const bool lower = (lane & stride) == 0;
-      const bool keep_max = lower == ((lane & size) == 0 || size == 64);
-      const bool take = keep_max ? pk > key : pk < key;
-      key = take ? pk : key;
-      val = take ? pv : val;
-    }
-  }
-}
-
 template <int EPL>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, int64_t ld, const float* __restrict__ bias, int T, int E, int k, int act,
@@ -115,7 +98,16 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
   if (act == LMOE_ACT_SIGMOID && scores_out == nullptr && k <= kWave) {
     __shared__ float s_logit[kWavesPerBlock][kWave];
     __shared__ int32_t s_expert[kWavesPerBlock][kWave];
+    __shared__ __attribute__((aligned(16))) uint64_t s_key[kWavesPerBlock][kWave];
+    __shared__ __attribute__((aligned(16))) float s_w[kWavesPerBlock][kWave];
     const int wv = threadIdx.x / kWave;
+    // the bias loads go out with the logits loads (one memory round trip)
+    float bv[EPL];
+#pragma unroll
+    for (int c = 0; c < EPL; ++c) {
+      const int e = c * kWave + lane;
+      bv[c] = bias ? bias[e < E ? e : 0] : 0.0f;
+    }
     // approximate selection keys and their lane maximum
     float ap[EPL];
     uint32_t lmax = 0;
@@ -123,7 +115,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     for (int c = 0; c < EPL; ++c) {
       const int e = c * kWave + lane;
       const float sg = __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(s[c] * -1.44269504088896341f));
-      ap[c] = sg + (bias ? bias[e < E ? e : 0] : 0.0f);
+      ap[c] = sg + bv[c];
       if (e < E) lmax = max(lmax, ordered_bits(ap[c]));
     }
     const float th = from_ordered(wave_kth_largest(lmax, k));
@@ -155,15 +147,36 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
         const float sel = bias ? __fadd_rn(cs, bias[e]) : __fadd_rn(cs, 0.0f);
         ck = (static_cast<uint64_t>(ordered_bits(sel)) << 32) | (0xffffffffu - static_cast<uint32_t>(e));
       }
-      wave_sort_desc(ck, cs, lane);
+      // rank of each candidate = number of larger keys (keys are distinct:
+      // the expert id is in the low word); the candidates broadcast from LDS
+      s_key[wv][lane] = ck;
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+      uint32_t rank = 0;
+      const int n_cand = static_cast<int>(total);
+      int j = 0;
+      for (; j + 1 < n_cand; j += 2) {
+        const ulonglong2 kk = *reinterpret_cast<const ulonglong2*>(&s_key[wv][j]);
+        rank += (kk.x > ck ? 1u : 0u) + (kk.y > ck ? 1u : 0u);
+      }
+      if (j < n_cand) rank += s_key[wv][j] > ck ? 1u : 0u;
+      // renormalisation sum in top-k order (sequential f32 adds)
+      const bool top = static_cast<uint32_t>(lane) < total && rank < static_cast<uint32_t>(k);
+      if (top) s_w[wv][rank] = cs;
+      __builtin_amdgcn_wave_barrier();
+      asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
       float sum = 0.0f;
-      for (int j = 0; j < k; ++j)
-        sum = __fadd_rn(sum, __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, cs), j)));
-      if (lane < k) {
+      int q = 0;
+      for (; q + 3 < k; q += 4) {
+        const float4 v = *reinterpret_cast<const float4*>(&s_w[wv][q]);
+        sum = __fadd_rn(__fadd_rn(__fadd_rn(__fadd_rn(sum, v.x), v.y), v.z), v.w);
+      }
+      for (; q < k; ++q) sum = __fadd_rn(sum, s_w[wv][q]);
+      if (top) {
         float w = cs;
         if (renorm && k > 1) w = __fdiv_rn(w, __fadd_rn(sum, 1e-20f));
         w = __fmul_rn(w, scale);
-        const int64_t o = static_cast<int64_t>(t) * k + lane;
+        const int64_t o = static_cast<int64_t>(t) * k + rank;
         idx_out[o] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ck));
         store_from_f32(w_out, o, w, wdtype);
       }
