@@ -54,6 +54,48 @@ __device__ __forceinline__ void load_vec(const void* p, int64_t i, int dtype, fl
   }
 }
 
+// VEC elements of either dtype kept as raw 32-bit words (bf16: the first
+// VEC/2 words), to be converted later: a load issued early without holding
+// VEC floats.
+template <int VEC>
+struct RawVec {
+  uint32_t w[VEC];
+};
+
+template <int VEC>
+__device__ __forceinline__ RawVec<VEC> load_raw(const void* p, int64_t i, int dtype) {
+  RawVec<VEC> r{};
+  if (dtype == LMOE_BF16) {
+    const uint16_t* q = static_cast<const uint16_t*>(p) + i;
+    if constexpr (VEC == 8) {
+      const uint4 v = *reinterpret_cast<const uint4*>(q);
+      r.w[0] = v.x, r.w[1] = v.y, r.w[2] = v.z, r.w[3] = v.w;
+    } else {
+#pragma unroll
+      for (int j = 0; j < VEC / 2; ++j) r.w[j] = static_cast<uint32_t>(q[2 * j]) | (static_cast<uint32_t>(q[2 * j + 1]) << 16);
+    }
+  } else {
+    const float* q = static_cast<const float*>(p) + i;
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) r.w[j] = __float_as_uint(q[j]);
+  }
+  return r;
+}
+
+template <int VEC>
+__device__ __forceinline__ void unpack_raw(const RawVec<VEC>& r, int dtype, float* out) {
+  if (dtype == LMOE_BF16) {
+#pragma unroll
+    for (int j = 0; j < VEC / 2; ++j) {
+      out[2 * j] = __uint_as_float(r.w[j] << 16);
+      out[2 * j + 1] = __uint_as_float(r.w[j] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < VEC; ++j) out[j] = __uint_as_float(r.w[j]);
+  }
+}
+
 template <int VEC>
 __device__ __forceinline__ void store_vec(void* p, int64_t i, int dtype, const float* v) {
   if (dtype == LMOE_BF16) {
@@ -246,6 +288,13 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
   const int t = blockIdx.x * kTokensPerBlock + wave;
   if (t >= T) return;
+  // the norm scale does not depend on the routing: its loads go out first
+  RawVec<VEC> sc_raw[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int64_t c0 = static_cast<int64_t>(r) * kWave * VEC + static_cast<int64_t>(lane) * VEC;
+    if (c0 < lat) sc_raw[r] = load_raw<VEC>(norm_scale, c0, odt);
+  }
   int p = -1;
   if (lane < k) p = slot_pos[static_cast<int64_t>(t) * k + lane];
   const bool slot_sum = mode == LMOE_COMBINE_SLOT_SUM;
@@ -255,16 +304,23 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(
     wts_s[wave][lane] = lane < k ? load_as_f32(w, static_cast<int64_t>(t) * k + lane, wdt) : 0.0f;
     n = k;
   } else {
+    // ascending row order: rank = number of this token's kept rows below p,
+    // counted against the k slots broadcast from LDS (the weight load is in
+    // flight meanwhile)
     const bool valid = lane < k && p >= 0;
+    const float wp = valid ? load_as_f32(w, p, wdt) : 0.0f;
+    rows_s[wave][lane] = p;
+    wave_sync();
     int rank = 0;
     for (int j = 0; j < k; ++j) {
-      const int pj = __shfl(p, j, kWave);
+      const int pj = rows_s[wave][j];
       rank += (pj >= 0 && pj < p) ? 1 : 0;
     }
     n = __popcll(__ballot(valid));
+    wave_sync();
     if (valid) {
       rows_s[wave][rank] = p;
-      wts_s[wave][rank] = load_as_f32(w, p, wdt);
+      wts_s[wave][rank] = wp;
     }
   }
   wave_sync();
@@ -328,7 +384,7 @@ __global__ __launch_bounds__(256) void combine_norm_kernel(
     const int64_t c0 = static_cast<int64_t>(r) * kWave * VEC + static_cast<int64_t>(lane) * VEC;
     if (c0 >= lat) continue;
     float sc[VEC], o[VEC];
-    load_vec<VEC>(norm_scale, c0, odt, sc);
+    unpack_raw<VEC>(sc_raw[r], odt, sc);
 #pragma unroll
     for (int q = 0; q < VEC; ++q) o[q] = __fmul_rn(round_to(__fmul_rn(v[r][q], inv), odt), sc[q]);
     store_vec<VEC>(normed_out, static_cast<int64_t>(t) * lat + c0, odt, o);
