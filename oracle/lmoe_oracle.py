@@ -799,6 +799,108 @@ def ragged_dot_mxfp8_mxfp4(lhs_codes, lhs_scales, w_packed, w_scale, group_sizes
 
 
 # ---------------------------------------------------------------------------
+# MXFP6 activations x MXFP4 weights: the scaled MFMA at the FP4/FP6 rate
+# ---------------------------------------------------------------------------
+# No reference counterpart either: OCP MX v1.0 FP6 E2M3 elements (sign, 2-bit
+# exponent with bias 1, 3-bit mantissa; no infinities or NaN; max 7.5,
+# subnormal spacing 1/8) with one E8M0 scale per 32 elements along K.  The
+# shared exponent is floor(log2(amax)) - 2 (emax_elem = 2 for E2M3); scaled
+# elements are rounded to nearest-even and saturate to +-7.5.  The packed
+# layout (the build's own) puts element j of a 32-element block at bits
+# 6j .. 6j+5 of the block's 24 little-endian bytes, i.e. (M, K) codes become
+# (M, K*3/4) bytes.
+
+E2M3_MAX = 7.5
+
+
+def fp6_e2m3_to_f32(code) -> np.ndarray:
+  """E2M3 code (6 bits) -> float32: sign bit 5, exponent bits 4..3 (bias 1),
+  mantissa bits 2..0; exponent 0 is subnormal (m/8)."""
+  c = np.asarray(code).astype(np.int64)
+  e = (c >> 3) & 3
+  m = c & 7
+  mag = np.where(e == 0, m / 8.0, (1.0 + m / 8.0) * np.ldexp(1.0, e - 1))
+  return np.where((c & 0x20) != 0, -mag, mag).astype(F32)
+
+
+def f32_to_fp6_e2m3(x) -> np.ndarray:
+  """float -> E2M3 code, round to nearest even on the representable grid,
+  saturating to +-7.5 (infinities too); NaN -> 0.  The grid spacing is 1/8
+  below 2, 1/4 in [2, 4) and 1/2 in [4, 8), and the code of a magnitude is
+  8 * binade + the rounded mantissa count, so a carry out of the mantissa
+  moves into the next binade by itself."""
+  x = np.asarray(x, np.float64)
+  sign = np.where(np.signbit(x), 0x20, 0).astype(np.int64)
+  a = np.minimum(np.abs(np.nan_to_num(x, nan=0.0, posinf=E2M3_MAX, neginf=-E2M3_MAX)), E2M3_MAX)
+  code = np.where(a < 2.0, np.rint(a * 8.0),
+                  np.where(a < 4.0, 8 + np.rint(a * 4.0), 16 + np.rint(a * 2.0))).astype(np.int64)
+  return (code | sign).astype(np.uint8)
+
+
+def quantize_mxfp6(x) -> tuple[np.ndarray, np.ndarray]:
+  """(M, K) float -> (codes (M, K) u8 E2M3 (6 bits used), scales (M, K/32) u8
+  E8M0): shared exponent floor(log2(max|x|)) - 2 over the block's finite
+  values, clamped to [-127, 127] (an all-zero block gets byte 0)."""
+  x = np.asarray(x, np.float64)
+  m, k = x.shape
+  blocks = x.reshape(m, k // 32, 32)
+  fin = np.where(np.isfinite(blocks), np.abs(blocks), 0.0)
+  amax = fin.max(axis=-1)
+  with np.errstate(divide="ignore"):
+    ex = np.where(amax > 0, np.floor(np.log2(np.where(amax > 0, amax, 1.0))) - 2, -127)
+  ex = np.clip(ex, -127, 127).astype(np.int64)
+  scaled = blocks * np.ldexp(1.0, -ex)[..., None]
+  codes = f32_to_fp6_e2m3(scaled).reshape(m, k)
+  return codes, (ex + 127).astype(np.uint8)
+
+
+def pack_fp6(codes) -> np.ndarray:
+  """(M, K) 6-bit codes -> (M, K*3/4) bytes: element j of each 32-element
+  block at bits 6j .. 6j+5 of the block's 24 little-endian bytes."""
+  c = np.asarray(codes).astype(np.uint64)
+  m, k = c.shape
+  blk = c.reshape(m, k // 32, 8, 4)  # 4 elements -> 3 bytes
+  v = blk[..., 0] | (blk[..., 1] << 6) | (blk[..., 2] << 12) | (blk[..., 3] << 18)
+  out = np.stack([(v >> (8 * b)) & 0xFF for b in range(3)], axis=-1).astype(np.uint8)
+  return out.reshape(m, k * 3 // 4)
+
+
+def unpack_fp6(packed, k: int) -> np.ndarray:
+  """Inverse of ``pack_fp6``."""
+  p = np.asarray(packed).astype(np.uint64)
+  m = p.shape[0]
+  t = p.reshape(m, k // 4, 3)
+  v = t[..., 0] | (t[..., 1] << 8) | (t[..., 2] << 16)
+  return np.stack([(v >> (6 * e)) & 0x3F for e in range(4)], axis=-1).reshape(m, k).astype(np.uint8)
+
+
+def dequantize_mxfp6(codes, scales) -> np.ndarray:
+  """E2M3 codes (M, K) x E8M0 scales (M, K/32) -> float64 values (exact)."""
+  v = fp6_e2m3_to_f32(codes).astype(np.float64)
+  s = np.ldexp(1.0, np.asarray(scales).astype(np.int64) - 127)
+  return v * np.repeat(s, 32, axis=-1)
+
+
+def ragged_dot_mxfp6_mxfp4(lhs_codes, lhs_scales, w_packed, w_scale, group_sizes, dtype: str = "f32"
+                           ) -> np.ndarray:
+  """Grouped deq(A) @ deq(W_g)^T with MXFP6 activations (unpacked codes) and
+  MXFP4 weights in checkpoint (N, K/2) layout; float64 sums rounded once to
+  ``dtype``.  Rows past sum(group_sizes) are zero."""
+  a = dequantize_mxfp6(lhs_codes, lhs_scales)
+  gs = np.asarray(group_sizes).astype(np.int64)
+  n_out = np.asarray(w_packed).shape[1]
+  acc = np.zeros((a.shape[0], n_out), np.float64)
+  start = 0
+  for g, n in enumerate(gs):
+    n = int(n)
+    if n:
+      wd = dequantize_mxfp4(w_packed[g], w_scale[g]).astype(np.float64)
+      acc[start:start + n] = a[start:start + n] @ wd.T
+    start += n
+  return cast(acc.astype(F32), dtype)
+
+
+# ---------------------------------------------------------------------------
 # Block-scaled fp8 weights (a19)
 # ---------------------------------------------------------------------------
 
@@ -843,4 +945,6 @@ PINNING = {
     "ragged_dot_mxfp8_mxfp4": "brute-force triple loop on small inputs; equals the bf16 oracle when the activations are on the E4M3 grid",
     "gate_exp64 / gate_sigmoid / gate_softmax": "libm exp within 1 ulp (planted ln2/Taylor mistakes fail), sigmoid correctly rounded vs extended precision, softmax within 1 ulp",
     "dequantize_fp8_blockscaled / ragged_dot_fp8_scaled": "torch float8_e4m3fn -> f32 * scale -> bf16 casts, all 256 codes x block sizes K and 32",
+    "fp6_e2m3_to_f32 / f32_to_fp6_e2m3 / quantize_mxfp6 / pack_fp6": "the OCP E2M3 value table (monotone codes, spacing 1/8, 1/4, 1/2), brute-force nearest-even search over a dense sweep with every midpoint, the MX exponent closed form (amax / 2^X in [4, 8)), grid values round-trip, a planted emax mistake fails, one-hot bit placement of the packing",
+    "ragged_dot_mxfp6_mxfp4": "brute-force triple loop on small inputs",
 }
