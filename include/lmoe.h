@@ -242,6 +242,28 @@ int lmoe_ragged_dot_mxfp8_mxfp4(const uint8_t* lhs_q, const uint8_t* lhs_scale_t
                                 int64_t N, int64_t G, int zero_group, int epilogue, float beta, float beta_lin,
                                 void* out, int out_dtype, void* stream);
 
+/* ---- north star (c), FP4/FP6 rate: MXFP6 activations x MXFP4 weights ---------------
+ * No counterpart in the reference (its MXFP4 paths dequantise to bf16).  The
+ * 32x32x64 block-scaled MFMA runs at the FP4/FP6 rate only with both operands
+ * 6 bits or narrower, so activations are quantised to OCP MX FP6 E2M3.
+ * lmoe_quantize_mxfp6: x (M, K) bf16/f32 -> q (M, K*3/4) packed E2M3 codes (32
+ * codes in 24 little-endian bytes, code j at bits 6j..6j+5; x 16-byte and q
+ * 8-byte aligned), scale_t as lmoe_quantize_mxfp8 (lmoe_mxfp8_scale_bytes(M,
+ * K) bytes).  Shared exponent floor(log2(max|x|)) - 2 over a block's finite
+ * values, clamped to [-127, 127]; elements round to nearest even and
+ * saturate to +-7.5; NaN -> +-0.  K % 128 == 0.
+ * lmoe_ragged_dot_mxfp6_mxfp4: grouped deq(q) @ deq(W_g)^T with weights from
+ * lmoe_mxfp4_tile; out (M, N) bf16 or f32; rows past sum(group_sizes) and of
+ * zero_group are zero.  K % 128 == 0, N % 8 == 0; q and weights 16-byte
+ * aligned.  The instruction's block dot is accumulated below fp32 precision,
+ * as on the MXFP8 path.
+ */
+int lmoe_quantize_mxfp6(const void* x, int x_dtype, int64_t M, int64_t K, uint8_t* q, uint8_t* scale_t,
+                        void* stream);
+int lmoe_ragged_dot_mxfp6_mxfp4(const uint8_t* lhs_q, const uint8_t* lhs_scale_t, const uint8_t* w_packed_t,
+                                const uint8_t* w_scale_t, const int32_t* group_sizes, int64_t M, int64_t K,
+                                int64_t N, int64_t G, int zero_group, void* out, int out_dtype, void* stream);
+
 /* ---- a3: router top-k --------------------------------------------------------------
  * Replaces the gate math of _router_gate (ref.py:601-631) / latent_moe_forward
  * step 1 (ref.py:347-361) given f32 logits (T, E): scores = act(logits);

@@ -57,6 +57,8 @@ SIGNATURES = {
     "lmoe_mxfp4_tile": ([P, P, I64, I64, I64, P, P, P], I32),
     "lmoe_mxfp8_scale_bytes": ([I64, I64], I64),
     "lmoe_quantize_mxfp8": ([P, I32, I64, I64, P, P, P], I32),
+    "lmoe_quantize_mxfp6": ([P, I32, I64, I64, P, P, P], I32),
+    "lmoe_ragged_dot_mxfp6_mxfp4": ([P, P, P, P, P, I64, I64, I64, I64, I32, P, I32, P], I32),
     "lmoe_ragged_dot_mxfp8_mxfp4": ([P, P, P, P, P, I64, I64, I64, I64, I32, I32, F, F, P, I32, P], I32),
     "lmoe_router_topk": ([P, P, I64, I64, I64, I32, I32, F, I32, P, P, P, P], I32),
     "lmoe_router_topk_ld": ([P, I64, P, I64, I64, I64, I32, I32, F, I32, P, P, P, P], I32),

@@ -180,6 +180,13 @@ def bench_cfg4(dev, rounds, calls):
                  name=f"cfg4 mxfp8 x mxfp4 scaled MFMA M={m}")
     report(f"cfg4 mxfp8 x mxfp4 scaled MFMA M={m}", ms, flops, nbytes - m * k_ * (1 - 1 / 32),
            peak_key="fp8", m=m)
+    ms = time_fn(lambda: ops.quantize_mxfp6(a), rounds, calls, name=f"cfg4 mxfp6 quantise M={m}")
+    report(f"cfg4 mxfp6 quantise M={m}", ms, 0, m * k_ * (2 + 0.75 + 1 / 32), m=m)
+    q6, qs6 = ops.quantize_mxfp6(a)
+    ms = time_fn(lambda: ops.ragged_dot_mxfp6_mxfp4(q6, qs6, tpk, tsc, g), rounds, calls,
+                 name=f"cfg4 mxfp6 x mxfp4 scaled MFMA (FP4 rate) M={m}")
+    report(f"cfg4 mxfp6 x mxfp4 scaled MFMA (FP4 rate) M={m}", ms, flops, nbytes - m * k_ * (1.25 - 1 / 32),
+           peak_key="mxfp4", m=m)
 
 
 def bench_cfg5(dev, rounds, calls):

@@ -287,7 +287,7 @@ def dequantize_mxfp4(weight_packed: torch.Tensor, weight_scale: torch.Tensor,
   return out
 
 
-_MX_MODES = {"lds_dequant": _lib.MXFP4_LDS_DEQUANT, "scaled_mfma": _lib.MXFP4_SCALED_MFMA, "skinny": -1}
+_MX_MODES = {"lds_dequant": _lib.MXFP4_LDS_DEQUANT, "scaled_mfma": _lib.MXFP4_SCALED_MFMA, "skinny": -1, "scaled_mfma_fp6": -1}
 
 
 def skinny_supported(k: int, n: int, g: int, situ: bool) -> bool:
@@ -366,6 +366,50 @@ def ragged_dot_mxfp8_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
   return out
 
 
+def quantize_mxfp6(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+  """OCP MX FP6 E2M3 quantisation of activations (no reference counterpart;
+  the scaled-MFMA path at the FP4/FP6 rate): x (M, K) bf16/f32 -> packed codes
+  (M, K*3/4) uint8 (32 codes in 24 bytes, code j at bits 6j..6j+5) and E8M0
+  scales (K/128, roundup(M, 4), 4) uint8.  One shared exponent
+  floor(log2 max|x|) - 2 per 32 along K; elements round to nearest even and
+  saturate to +-7.5."""
+  _dev(x)
+  if x.dim() != 2 or x.dtype not in (torch.bfloat16, torch.float32):
+    raise ValueError(f"x must be (M, K) bf16/f32, got {tuple(x.shape)} {x.dtype}")
+  m, k = x.shape
+  if k % 128:
+    raise NotImplementedError(f"MXFP6 quantisation needs K % 128 == 0 (K={k})")
+  x = x.contiguous()
+  m4 = (m + 3) // 4 * 4
+  q = torch.empty((m, k * 3 // 4), dtype=torch.uint8, device=x.device)
+  sc = torch.empty((k // 128, m4, 4), dtype=torch.uint8, device=x.device)
+  check(lib().lmoe_quantize_mxfp6(_p(x), _dt(x), m, k, _p(q), _p(sc), _stream()), "quantize_mxfp6")
+  return q, sc
+
+
+def ragged_dot_mxfp6_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packed: torch.Tensor,
+                           w_scale: torch.Tensor, group_sizes: torch.Tensor, *, zero_group: int = -1,
+                           out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+  """Grouped deq(A) @ deq(W_g)^T on the 32x32x64 block-scaled MFMA at the
+  FP4/FP6 rate: A from ``quantize_mxfp6``, W from ``mxfp4_tile_weights``."""
+  _dev(lhs_q, lhs_scale, w_packed, w_scale, group_sizes)
+  m, kp = lhs_q.shape
+  k = kp * 4 // 3
+  if w_packed.dim() != 4 or w_packed.shape[3] != 32:
+    raise ValueError(f"weights must be tiled (G, K/64, N, 32), got {tuple(w_packed.shape)}")
+  g, _, n, _ = w_packed.shape
+  m4 = (m + 3) // 4 * 4
+  if (lhs_q.dtype != torch.uint8 or kp % 96 or tuple(lhs_scale.shape) != (k // 128, m4, 4)
+      or tuple(w_packed.shape) != (g, k // 64, n, 32) or tuple(w_scale.shape) != (g, k // 64, n, 2)):
+    raise ValueError(f"shapes: lhs {tuple(lhs_q.shape)} scale {tuple(lhs_scale.shape)} "
+                     f"w {tuple(w_packed.shape)} w_scale {tuple(w_scale.shape)}")
+  out = torch.empty((m, n), dtype=out_dtype, device=lhs_q.device)
+  check(lib().lmoe_ragged_dot_mxfp6_mxfp4(_p(lhs_q), _p(lhs_scale), _p(w_packed), _p(w_scale), _p(group_sizes),
+                                          m, k, n, g, zero_group, _p(out), _dt(out), _stream()),
+        "ragged_dot_mxfp6_mxfp4")
+  return out
+
+
 def mxfp4_k_split(m: int, n: int, k: int, g: int) -> int:
   """K ranges for the split-K MXFP4 kernel (1: no split).  One group only
   (the tile count of a grouped problem depends on device-side group sizes):
@@ -437,6 +481,13 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   if mode not in _MX_MODES:
     raise ValueError(f"mode {mode!r}")
   mode_id = _MX_MODES[mode]
+  if mode == "scaled_mfma_fp6":
+    if weight_layout != "tiled":
+      raise NotImplementedError("the MXFP6 scaled-MFMA path streams weights from mxfp4_tile_weights (weight_layout='tiled')")
+    if fuse_gateup_activation is not None:
+      raise NotImplementedError("the MXFP6 scaled-MFMA path has no fused SiTU epilogue")
+    q, qs = quantize_mxfp6(lhs)
+    return ragged_dot_mxfp6_mxfp4(q, qs, w_packed, w_scale, group_sizes, zero_group=zero_group)
   if mode == "scaled_mfma":
     if weight_layout != "tiled":
       raise NotImplementedError("the scaled-MFMA path streams weights from mxfp4_tile_weights (weight_layout='tiled')")
