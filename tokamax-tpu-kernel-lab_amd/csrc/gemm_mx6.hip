@@ -25,7 +25,12 @@
 //
 // Pipeline: one block per 128x128 tile, 4 waves as 2 x 2 (64x64 each, 2 x 2
 // MFMA sub-tiles), an NS-deep LDS ring filled by global_load_lds with one
-// vmcnt wait + s_barrier per 128-deep k step.  A rows are 96 bytes in LDS with
+// vmcnt wait + s_barrier per 128-deep k step.  Measured at config 4 (K = 7168,
+// N = 2048): 72.5 us at M = 4096 (1.66 PFLOP/s) and 130 us at M = 8192;
+// 256x128 tiles of 4 x 2 waves 78.5 / 148 us; 256x256 tiles 107 / 115 us
+// (2.09 PFLOP/s at M = 8192, too few tiles below).  Each block keeps two
+// 21.5 KB steps in flight, and the step time (about 1.3 us) is that DMA round
+// trip, not the 8 MFMAs per wave of a step.  A rows are 96 bytes in LDS with
 // their 16-byte chunks rotated by one position for rows 8..15 and 24..31 of
 // every 32: the three 8-byte reads that fetch a lane's 24-byte run then fall
 // on all 64 banks twice (the minimum for 512 bytes).
@@ -133,23 +138,24 @@ __global__ __launch_bounds__(256) void quantize_mxfp6_kernel(const T* __restrict
 }
 
 // ---- grouped GEMM ------------------------------------------------------------
-template <int NS>
+template <int BM_, int BN_, int WM, int WN, int NS>
 struct X6Cfg {
-  static constexpr int BM = 128, BN = 128;
-  static constexpr int kWM = 2, kWN = 2, kThreads = 256;
-  static constexpr int kTM = BM / kWM / 32, kTN = BN / kWN / 32;  // 32x32 sub-tiles per wave (2 x 2)
+  static constexpr int BM = BM_, BN = BN_;
+  static constexpr int kWM = WM, kWN = WN, kThreads = 64 * WM * WN;
+  static constexpr int kTM = BM / kWM / 32, kTN = BN / kWN / 32;  // 32x32 sub-tiles per wave
   static constexpr int kABytes = BM * kARow6;   // packed E2M3 codes
   static constexpr int kASBytes = BM * 4;       // A scales: 4 k-blocks per row
   static constexpr int kBBytes = 2 * BN * 32;   // two 64-k records of packed E2M1
   static constexpr int kBSBytes = 2 * BN * 2;   // their scales
   static constexpr int kSlot = kABytes + kASBytes + kBBytes + kBSBytes;
-  static constexpr int kAOps = BM * (kARow6 / 16) / kThreads;  // 16-byte A chunks per thread (3)
-  static constexpr int kBOps = BN * 4 / kThreads;               // (2)
-  static constexpr int kASOps = BM / 64;                        // wave 0: one dword lane per row (2)
+  static constexpr int kAOps = BM * (kARow6 / 16) / kThreads;  // 16-byte A chunks per thread
+  static constexpr int kBOps = BN * 4 / kThreads;
+  static constexpr int kASOps = BM / 64;                        // wave 0: one dword lane per row
   static constexpr int kOps = kAOps + kBOps;
   static constexpr int kOps0 = kOps + kASOps + 1;  // wave 0 also fetches both scale sets
   static constexpr int kBSLanes = BN / 4;          // 16-byte lanes of the B-scale DMA
   static_assert(BM * (kARow6 / 16) % kThreads == 0 && BN * 4 % kThreads == 0, "DMA split");
+  static_assert(kTM >= 1 && kTN >= 1 && BM % 64 == 0, "wave tile");
   static_assert(kBSLanes <= 64 && kSlot % 16 == 0, "scale DMA / slot alignment");
   static_assert((NS - 2) * kOps0 < 64, "vmcnt range");
   static constexpr int kLdsBlocks = 163840 / (NS * kSlot + 64);
@@ -167,10 +173,11 @@ __device__ __forceinline__ int aphys6(int r, int o) {
   return r * kARow6 + c * 16 + o % 16;
 }
 
-template <int NS>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(X6Cfg<NS>::kLdsBlocks < 1 ? 1 : X6Cfg<NS>::kLdsBlocks)))
+template <int BM_, int BN_, int WM, int WN, int NS>
+__global__ __launch_bounds__(64 * WM * WN) __attribute__((amdgpu_waves_per_eu(
+    X6Cfg<BM_, BN_, WM, WN, NS>::kLdsBlocks * WM * WN / 4 < 1 ? 1 : X6Cfg<BM_, BN_, WM, WN, NS>::kLdsBlocks * WM * WN / 4)))
 void grouped_gemm_mx6_kernel(Params p, int64_t n_tiles, int gm) {
-  using C = X6Cfg<NS>;
+  using C = X6Cfg<BM_, BN_, WM, WN, NS>;
   constexpr int BM = C::BM, BN = C::BN;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ TileInfo s_tile;
@@ -348,9 +355,9 @@ void grouped_gemm_mx6_kernel(Params p, int64_t n_tiles, int gm) {
   }
 }
 
-template <int NS>
+template <int BM_, int BN_, int WM, int WN, int NS>
 int launch_mx6(const Params& p, hipStream_t st, const char* name) {
-  using C = X6Cfg<NS>;
+  using C = X6Cfg<BM_, BN_, WM, WN, NS>;
   const int64_t ntiles = ceil_div(p.N, C::BN);
   const int64_t mtiles = ceil_div(p.M, C::BM) + p.G + 1;
   if (ntiles == 0 || p.M == 0) return LMOE_OK;
@@ -368,14 +375,37 @@ int launch_mx6(const Params& p, hipStream_t st, const char* name) {
   LMOE_CHECK_SUPPORTED(blocks < (1ll << 31), "%s: grid too large", name);
   LMOE_CHECK_SUPPORTED(p.N * p.K / 2 < (1ll << 32) && C::BM * p.K < (1ll << 32), "%s: group too large", name);
   const size_t lds = static_cast<size_t>(NS) * C::kSlot;
-  static const hipError_t attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_mx6_kernel<NS>),
+  static const hipError_t attr_rc = hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_mx6_kernel<BM_, BN_, WM, WN, NS>),
                                                         hipFuncAttributeMaxDynamicSharedMemorySize,
                                                         static_cast<int>(lds));
   if (attr_rc != hipSuccess)
     return fail(LMOE_ERR_HIP, "%s: LDS size attribute (%zu bytes): %s", name, lds, hipGetErrorString(attr_rc));
-  grouped_gemm_mx6_kernel<NS><<<dim3(static_cast<unsigned>(blocks)), C::kThreads, lds, st>>>(p, ntiles, gm);
+  grouped_gemm_mx6_kernel<BM_, BN_, WM, WN, NS><<<dim3(static_cast<unsigned>(blocks)), C::kThreads, lds, st>>>(p, ntiles, gm);
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;
+}
+
+// Tile shape: LMOE_MX6_CFG = "BMxBN_WMxWN_NS" picks an instantiated variant
+// (tuning sweeps).
+int mx6_variant() {
+  static const int v = [] {
+    const char* e = std::getenv("LMOE_MX6_CFG");
+    if (!e) return -1;
+    const char* names[] = {"128x128_2x2_3", "256x128_4x2_3", "256x128_4x2_2", "256x256_4x2_2"};
+    for (int i = 0; i < 4; ++i)
+      if (std::strcmp(e, names[i]) == 0) return i;
+    return -1;
+  }();
+  return v;
+}
+
+int run_mx6(const Params& p, hipStream_t st, const char* name) {
+  switch (mx6_variant()) {
+    case 1: return launch_mx6<256, 128, 4, 2, 3>(p, st, name);
+    case 2: return launch_mx6<256, 128, 4, 2, 2>(p, st, name);
+    case 3: return launch_mx6<256, 256, 4, 2, 2>(p, st, name);
+    default: return launch_mx6<128, 128, 2, 2, 3>(p, st, name);
+  }
 }
 
 }  // namespace
@@ -425,5 +455,5 @@ extern "C" int lmoe_ragged_dot_mxfp6_mxfp4(const uint8_t* lhs_q, const uint8_t* 
                        "%s: alignment", name);
   Params p{reinterpret_cast<const uint16_t*>(lhs_q), w_packed_t, w_scale_t, group_sizes, M, K, N, G, zero_group,
            out, out_dtype, 0.f, 0.f, 0, lhs_scale_t};
-  return launch_mx6<3>(p, static_cast<hipStream_t>(stream), name);
+  return run_mx6(p, static_cast<hipStream_t>(stream), name);
 }
