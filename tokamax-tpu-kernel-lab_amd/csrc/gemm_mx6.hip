@@ -28,9 +28,12 @@
 // vmcnt wait + s_barrier per 128-deep k step.  Measured at config 4 (K = 7168,
 // N = 2048): 72.5 us at M = 4096 (1.66 PFLOP/s) and 130 us at M = 8192;
 // 256x128 tiles of 4 x 2 waves 78.5 / 148 us; 256x256 tiles 107 / 115 us
-// (2.09 PFLOP/s at M = 8192, too few tiles below).  Each block keeps two
-// 21.5 KB steps in flight, and the step time (about 1.3 us) is that DMA round
-// trip, not the 8 MFMAs per wave of a step.  A rows are 96 bytes in LDS with
+// (2.09 PFLOP/s at M = 8192, too few tiles below).  One tile's K loop takes
+// about 0.86 us per 128-deep step even when only 16 tiles run (M = 128), and
+// deeper rings (5 or 6 slots, one block per CU; 4 slots at 256x128) do not
+// shorten it: the per-block stream of DMA issues and barriers (about 25 GB/s
+// per block, as in the bf16 kernels) sets the pace, not the 8 MFMAs per wave
+// of a step.  A rows are 96 bytes in LDS with
 // their 16-byte chunks rotated by one position for rows 8..15 and 24..31 of
 // every 32: the three 8-byte reads that fetch a lane's 24-byte run then fall
 // on all 64 banks twice (the minimum for 512 bytes).
