@@ -370,17 +370,32 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 struct SituConsts {
   float kg, ku;  // 2*log2(e)/beta, 2*log2(e)/beta_lin
   float bbl;     // beta*beta_lin
+  bool beta4;    // beta == 4 (the model's value): one exponential serves tanh(g/4) and sigmoid(g)
 };
 __device__ __forceinline__ SituConsts situ_consts(float beta, float beta_lin) {
   constexpr float kL2e = 1.44269504088896341f;
-  return SituConsts{2.0f * kL2e / beta, 2.0f * kL2e / beta_lin, beta * beta_lin};
+  return SituConsts{2.0f * kL2e / beta, 2.0f * kL2e / beta_lin, beta * beta_lin, beta == 4.0f};
 }
+// SiTU-GLU of one (gate, up) pair: beta tanh(g/beta) sigmoid(g) * beta_lin
+// tanh(u/beta_lin), with tanh(x) = (e^2x - 1)/(e^2x + 1) and the exponentials
+// clamped to 2^+-26 (tanh is +-1 to f32 precision there).  With beta == 4,
+// a = e^(g/2) gives tanh(g/4) = (a-1)/(a+1) and sigmoid(g) = a^2/(1+a^2), so
+// the pair costs two exponentials and one reciprocal (numerator and
+// denominator stay below 2^104); otherwise sigmoid takes its own exponential
+// and reciprocal.  NaN in either input gives NaN.  Every fused kernel uses
+// this one function, so they agree bit for bit.
 __device__ __forceinline__ float situ_epi(float g, float u, const SituConsts& c) {
   const float a = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(g * c.kg, -26.0f, 26.0f));
   const float b = __builtin_amdgcn_exp2f(__builtin_amdgcn_fmed3f(u * c.ku, -26.0f, 26.0f));
-  const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
-  const float q = (a - 1.0f) * (b - 1.0f) * __builtin_amdgcn_rcpf((a + 1.0f) * (b + 1.0f));
-  const float r = c.bbl * q * __builtin_amdgcn_rcpf(1.0f + e);
+  float r;
+  if (c.beta4) {
+    const float a2 = a * a;
+    r = c.bbl * ((a - 1.0f) * a2 * (b - 1.0f)) * __builtin_amdgcn_rcpf((a + 1.0f) * (1.0f + a2) * (b + 1.0f));
+  } else {
+    const float e = __builtin_amdgcn_exp2f(g * -1.44269504088896341f);
+    const float q = (a - 1.0f) * (b - 1.0f) * __builtin_amdgcn_rcpf((a + 1.0f) * (b + 1.0f));
+    r = c.bbl * q * __builtin_amdgcn_rcpf(1.0f + e);
+  }
   return __builtin_isunordered(g, u) ? __builtin_nanf("") : r;
 }
 
