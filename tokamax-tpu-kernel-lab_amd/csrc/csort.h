@@ -220,6 +220,95 @@ __global__ __launch_bounds__(64) void place_kernel(KeyFn key, int64_t n, int nbi
   }
 }
 
+// place with four waves per chunk: wave w takes the chunk's w-th quarter of
+// slots (CHUNK / 256 rounds of 64).  A first pass finds every round's
+// match-any groups and counts each wave's keys per bin in LDS; the counts
+// then become per-wave starting positions (the chunk's base plus the counts
+// of the earlier waves), and a second pass places the slots exactly as the
+// one-wave kernel does, so the positions are the same and stable.  Four
+// times the slots in flight per chunk and a quarter of the serial rounds per
+// wave; LDS 16 * nbins bytes (the caller keeps it within 64 KB).
+template <int CHUNK, class KeyFn, class Sink>
+__global__ __launch_bounds__(256) void place4_kernel(KeyFn key, int64_t n, int nbins, int key_bits, int64_t chunks,
+                                                     const int32_t* __restrict__ base, Sink sink) {
+  constexpr int kW = 4, IT = CHUNK / 64 / kW;
+  static_assert(CHUNK % (64 * kW) == 0, "chunk split over the waves");
+  extern __shared__ int32_t off[];  // [kW][nbins]
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int64_t wave_base = static_cast<int64_t>(blockIdx.x) * CHUNK + wave * (CHUNK / kW);
+  int keys[IT];
+  uint32_t loaded[IT];
+  uint64_t peer_sets[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t s = wave_base + it * 64 + lane;
+    keys[it] = s < n ? key(s) : nbins;
+    loaded[it] = s < n ? sink.load(s) : 0u;
+  }
+  for (int i = threadIdx.x; i < kW * nbins; i += 256) off[i] = 0;
+  __syncthreads();
+  const uint64_t below = (1ull << lane) - 1ull;
+  int32_t* mine = off + wave * nbins;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t s = wave_base + it * 64 + lane;
+    const int kk = keys[it];
+    const bool real = s < n && kk < nbins;
+    uint64_t peers = __ballot(real);
+    for (int b = 0; b < key_bits; ++b) {
+      const bool bit = (kk >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      peers &= bit ? bb : ~bb;
+    }
+    peer_sets[it] = peers;
+    if (real && (peers & below) == 0) mine[kk] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < nbins; b += 256) {
+    int32_t acc = base[b * chunks + blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      const int32_t c = off[w * nbins + b];
+      off[w * nbins + b] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    if (wave_base + it * 64 >= n) break;  // uniform across the wave
+    const int64_t s = wave_base + it * 64 + lane;
+    const bool active = s < n;
+    const int kk = keys[it];
+    const bool real = active && kk < nbins;
+    const uint64_t peers = peer_sets[it];
+    int pos = 0;
+    if (real) pos = mine[kk] + __popcll(peers & below);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    if (real && (peers & below) == 0) mine[kk] = pos + __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    if (active) sink(s, kk, pos, real, loaded[it]);
+  }
+}
+
+// place over all chunks: the four-wave kernel when its per-wave counts fit
+// in 64 KB of LDS, else the one-wave kernel.
+template <int CHUNK, class KeyFn, class Sink>
+inline void launch_place(KeyFn key, int64_t n, int nbins, int64_t chunks, const int32_t* base, Sink sink,
+                         hipStream_t st) {
+  const int bits = key_bits_for(nbins);
+  if (static_cast<int64_t>(nbins) * 16 <= 65536)
+    place4_kernel<CHUNK><<<dim3(static_cast<unsigned>(chunks)), 256, nbins * 16, st>>>(key, n, nbins, bits, chunks,
+                                                                                       base, sink);
+  else
+    place_kernel<CHUNK><<<dim3(static_cast<unsigned>(chunks)), 64, nbins * sizeof(int32_t), st>>>(
+        key, n, nbins, bits, chunks, base, sink);
+}
+
 }  // namespace
 }  // namespace csort
 }  // namespace lmoe

@@ -228,8 +228,7 @@ extern "C" int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, 
   if (n > 0) {
     DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
                       padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
-    csort::place_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 64, L * sizeof(int32_t), st>>>(
-        key, n, Li, csort::key_bits_for(Li), chunks, w.base, sink);
+    csort::launch_place<kDispatchChunk>(key, n, Li, chunks, w.base, sink, st);
     LMOE_CHECK_LAUNCH("dispatch_place");
   }
   // The gather also finalises group_sizes[L] and per_expert_counts (block 0),
@@ -321,8 +320,7 @@ extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* top
   if (n > 0) {
     DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
                       padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
-    csort::place_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 64, L * sizeof(int32_t), st>>>(
-        key, n, Li, csort::key_bits_for(Li), chunks, w.base, sink);
+    csort::launch_place<kDispatchChunk>(key, n, Li, chunks, w.base, sink, st);
     LMOE_CHECK_LAUNCH("dispatch_place");
   }
   const unsigned blocks = static_cast<unsigned>(m_padded > 0 ? ceil_div(m_padded, kGatherRows) : 1);
