@@ -295,6 +295,155 @@ __global__ __launch_bounds__(256) void place4_kernel(KeyFn key, int64_t n, int n
   }
 }
 
+// Scan for few bins, split over the bins instead of one block: wave b scans
+// bin b's chunk counts hist[b * chunks + c] in chunk order and writes their
+// exclusive prefix (the position of the chunk's first key relative to the
+// bin's first position) to rel[b * chunks + c], then the bin's total over
+// hist[b * chunks].  Lane i owns the contiguous run [i * per, (i + 1) * per)
+// of chunks; up to kHeld counts per lane are loaded at once (one memory round
+// trip for up to 64 * kHeld chunks).  The bin offsets (an exclusive prefix
+// over the bins) are left to place_scanned_kernel, which needs them anyway,
+// so no kernel reads the whole histogram.
+__global__ __launch_bounds__(64) void scan_bins_kernel(int32_t* __restrict__ hist, int64_t chunks,
+                                                       int32_t* __restrict__ rel) {
+  constexpr int kHeld = 16;
+  const int lane = threadIdx.x;
+  int32_t* h = hist + static_cast<int64_t>(blockIdx.x) * chunks;
+  int32_t* r = rel + static_cast<int64_t>(blockIdx.x) * chunks;
+  const int64_t per = (chunks + 63) / 64;
+  const int64_t i0 = lane * per;
+  const int64_t i1 = i0 + per < chunks ? i0 + per : chunks;
+  int32_t held[kHeld];
+#pragma unroll
+  for (int q = 0; q < kHeld; ++q) held[q] = i0 + q < i1 ? h[i0 + q] : 0;
+  uint32_t local = 0;
+#pragma unroll
+  for (int q = 0; q < kHeld; ++q) local += static_cast<uint32_t>(held[q]);
+  for (int64_t i = i0 + kHeld; i < i1; ++i) local += static_cast<uint32_t>(h[i]);
+  const uint32_t incl = wave_scan_sat(local, 0x7fffffffu);
+  const uint32_t total = __builtin_amdgcn_readlane(incl, 63);
+  uint32_t run = incl - local;
+#pragma unroll
+  for (int q = 0; q < kHeld; ++q)
+    if (i0 + q < i1) {
+      r[i0 + q] = static_cast<int32_t>(run);
+      run += static_cast<uint32_t>(held[q]);
+    }
+  for (int64_t i = i0 + kHeld; i < i1; ++i) {
+    const int32_t v = h[i];
+    r[i] = static_cast<int32_t>(run);
+    run += static_cast<uint32_t>(v);
+  }
+  if (lane == 0) h[0] = static_cast<int32_t>(total);  // only lane 0 read h[0], above
+}
+
+// place4_kernel for the scan_bins_kernel layout: every block first turns the
+// bin totals (hist[b * chunks]) into bin offsets with a block-wide exclusive
+// scan, so a chunk's start in bin b is offset[b] + rel[b * chunks + c].
+// Block 0 also writes bin_kept[b] (positions below limit) and *num_kept, the
+// outputs of the one-block scan.  Runs for n == 0 too (one chunk).  LDS
+// 20 * nbins bytes.
+template <int CHUNK, class KeyFn, class Sink>
+__global__ __launch_bounds__(256) void place_scanned_kernel(KeyFn key, int64_t n, int nbins, int key_bits,
+                                                            int64_t chunks, const int32_t* __restrict__ totals,
+                                                            const int32_t* __restrict__ rel, int64_t limit,
+                                                            int32_t* __restrict__ bin_kept,
+                                                            int32_t* __restrict__ num_kept, Sink sink) {
+  constexpr int kW = 4, IT = CHUNK / 64 / kW;
+  static_assert(CHUNK % (64 * kW) == 0, "chunk split over the waves");
+  extern __shared__ int32_t off[];  // [kW][nbins], then the bin offsets [nbins]
+  __shared__ uint32_t s_part[kW];
+  int32_t* bin_off = off + kW * nbins;
+  const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+  const int64_t wave_base = static_cast<int64_t>(blockIdx.x) * CHUNK + wave * (CHUNK / kW);
+  int keys[IT];
+  uint32_t loaded[IT];
+  uint64_t peer_sets[IT];
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t s = wave_base + it * 64 + lane;
+    keys[it] = s < n ? key(s) : nbins;
+    loaded[it] = s < n ? sink.load(s) : 0u;
+  }
+  // bin offsets: thread t owns the contiguous bins [t * per, (t + 1) * per)
+  const int per = (nbins + 255) / 256;
+  const int b0 = threadIdx.x * per, b1 = b0 + per < nbins ? b0 + per : nbins;
+  uint32_t mine_sum = 0;
+  for (int b = b0; b < b1; ++b) {
+    const uint32_t t = static_cast<uint32_t>(totals[static_cast<int64_t>(b) * chunks]);
+    bin_off[b] = static_cast<int32_t>(t);
+    mine_sum += t;
+  }
+  for (int i = threadIdx.x; i < kW * nbins; i += 256) off[i] = 0;
+  const uint32_t incl = wave_scan_sat(mine_sum, 0x7fffffffu);
+  if (lane == 63) s_part[wave] = incl;
+  __syncthreads();
+  uint32_t run = incl - mine_sum, grand = 0;
+  for (int w = 0; w < kW; ++w) {
+    if (w < wave) run += s_part[w];
+    grand += s_part[w];
+  }
+  for (int b = b0; b < b1; ++b) {
+    const uint32_t t = static_cast<uint32_t>(bin_off[b]);
+    bin_off[b] = static_cast<int32_t>(run);
+    if (blockIdx.x == 0) {
+      int64_t kept = limit - static_cast<int64_t>(run);
+      kept = kept < 0 ? 0 : (kept > t ? t : kept);
+      bin_kept[b] = static_cast<int32_t>(kept);
+    }
+    run += t;
+  }
+  if (blockIdx.x == 0 && threadIdx.x == 0)
+    *num_kept = static_cast<int32_t>(static_cast<int64_t>(grand) < limit ? static_cast<int64_t>(grand) : limit);
+  __syncthreads();
+  const uint64_t below = (1ull << lane) - 1ull;
+  int32_t* mine = off + wave * nbins;
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    const int64_t s = wave_base + it * 64 + lane;
+    const int kk = keys[it];
+    const bool real = s < n && kk < nbins;
+    uint64_t peers = __ballot(real);
+    for (int b = 0; b < key_bits; ++b) {
+      const bool bit = (kk >> b) & 1;
+      const uint64_t bb = __ballot(bit);
+      peers &= bit ? bb : ~bb;
+    }
+    peer_sets[it] = peers;
+    if (real && (peers & below) == 0) mine[kk] += __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+  }
+  __syncthreads();
+  for (int b = threadIdx.x; b < nbins; b += 256) {
+    int32_t acc = bin_off[b] + rel[static_cast<int64_t>(b) * chunks + blockIdx.x];
+#pragma unroll
+    for (int w = 0; w < kW; ++w) {
+      const int32_t c = off[w * nbins + b];
+      off[w * nbins + b] = acc;
+      acc += c;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int it = 0; it < IT; ++it) {
+    if (wave_base + it * 64 >= n) break;  // uniform across the wave
+    const int64_t s = wave_base + it * 64 + lane;
+    const bool active = s < n;
+    const int kk = keys[it];
+    const bool real = active && kk < nbins;
+    const uint64_t peers = peer_sets[it];
+    int pos = 0;
+    if (real) pos = mine[kk] + __popcll(peers & below);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    if (real && (peers & below) == 0) mine[kk] = pos + __popcll(peers);
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("s_waitcnt lgkmcnt(0)" : : : "memory");
+    if (active) sink(s, kk, pos, real, loaded[it]);
+  }
+}
+
 // place over all chunks: the four-wave kernel when its per-wave counts fit
 // in 64 KB of LDS, else the one-wave kernel.
 template <int CHUNK, class KeyFn, class Sink>
@@ -307,6 +456,28 @@ inline void launch_place(KeyFn key, int64_t n, int nbins, int64_t chunks, const 
   else
     place_kernel<CHUNK><<<dim3(static_cast<unsigned>(chunks)), 64, nbins * sizeof(int32_t), st>>>(
         key, n, nbins, bits, chunks, base, sink);
+}
+
+// Scan + place of a counting sort whose histogram hist (bin-major, chunks
+// per bin) is already built: bin_kept[b] and *num_kept as the one-block scan
+// gives them, and sink(...) for every slot.  Few bins (20 * nbins bytes of
+// LDS, with the static wave totals, fit in 64 KB): scan_bins_kernel and
+// place_scanned_kernel; else the one-block scan and the place kernels.  base
+// (nbins * chunks ints) receives the scanned chunk starts; hist is
+// overwritten.
+template <int CHUNK, class KeyFn, class Sink>
+inline hipError_t scan_and_place(KeyFn key, int64_t n, int nbins, int64_t chunks, int64_t limit, int32_t* hist,
+                                 int32_t* base, int32_t* bin_kept, int32_t* num_kept, Sink sink, hipStream_t st) {
+  if (static_cast<int64_t>(nbins) * 20 <= 65536 - 256) {
+    scan_bins_kernel<<<dim3(static_cast<unsigned>(nbins)), 64, 0, st>>>(hist, chunks, base);
+    place_scanned_kernel<CHUNK><<<dim3(static_cast<unsigned>(chunks)), 256, nbins * 20, st>>>(
+        key, n, nbins, key_bits_for(nbins), chunks, hist, base, limit, bin_kept, num_kept, sink);
+    return hipSuccess;
+  }
+  const hipError_t e = launch_scan(hist, chunks, nbins, limit, base, bin_kept, nullptr, num_kept, st);
+  if (e != hipSuccess) return e;
+  if (n > 0) launch_place<CHUNK>(key, n, nbins, chunks, base, sink, st);
+  return hipSuccess;
 }
 
 }  // namespace

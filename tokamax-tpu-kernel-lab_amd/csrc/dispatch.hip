@@ -222,14 +222,13 @@ extern "C" int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, 
   csort::hist_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 256, (L + 1) * sizeof(int32_t), st>>>(
       key, n, Li, chunks, w.hist);
   LMOE_CHECK_LAUNCH("dispatch_hist");
-  if (csort::launch_scan(w.hist, chunks, Li, m_padded, w.base, group_sizes, nullptr, w.num_kept, st) != hipSuccess)
-    return fail(LMOE_ERR_HIP, "dispatch_scan: LDS attribute");
-  LMOE_CHECK_LAUNCH("dispatch_scan");
-  if (n > 0) {
+  {
     DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
                       padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
-    csort::launch_place<kDispatchChunk>(key, n, Li, chunks, w.base, sink, st);
-    LMOE_CHECK_LAUNCH("dispatch_place");
+    if (csort::scan_and_place<kDispatchChunk>(key, n, Li, chunks, m_padded, w.hist, w.base, group_sizes,
+                                              w.num_kept, sink, st) != hipSuccess)
+      return fail(LMOE_ERR_HIP, "dispatch_scan: LDS attribute");
+    LMOE_CHECK_LAUNCH("dispatch_scan_place");
   }
   // The gather also finalises group_sizes[L] and per_expert_counts (block 0),
   // so it runs even when m_padded == 0.
@@ -314,14 +313,13 @@ extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* top
   csort::hist_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 256, (L + 1) * sizeof(int32_t), st>>>(
       key, n, Li, chunks, w.hist);
   LMOE_CHECK_LAUNCH("dispatch_hist");
-  if (csort::launch_scan(w.hist, chunks, Li, m_padded, w.base, group_sizes, nullptr, w.num_kept, st) != hipSuccess)
-    return fail(LMOE_ERR_HIP, "dispatch_scan: LDS attribute");
-  LMOE_CHECK_LAUNCH("dispatch_scan");
-  if (n > 0) {
+  {
     DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
                       padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
-    csort::launch_place<kDispatchChunk>(key, n, Li, chunks, w.base, sink, st);
-    LMOE_CHECK_LAUNCH("dispatch_place");
+    if (csort::scan_and_place<kDispatchChunk>(key, n, Li, chunks, m_padded, w.hist, w.base, group_sizes,
+                                              w.num_kept, sink, st) != hipSuccess)
+      return fail(LMOE_ERR_HIP, "dispatch_scan: LDS attribute");
+    LMOE_CHECK_LAUNCH("dispatch_scan_place");
   }
   const unsigned blocks = static_cast<unsigned>(m_padded > 0 ? ceil_div(m_padded, kGatherRows) : 1);
   const int skip = (flags & LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS) != 0;
