@@ -44,33 +44,45 @@ namespace {
 
 using namespace lmoe::dma;
 
-template <int BM, int BN, int NS>
+// KG wave groups of 2 x 2 waves split every 64-deep step's four 16-deep
+// sub-steps between them (group g takes sub-steps [g * 4 / KG, +4 / KG)); the
+// groups' accumulators are added through LDS after the K loop.  KG = 2 puts
+// two waves on each SIMD: twice the waves issuing the DMA (one wave moves
+// about 20 GB/s through global_load_lds, so four waves cannot feed a
+// 256 x 128 tile at the MFMA rate) and a second wave to issue MFMAs while the
+// first waits, with the same per-wave fragment traffic.
+template <int BM, int BN, int NS, int KG>
 struct DenseCfg {
-  static constexpr int kThreads = 256, kWaves = 4, kWM = 2, kWN = 2;
+  static constexpr int kThreads = 256 * KG, kWaves = 4 * KG, kWM = 2, kWN = 2;
   static constexpr int kWTM = BM / kWM, kWTN = BN / kWN;  // wave tile
   static constexpr int kTM = kWTM / 32, kTN = kWTN / 32;  // 32x32 sub-tiles per wave
-  static constexpr int kKS = 4;                           // 16-deep MFMA sub-steps per 64-deep step
+  static constexpr int kKS = 4 / KG;                      // 16-deep MFMA sub-steps per wave per 64-deep step
   static constexpr int kABytes = BM * 128, kBBytes = BN * 128;
   static constexpr int kSlot = kABytes + kBBytes;
   static constexpr int kAOps = BM * 8 / kThreads, kBOps = BN * 8 / kThreads;  // DMA per thread per step
   static constexpr int kOps = kAOps + kBOps;
+  static constexpr int kRedBytes = (KG - 1) * 4 * kTM * kTN * 16 * 64 * 4;  // group 1's accumulators
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile");
+  static_assert(KG == 1 || KG == 2, "wave groups");
+  static_assert(kAOps * kThreads == BM * 8 && kBOps * kThreads == BN * 8, "DMA split");
   static_assert((NS - 1) * kOps < 64, "vmcnt range");
-  static_assert(NS * kSlot <= 163840, "LDS ring");
+  static_assert(NS * kSlot <= 163840 && kRedBytes <= NS * kSlot, "LDS ring");
 };
 
-template <int BM, int BN, int NS, bool F32>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+template <int BM, int BN, int NS, int KG, bool F32>
+__global__ __launch_bounds__(256 * KG) __attribute__((amdgpu_waves_per_eu(KG, KG)))
 void dense_gemm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restrict__ w, int M, int N, int K,
                        int n_tiles, int tiles, int per_xcd, void* __restrict__ out) {
-  using C = DenseCfg<BM, BN, NS>;
+  using C = DenseCfg<BM, BN, NS, KG>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const int b = blockIdx.x;
   const int t = (b % kXcds) * per_xcd + b / kXcds;
   if (b / kXcds >= per_xcd || t >= tiles) return;
   const int mt = t / n_tiles, nt = t % n_tiles;
   const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
-  const int wm = wave / C::kWN, wn = wave % C::kWN;
+  const int kg = wave / 4, wq = wave % 4;  // wave group, wave within the group
+  const int wm = wq / C::kWN, wn = wq % C::kWN;
+  const int kb = kg * C::kKS;  // this group's first sub-step
   const int nk = K / 64;
 
   // DMA addressing: SGPR bases advanced by one step (128 bytes) per step,
@@ -141,7 +153,6 @@ void dense_gemm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restric
       for (int j = 0; j < C::kTN; ++j)
         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[j], f.a[i], acc[i][j], 0, 0, 0);
   };
-
   // wait until a step has landed when `younger` (0 .. NS-1) later steps were
   // issued after it (anything else waits for every DMA), then barrier
   auto land = [&](int younger) __attribute__((always_inline)) {
@@ -163,7 +174,7 @@ void dense_gemm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restric
   });
   Frag fa, fb;
   land((nk - 1 < NS - 1 ? nk - 1 : NS - 1));
-  read_frag(0, 0, fa);
+  read_frag(0, kb, fa);
   // Sub-step (k, kk) computes from registers while the next sub-step's
   // fragments are read.  Before the read of (k+1, 0): step k+1 lands and the
   // barrier also makes every wave's reads of step k complete, so slot k % NS
@@ -171,20 +182,56 @@ void dense_gemm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restric
   // each step starts from fa.
   for (int k = 0; k < nk; ++k) {
     const int slot = k % NS;
-    read_frag(slot, 1, fb);
+    read_frag(slot, kb + 1, fb);
     compute(fa);
-    read_frag(slot, 2, fa);
-    compute(fb);
-    read_frag(slot, 3, fb);
-    compute(fa);
+    if constexpr (C::kKS == 4) {
+      read_frag(slot, kb + 2, fa);
+      compute(fb);
+      read_frag(slot, kb + 3, fb);
+      compute(fa);
+    }
     if (k + 1 < nk) {
       // steps issued after k+1: k+2 .. min(k+NS-1, nk-1)
       const int last = nk - 1 < k + NS - 1 ? nk - 1 : k + NS - 1;
       land(last - (k + 1));
       if (k + NS < nk) issue(k + NS, slot);
-      read_frag((k + 1) % NS, 0, fa);
+      read_frag((k + 1) % NS, kb, fa);
     }
     compute(fb);
+  }
+
+  if constexpr (KG == 2) {
+    // group 1 hands its accumulators to group 0 through the (drained) ring:
+    // lane-contiguous float4 runs, conflict-free both ways
+    float4* red = reinterpret_cast<float4*>(smem);
+    auto red_at = [&](int i, int j, int q) __attribute__((always_inline)) {
+      return ((wq * C::kTM * C::kTN + i * C::kTN + j) * 4 + q) * 64 + lane;
+    };
+    __syncthreads();  // every wave's last fragment reads of the ring are done
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < C::kTM; ++i)
+#pragma unroll
+        for (int j = 0; j < C::kTN; ++j)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            red[red_at(i, j, q)] = float4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2],
+                                          acc[i][j][4 * q + 3]};
+    }
+    __syncthreads();
+    if (kg == 1) return;
+#pragma unroll
+    for (int i = 0; i < C::kTM; ++i)
+#pragma unroll
+      for (int j = 0; j < C::kTN; ++j)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const float4 v = red[red_at(i, j, q)];
+          acc[i][j][4 * q] += v.x;
+          acc[i][j][4 * q + 1] += v.y;
+          acc[i][j][4 * q + 2] += v.z;
+          acc[i][j][4 * q + 3] += v.w;
+        }
   }
 
   // epilogue: lane holds output row (lane % 32) of sub-tile i and, for
@@ -213,18 +260,18 @@ void dense_gemm_kernel(const uint16_t* __restrict__ x, const uint16_t* __restric
   }
 }
 
-template <int BM, int BN, int NS, bool F32>
+template <int BM, int BN, int NS, int KG, bool F32>
 int launch_dense(const uint16_t* x, const uint16_t* w, int64_t M, int64_t N, int64_t K, void* out, hipStream_t st) {
-  using C = DenseCfg<BM, BN, NS>;
+  using C = DenseCfg<BM, BN, NS, KG>;
   const int64_t n_tiles = ceil_div(N, BN), tiles = ceil_div(M, BM) * n_tiles;
   const int64_t per_xcd = ceil_div(tiles, kXcds);
   const size_t lds = static_cast<size_t>(NS) * C::kSlot;
   static const hipError_t attr_rc = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&dense_gemm_kernel<BM, BN, NS, F32>),
+      reinterpret_cast<const void*>(&dense_gemm_kernel<BM, BN, NS, KG, F32>),
       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr_rc != hipSuccess)
     return fail(LMOE_ERR_HIP, "dense_gemm: LDS size attribute: %s", hipGetErrorString(attr_rc));
-  dense_gemm_kernel<BM, BN, NS, F32><<<dim3(static_cast<unsigned>(kXcds * per_xcd)), C::kThreads, lds, st>>>(
+  dense_gemm_kernel<BM, BN, NS, KG, F32><<<dim3(static_cast<unsigned>(kXcds * per_xcd)), C::kThreads, lds, st>>>(
       x, w, static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), static_cast<int>(n_tiles),
       static_cast<int>(tiles), static_cast<int>(per_xcd), out);
   LMOE_CHECK_LAUNCH("dense_gemm");
@@ -252,6 +299,16 @@ extern "C" int lmoe_dense(const void* x, const void* w_nk, int64_t M, int64_t K,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(w_nk);
-  if (out_dtype == LMOE_F32) return launch_dense<256, 128, 3, true>(xp, wp, M, N, K, out, st);
-  return launch_dense<256, 128, 3, false>(xp, wp, M, N, K, out, st);
+  // LMOE_DENSE_CFG selects a variant for A/B measurements ("kg1": one wave
+  // per SIMD); the default is the two-group kernel
+  static const int kg1 = [] {
+    const char* e = std::getenv("LMOE_DENSE_CFG");
+    return e && std::strcmp(e, "kg1") == 0;
+  }();
+  if (kg1) {
+    if (out_dtype == LMOE_F32) return launch_dense<256, 128, 3, 1, true>(xp, wp, M, N, K, out, st);
+    return launch_dense<256, 128, 3, 1, false>(xp, wp, M, N, K, out, st);
+  }
+  if (out_dtype == LMOE_F32) return launch_dense<256, 128, 3, 2, true>(xp, wp, M, N, K, out, st);
+  return launch_dense<256, 128, 3, 2, false>(xp, wp, M, N, K, out, st);
 }
