@@ -29,6 +29,20 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
       reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
 }
 
+// Load from an LDS byte address.
+template <class T>
+__device__ __forceinline__ T lds_load(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) T*>(static_cast<uintptr_t>(addr));
+}
+
+// x through an opaque move: the compiler keeps the value in a register
+// instead of recomputing it where it is used.
+__device__ __forceinline__ uint32_t opaque_u32(uint32_t x) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
+
 // Wave-uniform copy of a pointer (lives in an SGPR pair).
 __device__ __forceinline__ const uint8_t* uniform_ptr(const void* p) {
   const uint64_t v = reinterpret_cast<uint64_t>(p);

@@ -829,7 +829,47 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
         uint32_t bw[C::kKS][C::kTN];
         uint32_t s2[C::kTN];
       };
+      // MF == 32: the lane's LDS byte offsets inside a ring slot, computed once
+      // per tile and held in registers for the K loop (the opaque moves keep
+      // the compiler from recomputing them every step): one per A k sub-step
+      // (row sub-tile i adds i * MF rows: swz8 depends on the low four row
+      // bits only), one for the weights and one for the scales (column
+      // sub-tile j adds a constant column offset).  A step then adds the
+      // slot base to these six registers and reads with immediate offsets.
+      uint32_t fo_a[C::kKS], fo_b = 0, fo_s = 0;
+      if constexpr (MF == 32) {
+#pragma unroll
+        for (int kk = 0; kk < C::kKS; ++kk) {
+          const int kc = kk * 2 + f_kc;
+          fo_a[kk] = opaque_u32(static_cast<uint32_t>(f_rc * 128 + ((kc ^ swz8(f_rc)) * 16)));
+        }
+        const int c0 = dlds_col<BN, C::kTN, EPI, MF>(wn, 0) + f_rc;
+        fo_b = opaque_u32(static_cast<uint32_t>(C::kABytes + c0 * 32 + f_kc * 16));
+        fo_s = opaque_u32(static_cast<uint32_t>(C::kABytes + C::kBBytes + c0 * 2));
+      }
       auto read_frags = [&](int slot, Frags& f) __attribute__((always_inline)) {
+        if constexpr (MF == 32) {
+          const uint32_t sb = lds_offset(smem) + static_cast<uint32_t>(slot * C::kSlot);
+          const uint32_t pa0 = sb + fo_a[0], pb = sb + fo_b, ps = sb + fo_s;
+#pragma unroll
+          for (int j = 0; j < C::kTN; ++j) {
+            const int dc = dlds_col<BN, C::kTN, EPI, MF>(0, j) - dlds_col<BN, C::kTN, EPI, MF>(0, 0);
+            f.s2[j] = lds_load<uint16_t>(ps + dc * 2);
+            typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+            const u32x4_t w = lds_load<u32x4_t>(pb + dc * 32);
+            f.bw[0][j] = w[0];
+            f.bw[1][j] = w[1];
+            f.bw[2][j] = w[2];
+            f.bw[3][j] = w[3];
+          }
+#pragma unroll
+          for (int kk = 0; kk < C::kKS; ++kk) {
+            const uint32_t pa = kk == 0 ? pa0 : sb + fo_a[kk];
+#pragma unroll
+            for (int i = 0; i < C::kTM; ++i) f.af[kk][i] = lds_load<bf16x8_t>(pa + i * MF * 128);
+          }
+          return;
+        }
         const uint8_t* as = smem + slot * C::kSlot;
         const uint8_t* bs = as + C::kABytes;
         const uint8_t* ss = bs + C::kBBytes;
@@ -911,12 +951,15 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
           }
       };
       auto k_loop = [&](auto full_tag) __attribute__((always_inline)) {
-        int slot = slot0;  // slot of step kt
-        for (int64_t kt = 0; kt < nk; ++kt) {
+        // 32-bit wave-uniform loop state, so the loop control, slot rotation
+        // and DMA bases stay on the scalar unit
+        int slot = __builtin_amdgcn_readfirstlane(slot0);  // slot of step kt
+        const int nk32 = static_cast<int>(nk);
+        for (int kt = 0; kt < nk32; ++kt) {
           // wait for step kt: (a) later DMA steps issued, (b) prefetched
           // tiles' first steps are older than the previous epilogue's stores
-          const int64_t left = nk - 1 - kt;
-          const int a = pf || left >= NS - 2 ? NS - 2 : static_cast<int>(left);
+          const int left = nk32 - 1 - kt;
+          const int a = pf || left >= NS - 2 ? NS - 2 : left;
           const int b = (cur_pf && kt <= NS - 2) ? prev_rounds : 0;
           if (__builtin_expect(a == NS - 2 && b == 0, 1)) {  // steady state: one test
             if (wave == 0)
@@ -931,12 +974,12 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
           barrier();
           // refill the slot of step kt-1: this tile's step kt+NS-1, or the
           // next tile's step kt+NS-1-nk
-          const int wslot = slot == 0 ? NS - 1 : slot - 1;
-          const int64_t s = kt + NS - 1;
-          if (s < nk)
+          const int wslot = __builtin_amdgcn_readfirstlane(slot == 0 ? NS - 1 : slot - 1);
+          const int s = kt + NS - 1;
+          if (s < nk32)
             issue(ca, s, wslot);
           else if (pf)
-            issue(make_addr(nxt, nt_n, tid), s - nk, wslot);
+            issue(make_addr(nxt, nt_n, tid), s - nk32, wslot);
           Frags f;
           read_frags(slot, f);
           compute(f, full_tag);
