@@ -139,6 +139,24 @@ int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, const uint8_
                           int zero_group, int mode, int epilogue, float beta, float beta_lin,
                           void* out, void* stream);
 
+/* ---- a11/a12 + a18: the expert GEMM on gathered token rows --------------------------
+ * lmoe_ragged_dot_mxfp4 (tiled weights, LMOE_MXFP4_LDS_DEQUANT_TILED) whose
+ * grouped lhs is gathered from a token array: row r of the grouped problem is
+ * row row_index[r] of lhs (lhs_rows, K) bf16 -- the composition
+ * ragged_dot(x[padded_token_idx], W, group_sizes) that rd.py:604-607 (and the
+ * fused gate/up of rd.py:644-723) run on the dispatch's sorted_tokens, without
+ * materialising sorted_tokens.  row_index is the dispatch's padded_token_idx
+ * (M entries; only rows inside the groups are read, indices are clamped into
+ * [0, lhs_rows)).  Same results as gathering first, bit for bit.  The streamed
+ * kernel only: LMOE_ERR_UNSUPPORTED when it does not apply (lhs_rows > 65536,
+ * or more than 8 tiles per resident block).  Optional
+ * LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS.
+ */
+int lmoe_ragged_dot_mxfp4_rows(const void* lhs, int64_t lhs_rows, const int32_t* row_index,
+                               const uint8_t* w_packed, const uint8_t* w_scale, const int32_t* group_sizes,
+                               int64_t M, int64_t K, int64_t N, int64_t G, int zero_group, int mode,
+                               int epilogue, float beta, float beta_lin, void* out, void* stream);
+
 /* ---- a18, few long-K tiles: split-K grouped GEMM on tiled MXFP4 weights ---------
  * Same operation as lmoe_ragged_dot_mxfp4 with LMOE_MXFP4_LDS_DEQUANT_TILED
  * (the config-4 matmul of odq.py:65-172 / mxfp4_online_dequant_matmul_pallas.py:94-157
@@ -281,6 +299,17 @@ int lmoe_router_topk(const float* logits, const float* bias, int64_t T, int64_t 
 int lmoe_router_topk_ld(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E,
                         int64_t k, int act, int renorm, float scale, int weight_dtype,
                         int32_t* topk_idx, void* topk_w, float* scores_out, void* stream);
+/* router_and_projection (ref.py:634-655) given the GEMM that computes the
+ * router logits and the latent projection x = h @ down_proj together (f32
+ * rows of ld floats: logits at columns [0, E), x at x_src = logits + E or any
+ * rows of x_ld floats): lmoe_router_topk_ld's (topk_idx, topk_w) and x as bf16
+ * (T, lat), rounded to nearest even -- the projection's output dtype -- by the
+ * same launch.  lat <= 1024, lat % 4 == 0, x_ld % 4 == 0, x_src 16-byte and
+ * x_out 8-byte aligned. */
+int lmoe_router_topk_proj(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E,
+                          int64_t k, int act, int renorm, float scale, int weight_dtype,
+                          int32_t* topk_idx, void* topk_w, const float* x_src, int64_t x_ld,
+                          int64_t lat, uint16_t* x_out, void* stream);
 
 /* ---- a7: local-shard dispatch ------------------------------------------------------
  * Replaces filter_and_pad_to_shard_jittable (ref.py:754-877), bit-identical to
@@ -329,6 +358,10 @@ int lmoe_dispatch_local_noalloc(const int32_t* topk_idx, const void* topk_w, int
  * callers that never read them.  No workspace.
  */
 #define LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS 0x1
+/* lmoe_dispatch_local_rows only: write every output but sorted_tokens (x and
+ * sorted_tokens may be null), for callers whose expert GEMM gathers the token
+ * rows itself (lmoe_ragged_dot_mxfp4_rows); the counting-sort path at every size. */
+#define LMOE_DISPATCH_FLAG_NO_ROWS 0x2
 int lmoe_dispatch_local_small(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
                               int x_dtype, int64_t x_ld, int64_t T, int64_t k, int64_t lat,
                               int64_t local_start, int64_t L, int64_t m_padded, uint16_t* sorted_tokens,

@@ -341,8 +341,11 @@ __global__ __launch_bounds__(64) void scan_bins_kernel(int32_t* __restrict__ his
 // bin totals (hist[b * chunks]) into bin offsets with a block-wide exclusive
 // scan, so a chunk's start in bin b is offset[b] + rel[b * chunks + c].
 // Block 0 also writes bin_kept[b] (positions below limit) and *num_kept, the
-// outputs of the one-block scan.  Runs for n == 0 too (one chunk).  LDS
-// 20 * nbins bytes.
+// outputs of the one-block scan.  Every block knows the kept total, so the
+// sink may also write per-position outputs here: sink.bin_kept(b, kept) runs
+// in block 0 for every bin, sink.positions(num_kept, block, blocks) in every
+// block (no-ops for sinks without such outputs).  Runs for n == 0 too (one
+// chunk).  LDS 20 * nbins bytes.
 template <int CHUNK, class KeyFn, class Sink>
 __global__ __launch_bounds__(256) void place_scanned_kernel(KeyFn key, int64_t n, int nbins, int key_bits,
                                                             int64_t chunks, const int32_t* __restrict__ totals,
@@ -390,11 +393,13 @@ __global__ __launch_bounds__(256) void place_scanned_kernel(KeyFn key, int64_t n
       int64_t kept = limit - static_cast<int64_t>(run);
       kept = kept < 0 ? 0 : (kept > t ? t : kept);
       bin_kept[b] = static_cast<int32_t>(kept);
+      sink.bin_kept(b, static_cast<int32_t>(kept));
     }
     run += t;
   }
-  if (blockIdx.x == 0 && threadIdx.x == 0)
-    *num_kept = static_cast<int32_t>(static_cast<int64_t>(grand) < limit ? static_cast<int64_t>(grand) : limit);
+  const int64_t total_kept = static_cast<int64_t>(grand) < limit ? static_cast<int64_t>(grand) : limit;
+  if (blockIdx.x == 0 && threadIdx.x == 0) *num_kept = static_cast<int32_t>(total_kept);
+  sink.positions(total_kept, blockIdx.x, gridDim.x);
   __syncthreads();
   const uint64_t below = (1ull << lane) - 1ull;
   int32_t* mine = off + wave * nbins;
@@ -465,10 +470,14 @@ inline void launch_place(KeyFn key, int64_t n, int nbins, int64_t chunks, const 
 // place_scanned_kernel; else the one-block scan and the place kernels.  base
 // (nbins * chunks ints) receives the scanned chunk starts; hist is
 // overwritten.
+// scan_and_place takes scan_bins_kernel + place_scanned_kernel (whose sink
+// hooks run) for this many bins
+inline bool scanned_place(int nbins) { return static_cast<int64_t>(nbins) * 20 <= 65536 - 256; }
+
 template <int CHUNK, class KeyFn, class Sink>
 inline hipError_t scan_and_place(KeyFn key, int64_t n, int nbins, int64_t chunks, int64_t limit, int32_t* hist,
                                  int32_t* base, int32_t* bin_kept, int32_t* num_kept, Sink sink, hipStream_t st) {
-  if (static_cast<int64_t>(nbins) * 20 <= 65536 - 256) {
+  if (scanned_place(nbins)) {
     scan_bins_kernel<<<dim3(static_cast<unsigned>(nbins)), 64, 0, st>>>(hist, chunks, base);
     place_scanned_kernel<CHUNK><<<dim3(static_cast<unsigned>(chunks)), 256, nbins * 20, st>>>(
         key, n, nbins, key_bits_for(nbins), chunks, hist, base, limit, bin_kept, num_kept, sink);

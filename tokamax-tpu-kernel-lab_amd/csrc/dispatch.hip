@@ -33,7 +33,32 @@ struct DispatchSink {
   int32_t* tok_out;
   uint8_t* w_out;
   int32_t* slot_pos;
-  int64_t limit;
+  int64_t limit;  // m_padded
+  // metadata written by the place kernel (LMOE_DISPATCH_FLAG_NO_ROWS, no
+  // gather launch after it): valid, the padding rows' token (-1) and weight
+  // (0), per_expert_counts and the padding bucket's size group_sizes[L]
+  uint8_t* valid = nullptr;
+  int32_t* per_expert = nullptr;
+  int32_t* pad_group = nullptr;
+  __device__ __forceinline__ void bin_kept(int b, int32_t kept) const {
+    if (per_expert) per_expert[b] = kept;
+  }
+  __device__ __forceinline__ void positions(int64_t nk, int block, int blocks) const {
+    if (!valid) return;
+    if (block == 0 && threadIdx.x == 0) *pad_group = static_cast<int32_t>(limit - nk);
+    const int64_t per = (limit + blocks - 1) / blocks;
+    const int64_t p0 = static_cast<int64_t>(block) * per, p1 = p0 + per < limit ? p0 + per : limit;
+    for (int64_t p = p0 + threadIdx.x; p < p1; p += blockDim.x) {
+      valid[p] = p < nk ? 1 : 0;
+      if (p >= nk) {
+        tok_out[p] = -1;
+        if (wsize == 4)
+          reinterpret_cast<uint32_t*>(w_out)[p] = 0u;
+        else
+          reinterpret_cast<uint16_t*>(w_out)[p] = 0;
+      }
+    }
+  }
   // the slot's combine weight bits, read before the ranks are known
   __device__ __forceinline__ uint32_t load(int64_t s) const {
     return wsize == 4 ? reinterpret_cast<const uint32_t*>(w)[s] : reinterpret_cast<const uint16_t*>(w)[s];
@@ -132,6 +157,31 @@ __global__ __launch_bounds__(256) void gather_rows_kernel(
       }
     }
     reinterpret_cast<uint4*>(out + p * lat)[v] = o;
+  }
+}
+
+// The gather's metadata without the rows (LMOE_DISPATCH_FLAG_NO_ROWS): a
+// small grid striding over the rows, since there is no row data to spread.
+__global__ __launch_bounds__(256) void dispatch_meta_kernel(const int32_t* __restrict__ num_kept_p, int64_t m_padded,
+                                                            uint8_t* __restrict__ valid, int32_t* __restrict__ tok,
+                                                            uint8_t* __restrict__ w_out, int wsize,
+                                                            int32_t* __restrict__ group_sizes,
+                                                            int32_t* __restrict__ per_expert, int L) {
+  const int nk = *num_kept_p;
+  if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < L; i += blockDim.x) per_expert[i] = group_sizes[i];
+    if (threadIdx.x == 0) group_sizes[L] = static_cast<int32_t>(m_padded - nk);
+  }
+  for (int64_t p = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; p < m_padded;
+       p += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    valid[p] = p < nk ? 1 : 0;
+    if (p >= nk) {
+      tok[p] = -1;
+      if (wsize == 4)
+        reinterpret_cast<uint32_t*>(w_out)[p] = 0;
+      else
+        reinterpret_cast<uint16_t*>(w_out)[p] = 0;
+    }
   }
 }
 
@@ -284,24 +334,26 @@ extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* top
   LMOE_CHECK_ARG(T >= 0 && k > 0 && lat > 0 && L > 0 && m_padded >= 0 && local_start >= 0 && x_ld >= lat,
                  "%s: bad sizes", name);
   LMOE_CHECK_ARG(valid_dtype(w_dtype) && valid_dtype(x_dtype), "%s: bad dtype", name);
-  LMOE_CHECK_ARG((flags & ~LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS) == 0, "%s: unknown flags 0x%x", name, flags);
+  LMOE_CHECK_ARG((flags & ~(LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS | LMOE_DISPATCH_FLAG_NO_ROWS)) == 0,
+                 "%s: unknown flags 0x%x", name, flags);
+  const bool no_rows = (flags & LMOE_DISPATCH_FLAG_NO_ROWS) != 0;
   // decode-sized batches: one launch
-  if (T * k <= 8192 && m_padded <= 8192 && L + 1 <= 1024)
+  if (!no_rows && T * k <= 8192 && m_padded <= 8192 && L + 1 <= 1024)
     return lmoe_dispatch_local_small(topk_idx, topk_w, w_dtype, x, x_dtype, x_ld, T, k, lat, local_start, L,
                                      m_padded, sorted_tokens, group_sizes, valid, per_expert_counts,
                                      padded_token_idx, padded_w, slot_pos, flags, stream);
   LMOE_CHECK_SUPPORTED(T * k < (1ll << 31) && m_padded < (1ll << 31) && L < (1 << 20),
                        "%s: sizes exceed int32 indexing", name);
   LMOE_CHECK_SUPPORTED(L + 1 <= 12288, "%s: L=%lld exceeds the LDS histogram", name, (long long)L);
-  LMOE_CHECK_SUPPORTED(lat % 8 == 0 && x_ld % (x_dtype == LMOE_F32 ? 4 : 8) == 0 && aligned(x, 16) &&
-                           aligned(sorted_tokens, 16),
+  LMOE_CHECK_SUPPORTED(no_rows || (lat % 8 == 0 && x_ld % (x_dtype == LMOE_F32 ? 4 : 8) == 0 && aligned(x, 16) &&
+                                    aligned(sorted_tokens, 16)),
                        "%s: lat %% 8 == 0 and 16-byte aligned rows", name);
   const int64_t need = workspace_bytes(T * k, L);
   if (!workspace || workspace_size < need)
     return fail(LMOE_ERR_WORKSPACE, "%s: workspace %lld bytes < %lld", name, (long long)workspace_size,
                 (long long)need);
   LMOE_CHECK_ARG(group_sizes && valid && per_expert_counts && padded_token_idx && padded_w && topk_idx && topk_w &&
-                     (sorted_tokens || m_padded == 0),
+                     (no_rows || sorted_tokens || m_padded == 0),
                  "%s: null output", name);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t n = T * k;
@@ -313,13 +365,30 @@ extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* top
   csort::hist_kernel<kDispatchChunk><<<dim3(static_cast<unsigned>(chunks)), 256, (L + 1) * sizeof(int32_t), st>>>(
       key, n, Li, chunks, w.hist);
   LMOE_CHECK_LAUNCH("dispatch_hist");
+  // without rows the place kernel also writes the metadata when it is the
+  // scanned one (few bins): no launch after it
+  const bool meta_in_place = no_rows && csort::scanned_place(Li);
   {
     DispatchSink sink{static_cast<int>(k), static_cast<const uint8_t*>(topk_w), dtype_size(w_dtype),
                       padded_token_idx, static_cast<uint8_t*>(padded_w), slot_pos, m_padded};
+    if (meta_in_place) {
+      sink.valid = valid;
+      sink.per_expert = per_expert_counts;
+      sink.pad_group = group_sizes + L;
+    }
     if (csort::scan_and_place<kDispatchChunk>(key, n, Li, chunks, m_padded, w.hist, w.base, group_sizes,
                                               w.num_kept, sink, st) != hipSuccess)
       return fail(LMOE_ERR_HIP, "dispatch_scan: LDS attribute");
     LMOE_CHECK_LAUNCH("dispatch_scan_place");
+  }
+  if (meta_in_place) return LMOE_OK;
+  if (no_rows) {
+    const int64_t mb = ceil_div(m_padded > 0 ? m_padded : 1, 1024);
+    dispatch_meta_kernel<<<static_cast<unsigned>(mb < 64 ? mb : 64), 256, 0, st>>>(
+        w.num_kept, m_padded, valid, padded_token_idx, static_cast<uint8_t*>(padded_w), dtype_size(w_dtype),
+        group_sizes, per_expert_counts, Li);
+    LMOE_CHECK_LAUNCH("dispatch_meta");
+    return LMOE_OK;
   }
   const unsigned blocks = static_cast<unsigned>(m_padded > 0 ? ceil_div(m_padded, kGatherRows) : 1);
   const int skip = (flags & LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS) != 0;

@@ -159,6 +159,37 @@ extern "C" int lmoe_ragged_dot_mxfp4(const void* lhs, const uint8_t* w_packed, c
   return fail(LMOE_ERR_INVALID, "%s: bad mode %d", name, mode);
 }
 
+extern "C" int lmoe_ragged_dot_mxfp4_rows(const void* lhs, int64_t lhs_rows, const int32_t* row_index,
+                                          const uint8_t* w_packed, const uint8_t* w_scale,
+                                          const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
+                                          int zero_group, int mode, int epilogue, float beta, float beta_lin,
+                                          void* out, void* stream) {
+  const char* name = "ragged_dot_mxfp4_rows";
+  const int skip_zero_rows = (mode & LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS) != 0;
+  mode &= ~LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS;
+  int rc = check_common(lhs, w_packed, group_sizes, M, K, N, G, zero_group, out, name);
+  if (rc) return rc;
+  LMOE_CHECK_ARG(w_scale || M == 0, "%s: null scale", name);
+  LMOE_CHECK_ARG(row_index || M == 0, "%s: null row index", name);
+  LMOE_CHECK_ARG(lhs_rows > 0 || M == 0, "%s: lhs_rows=%lld", name, (long long)lhs_rows);
+  LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
+  LMOE_CHECK_SUPPORTED(mode == LMOE_MXFP4_LDS_DEQUANT_TILED, "%s: tiled weights only (mode %d)", name, mode);
+  LMOE_CHECK_SUPPORTED(K % 64 == 0, "%s: needs K %% 64 == 0 (K=%lld)", name, (long long)K);
+  LMOE_CHECK_SUPPORTED(N % (epilogue == LMOE_EPI_SITU ? 16 : 8) == 0, "%s: N=%lld", name, (long long)N);
+  LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(w_packed, 16) && aligned(w_scale, 16), "%s: 16-byte alignment",
+                       name);
+  // per-lane DMA offsets are 32-bit: any row of lhs
+  LMOE_CHECK_SUPPORTED(lhs_rows * K * 2 < (1ll << 32) && lhs_rows <= 65536, "%s: lhs too large (%lld rows)", name,
+                       (long long)lhs_rows);
+  if (M == 0) return LMOE_OK;
+  Params p{static_cast<const uint16_t*>(lhs), w_packed, w_scale, group_sizes, M, K, N, G, zero_group,
+           out, LMOE_BF16, beta, beta_lin, 1};
+  p.skip_zero_rows = skip_zero_rows;
+  p.a_index = row_index;
+  p.a_rows = lhs_rows;
+  return run_dma(p, kMXFP4, epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone, static_cast<hipStream_t>(stream), name);
+}
+
 extern "C" int lmoe_ragged_dot_mxfp4_splitk(const void* lhs, const uint8_t* w_packed, const uint8_t* w_scale,
                                             const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
                                             int zero_group, int64_t k_split, float* workspace,

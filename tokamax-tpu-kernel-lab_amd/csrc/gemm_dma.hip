@@ -664,6 +664,11 @@ struct SCfg {
   static_assert(kStageRows >= MF && BM % kStageRows == 0, "staging rounds");
   static_assert(kStageRows * kChunks % C::kThreads == 0, "staged store split");
   static_assert((NS - 2) * C::kOps0 + kRounds * kStoresPerRound < 64, "vmcnt range");
+  // gathered rows: the lhs row (< 65536) of every row of the block's tiles,
+  // loaded into LDS once at the start (at most kIdxTiles tiles per block);
+  // small enough to keep three blocks per CU
+  static constexpr int kIdxTiles = 8;
+  static constexpr int kIdxBytes = kIdxTiles * BM * 2;
 };
 
 // s_waitcnt vmcnt(a * OPS + r * SPR) lgkmcnt(0) for runtime a in [0, NS-2]
@@ -708,6 +713,7 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
   // held across the K loop)
   // m-tiles before a trailing zero group (the padding bucket): the real work
   const int64_t tm_work = p.zero_group == G - 1 ? static_cast<int64_t>(tt[G - 1]) : tm;
+  uint16_t* s_idx = reinterpret_cast<uint16_t*>(tr + (G + 1));  // gathered rows: kIdxTiles x BM
   auto sched = [&](int64_t vb, int64_t& nt, int lane) __attribute__((always_inline)) {
     TileInfo t = schedule_tile_with(n_tiles, gm, vb, tm, nt, [&](int64_t mt) {
       return locate_tile_lds<BM>(tt, tr, G, p.M, p.zero_group, mt, lane);
@@ -731,14 +737,15 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
     uint32_t b_off[C::kBOps];
     uint32_t s_off;
   };
-  auto make_addr = [&](const TileInfo& t, int64_t nt, int tid) __attribute__((always_inline)) {
+  auto make_addr = [&](const TileInfo& t, int64_t nt, int tid, int ordinal) __attribute__((always_inline)) {
     Addr d;
-    d.a_base = uniform_ptr(p.lhs + t.row0 * K);
+    const bool gathered = p.a_index != nullptr;
+    d.a_base = uniform_ptr(gathered ? p.lhs : p.lhs + t.row0 * K);
 #pragma unroll
     for (int v = 0; v < C::kAOps; ++v) {
       const int q = tid + C::kThreads * v;
       const int row = q / 8, kc = (q % 8) ^ swz8(row);
-      const int rr = row < t.rows ? row : 0;
+      const int rr = gathered ? static_cast<int>(s_idx[ordinal * BM + row]) : (row < t.rows ? row : 0);
       d.a_off[v] = static_cast<uint32_t>(rr * K * 2 + kc * 16);
     }
     d.b_base = uniform_ptr(static_cast<const uint8_t*>(p.rhs) + t.group * N * (K / 2));
@@ -763,8 +770,28 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
     return d;
   };
 
+  if (p.a_index != nullptr) {
+    // Gathered rows: wave w looks up the block's tiles w, w + kWaves, ... and
+    // stores the lhs row of each tile row (rows past the tile's valid rows
+    // repeat its first row; indices clamped into [0, a_rows)).  Done before
+    // any DMA is issued, so the loads' waits hold up nothing.
+    const int wave = static_cast<int>(threadIdx.x) / 64, lane = static_cast<int>(threadIdx.x) % 64;
+    const int64_t n_my = blockIdx.x < n_virtual ? (n_virtual - blockIdx.x + gridDim.x - 1) / gridDim.x : 0;
+    for (int64_t i = wave; i < n_my && i < S::kIdxTiles; i += C::kWaves) {
+      int64_t nti = 0;
+      const TileInfo ti = sched(blockIdx.x + i * gridDim.x, nti, lane);
+      if (ti.group < 0 || ti.zero) continue;
+      for (int r = lane; r < BM; r += 64) {
+        int32_t src = p.a_index[ti.row0 + (r < ti.rows ? r : 0)];
+        src = src < 0 ? 0 : (src >= p.a_rows ? static_cast<int32_t>(p.a_rows - 1) : src);
+        s_idx[i * BM + r] = static_cast<uint16_t>(src);
+      }
+    }
+    __syncthreads();
+  }
   int64_t vb = blockIdx.x;
   int64_t nt = 0;
+  int ord = 0;  // ordinal of cur among this block's virtual tiles
   TileInfo cur = vb < n_virtual ? sched(vb, nt, static_cast<int>(threadIdx.x % 64)) : TileInfo{-1, 0, 0, false};
   bool cur_pf = false;  // cur's first NS-1 steps were issued during the previous tile
   int prev_rounds = 0;  // store rounds of the previous tile's epilogue
@@ -799,7 +826,7 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
     if (cur.group < 0) {
       // no work (virtual tiles past the last m-tile)
     } else if (!cur.zero) {
-      const Addr ca = make_addr(cur, nt, tid);
+      const Addr ca = make_addr(cur, nt, tid, ord);
       const uint32_t lds_wave = __builtin_amdgcn_readfirstlane(lds_offset(smem) + wave * 64 * 16);
       auto issue = [&](const Addr& d, int64_t step, int slot) __attribute__((always_inline)) {
         const uint32_t base = lds_wave + slot * C::kSlot;
@@ -979,7 +1006,7 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
           if (s < nk32)
             issue(ca, s, wslot);
           else if (pf)
-            issue(make_addr(nxt, nt_n, tid), s - nk32, wslot);
+            issue(make_addr(nxt, nt_n, tid, ord + 1), s - nk32, wslot);
           Frags f;
           read_frags(slot, f);
           compute(f, full_tag);
@@ -1061,6 +1088,7 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
     cur = nxt;
     nt = nt_n;
     vb = vb_n;
+    ++ord;
     cur_pf = pf;
     prev_rounds = rounds;
   }
@@ -1184,7 +1212,7 @@ int try_stream(const Params& p, hipStream_t st, const char* name, int* rc) {
   if (!stream_enabled() || p.G < 1 || p.M == 0) return 0;
   if (EPI != kEpiSitu && p.out_dtype != LMOE_BF16) return 0;
   const int64_t ring = static_cast<int64_t>(NS) * C::kSlot;
-  const int64_t lds = ring + ((8 * (p.G + 1) + 15) / 16) * 16;
+  const int64_t lds = ring + ((8 * (p.G + 1) + 15) / 16) * 16 + (p.a_index ? S::kIdxBytes : 0);
   const int64_t per_cu = 163840 / (lds + 64);
   if (per_cu < 1 || per_cu < C::kLdsBlocks) return 0;
   const int64_t out_cols = EPI == kEpiSitu ? p.N / 2 : p.N;
@@ -1229,6 +1257,11 @@ int try_stream(const Params& p, hipStream_t st, const char* name, int* rc) {
   }
   const int64_t resident = kXcds * ((static_cast<int64_t>(cu_count()) * C::kLdsBlocks) / kXcds);
   const int64_t grid = resident >= kXcds && resident < blocks ? resident : blocks;
+  if (p.a_index && ceil_div(blocks, grid) > S::kIdxTiles) {
+    *rc = fail(LMOE_ERR_UNSUPPORTED, "%s: gathered rows need <= %d tiles per block (%lld)", name, S::kIdxTiles,
+               (long long)ceil_div(blocks, grid));
+    return 1;
+  }
   grouped_gemm_stream_kernel<BM, BN, EPI, NS, MF>
       <<<dim3(static_cast<unsigned>(grid)), C::kThreads, static_cast<size_t>(lds), st>>>(p, ntiles, gm, blocks);
   const hipError_t e = hipGetLastError();
@@ -1293,6 +1326,13 @@ int run_mx_shape(const Params& p, hipStream_t st, const char* name) {
   // 3 for the fused gate/up and 4 for the down projection.
   int v = mx_variant();
   int rc = LMOE_OK;
+  if (p.a_index) {
+    // gathered rows: the streamed kernel only
+    if constexpr (MF == 32) {
+      if (try_stream<64, 256, EPI, 3, MF>(p, st, name, &rc)) return rc;
+    }
+    return fail(LMOE_ERR_UNSUPPORTED, "%s: gathered rows need the streamed 64x256 kernel", name);
+  }
   if ((v < 0 || v == 3) && try_stream<64, 256, EPI, 3, MF>(p, st, name, &rc)) return rc;
   if (v == 2 && try_stream<64, 256, EPI, 4, MF>(p, st, name, &rc)) return rc;
   if (v < 0) v = EPI == kEpiSitu ? 3 : 2;

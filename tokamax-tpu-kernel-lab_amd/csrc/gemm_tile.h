@@ -58,6 +58,10 @@ struct Params {
   // plane r of out, split_stride elements apart
   int64_t k_split = 1;
   int64_t split_stride = 0;
+  // gathered rows (streamed MXFP4 kernel only): row r of the grouped problem
+  // is row a_index[r] of lhs, an (a_rows, K) array; nullptr: row r of lhs
+  const int32_t* a_index = nullptr;
+  int64_t a_rows = 0;
 };
 
 struct TileInfo {

@@ -78,11 +78,18 @@ __device__ __forceinline__ uint32_t wave_kth_largest(uint32_t x, int k) {
   return prefix;
 }
 
-template <int EPL>
+// CAST: the same wave also rounds the token's projection row xsrc[t, :lat]
+// (f32, row stride xld) to bf16 into xout[t, :] (lat <= kCastCols, lat % 4
+// == 0): its loads go out with the logits loads and its stores come last, so
+// the latency-bound selection hides them.
+constexpr int kCastCols = 4 * 4 * kWave;
+
+template <int EPL, bool CAST>
 __global__ __launch_bounds__(256) void router_topk_kernel(
     const float* __restrict__ logits, int64_t ld, const float* __restrict__ bias, int T, int E, int k, int act,
     int renorm, float scale, int wdtype, int32_t* __restrict__ idx_out, void* __restrict__ w_out,
-    float* __restrict__ scores_out) {
+    float* __restrict__ scores_out, const float* __restrict__ xsrc, int64_t xld, int lat,
+    uint16_t* __restrict__ xout) {
   const int lane = threadIdx.x % kWave;
   const int t = blockIdx.x * kWavesPerBlock + threadIdx.x / kWave;
   if (t >= T) return;
@@ -95,6 +102,30 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     const int e = c * kWave + lane;
     s[c] = e < E ? row[e] : -INFINITY;
   }
+  float4 xv[CAST ? 4 : 1];
+  if constexpr (CAST) {
+    const float* xr = xsrc + static_cast<int64_t>(t) * xld;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int col = c * 4 * kWave + 4 * lane;
+      if (col < lat) xv[c] = *reinterpret_cast<const float4*>(xr + col);
+    }
+  }
+  auto emit_x = [&]() __attribute__((always_inline)) {
+    if constexpr (CAST) {
+      typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
+      uint16_t* xo = xout + static_cast<int64_t>(t) * lat;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int col = c * 4 * kWave + 4 * lane;
+        if (col < lat) {
+          const bf16x2_v a = {static_cast<__bf16>(xv[c].x), static_cast<__bf16>(xv[c].y)};
+          const bf16x2_v b = {static_cast<__bf16>(xv[c].z), static_cast<__bf16>(xv[c].w)};
+          *reinterpret_cast<uint2*>(xo + col) = uint2{__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b)};
+        }
+      }
+    }
+  };
   if (act == LMOE_ACT_SIGMOID && scores_out == nullptr && k <= kWave) {
     __shared__ float s_logit[kWavesPerBlock][kWave];
     __shared__ int32_t s_expert[kWavesPerBlock][kWave];
@@ -180,6 +211,7 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
         idx_out[o] = static_cast<int32_t>(0xffffffffu - static_cast<uint32_t>(ck));
         store_from_f32(w_out, o, w, wdtype);
       }
+      emit_x();
       return;
     }
   }
@@ -264,22 +296,29 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     idx_out[o] = my_idx;
     store_from_f32(w_out, o, w, wdtype);
   }
+  emit_x();
 }
 
 template <int EPL>
 void launch_router(const float* logits, int64_t ld, const float* bias, int T, int E, int k, int act, int renorm,
-                   float scale, int wdtype, int32_t* idx, void* w, float* scores, hipStream_t st) {
+                   float scale, int wdtype, int32_t* idx, void* w, float* scores, hipStream_t st,
+                   const float* xsrc = nullptr, int64_t xld = 0, int lat = 0, uint16_t* xout = nullptr) {
   dim3 grid(static_cast<unsigned>(ceil_div(T, kWavesPerBlock)));
-  router_topk_kernel<EPL><<<grid, 256, 0, st>>>(logits, ld, bias, T, E, k, act, renorm, scale, wdtype,
-                                                 idx, w, scores);
+  if (xout)
+    router_topk_kernel<EPL, true><<<grid, 256, 0, st>>>(logits, ld, bias, T, E, k, act, renorm, scale, wdtype,
+                                                         idx, w, scores, xsrc, xld, lat, xout);
+  else
+    router_topk_kernel<EPL, false><<<grid, 256, 0, st>>>(logits, ld, bias, T, E, k, act, renorm, scale, wdtype,
+                                                          idx, w, scores, nullptr, 0, 0, nullptr);
 }
 
 }  // namespace
 }  // namespace lmoe
 
-extern "C" int lmoe_router_topk_ld(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E,
-                                   int64_t k, int act, int renorm, float scale, int weight_dtype,
-                                   int32_t* topk_idx, void* topk_w, float* scores_out, void* stream) {
+namespace {
+int router_impl(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E, int64_t k, int act,
+                int renorm, float scale, int weight_dtype, int32_t* topk_idx, void* topk_w, float* scores_out,
+                const float* x_src, int64_t x_ld, int64_t lat, uint16_t* x_out, void* stream) {
   using namespace lmoe;
   LMOE_CHECK_ARG(T >= 0 && E > 0 && k > 0, "router_topk: bad sizes T=%lld E=%lld k=%lld",
                  (long long)T, (long long)E, (long long)k);
@@ -298,7 +337,7 @@ extern "C" int lmoe_router_topk_ld(const float* logits, int64_t ld, const float*
 #define LMOE_ROUTER_CASE(N)                                                                   \
   if (epl <= N) {                                                                             \
     launch_router<N>(logits, ld, bias, Ti, Ei, ki, act, renorm, scale, weight_dtype, topk_idx, \
-                     topk_w, scores_out, st);                                                 \
+                     topk_w, scores_out, st, x_src, x_ld, static_cast<int>(lat), x_out);      \
     LMOE_CHECK_LAUNCH("router_topk");                                                         \
     return LMOE_OK;                                                                           \
   }
@@ -311,6 +350,29 @@ extern "C" int lmoe_router_topk_ld(const float* logits, int64_t ld, const float*
   LMOE_ROUTER_CASE(64)
 #undef LMOE_ROUTER_CASE
   return fail(LMOE_ERR_UNSUPPORTED, "router_topk: E=%lld", (long long)E);
+}
+}  // namespace
+
+extern "C" int lmoe_router_topk_ld(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E,
+                                   int64_t k, int act, int renorm, float scale, int weight_dtype,
+                                   int32_t* topk_idx, void* topk_w, float* scores_out, void* stream) {
+  return router_impl(logits, ld, bias, T, E, k, act, renorm, scale, weight_dtype, topk_idx, topk_w, scores_out,
+                     nullptr, 0, 0, nullptr, stream);
+}
+
+extern "C" int lmoe_router_topk_proj(const float* logits, int64_t ld, const float* bias, int64_t T, int64_t E,
+                                     int64_t k, int act, int renorm, float scale, int weight_dtype,
+                                     int32_t* topk_idx, void* topk_w, const float* x_src, int64_t x_ld,
+                                     int64_t lat, uint16_t* x_out, void* stream) {
+  using namespace lmoe;
+  LMOE_CHECK_ARG(lat > 0 && x_ld >= lat, "router_topk_proj: bad latent sizes lat=%lld x_ld=%lld", (long long)lat,
+                 (long long)x_ld);
+  LMOE_CHECK_SUPPORTED(lat <= kCastCols && lat % 4 == 0 && x_ld % 4 == 0,
+                       "router_topk_proj: lat=%lld (<= %d, lat %% 4 == 0)", (long long)lat, kCastCols);
+  LMOE_CHECK_ARG(T == 0 || (x_src && x_out), "router_topk_proj: null pointer");
+  LMOE_CHECK_SUPPORTED(aligned(x_src, 16) && aligned(x_out, 8), "router_topk_proj: x_src 16-, x_out 8-byte aligned");
+  return router_impl(logits, ld, bias, T, E, k, act, renorm, scale, weight_dtype, topk_idx, topk_w, nullptr, x_src,
+                     x_ld, lat, x_out, stream);
 }
 
 extern "C" int lmoe_router_topk(const float* logits, const float* bias, int64_t T, int64_t E, int64_t k, int act,

@@ -35,6 +35,7 @@ MXFP4_SCALED_MFMA = 1
 MXFP4_LDS_DEQUANT_TILED = 2
 MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS = 0x100
 DISPATCH_FLAG_SKIP_PADDING_ROWS = 0x1
+DISPATCH_FLAG_NO_ROWS = 0x2
 COMBINE_SCATTER_ADD = 0
 COMBINE_SLOT_SUM = 1
 
@@ -52,6 +53,7 @@ SIGNATURES = {
     "lmoe_ragged_dot_fp8_scaled": ([P, P, P, I64, P, I64, I64, I64, I64, I32, I32, F, F, P, P], I32),
     "lmoe_mxfp4_dequant": ([P, P, I64, I64, I64, I64, P, I32, P], I32),
     "lmoe_ragged_dot_mxfp4": ([P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, P, P], I32),
+    "lmoe_ragged_dot_mxfp4_rows": ([P, I64, P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, P, P], I32),
     "lmoe_ragged_dot_mxfp4_splitk": ([P, P, P, P, I64, I64, I64, I64, I32, I64, P, I64, I32, F, F, P, P], I32),
     "lmoe_ragged_dot_mxfp4_skinny": ([P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, I64, P, P], I32),
     "lmoe_mxfp4_tile": ([P, P, I64, I64, I64, P, P, P], I32),
@@ -62,6 +64,7 @@ SIGNATURES = {
     "lmoe_ragged_dot_mxfp8_mxfp4": ([P, P, P, P, P, I64, I64, I64, I64, I32, I32, F, F, P, I32, P], I32),
     "lmoe_router_topk": ([P, P, I64, I64, I64, I32, I32, F, I32, P, P, P, P], I32),
     "lmoe_router_topk_ld": ([P, I64, P, I64, I64, I64, I32, I32, F, I32, P, P, P, P], I32),
+    "lmoe_router_topk_proj": ([P, I64, P, I64, I64, I64, I32, I32, F, I32, P, P, P, I64, I64, P, P], I32),
     "lmoe_dispatch_workspace_size": ([I64, I64, I64], I64),
     "lmoe_dispatch_local": ([P, P, I32, P, I32, I64, I64, I64, I64, I64, I64, P, P, P, P, P, P, P, P,
                              I64, P], I32),

@@ -207,31 +207,57 @@ class LocalShardLatentMoE:
     decode = (self._decode_path(t) and hidden.dtype == torch.bfloat16
               and ops.small_dispatch_supported(t, c.top_k, c.latent_size, self.L, m_padded))
     x_src = None
-    if self.router_down_nk is not None and hidden.dtype == torch.bfloat16:
-      e = self.router_nk.shape[0]
-      rd = self._dense(hidden, self.router_down_nk, torch.float32)
-      logits = rd[:, :e]
-      # the dispatch rounds the f32 latent rows to bf16 as it gathers them:
-      # no separate cast (x itself is materialised only for the stages)
-      x_src = rd[:, e:]
-      x = ops.cast_rows(x_src, hidden.dtype) if return_stages else None
-    else:
-      logits = self._dense(hidden, self.router_nk, torch.float32)
-      x = self._dense(hidden, self.down_nk)
-    idx, w = ops.router_topk_from_logits(logits, self.bias, c.top_k, c.moe_renormalize,
-                                         c.routed_scaling_factor, self.act, hidden.dtype)
-    # padding rows of the sorted tokens are read by no later stage (the MXFP4
-    # expert GEMMs skip the padding bucket) unless the stages are returned
-    skip = self.expert_format == "mxfp4" and not return_stages
-    d = ops.dispatch_local(idx, w, x_src if x_src is not None else x, self.start, self.L, m_padded,
-                           path="small" if decode else "sort", skip_padding_rows=skip)
     E = self.experts
     mx_mode, mx_kw = self.mxfp4_mode, {}
     if self.expert_format == "mxfp4" and self._decode_path(t):
       mx_mode, mx_kw = "skinny", {"max_group_rows": t}
-    if "gateup" in ev:
-      ev["gateup"][0].record()
-    if self.expert_format == "mxfp4":
+    # Gathered rows (prefill, tiled MXFP4 experts, stages not returned): the
+    # router launch also rounds the latent projection to bf16 (T rows), the
+    # dispatch writes only its metadata, and the gate/up GEMM reads each
+    # sorted row straight from its token's row -- no sorted_tokens copy.
+    rows_path = (self.router_down_nk is not None and hidden.dtype == torch.bfloat16 and not return_stages
+                 and self.expert_format == "mxfp4" and self.weight_layout == "tiled" and mx_mode == "lds_dequant"
+                 and c.latent_size <= 1024 and c.latent_size % 4 == 0)
+    act = None
+    if rows_path:
+      e = self.router_nk.shape[0]
+      rd = self._dense(hidden, self.router_down_nk, torch.float32)
+      logits, x_src = rd[:, :e], rd[:, e:]
+      idx, w, x = ops.router_topk_project(logits, x_src, self.bias, c.top_k, c.moe_renormalize,
+                                          c.routed_scaling_factor, self.act, hidden.dtype)
+      d = ops.dispatch_local(idx, w, None, self.start, self.L, m_padded, gather_rows=False, lat=c.latent_size)
+      if "gateup" in ev:
+        ev["gateup"][0].record()
+      try:
+        act = ops.ragged_dot_mxfp4(x, E["gu_packed" + self._sfx], E["gu_scale" + self._sfx], d.group_sizes,
+                                   fuse_gateup_activation=f"situ:{b}:{bl}", mode=mx_mode, zero_group=self.L,
+                                   weight_layout=self.weight_layout, skip_zero_group_rows=True,
+                                   lhs_row_index=d.padded_token_idx)
+      except NotImplementedError:
+        # the streamed kernel does not take this size: gather the rows
+        d = ops.dispatch_local(idx, w, x, self.start, self.L, m_padded, path="sort", skip_padding_rows=True)
+    else:
+      if self.router_down_nk is not None and hidden.dtype == torch.bfloat16:
+        e = self.router_nk.shape[0]
+        rd = self._dense(hidden, self.router_down_nk, torch.float32)
+        logits = rd[:, :e]
+        # the dispatch rounds the f32 latent rows to bf16 as it gathers them:
+        # no separate cast (x itself is materialised only for the stages)
+        x_src = rd[:, e:]
+        x = ops.cast_rows(x_src, hidden.dtype) if return_stages else None
+      else:
+        logits = self._dense(hidden, self.router_nk, torch.float32)
+        x = self._dense(hidden, self.down_nk)
+      idx, w = ops.router_topk_from_logits(logits, self.bias, c.top_k, c.moe_renormalize,
+                                           c.routed_scaling_factor, self.act, hidden.dtype)
+      # padding rows of the sorted tokens are read by no later stage (the MXFP4
+      # expert GEMMs skip the padding bucket) unless the stages are returned
+      skip = self.expert_format == "mxfp4" and not return_stages
+      d = ops.dispatch_local(idx, w, x_src if x_src is not None else x, self.start, self.L, m_padded,
+                             path="small" if decode else "sort", skip_padding_rows=skip)
+      if "gateup" in ev:
+        ev["gateup"][0].record()
+    if act is None and self.expert_format == "mxfp4":
       # padding-bucket rows (zero_group L) are never read downstream: left
       # unwritten unless the stages are returned
       act = ops.ragged_dot_mxfp4(d.sorted_tokens, E["gu_packed" + self._sfx], E["gu_scale" + self._sfx],
@@ -239,7 +265,7 @@ class LocalShardLatentMoE:
                                  fuse_gateup_activation=f"situ:{b}:{bl}", mode=mx_mode,
                                  zero_group=self.L, weight_layout=self.weight_layout,
                                  skip_zero_group_rows=not return_stages, **mx_kw)
-    else:
+    elif act is None:
       act = ops.ragged_dot_gateup_situ(d.sorted_tokens, E["gu_nk"], d.group_sizes, b, bl,
                                        rhs_layout="gnk", zero_group=self.L)
     if "gateup" in ev:

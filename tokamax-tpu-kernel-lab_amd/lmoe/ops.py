@@ -429,7 +429,8 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
                      group_sizes: torch.Tensor, *, fuse_gateup_activation: str | None = None,
                      mode: str = "lds_dequant", zero_group: int = -1,
                      weight_layout: str = "checkpoint", skip_zero_group_rows: bool = False,
-                     max_group_rows: int = 0, k_split: int | None = None) -> torch.Tensor:
+                     max_group_rows: int = 0, k_split: int | None = None,
+                     lhs_row_index: torch.Tensor | None = None) -> torch.Tensor:
   """Grouped lhs @ deq(W_g)^T with W_g in checkpoint (N, K/2) layout
   (orientation of mxfp4_online_dequant_matmul_pallas.py:1-36) and block-32
   E8M0 scales (G, N, K/32), or with ``weight_layout="tiled"`` the
@@ -450,7 +451,19 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   for groups of a few rows -- each weight byte of a group with rows read once
   per pass of up to 16, 32, 64 or 128 rows, sized from min(M,
   ``max_group_rows``) (0: unknown).  Equal to the other modes within bf16
-  rounding (another f32 summation order), not bit for bit."""
+  rounding (another f32 summation order), not bit for bit.
+
+  ``lhs_row_index`` (int32 (M,), tiled weights, ``mode="lds_dequant"``):
+  the grouped lhs is gathered from ``lhs`` (rows, K) -- row r is
+  ``lhs[lhs_row_index[r]]`` -- inside the kernel, i.e.
+  ``ragged_dot(lhs[lhs_row_index], W, group_sizes)`` without the gathered copy
+  (the dispatch's padded_token_idx over the token rows).  Raises
+  NotImplementedError where the streamed kernel does not apply."""
+  if lhs_row_index is not None:
+    return _ragged_dot_mxfp4_rows(lhs, lhs_row_index, w_packed, w_scale, group_sizes,
+                                  fuse_gateup_activation=fuse_gateup_activation, mode=mode,
+                                  zero_group=zero_group, weight_layout=weight_layout,
+                                  skip_zero_group_rows=skip_zero_group_rows)
   _dev(lhs, w_packed, w_scale, group_sizes)
   if lhs.dtype != torch.bfloat16:
     raise NotImplementedError("MXFP4 GEMM takes bf16 activations")
@@ -525,6 +538,39 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   return out
 
 
+def _ragged_dot_mxfp4_rows(lhs, row_index, w_packed, w_scale, group_sizes, *, fuse_gateup_activation, mode,
+                           zero_group, weight_layout, skip_zero_group_rows):
+  _dev(lhs, row_index, w_packed, w_scale, group_sizes)
+  if lhs.dtype != torch.bfloat16 or lhs.dim() != 2 or not lhs.is_contiguous():
+    raise NotImplementedError("gathered rows: lhs must be a contiguous bf16 (rows, K) array")
+  if row_index.dtype != torch.int32 or row_index.dim() != 1:
+    raise ValueError("lhs_row_index must be int32 (M,)")
+  if w_packed.dtype != torch.uint8 or w_scale.dtype != torch.uint8:
+    raise ValueError(f"MXFP4 weights must be uint8 packed codes and E8M0 scale bytes, got "
+                     f"{w_packed.dtype} / {w_scale.dtype}")
+  if group_sizes.dtype != torch.int32:
+    raise ValueError("group_sizes must be int32")
+  if weight_layout != "tiled" or mode != "lds_dequant":
+    raise NotImplementedError("gathered rows: tiled weights on the lds_dequant streamed kernel only")
+  rows, k = lhs.shape
+  m = row_index.shape[0]
+  if w_packed.dim() != 4 or w_packed.shape[3] != 32:
+    raise ValueError(f"tiled packed weights must be (G, K/64, N, 32), got {tuple(w_packed.shape)}")
+  g, _, n, _ = w_packed.shape
+  if (tuple(w_packed.shape), tuple(w_scale.shape)) != ((g, k // 64, n, 32), (g, k // 64, n, 2)):
+    raise ValueError(f"mxfp4 shapes lhs {tuple(lhs.shape)} packed {tuple(w_packed.shape)} scale {tuple(w_scale.shape)}")
+  epi, b, bl, width = _lib.EPI_NONE, 0.0, 0.0, n
+  if fuse_gateup_activation is not None:
+    b, bl = parse_fused_activation(fuse_gateup_activation)
+    epi, width = _lib.EPI_SITU, n // 2
+  mode_id = _lib.MXFP4_LDS_DEQUANT_TILED | (_lib.MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS if skip_zero_group_rows else 0)
+  out = torch.empty((m, width), dtype=torch.bfloat16, device=lhs.device)
+  check(lib().lmoe_ragged_dot_mxfp4_rows(_p(lhs), rows, _p(row_index), _p(w_packed), _p(w_scale), _p(group_sizes),
+                                         m, k, n, g, zero_group, mode_id, epi, b, bl, _p(out), _stream()),
+        "ragged_dot_mxfp4_rows")
+  return out
+
+
 # ---------------------------------------------------------------------------
 # a3 / a4: router
 # ---------------------------------------------------------------------------
@@ -553,6 +599,34 @@ def router_topk_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top
                                   int(renormalize), scaling, _dt(w), _p(idx), _p(w), _p(scores), _stream()),
         "router_topk")
   return (idx, w, scores) if return_scores else (idx, w)
+
+
+def router_topk_project(logits: torch.Tensor, x: torch.Tensor, bias: torch.Tensor | None, top_k: int,
+                        renormalize: bool = True, scaling: float = 1.0, act: str = "sigmoid",
+                        weight_dtype: torch.dtype = torch.float32):
+  """router_and_projection's outputs (ref.py:634-655) from one GEMM that
+  computed the router logits and the latent projection together: the gate of
+  ``router_topk_from_logits`` on ``logits`` (T, E) f32 plus ``x`` (T, lat)
+  f32 rounded to bf16 (nearest even), in one launch.  Both may be row-strided
+  views (unit column stride).  Returns (topk_idx, topk_weight, x_bf16)."""
+  logits, x = _dev_rows(logits), _dev_rows(x)
+  _dev(bias)
+  if logits.dtype != torch.float32 or x.dtype != torch.float32:
+    raise ValueError("router logits and the projection must be float32 GEMM outputs")
+  if bias is not None and bias.dtype != torch.float32:
+    bias = bias.float().contiguous()
+  t, e = logits.shape
+  lat = x.shape[1]
+  if x.shape[0] != t:
+    raise ValueError(f"logits {tuple(logits.shape)} and x {tuple(x.shape)} differ in rows")
+  idx = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
+  w = torch.empty((t, top_k), dtype=weight_dtype, device=logits.device)
+  xb = torch.empty((t, lat), dtype=torch.bfloat16, device=logits.device)
+  check(lib().lmoe_router_topk_proj(_p(logits), max(logits.stride(0), e), _p(bias), t, e, top_k, _ACTS[act],
+                                    int(renormalize), scaling, _dt(w), _p(idx), _p(w), _p(x),
+                                    max(x.stride(0), lat), lat, _p(xb), _stream()),
+        "router_topk_proj")
+  return idx, w, xb
 
 
 def cast_rows(x: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -724,9 +798,29 @@ def small_dispatch_supported(t: int, k: int, lat: int, L: int, m_padded: int) ->
   return t * k <= SMALL_DISPATCH_SLOTS and m_padded <= 8192 and L + 1 <= 1024 and lat % 8 == 0
 
 
-def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.Tensor,
+def _dispatch_metadata(topk_idx, topk_weight, local_expert_start, L, m_padded, lat):
+  _dev(topk_idx, topk_weight)
+  if lat is None:
+    raise ValueError("dispatch without rows: give x or lat")
+  t, k = topk_idx.shape
+  dev = topk_idx.device
+  group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
+  valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
+  counts = torch.empty((L,), dtype=torch.int32, device=dev)
+  tok = torch.empty((m_padded,), dtype=torch.int32, device=dev)
+  w = torch.empty((m_padded,), dtype=topk_weight.dtype, device=dev)
+  slot_pos = torch.empty((t * k,), dtype=torch.int32, device=dev)
+  ws = _workspace(lib().lmoe_dispatch_workspace_size(t, k, L), dev)
+  check(lib().lmoe_dispatch_local_rows(_p(topk_idx), _p(topk_weight), _dt(topk_weight), None, _lib.BF16, lat, t, k,
+                                       lat, local_expert_start, L, m_padded, None, _p(group_sizes), _p(valid),
+                                       _p(counts), _p(tok), _p(w), _p(slot_pos), _lib.DISPATCH_FLAG_NO_ROWS, _p(ws),
+                                       ws.numel(), _stream()), "dispatch_local_rows")
+  return Dispatch(None, group_sizes, valid, counts, tok, w, slot_pos)
+
+
+def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.Tensor | None,
                    local_expert_start: int, local_num_experts: int, m_padded: int, *, path: str = "auto",
-                   skip_padding_rows: bool = False) -> Dispatch:
+                   skip_padding_rows: bool = False, gather_rows: bool = True, lat: int | None = None) -> Dispatch:
   """The GPU dispatch with an explicit m_padded; also returns slot_pos (T*k,).
 
   ``path``: "sort" (the multi-block counting sort + gather), "small" (one
@@ -735,10 +829,18 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
   bit.  A contiguous x keeps its dtype in sorted_tokens; a row-strided view
   (unit column stride) of bf16 or f32 values, or ``skip_padding_rows``, gives
   bf16 sorted tokens (f32 rounded to nearest even), and ``skip_padding_rows``
-  leaves their padding rows unwritten."""
+  leaves their padding rows unwritten.
+
+  ``gather_rows=False``: every output but the rows (``sorted_tokens`` is
+  None; ``x`` may be None, then ``lat`` gives the row width), for an expert
+  GEMM that gathers the token rows itself (``ragged_dot_mxfp4(...,
+  lhs_row_index=padded_token_idx)``); the counting-sort path at every size."""
   if topk_idx.dtype != torch.int32:
     raise ValueError("topk_idx must be int32")
   t, k = topk_idx.shape
+  if not gather_rows:
+    return _dispatch_metadata(topk_idx, topk_weight, local_expert_start, local_num_experts, m_padded,
+                              x.shape[-1] if x is not None else lat)
   lat = x.shape[-1]
   L = local_num_experts
   small_ok = small_dispatch_supported(t, k, lat, L, m_padded)
