@@ -262,6 +262,10 @@ def main():
       log(f"graph replay: {ms_per_step:.3f} ms/step")
   tokens_per_s = c.tokens / (ms_per_step / 1000.0)
 
+  # the timed forward (no stage outputs: gathered-row expert GEMM, no sorted
+  # copy) against the forward whose stages the parity check below reads
+  timed_equals_checked = bool(torch.equal(layer.forward(hidden), out_stages))
+  log(f"timed forward == checked forward, bit for bit: {timed_equals_checked}")
   achieved = nbytes / (gateup_ms / 1000.0) / 1e9
   tflops = flops / (gateup_ms / 1000.0) / 1e12
   # the HBM rate a plain 256 MiB device copy reaches on this GPU (read +
@@ -309,6 +313,7 @@ def main():
     cpu, own = cpu_baseline(inputs, c, args.cpu_sample_tokens, args.cpu_reps)
     log("parity of the benchmarked forward against the oracle")
     par = parity(inputs, c, out_stages, st, own if args.cpu_sample_tokens == c.tokens else None)
+    par["timed_forward_equals_checked_forward"] = timed_equals_checked
     log(f"parity: {par}")
 
   line = {
