@@ -346,7 +346,13 @@ __global__ __launch_bounds__(64) void scan_bins_kernel(int32_t* __restrict__ his
 // in block 0 for every bin, sink.positions(num_kept, block, blocks) in every
 // block (no-ops for sinks without such outputs).  Runs for n == 0 too (one
 // chunk).  LDS 20 * nbins bytes.
-template <int CHUNK, class KeyFn, class Sink>
+//
+// FROM_HIST (nbins <= 256): no scan_bins_kernel before it -- `totals` is the
+// raw histogram (hist[b * chunks + c]) and each block sums every bin's chunk
+// counts itself (the bin total and this chunk's start in the bin; 4 * chunks
+// bytes per bin, read from L2 after the histogram pass), one launch fewer.
+// LDS 24 * nbins bytes.
+template <int CHUNK, class KeyFn, class Sink, bool FROM_HIST = false>
 __global__ __launch_bounds__(256) void place_scanned_kernel(KeyFn key, int64_t n, int nbins, int key_bits,
                                                             int64_t chunks, const int32_t* __restrict__ totals,
                                                             const int32_t* __restrict__ rel, int64_t limit,
@@ -354,9 +360,10 @@ __global__ __launch_bounds__(256) void place_scanned_kernel(KeyFn key, int64_t n
                                                             int32_t* __restrict__ num_kept, Sink sink) {
   constexpr int kW = 4, IT = CHUNK / 64 / kW;
   static_assert(CHUNK % (64 * kW) == 0, "chunk split over the waves");
-  extern __shared__ int32_t off[];  // [kW][nbins], then the bin offsets [nbins]
+  extern __shared__ int32_t off[];  // [kW][nbins], the bin offsets [nbins], FROM_HIST: chunk starts [nbins]
   __shared__ uint32_t s_part[kW];
   int32_t* bin_off = off + kW * nbins;
+  int32_t* rel_s = bin_off + nbins;
   const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
   const int64_t wave_base = static_cast<int64_t>(blockIdx.x) * CHUNK + wave * (CHUNK / kW);
   int keys[IT];
@@ -368,12 +375,69 @@ __global__ __launch_bounds__(256) void place_scanned_kernel(KeyFn key, int64_t n
     keys[it] = s < n ? key(s) : nbins;
     loaded[it] = s < n ? sink.load(s) : 0u;
   }
+  if constexpr (FROM_HIST) {
+    // nbins <= 256: bin b's chunk counts are summed by the G adjacent lanes
+    // of group b (G the largest power of two <= 64 with G * nbins <= 256),
+    // each lane V counts per load with 8 loads in flight; the group's
+    // partials are added by lane shuffles.  Bin total -> bin_off[b], this
+    // chunk's start within the bin -> rel_s[b].
+    int G = 64;
+    while (G > 1 && G * nbins > 256) G >>= 1;
+    const int g = threadIdx.x / G, sub = threadIdx.x % G;
+    const int64_t me = blockIdx.x;
+    uint32_t tot = 0, pre = 0;
+    auto sum_row = [&](auto vtag) {
+      constexpr int V = decltype(vtag)::value;
+      const int32_t* h = totals + static_cast<int64_t>(g) * chunks;
+      const int64_t nq = chunks / V;
+      for (int64_t q0 = sub; q0 < nq; q0 += 8 * G) {
+        uint32_t v[8][V];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int64_t q = q0 + static_cast<int64_t>(j) * G;
+          if constexpr (V == 4) {
+            const int4 x = q < nq ? *reinterpret_cast<const int4*>(h + 4 * q) : make_int4(0, 0, 0, 0);
+            v[j][0] = static_cast<uint32_t>(x.x);
+            v[j][1] = static_cast<uint32_t>(x.y);
+            v[j][2] = static_cast<uint32_t>(x.z);
+            v[j][3] = static_cast<uint32_t>(x.w);
+          } else {
+            v[j][0] = q < nq ? static_cast<uint32_t>(h[q]) : 0u;
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+#pragma unroll
+          for (int e = 0; e < V; ++e) {
+            const int64_t c = (q0 + static_cast<int64_t>(j) * G) * V + e;
+            tot += v[j][e];
+            pre += c < me ? v[j][e] : 0u;
+          }
+      }
+    };
+    if (g < nbins) {
+      if (chunks % 4 == 0 && reinterpret_cast<uintptr_t>(totals) % 16 == 0)
+        sum_row(std::integral_constant<int, 4>{});
+      else
+        sum_row(std::integral_constant<int, 1>{});
+    }
+    for (int m = 1; m < G; m <<= 1) {
+      tot += __shfl_xor(tot, m);
+      pre += __shfl_xor(pre, m);
+    }
+    if (g < nbins && sub == 0) {
+      bin_off[g] = static_cast<int32_t>(tot);
+      rel_s[g] = static_cast<int32_t>(pre);
+    }
+    __syncthreads();
+  }
   // bin offsets: thread t owns the contiguous bins [t * per, (t + 1) * per)
   const int per = (nbins + 255) / 256;
   const int b0 = threadIdx.x * per, b1 = b0 + per < nbins ? b0 + per : nbins;
   uint32_t mine_sum = 0;
   for (int b = b0; b < b1; ++b) {
-    const uint32_t t = static_cast<uint32_t>(totals[static_cast<int64_t>(b) * chunks]);
+    const uint32_t t = FROM_HIST ? static_cast<uint32_t>(bin_off[b])
+                                 : static_cast<uint32_t>(totals[static_cast<int64_t>(b) * chunks]);
     bin_off[b] = static_cast<int32_t>(t);
     mine_sum += t;
   }
@@ -421,7 +485,7 @@ __global__ __launch_bounds__(256) void place_scanned_kernel(KeyFn key, int64_t n
   }
   __syncthreads();
   for (int b = threadIdx.x; b < nbins; b += 256) {
-    int32_t acc = bin_off[b] + rel[static_cast<int64_t>(b) * chunks + blockIdx.x];
+    int32_t acc = bin_off[b] + (FROM_HIST ? rel_s[b] : rel[static_cast<int64_t>(b) * chunks + blockIdx.x]);
 #pragma unroll
     for (int w = 0; w < kW; ++w) {
       const int32_t c = off[w * nbins + b];
@@ -478,6 +542,12 @@ template <int CHUNK, class KeyFn, class Sink>
 inline hipError_t scan_and_place(KeyFn key, int64_t n, int nbins, int64_t chunks, int64_t limit, int32_t* hist,
                                  int32_t* base, int32_t* bin_kept, int32_t* num_kept, Sink sink, hipStream_t st) {
   if (scanned_place(nbins)) {
+    if (chunks <= 256 && nbins <= 256) {
+      // few chunks: the place pass sums the histogram itself (no scan launch)
+      place_scanned_kernel<CHUNK, KeyFn, Sink, true><<<dim3(static_cast<unsigned>(chunks)), 256, nbins * 24, st>>>(
+          key, n, nbins, key_bits_for(nbins), chunks, hist, nullptr, limit, bin_kept, num_kept, sink);
+      return hipSuccess;
+    }
     scan_bins_kernel<<<dim3(static_cast<unsigned>(nbins)), 64, 0, st>>>(hist, chunks, base);
     place_scanned_kernel<CHUNK><<<dim3(static_cast<unsigned>(chunks)), 256, nbins * 20, st>>>(
         key, n, nbins, key_bits_for(nbins), chunks, hist, base, limit, bin_kept, num_kept, sink);
