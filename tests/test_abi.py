@@ -82,6 +82,6 @@ def test_ops_refuse_cpu_tensors():
 def test_default_split_choice():
   """The split-K heuristic: a split only for one group with few tiles."""
   from lmoe.ops import mxfp4_k_split
-  assert [mxfp4_k_split(m, 2048, 7168, 1) for m in (1, 128, 1024, 4096)] == [7, 7, 2, 1]
+  assert [mxfp4_k_split(m, 2048, 7168, 1) for m in (1, 128, 1024, 4096)] == [14, 8, 4, 1]
   assert mxfp4_k_split(8804, 4096, 1024, 113) == 1  # grouped: never
   assert mxfp4_k_split(64, 256, 256, 1) == 1        # too few K steps

@@ -319,6 +319,50 @@ def test_mxfp4_tiled_edge_scales(gpu_device):
     assert torch.equal(a[fin], x[fin])
 
 
+@pytest.mark.parametrize("situ,gather", [(False, False), (True, False), (False, True), (True, True)])
+def test_mxfp4_streamed_edge_scales_late_step(gpu_device, situ, gather):
+  """The streamed kernel converts with the hardware instruction inside the K
+  loop and lets a wave that met a scale byte outside 3..252 recompute its
+  tile exactly afterwards.  Edge bytes only in the last K steps of a few
+  columns (so some waves of a tile recompute and others do not, after their
+  accumulators already hold hardware-converted steps), in gate and up
+  columns, with and without gathered rows: bit-equal (NaN-aware) to the
+  checkpoint-scale kernel, which converts every block exactly."""
+  from lmoe import ops
+  rng = np.random.default_rng(11 + 2 * situ + gather)
+  m, k, n, g = 200, 512, 512, 3
+  gs = np.array([70, 1, 129], np.int32)
+  packed = rng.integers(0, 256, (g, n, k // 2), dtype=np.uint8)
+  scale = rng.integers(118, 130, (g, n, k // 32), dtype=np.uint8)
+  scale[0, 5, -1] = 0          # last step, one column of wave 0 (gate half with SiTU)
+  scale[0, 300, -2] = 254      # an up column with SiTU, a later wave's column without
+  scale[2, 130:134, -3] = 2    # a run of columns of the large group
+  scale[2, 480, -1] = 255
+  fa = "situ:4.0:25.0" if situ else None
+  tpk, tsc = ops.mxfp4_tile_weights(to_dev(packed), to_dev(scale))
+  gs_d = to_dev(gs)
+  if gather:
+    t = 90
+    tokens = O.bf16_round(rng.standard_normal((t, k)))
+    idx = rng.integers(0, t, m).astype(np.int32)
+    idx[int(gs.sum()):] = -1
+    lhs = tokens[np.maximum(idx, 0)]
+    a = ops.ragged_dot_mxfp4(to_dev(tokens, "bf16"), tpk, tsc, gs_d, fuse_gateup_activation=fa,
+                             weight_layout="tiled", skip_zero_group_rows=True, lhs_row_index=to_dev(idx))
+  else:
+    lhs = O.bf16_round(rng.standard_normal((m, k)))
+    a = ops.ragged_dot_mxfp4(to_dev(lhs, "bf16"), tpk, tsc, gs_d, fuse_gateup_activation=fa,
+                             weight_layout="tiled", k_split=1)
+  b = ops.ragged_dot_mxfp4(to_dev(lhs, "bf16"), to_dev(packed), to_dev(scale), gs_d, fuse_gateup_activation=fa)
+  rows = int(gs.sum())
+  a, b = a[:rows], b[:rows]
+  assert torch.equal(torch.isnan(a), torch.isnan(b))
+  fin = ~torch.isnan(a)
+  assert torch.equal(a[fin], b[fin])
+  # the edge columns really produced non-finite or denormal-scale outputs
+  assert bool(torch.isnan(a).any() or torch.isinf(a).any())
+
+
 def test_elementwise_rms_norm_and_situ(gpu_device):
   from lmoe import ops
   rng = np.random.default_rng(7)

@@ -1,6 +1,6 @@
 """Split-K MXFP4 grouped GEMM (lmoe_ragged_dot_mxfp4_splitk): the K steps of
-every 64x128 tile are computed as k_split f32 partial planes and summed in
-order by a second kernel.
+every tile (64x128 up to M = 256, 64x256 above) are computed as k_split f32
+partial planes and summed in order by a second kernel.
 
 * parity with the oracle (dequantise, then ragged_dot; odq.py:65-172) within
   the bf16 bar, for one and several groups, a zero group and tail rows, the
@@ -30,11 +30,14 @@ def _mx_weights(rng, g, n, k):
 
 SPLIT_CASES = [
     # m, k, n, g, k_split, situ, zero_group, tail rows
-    (300, 1024, 256, 1, 3, False, -1, 0),     # 16 steps -> ranges 6, 6, 4
+    (300, 1024, 256, 1, 3, False, -1, 0),     # 64x256 tiles; 16 steps -> ranges 6, 6, 4
     (130, 1024, 512, 1, 16, True, -1, 0),     # one step per range, SiTU
     (200, 2048, 512, 3, 5, False, 1, 7),      # groups, a zero group, tail rows
     (77, 640, 136, 2, 4, False, -1, 5),       # partial tiles in M and N; 10 steps -> 3, 3, 3, 1
-    (128, 7168, 2048, 1, 7, False, -1, 0),    # config 4, M = 128 (the default split)
+    (600, 640, 136, 2, 4, False, 0, 9),       # 64x256 tiles: partial n-tile, zero group, tail rows
+    (520, 1024, 512, 1, 5, True, -1, 0),      # 64x256 tiles with the SiTU epilogue
+    (128, 7168, 2048, 1, 8, False, -1, 0),    # config 4, M = 128 (the default split)
+    (1024, 7168, 2048, 1, 4, False, -1, 0),   # config 4, M = 1024 (the default split, 64x256 tiles)
 ]
 
 

@@ -934,12 +934,19 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
       // with v_cvt_scalef32_pk_bf16_fp4, rewritten by the exact per-byte
       // conversion behind one wave-uniform branch when some lane holds a
       // scale byte outside 3..252, then the MFMAs.
+      uint64_t edge_seen = 0;  // lanes that met a scale byte outside 3..252 in this tile
       auto compute = [&](const Frags& f, auto full_tag) __attribute__((always_inline)) {
         constexpr bool kFull = decltype(full_tag)::value;
         bool edge_lane = false;
 #pragma unroll
         for (int j = 0; j < C::kTN; ++j) edge_lane |= !hw_scale_ok(f.s2[j] & 0xffu) || !hw_scale_ok(f.s2[j] >> 8);
-        const bool edge = __builtin_amdgcn_ballot_w64(edge_lane) != 0;
+        const uint64_t edge_mask = __builtin_amdgcn_ballot_w64(edge_lane);
+        // MF == 32: no branch inside the step, so the conversions and the
+        // MFMAs stay one basic block; a wave that met an edge scale byte
+        // recomputes its tile exactly after the K loop (exact_tile below).
+        // MF == 16: the exact conversion replaces the step's values here.
+        const bool edge = MF == 32 ? false : edge_mask != 0;
+        if constexpr (MF == 32) edge_seen |= edge_mask;
         uint32_t bq[C::kKS][C::kTN][4];
 #pragma unroll
         for (int kk = 0; kk < C::kKS; ++kk)
@@ -1017,6 +1024,65 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
         k_loop(std::true_type{});
       else
         k_loop(std::false_type{});
+
+      // exact_tile: a wave whose columns met a scale byte outside 3..252 in
+      // this tile (the hardware conversion is exact only inside that range;
+      // such bytes mean weights below 2^-124 or above 2^125) recomputes its
+      // accumulators from global memory with the exact per-byte conversion,
+      // the fragments read exactly as the K loop reads them from LDS.  It
+      // touches neither the LDS ring nor the DMA stream; waiting for its loads
+      // (vmcnt(0)) only waits longer than the stream's own counts require.
+      if constexpr (MF == 32) {
+        if (__builtin_expect(edge_seen != 0, 0)) {
+          const bool gathered = p.a_index != nullptr;
+          const uint16_t* arow[C::kTM];
+#pragma unroll
+          for (int i = 0; i < C::kTM; ++i) {
+            const int row = i * MF + f_rc;
+            arow[i] = gathered ? p.lhs + static_cast<int64_t>(s_idx[ord * BM + row]) * K
+                               : p.lhs + (cur.row0 + (row < cur.rows ? row : 0)) * K;
+          }
+          const uint8_t* wg = static_cast<const uint8_t*>(p.rhs) + cur.group * N * (K / 2);
+          const uint8_t* sg = p.scale + cur.group * (K / 64) * N * 2;
+          int64_t gcol[C::kTN];
+#pragma unroll
+          for (int j = 0; j < C::kTN; ++j) gcol[j] = drhs_col<BN, EPI>(nt, dlds_col<BN, C::kTN, EPI, MF>(wn, j) + f_rc, N);
+#pragma unroll
+          for (int i = 0; i < C::kTM; ++i)
+#pragma unroll
+            for (int j = 0; j < C::kTN; ++j)
+#pragma unroll
+              for (int e = 0; e < C::kAccN; ++e) acc[i][j][e] = 0.f;
+          for (int64_t kt = 0; kt < nk; ++kt) {
+            uint4 w[C::kTN];
+            uint32_t s2[C::kTN];
+#pragma unroll
+            for (int j = 0; j < C::kTN; ++j) {
+              w[j] = *reinterpret_cast<const uint4*>(wg + kt * (N * 32) + gcol[j] * 32 + f_kc * 16);
+              s2[j] = *reinterpret_cast<const uint16_t*>(sg + kt * (N * 2) + gcol[j] * 2);
+            }
+#pragma unroll
+            for (int kk = 0; kk < C::kKS; ++kk) {
+              const int kc = kk * 2 + f_kc;
+#pragma unroll
+              for (int j = 0; j < C::kTN; ++j) {
+                const uint32_t wd = kk == 0 ? w[j].x : kk == 1 ? w[j].y : kk == 2 ? w[j].z : w[j].w;
+                const uint32_t sb = (s2[j] >> (8 * (kk / (C::kKS / 2)))) & 0xffu;
+                uint32_t q[4];
+#pragma unroll
+                for (int b = 0; b < 4; ++b) q[b] = dequant_byte((wd >> (8 * b)) & 0xffu, sb);
+                const bf16x8_t bfr = __builtin_bit_cast(bf16x8_t, uint4{q[0], q[1], q[2], q[3]});
+#pragma unroll
+                for (int i = 0; i < C::kTM; ++i) {
+                  if (i >= tm_eff) break;
+                  const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(arow[i] + kt * kSK + kc * 8);
+                  acc[i][j] = mfma(bfr, af, acc[i][j]);
+                }
+              }
+            }
+          }
+        }
+      }
 
       // Epilogue: stage in the slot of the last step, round by round.
       const int stage_slot = static_cast<int>((slot0 + nk - 1) % NS);
@@ -1472,11 +1538,14 @@ int run_gkn(const Params& p, hipStream_t st, const char* name) {
 
 }  // namespace
 
-// Split-K: the DMA kernel with 64x128 tiles computes k_split K ranges of
-// every tile as f32 partial planes in `ws` (k_split * M * N floats), then
+// Split-K: the DMA kernel (64x128 tiles, 64x256 for M > kSplitWideM)
+// computes k_split K ranges of every tile as f32 partial planes in `ws`
+// (k_split * M * N floats), then
 // splitk_reduce_kernel sums them in order and applies the epilogue.  For a
 // few long-K tiles (one group, M <= ~1024) the tile grid alone leaves most of
 // the chip idle and each tile's K loop is latency-bound.
+constexpr int64_t kSplitWideM = 256;
+
 int run_dma_splitk(const Params& p, int layout, int epi, int64_t k_split, float* ws, hipStream_t st,
                    const char* name) {
   Params q = p;
@@ -1486,7 +1555,12 @@ int run_dma_splitk(const Params& p, int layout, int epi, int64_t k_split, float*
   q.out_dtype = LMOE_F32;
   q.skip_zero_rows = 0;
   int rc;
-  if (layout == kMXFP4)
+  // MXFP4: 64 x 128 tiles for a few m-tiles (M <= 256), 64 x 256 above, where
+  // half as many n-tiles re-read each activation row (config 4, M = 1024 in
+  // 4 ranges: 45.5 us against 48.7 with 64 x 128 tiles in 2 ranges)
+  if (layout == kMXFP4 && p.M > kSplitWideM)
+    rc = launch_dma<64, 256, kDMX, kEpiNone, 4, 1, 4, 32>(q, st, name);
+  else if (layout == kMXFP4)
     rc = launch_dma<64, 128, kDMX, kEpiNone, 4, 1, 4, 32>(q, st, name);
   else if (layout == kGNK)
     rc = launch_dma<64, 128, kDGNK, kEpiNone, 3, 1, 4, 16>(q, st, name);

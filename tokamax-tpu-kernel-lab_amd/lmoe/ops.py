@@ -412,17 +412,22 @@ def ragged_dot_mxfp6_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
 
 def mxfp4_k_split(m: int, n: int, k: int, g: int) -> int:
   """K ranges for the split-K MXFP4 kernel (1: no split).  One group only
-  (the tile count of a grouped problem depends on device-side group sizes):
-  split until the 64x128 tiles times the ranges reach two per CU, keeping at
-  least 16 K steps (1024 of K) per range (measured at config 4, K = 7168,
-  N = 2048: M = 128 in 7 ranges 21 us against 80 unsplit, M = 1024 in 2
-  ranges 48 us against 84)."""
+  (the tile count of a grouped problem depends on device-side group sizes).
+  Up to M = 256 the kernel uses 64x128 tiles: split until the tiles times
+  the ranges reach one per CU, keeping at least 8 K steps (512 of K) per
+  range; above it 64x256 tiles: split until two per CU, at least 16 steps
+  per range.  Measured at config 4 (K = 7168, N = 2048): M = 1 in 14 ranges
+  12.9 us (7 ranges 14.2, unsplit 57), M = 128 in 8 ranges 20.4 us (7
+  ranges 20.8, unsplit 73), M = 1024 in 4 ranges of 64x256 tiles 45.5 us
+  (2 ranges of 64x128 tiles 48.7, unsplit 75)."""
   if g != 1 or k % 64 != 0:
     return 1
-  tiles = -(-m // 64) * -(-n // 128)
   steps = k // 64
-  want = -(-512 // max(tiles, 1))
-  return max(1, min(want, steps // 16))
+  if m <= 256:
+    tiles = -(-m // 64) * -(-n // 128)
+    return max(1, min(-(-256 // max(tiles, 1)), steps // 8))
+  tiles = -(-m // 64) * -(-n // 256)
+  return max(1, min(-(-512 // max(tiles, 1)), steps // 16))
 
 
 def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
