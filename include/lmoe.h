@@ -194,6 +194,30 @@ int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_tiled, const 
                                  int zero_group, int flags, int epilogue, float beta, float beta_lin,
                                  int64_t max_group_rows, void* out, void* stream);
 
+/* ---- f4, decode regime: the one-launch dispatch fused into the skinny gate/up --------
+ * lmoe_dispatch_local_small (ref.py:754-877: stable expert-major order, tail
+ * truncation at m_padded, padding bucket L) followed by
+ * lmoe_ragged_dot_mxfp4_skinny on the sorted rows (rd.py:610-723, gate/up
+ * with the SiTU epilogue, or a plain product) in one launch, for a decode
+ * step (rd.py:553-577).  Every dispatch output but sorted_tokens is written
+ * exactly as lmoe_dispatch_local_small writes it; out equals
+ * lmoe_ragged_dot_mxfp4_skinny(sorted_tokens, ..., group_sizes, M = m_padded,
+ * G = L + 1, zero_group = L, max_group_rows = T) bit for bit.  x: the (T, >= K)
+ * bf16 token rows, row stride x_ld elements (x_ld % 8 == 0); each block reads
+ * the row of its sorted row's token itself, so no sorted copy is written.
+ * w_tiled / s_tiled: the L + 1 experts' weights from lmoe_mxfp4_tile, (N, K)
+ * per expert.  T*k <= 1024, m_padded <= 2048, L <= 1023, K % 128 == 0,
+ * N % 16 == 0 (N % 32 with SiTU); topk_w bf16 or f32.  flags: 0 or
+ * LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS.  No workspace.
+ */
+int lmoe_dispatch_mxfp4_skinny(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
+                               int64_t x_ld, int64_t T, int64_t k, int64_t local_start, int64_t L,
+                               int64_t m_padded, const uint8_t* w_tiled, const uint8_t* s_tiled, int64_t K,
+                               int64_t N, int epilogue, float beta, float beta_lin, int flags,
+                               int32_t* group_sizes, uint8_t* valid, int32_t* per_expert_counts,
+                               int32_t* padded_token_idx, void* padded_w, int32_t* slot_pos, void* out,
+                               void* stream);
+
 /* ---- dense projections on hipBLASLt ------------------------------------------------
  * out (M, N) = x (M, K) @ w_nk^T, w_nk stored (N, K): the layer's plain dense
  * projections (x = hidden @ down_proj, ref.py:634-655; out = normed @ up_proj,

@@ -207,3 +207,48 @@ def test_skinny_empty_and_all_padding(gpu_device):
   out = ops.ragged_dot_mxfp4(x, tpk, tsc, to_dev(np.array([0, 0, 40], np.int32)), zero_group=2,
                              weight_layout="tiled", mode="skinny")
   assert out.shape == (40, n) and not out.any()
+
+
+FUSED_CASES = [
+    # T, E, k, start, L, lat, n, situ, capacity factor (m_padded), skip padding rows
+    (1, 896, 16, 0, 112, 1024, 4096, True, 2.0, True),      # config 5, one decode token
+    (16, 896, 16, 37, 112, 1024, 4096, True, 2.0, False),   # shard offset, padding rows zeroed
+    (64, 896, 16, 0, 112, 1024, 4096, True, 2.0, True),     # T*k = 1024 (the limit)
+    (40, 64, 8, 8, 48, 256, 512, False, 0.3, False),        # plain product; m_padded 128 < 240 local slots: tail truncation
+    (3, 32, 4, 0, 32, 128, 96, False, 2.0, True),           # every expert local, N = 96
+]
+
+
+@pytest.mark.parametrize("t,e,k,start,L,lat,n,situ,cf,skip", FUSED_CASES)
+def test_dispatch_skinny_fused_equals_two_launches(gpu_device, t, e, k, start, L, lat, n, situ, cf, skip):
+  """dispatch_ragged_dot_mxfp4_skinny (one launch) == dispatch_local(path="small")
+  followed by the skinny ragged_dot_mxfp4 on the sorted rows, bit for bit: every
+  dispatch output and the expert GEMM's rows (ref.py:754-877, rd.py:610-723)."""
+  from lmoe import ops
+  banner(f"fused decode dispatch T={t} E={e} k={k} start={start} L={L} lat={lat} n={n} situ={situ} cf={cf}")
+  gen = torch.Generator(device="cuda").manual_seed(t * 1000 + e)
+  idx = torch.argsort(torch.rand((t, e), generator=gen, device="cuda"), dim=1)[:, :k].to(torch.int32).contiguous()
+  w = torch.rand((t, k), generator=gen, device="cuda").to(torch.bfloat16)
+  x = torch.randn((t, lat), generator=gen, device="cuda").to(torch.bfloat16)
+  rng = np.random.default_rng(t + e + n)
+  packed, scale = _mx_weights(rng, L + 1, n, lat)
+  tpk, tsc = ops.mxfp4_tile_weights(to_dev(packed), to_dev(scale))
+  m_padded = ops.compute_m_padded(t, k, e, L, cf)
+  fa = "situ:4.0:25.0" if situ else None
+  d1, act1 = ops.dispatch_ragged_dot_mxfp4_skinny(idx, w, x, start, L, m_padded, tpk, tsc,
+                                                  fuse_gateup_activation=fa, skip_zero_group_rows=skip)
+  d0 = ops.dispatch_local(idx, w, x, start, L, m_padded, path="small")
+  act0 = ops.ragged_dot_mxfp4(d0.sorted_tokens, tpk, tsc, d0.group_sizes, fuse_gateup_activation=fa, mode="skinny",
+                              zero_group=L, weight_layout="tiled", skip_zero_group_rows=skip, max_group_rows=t)
+  torch.cuda.synchronize()
+  for name in ("group_sizes", "valid_mask", "per_expert_counts", "padded_token_idx", "padded_combine_weight",
+               "slot_pos"):
+    assert torch.equal(getattr(d1, name), getattr(d0, name)), name
+  assert d1.sorted_tokens is None
+  kept = int(d0.group_sizes[:L].sum())
+  banner(f"  m_padded={m_padded} kept rows {kept} of {t * k} slots")
+  if skip:
+    assert torch.equal(act1[:kept], act0[:kept])
+  else:
+    assert torch.equal(act1, act0)
+    assert bool((act1[kept:] == 0).all())

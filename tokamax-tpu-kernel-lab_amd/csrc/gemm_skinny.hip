@@ -50,7 +50,26 @@ struct SkinnyParams {
   float beta, beta_lin;
   uint16_t* out;         // (M, N) bf16, or (M, N/2) with the SiTU epilogue
   int n_ct;              // 16-column output tiles
+  // Fused dispatch (skinny_mx_kernel<..., true>): every block sorts the
+  // top-k slots in LDS as the one-launch dispatch does, block 0 writes the
+  // dispatch metadata, and x is the (T, >= K) bf16 token rows (row stride
+  // x_ld) read through the sorted order; then M = m_padded, G = L + 1 and
+  // zero_group = L.
+  const int32_t* d_idx = nullptr;  // (T*k,) global expert ids
+  const uint8_t* d_w_in = nullptr; // (T*k,) combine weights, d_wsize bytes each
+  int d_wsize = 0;
+  int64_t d_n = 0, d_k = 1, x_ld = 0;
+  int d_start = 0, d_L = 0;
+  int32_t* d_group_sizes = nullptr;  // (L + 1,)
+  uint8_t* d_valid = nullptr;        // (m_padded,)
+  int32_t* d_counts = nullptr;       // (L,)
+  int32_t* d_tok = nullptr;          // (m_padded,)
+  uint8_t* d_w_out = nullptr;        // (m_padded,) d_wsize bytes each
+  int32_t* d_slot_pos = nullptr;     // (T*k,) or null
 };
+
+constexpr int kSkDispSlots = 1024;  // T*k of the fused dispatch
+constexpr int kSkDispRows = 2048;   // its m_padded
 
 // One packed dword (8 e2m1 values, low nibble first) with its scale byte ->
 // 8 bf16, exactly as dequant32 does it.
@@ -99,7 +118,7 @@ __device__ __forceinline__ void store_out(const SkinnyParams& p, int64_t row, in
   *reinterpret_cast<uint2*>(p.out + row * nout + col) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
 }
 
-template <int EPI, int NC, int WAVES>
+template <int EPI, int NC, int WAVES, bool DISP = false>
 __global__ __launch_bounds__(WAVES * 64) void skinny_mx_kernel(SkinnyParams p) {
   constexpr int kThreads = WAVES * 64;
   constexpr int GPT = kSkMaxGroups / kThreads;       // groups per thread in the table scan
@@ -117,6 +136,97 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_mx_kernel(SkinnyParams p) {
   const int64_t M = p.M, K = p.K, N = p.N, G = p.G;
   const int64_t nout = N / NB;
 
+  // ---- fused dispatch: the sort of dispatch_small_kernel (stable expert-major
+  // order, tail truncation at m_padded = M, padding bucket L), in LDS
+  constexpr int kDS = DISP ? kSkDispSlots : 1, kDR = DISP ? kSkDispRows : 1, kDG = DISP ? kSkMaxGroups : 1;
+  __shared__ uint16_t s_key[kDS];
+  __shared__ int32_t s_row_slot[kDR];
+  __shared__ int32_t s_dcnt[kDG], s_doff[kDG], s_dgs[kDG];
+  __shared__ int32_t s_dtotal;
+  if constexpr (DISP) {
+    const int Ld = p.d_L;
+    const int64_t ns = p.d_n;
+    for (int e = t; e <= Ld; e += kThreads) {
+      s_dcnt[e] = 0;
+      s_dgs[e] = 0;  // the rank pass's per-expert run
+    }
+    for (int64_t r = t; r < M; r += kThreads) s_row_slot[r] = -1;
+    __syncthreads();
+    for (int64_t s = t; s < ns; s += kThreads) {
+      const int g = p.d_idx[s];
+      const int key = (g >= p.d_start && g < p.d_start + Ld) ? g - p.d_start : Ld;
+      s_key[s] = static_cast<uint16_t>(key);
+      if (key < Ld) atomicAdd(&s_dcnt[key], 1);
+    }
+    __syncthreads();
+    if (wv == 0) {  // exclusive offsets of the L experts, each lane a run of keys
+      const int per = (Ld + 63) / 64;
+      const int e0 = lane * per, e1 = e0 + per < Ld ? e0 + per : Ld;
+      int sum = 0;
+      for (int e = e0; e < e1; ++e) sum += s_dcnt[e];
+      int incl = sum;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+      }
+      int run = incl - sum;
+      for (int e = e0; e < e1; ++e) {
+        s_doff[e] = run;
+        run += s_dcnt[e];
+      }
+      if (lane == 63) s_dtotal = incl;
+    }
+    __syncthreads();
+    if (wv == 0) {  // stable ranks: wave 0 walks the slots in order, 64 at a time
+      int kb = 1;
+      while ((1 << kb) <= Ld) ++kb;
+      const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+      for (int64_t c = 0; c < ns; c += 64) {
+        const int64_t s = c + lane;
+        const int key = s < ns ? s_key[s] : Ld;
+        uint64_t m = __ballot(s < ns && key < Ld);
+        for (int b = 0; b < kb; ++b) {
+          const uint64_t bal = __ballot((key >> b) & 1);
+          m &= ((key >> b) & 1) ? bal : ~bal;
+        }
+        if (s < ns && key < Ld) {
+          const int base = s_dgs[key];
+          const int pos = s_doff[key] + base + __popcll(m & below);
+          const bool kept = pos < M;
+          if (kept) s_row_slot[pos] = static_cast<int32_t>(s);
+          if (blockIdx.x == 0 && p.d_slot_pos) p.d_slot_pos[s] = kept ? pos : -1;
+          if ((m & below) == 0) s_dgs[key] = base + __popcll(m);  // the group's lowest lane
+        } else if (s < ns && blockIdx.x == 0 && p.d_slot_pos) {
+          p.d_slot_pos[s] = -1;
+        }
+      }
+    }
+    __syncthreads();
+    const int64_t nkept = s_dtotal < M ? s_dtotal : M;
+    for (int e = t; e < Ld; e += kThreads) {
+      const int64_t room = M - s_doff[e];
+      s_dgs[e] = static_cast<int32_t>(room <= 0 ? 0 : (room < s_dcnt[e] ? room : s_dcnt[e]));
+    }
+    if (t == 0) s_dgs[Ld] = static_cast<int32_t>(M - nkept);
+    __syncthreads();
+    if (blockIdx.x == 0) {  // the dispatch's metadata, as lmoe_dispatch_local_small writes it
+      for (int e = t; e <= Ld; e += kThreads) {
+        p.d_group_sizes[e] = s_dgs[e];
+        if (e < Ld) p.d_counts[e] = s_dgs[e];
+      }
+      for (int64_t r = t; r < M; r += kThreads) {
+        const int32_t s = s_row_slot[r];
+        p.d_valid[r] = s >= 0 ? 1 : 0;
+        p.d_tok[r] = s >= 0 ? static_cast<int32_t>(s / p.d_k) : -1;
+        if (p.d_wsize == 4)
+          reinterpret_cast<uint32_t*>(p.d_w_out)[r] = s >= 0 ? reinterpret_cast<const uint32_t*>(p.d_w_in)[s] : 0u;
+        else
+          reinterpret_cast<uint16_t*>(p.d_w_out)[r] = s >= 0 ? reinterpret_cast<const uint16_t*>(p.d_w_in)[s] : 0;
+      }
+    }
+  }
+
   // ---- hit-group table: exclusive scan of (rows << 16 | hit) over <= 1024 groups
   if (t == 0) {
     s_misc[0] = 0;
@@ -127,7 +237,11 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_mx_kernel(SkinnyParams p) {
 #pragma unroll
   for (int i = 0; i < GPT; ++i) {
     const int64_t g = GPT * t + i;
-    const int32_t n = g < G ? p.gs[g] : 0;
+    int32_t n = 0;
+    if constexpr (DISP)
+      n = g < G ? s_dgs[g] : 0;
+    else
+      n = g < G ? p.gs[g] : 0;
     sz[i] = n > 0 ? n : 0;
     v += (static_cast<uint64_t>(sz[i]) << 16) + ((sz[i] > 0 && g != p.zero_group) ? 1u : 0u);
   }
@@ -214,8 +328,17 @@ __global__ __launch_bounds__(WAVES * 64) void skinny_mx_kernel(SkinnyParams p) {
       const int nrc = std::min(NC, (rows - rb + 15) / 16);
       auto ldx = [&](int pr, int rc, uint4 (&x)[4]) {
         const int lr = rb + rc * 16 + l16;
+        int64_t xrow = -1;  // this lane's activation row
         if (lr < rows) {
-          const uint16_t* xp = p.x + (r0 + lr) * K + (2 * static_cast<int64_t>(pr) + ks_off) * 64 + hh * 8;
+          if constexpr (DISP) {
+            const int32_t sl = s_row_slot[r0 + lr];
+            xrow = sl >= 0 ? static_cast<int64_t>(sl / p.d_k) * p.x_ld : -1;
+          } else {
+            xrow = (r0 + lr) * K;
+          }
+        }
+        if (xrow >= 0) {
+          const uint16_t* xp = p.x + xrow + (2 * static_cast<int64_t>(pr) + ks_off) * 64 + hh * 8;
 #pragma unroll
           for (int s = 0; s < 4; ++s) x[s] = *reinterpret_cast<const uint4*>(xp + 16 * s);
         } else {
@@ -425,7 +548,7 @@ int skinny_chunks(int64_t M, int64_t max_group_rows) {
 // Blocks of one instance resident at once on the device: the grid size (each
 // block walks items with a grid stride, so no block sits idle past the first
 // wave of blocks).
-template <int EPI, int NC, int WAVES>
+template <int EPI, int NC, int WAVES, bool DISP = false>
 unsigned resident_blocks() {
   static std::atomic<unsigned> cached{0};
   unsigned v = cached.load(std::memory_order_relaxed);
@@ -433,7 +556,7 @@ unsigned resident_blocks() {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, skinny_mx_kernel<EPI, NC, WAVES>, WAVES * 64, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, skinny_mx_kernel<EPI, NC, WAVES, DISP>, WAVES * 64, 0) !=
             hipSuccess ||
         cus <= 0 || per_cu <= 0) {
       cus = 256;
@@ -445,19 +568,19 @@ unsigned resident_blocks() {
   return v;
 }
 
-template <int EPI, int NC, int WAVES>
+template <int EPI, int NC, int WAVES, bool DISP = false>
 void launch_one(const SkinnyParams& p, int64_t upper, hipStream_t st) {
   const unsigned grid =
-      static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(upper, resident_blocks<EPI, NC, WAVES>())));
-  skinny_mx_kernel<EPI, NC, WAVES><<<grid, WAVES * 64, 0, st>>>(p);
+      static_cast<unsigned>(std::max<int64_t>(1, std::min<int64_t>(upper, resident_blocks<EPI, NC, WAVES, DISP>())));
+  skinny_mx_kernel<EPI, NC, WAVES, DISP><<<grid, WAVES * 64, 0, st>>>(p);
 }
 
-template <int EPI, int WAVES>
+template <int EPI, int WAVES, bool DISP = false>
 void launch_nc(const SkinnyParams& p, int nc, int64_t upper, hipStream_t st) {
   switch (nc) {
-    case 1: launch_one<EPI, 1, WAVES>(p, upper, st); break;
-    case 2: launch_one<EPI, 2, WAVES>(p, upper, st); break;
-    default: launch_one<EPI, 4, WAVES>(p, upper, st); break;
+    case 1: launch_one<EPI, 1, WAVES, DISP>(p, upper, st); break;
+    case 2: launch_one<EPI, 2, WAVES, DISP>(p, upper, st); break;
+    default: launch_one<EPI, 4, WAVES, DISP>(p, upper, st); break;
   }
 }
 
@@ -510,6 +633,74 @@ extern "C" int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_ti
       launch_nc<kEpiNone, 8>(p, nc, upper, st);
     else
       launch_nc<kEpiNone, 4>(p, nc, upper, st);
+  }
+  LMOE_CHECK_LAUNCH(name);
+  return LMOE_OK;
+}
+
+extern "C" int lmoe_dispatch_mxfp4_skinny(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
+                                          int64_t x_ld, int64_t T, int64_t k, int64_t local_start, int64_t L,
+                                          int64_t m_padded, const uint8_t* w_tiled, const uint8_t* s_tiled, int64_t K,
+                                          int64_t N, int epilogue, float beta, float beta_lin, int flags,
+                                          int32_t* group_sizes, uint8_t* valid, int32_t* per_expert_counts,
+                                          int32_t* padded_token_idx, void* padded_w, int32_t* slot_pos, void* out,
+                                          void* stream) {
+  const char* name = "dispatch_mxfp4_skinny";
+  LMOE_CHECK_ARG(T >= 0 && k > 0 && L > 0 && m_padded >= 0 && local_start >= 0 && K > 0 && N > 0 && x_ld >= K,
+                 "%s: bad sizes T=%lld k=%lld L=%lld m_padded=%lld K=%lld N=%lld x_ld=%lld", name, (long long)T,
+                 (long long)k, (long long)L, (long long)m_padded, (long long)K, (long long)N, (long long)x_ld);
+  LMOE_CHECK_ARG(w_dtype == LMOE_BF16 || w_dtype == LMOE_F32, "%s: combine weights must be bf16 or f32", name);
+  LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
+  LMOE_CHECK_ARG((flags & ~LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS) == 0, "%s: unknown flags 0x%x", name, flags);
+  const int epi = epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone;
+  LMOE_CHECK_SUPPORTED(T * k <= kSkDispSlots && m_padded <= kSkDispRows && L + 1 <= kSkMaxGroups,
+                       "%s: at most %d slots, %d rows and %d experts (T*k=%lld m_padded=%lld L=%lld)", name,
+                       kSkDispSlots, kSkDispRows, kSkMaxGroups - 1, (long long)(T * k), (long long)m_padded,
+                       (long long)L);
+  LMOE_CHECK_SUPPORTED(K % 128 == 0 && x_ld % 8 == 0, "%s: needs K %% 128 == 0 and 16-byte rows (K=%lld x_ld=%lld)",
+                       name, (long long)K, (long long)x_ld);
+  LMOE_CHECK_SUPPORTED(N % (epi == kEpiSitu ? 32 : 16) == 0, "%s: needs 16-column output tiles (N=%lld)", name,
+                       (long long)N);
+  LMOE_CHECK_ARG(group_sizes && valid && per_expert_counts && padded_token_idx && padded_w && w_tiled && s_tiled &&
+                     (T == 0 || (topk_idx && topk_w && x)) && (out || m_padded == 0),
+                 "%s: null pointer", name);
+  LMOE_CHECK_SUPPORTED((T == 0 || aligned(x, 16)) && aligned(w_tiled, 16) && aligned(out, 16) && aligned(s_tiled, 2),
+                       "%s: x, weights and out must be 16-byte aligned", name);
+  const int64_t G = L + 1;
+  const int nc = skinny_chunks(m_padded, T);
+  const int64_t nout = epi == kEpiSitu ? N / 2 : N;
+  const int64_t nct = nout / 16;
+  SkinnyParams p{static_cast<const uint16_t*>(x), w_tiled, s_tiled, group_sizes, m_padded, K, N, G,
+                 static_cast<int>(L), (flags & LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS) != 0, beta, beta_lin,
+                 static_cast<uint16_t*>(out), static_cast<int>(nct)};
+  p.d_idx = topk_idx;
+  p.d_w_in = static_cast<const uint8_t*>(topk_w);
+  p.d_wsize = dtype_size(w_dtype);
+  p.d_n = T * k;
+  p.d_k = k;
+  p.x_ld = x_ld;
+  p.d_start = static_cast<int>(local_start);
+  p.d_L = static_cast<int>(L);
+  p.d_group_sizes = group_sizes;
+  p.d_valid = valid;
+  p.d_counts = per_expert_counts;
+  p.d_tok = padded_token_idx;
+  p.d_w_out = static_cast<uint8_t*>(padded_w);
+  p.d_slot_pos = slot_pos;
+  const int64_t items_bound = std::min<int64_t>(G, std::max<int64_t>(m_padded, 1)) * nct;
+  const int64_t upper = std::max(items_bound, ceil_div(m_padded * nout / 8, 256));
+  const bool wide = items_bound < 256;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (epi == kEpiSitu) {
+    if (wide)
+      launch_nc<kEpiSitu, 8, true>(p, nc, upper, st);
+    else
+      launch_nc<kEpiSitu, 4, true>(p, nc, upper, st);
+  } else {
+    if (wide)
+      launch_nc<kEpiNone, 8, true>(p, nc, upper, st);
+    else
+      launch_nc<kEpiNone, 4, true>(p, nc, upper, st);
   }
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;

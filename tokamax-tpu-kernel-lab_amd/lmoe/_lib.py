@@ -56,6 +56,8 @@ SIGNATURES = {
     "lmoe_ragged_dot_mxfp4_rows": ([P, I64, P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, P, P], I32),
     "lmoe_ragged_dot_mxfp4_splitk": ([P, P, P, P, I64, I64, I64, I64, I32, I64, P, I64, I32, F, F, P, P], I32),
     "lmoe_ragged_dot_mxfp4_skinny": ([P, P, P, P, I64, I64, I64, I64, I32, I32, I32, F, F, I64, P, P], I32),
+    "lmoe_dispatch_mxfp4_skinny": ([P, P, I32, P, I64, I64, I64, I64, I64, I64, P, P, I64, I64, I32, F, F, I32,
+                                    P, P, P, P, P, P, P, P], I32),
     "lmoe_mxfp4_tile": ([P, P, I64, I64, I64, P, P, P], I32),
     "lmoe_mxfp8_scale_bytes": ([I64, I64], I64),
     "lmoe_quantize_mxfp8": ([P, I32, I64, I64, P, P, P], I32),

@@ -218,8 +218,26 @@ class LocalShardLatentMoE:
     rows_path = (self.router_down_nk is not None and hidden.dtype == torch.bfloat16 and not return_stages
                  and self.expert_format == "mxfp4" and self.weight_layout == "tiled" and mx_mode == "lds_dequant"
                  and c.latent_size <= 1024 and c.latent_size % 4 == 0)
+    # Decode step (skinny expert GEMMs, stages not returned): the router launch
+    # writes the bf16 token rows, and the one-launch dispatch runs inside the
+    # skinny gate/up launch, which reads each sorted row's token row itself.
+    fused_decode = (decode and mx_mode == "skinny" and not return_stages and self.router_down_nk is not None
+                    and ops.dispatch_skinny_supported(t, c.top_k, c.latent_size, 2 * c.intermediate_size, self.L,
+                                                      m_padded, True))
     act = None
-    if rows_path:
+    if fused_decode:
+      e = self.router_nk.shape[0]
+      rd = self._dense(hidden, self.router_down_nk, torch.float32)
+      logits, x_src = rd[:, :e], rd[:, e:]
+      idx, w, x = ops.router_topk_project(logits, x_src, self.bias, c.top_k, c.moe_renormalize,
+                                          c.routed_scaling_factor, self.act, hidden.dtype)
+      if "gateup" in ev:
+        ev["gateup"][0].record()
+      d, act = ops.dispatch_ragged_dot_mxfp4_skinny(idx, w, x, self.start, self.L, m_padded,
+                                                    E["gu_packed" + self._sfx], E["gu_scale" + self._sfx],
+                                                    fuse_gateup_activation=f"situ:{b}:{bl}",
+                                                    skip_zero_group_rows=True)
+    elif rows_path:
       e = self.router_nk.shape[0]
       rd = self._dense(hidden, self.router_down_nk, torch.float32)
       logits, x_src = rd[:, :e], rd[:, e:]

@@ -823,6 +823,63 @@ def _dispatch_metadata(topk_idx, topk_weight, local_expert_start, L, m_padded, l
   return Dispatch(None, group_sizes, valid, counts, tok, w, slot_pos)
 
 
+FUSED_DISPATCH_SLOTS, FUSED_DISPATCH_ROWS = 1024, 2048
+
+
+def dispatch_skinny_supported(t: int, k: int, lat: int, n: int, L: int, m_padded: int, situ: bool) -> bool:
+  """Sizes ``dispatch_ragged_dot_mxfp4_skinny`` takes (a decode step)."""
+  return (t * k <= FUSED_DISPATCH_SLOTS and m_padded <= FUSED_DISPATCH_ROWS and L + 1 <= 1024
+          and skinny_supported(lat, n, L + 1, situ))
+
+
+def dispatch_ragged_dot_mxfp4_skinny(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.Tensor,
+                                     local_expert_start: int, local_num_experts: int, m_padded: int,
+                                     w_tiled: torch.Tensor, s_tiled: torch.Tensor, *,
+                                     fuse_gateup_activation: str | None = None,
+                                     skip_zero_group_rows: bool = False) -> tuple[Dispatch, torch.Tensor]:
+  """``dispatch_local(..., path="small")`` and ``ragged_dot_mxfp4(sorted_tokens,
+  ..., mode="skinny", weight_layout="tiled", zero_group=L)`` in one launch (a
+  decode step, ref.py:754-877 then rd.py:610-723): the same dispatch outputs
+  except ``sorted_tokens`` (None: each block reads its rows' token rows of x
+  itself) and the same expert GEMM output, bit for bit.  x: bf16 token rows
+  (T, >= lat), unit column stride.  Sizes: ``dispatch_skinny_supported``."""
+  if topk_idx.dtype != torch.int32:
+    raise ValueError("topk_idx must be int32")
+  if x.dtype != torch.bfloat16:
+    raise NotImplementedError("the fused decode dispatch reads bf16 token rows")
+  if w_tiled.dtype != torch.uint8 or s_tiled.dtype != torch.uint8:
+    raise ValueError("tiled MXFP4 weights and scales must be uint8")
+  t, k = topk_idx.shape
+  L = local_num_experts
+  g, _, n, _ = w_tiled.shape
+  lat = x.shape[-1]
+  if g != L + 1 or tuple(w_tiled.shape) != (L + 1, lat // 64, n, 32) or tuple(s_tiled.shape) != (L + 1, lat // 64, n, 2):
+    raise ValueError(f"tiled weights {tuple(w_tiled.shape)} / {tuple(s_tiled.shape)} for L + 1 = {L + 1} experts, K = {lat}")
+  epi, b, bl, width = _lib.EPI_NONE, 0.0, 0.0, n
+  if fuse_gateup_activation is not None:
+    b, bl = parse_fused_activation(fuse_gateup_activation)
+    epi, width = _lib.EPI_SITU, n // 2
+  if not dispatch_skinny_supported(t, k, lat, n, L, m_padded, epi == _lib.EPI_SITU):
+    raise NotImplementedError(f"fused decode dispatch: T*k={t * k}, m_padded={m_padded}, L={L}, K={lat}, N={n}")
+  x = _dev_rows(x)
+  _dev(topk_idx, topk_weight, w_tiled, s_tiled)
+  dev = x.device
+  group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
+  valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
+  counts = torch.empty((L,), dtype=torch.int32, device=dev)
+  tok = torch.empty((m_padded,), dtype=torch.int32, device=dev)
+  w = torch.empty((m_padded,), dtype=topk_weight.dtype, device=dev)
+  slot_pos = torch.empty((t * k,), dtype=torch.int32, device=dev)
+  out = torch.empty((m_padded, width), dtype=torch.bfloat16, device=dev)
+  flags = _lib.MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS if skip_zero_group_rows else 0
+  check(lib().lmoe_dispatch_mxfp4_skinny(_p(topk_idx), _p(topk_weight), _dt(topk_weight), _p(x),
+                                         x.stride(0) if t > 0 else lat, t, k, local_expert_start, L, m_padded,
+                                         _p(w_tiled), _p(s_tiled), lat, n, epi, b, bl, flags, _p(group_sizes),
+                                         _p(valid), _p(counts), _p(tok), _p(w), _p(slot_pos), _p(out), _stream()),
+        "dispatch_mxfp4_skinny")
+  return Dispatch(None, group_sizes, valid, counts, tok, w, slot_pos), out
+
+
 def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.Tensor | None,
                    local_expert_start: int, local_num_experts: int, m_padded: int, *, path: str = "auto",
                    skip_padding_rows: bool = False, gather_rows: bool = True, lat: int | None = None) -> Dispatch:
