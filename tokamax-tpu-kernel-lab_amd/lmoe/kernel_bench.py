@@ -127,8 +127,8 @@ def bench_cfg3(dev, rounds, calls):
   ms = time_fn(lambda: ops.router_topk_from_logits(logits, None, k, True, 1.0, "sigmoid", torch.bfloat16),
                rounds, calls, name="cfg3 router_topk (2048x896, k=16)")
   report("cfg3 router_topk (2048x896, k=16)", ms, 0, t * e * 4 + t * k * 6)
-  ms = time_fn(lambda: ops.dispatch_local(idx, w, x, 0, L, m_padded), rounds, calls, name="cfg3 dispatch (hist+scan+place+gather)")
-  report("cfg3 dispatch (hist+scan+place+gather)", ms, 0,
+  ms = time_fn(lambda: ops.dispatch_local(idx, w, x, 0, L, m_padded), rounds, calls, name="cfg3 dispatch (counting sort + gather)")
+  report("cfg3 dispatch (counting sort + gather)", ms, 0,
          t * k * 4 + rows * lat * 2 * 2 + (m_padded - rows) * lat * 2 + m_padded * 11, rows=rows)
   f_gu = 2.0 * rows * lat * 2 * inter
   b_gu = hit * 2 * inter * lat * 2 + rows * lat * 2 + rows * inter * 2
