@@ -85,3 +85,21 @@ def test_default_split_choice():
   assert [mxfp4_k_split(m, 2048, 7168, 1) for m in (1, 128, 1024, 4096)] == [14, 8, 4, 1]
   assert mxfp4_k_split(8804, 4096, 1024, 113) == 1  # grouped: never
   assert mxfp4_k_split(64, 256, 256, 1) == 1        # too few K steps
+
+
+@pytest.mark.parametrize("e,lat", [(64, 128), (896, 1024), (4, 4), (896, 2048), (128, 1028), (896, 1026),
+                                   (898, 1024), (62, 128)])
+def test_router_project_predicate_matches_library(L, e, lat):
+  """The layer picks the one-launch router top-k + latent cast
+  (lmoe_router_topk_proj) by ops.router_topk_project_supported; on the layout
+  the layer passes -- logits and latent projection as the column blocks of one
+  (T, E + lat) f32 GEMM output, the projection starting 4 E bytes in -- the
+  predicate must agree with the library's own size checks (T = 0: the library
+  returns after its checks without touching the device)."""
+  from lmoe import ops
+  base = 1 << 20
+  rc = L.lmoe_router_topk_proj(ctypes.c_void_p(base), e + lat, None, 0, e, min(8, e), _lib.ACT_SIGMOID, 1, 1.0,
+                               _lib.F32, None, None, ctypes.c_void_p(base + 4 * e), e + lat, lat,
+                               ctypes.c_void_p(2 * base), None)
+  want = _lib.OK if ops.router_topk_project_supported(e, lat) else _lib.ERR_UNSUPPORTED
+  assert rc == want, L.lmoe_last_error()

@@ -364,8 +364,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 //   SiTU = beta*beta_lin * (a - 1)(c - 1) / ((a + 1)(c + 1)) / (1 + e),
 //   a = 2^(2 log2(e) g / beta), c = 2^(2 log2(e) u / beta_lin), e = 2^(-log2(e) g).
 // The tanh exponents are clamped to [-26, 26] (|x| <= 9: tanh(9) = 1 - 3e-8,
-// saturated in f32), so the tanh quotient cannot overflow; the sigmoid keeps
-// its own reciprocal and goes to 0 only where e^-g overflows (g < -88).  Near
+// saturated in f32), so the tanh quotient cannot overflow.  For beta != 4 the
+// sigmoid keeps its own reciprocal and goes to 0 where e^-g overflows
+// (g < -88).  For beta == 4 the sigmoid is built from the same clamped
+// exponential a = e^(g/2) (below), so for g < -36 it stays at 2^-52 instead of
+// decaying as e^g: the result there is at most beta*beta_lin*2^-52 in
+// magnitude instead of about 0, far below the bf16 rounding of any output of
+// ordinary size.  Near
 // g = 0 (u = 0) a - 1 (c - 1) cancels: the absolute error of the result stays
 // below beta*beta_lin*2^-23, far below the bf16 rounding of results of
 // ordinary size.  Hardware exp2 / reciprocal: a few f32 ulp.  A NaN gate or
@@ -385,7 +390,8 @@ __device__ __forceinline__ SituConsts situ_consts(float beta, float beta_lin) {
 // clamped to 2^+-26 (tanh is +-1 to f32 precision there).  With beta == 4,
 // a = e^(g/2) gives tanh(g/4) = (a-1)/(a+1) and sigmoid(g) = a^2/(1+a^2), so
 // the pair costs two exponentials and one reciprocal (numerator and
-// denominator stay below 2^104); otherwise sigmoid takes its own exponential
+// denominator stay below 2^104; with a clamped at 2^-26, sigmoid(g) bottoms
+// out at 2^-52 for g < -36); otherwise sigmoid takes its own exponential
 // and reciprocal.  NaN in either input gives NaN.  Every fused kernel uses
 // this one function, so they agree bit for bit.
 __device__ __forceinline__ float situ_epi(float g, float u, const SituConsts& c) {

@@ -211,17 +211,21 @@ class LocalShardLatentMoE:
     mx_mode, mx_kw = self.mxfp4_mode, {}
     if self.expert_format == "mxfp4" and self._decode_path(t):
       mx_mode, mx_kw = "skinny", {"max_group_rows": t}
+    # Both paths below take the router top-k and the bf16 latent rows from one
+    # launch over the fused router + down-projection output; it takes at most
+    # 1024 latent columns (other sizes run the separate top-k and cast).
+    proj_ok = (self.router_down_nk is not None
+               and ops.router_topk_project_supported(self.router_nk.shape[0], c.latent_size))
     # Gathered rows (prefill, tiled MXFP4 experts, stages not returned): the
     # router launch also rounds the latent projection to bf16 (T rows), the
     # dispatch writes only its metadata, and the gate/up GEMM reads each
     # sorted row straight from its token's row -- no sorted_tokens copy.
-    rows_path = (self.router_down_nk is not None and hidden.dtype == torch.bfloat16 and not return_stages
-                 and self.expert_format == "mxfp4" and self.weight_layout == "tiled" and mx_mode == "lds_dequant"
-                 and c.latent_size <= 1024 and c.latent_size % 4 == 0)
+    rows_path = (proj_ok and hidden.dtype == torch.bfloat16 and not return_stages
+                 and self.expert_format == "mxfp4" and self.weight_layout == "tiled" and mx_mode == "lds_dequant")
     # Decode step (skinny expert GEMMs, stages not returned): the router launch
     # writes the bf16 token rows, and the one-launch dispatch runs inside the
     # skinny gate/up launch, which reads each sorted row's token row itself.
-    fused_decode = (decode and mx_mode == "skinny" and not return_stages and self.router_down_nk is not None
+    fused_decode = (decode and mx_mode == "skinny" and not return_stages and proj_ok
                     and ops.dispatch_skinny_supported(t, c.top_k, c.latent_size, 2 * c.intermediate_size, self.L,
                                                       m_padded, True))
     act = None

@@ -606,6 +606,19 @@ def router_topk_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top
   return (idx, w, scores) if return_scores else (idx, w)
 
 
+ROUTER_PROJECT_MAX_LAT = 1024
+
+
+def router_topk_project_supported(e: int, lat: int) -> bool:
+  """Sizes ``router_topk_project`` takes when the router logits and the
+  latent projection are the column blocks [0, E) and [E, E + lat) of one
+  (T, E + lat) f32 GEMM output (the layer's fused router + down-projection):
+  at most 1024 latent columns, lat % 4 == 0, and E % 4 == 0, so that the
+  projection block starts 16-byte aligned and the row stride E + lat is a
+  multiple of 4.  These are the size checks of lmoe_router_topk_proj."""
+  return 0 < lat <= ROUTER_PROJECT_MAX_LAT and lat % 4 == 0 and e % 4 == 0
+
+
 def router_topk_project(logits: torch.Tensor, x: torch.Tensor, bias: torch.Tensor | None, top_k: int,
                         renormalize: bool = True, scaling: float = 1.0, act: str = "sigmoid",
                         weight_dtype: torch.dtype = torch.float32):
