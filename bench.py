@@ -286,8 +286,6 @@ def main():
   # that kernel at this workload (HBM bytes per launch), when there is one
   if args.mxfp4_mode == "scaled_mfma":
     kernel, traffic_file = "grouped_gemm_mx_kernel (MXFP8 x MXFP4 scaled MFMA, SiTU)", None
-  elif os.environ.get("LMOE_STREAM", "1") == "0":
-    kernel, traffic_file = "grouped_gemm_dma_kernel<MXFP4 tiled, SiTU> (one block per tile)", None
   else:
     kernel, traffic_file = ("grouped_gemm_stream_kernel<64, 256, MXFP4, SiTU> (fused gate/up + SiTU-GLU)",
                             "traffic_cfg5_gateup_mxfp4.json")

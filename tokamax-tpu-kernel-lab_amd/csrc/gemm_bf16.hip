@@ -19,8 +19,6 @@
 // range of the (m-tile, n-tile) work list, walked in groups of GM m-tiles
 // (n-tile outer, m-tile inner).  Blocks that run together on one XCD then share
 // A rows (and, with GM > 1, B columns) in that XCD's L2.
-#include <cstdlib>
-#include <cstring>
 #include <utility>
 
 #include "gemm_tile.h"
@@ -422,41 +420,20 @@ int launch(const Params& p, hipStream_t st, const char* name) {
 
 // Tile shape: BM = 64 measured best for every grouped and dense shape of the
 // BASELINE configs (two 4-wave blocks per CU; BM = 128 halves occupancy, BM =
-// 32 re-reads weights too often).  LMOE_GEMM_BM=32|64|128 overrides it.
-// LMOE_GEMM_BM=64|128 forces the m-tile height (tuning sweeps); unset = heuristic.
-int forced_bm() {
-  static const int v = [] {
-    const char* e = std::getenv("LMOE_GEMM_BM");
-    return e ? std::atoi(e) : 0;
-  }();
-  return v;
-}
-
+// 32 re-reads weights too often).
 template <int LAYOUT, int EPI>
 int dispatch_shape(const Params& p, hipStream_t st, const char* name) {
-  constexpr int S = 2;
-  const int bm = forced_bm();
-  if (bm == 32) return launch<32, 128, 2, 2, LAYOUT, EPI, S>(p, st, name);
-  if (bm == 128) return launch<128, 128, 2, 2, LAYOUT, EPI, S>(p, st, name);
-  return launch<64, 128, 2, 2, LAYOUT, EPI, S>(p, st, name);
+  return launch<64, 128, 2, 2, LAYOUT, EPI, 2>(p, st, name);
 }
 
 }  // namespace
 
 int run_dma(const Params& p, int layout, int epi, hipStream_t st, const char* name);
 
-// LMOE_GEMM_PATH=regs keeps k-contiguous bf16 weights on the register-staged
-// kernel above (for A/B timing); the default sends them to the DMA kernel.
-static bool use_dma_path() {
-  static const bool v = [] {
-    const char* e = std::getenv("LMOE_GEMM_PATH");
-    return !(e && std::strcmp(e, "regs") == 0);
-  }();
-  return v;
-}
-
+// bf16 weights with K % 64 == 0 go to the DMA kernel (faster on every
+// BASELINE shape); the register-staged kernel above takes the rest.
 int run_bf16(const Params& p, int layout, int epi, hipStream_t st, const char* name) {
-  if ((layout == kGNK || layout == kGKN) && p.K % 64 == 0 && use_dma_path()) return run_dma(p, layout, epi, st, name);
+  if ((layout == kGNK || layout == kGKN) && p.K % 64 == 0) return run_dma(p, layout, epi, st, name);
   if (layout == kGKN && epi == kEpiNone) return dispatch_shape<kGKN, kEpiNone>(p, st, name);
   if (layout == kGKN && epi == kEpiSitu) return dispatch_shape<kGKN, kEpiSitu>(p, st, name);
   if (layout == kGNK && epi == kEpiNone) return dispatch_shape<kGNK, kEpiNone>(p, st, name);

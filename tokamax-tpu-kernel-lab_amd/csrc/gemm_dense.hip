@@ -32,8 +32,6 @@
 // Tile order: tile t = mt * n_tiles + nt; XCD x (block b runs on XCD b % 8)
 // takes the contiguous range of tiles [x T / 8, (x + 1) T / 8), so an XCD
 // works on a few m-panels and reads each of their A rows from its own L2.
-#include <cstdlib>
-#include <cstring>
 
 #include "dma_util.h"
 #include "gemm_tile.h"
@@ -299,16 +297,7 @@ extern "C" int lmoe_dense(const void* x, const void* w_nk, int64_t M, int64_t K,
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(w_nk);
-  // LMOE_DENSE_CFG selects a variant for A/B measurements ("kg1": one wave
-  // per SIMD); the default is the two-group kernel
-  static const int kg1 = [] {
-    const char* e = std::getenv("LMOE_DENSE_CFG");
-    return e && std::strcmp(e, "kg1") == 0;
-  }();
-  if (kg1) {
-    if (out_dtype == LMOE_F32) return launch_dense<256, 128, 3, 1, true>(xp, wp, M, N, K, out, st);
-    return launch_dense<256, 128, 3, 1, false>(xp, wp, M, N, K, out, st);
-  }
+  // two wave groups (KG = 2): measured faster than one wave per SIMD
   if (out_dtype == LMOE_F32) return launch_dense<256, 128, 3, 2, true>(xp, wp, M, N, K, out, st);
   return launch_dense<256, 128, 3, 2, false>(xp, wp, M, N, K, out, st);
 }

@@ -32,8 +32,6 @@
 // (G, K/64, N, 32) and scales (G, K/64, N, 2), so that one step's weights for
 // a run of columns are one contiguous stretch of memory.  K % 64 == 0.
 #include <atomic>
-#include <cstdlib>
-#include <cstring>
 #include <type_traits>
 #include <utility>
 
@@ -1180,33 +1178,6 @@ int cu_count() {
   return cache[dev];
 }
 
-// LMOE_PERSIST=1 launches only as many blocks as fit on the device at once,
-// each looping over tiles; the default launches one block per tile (measured
-// equal or faster on the expert shapes, where the hardware's block refill
-// overlaps one block's epilogue with its neighbours' main loops).
-bool persistent_blocks() {
-  static const bool v = [] {
-    const char* e = std::getenv("LMOE_PERSIST");
-    return e && std::strcmp(e, "1") == 0;
-  }();
-  return v;
-}
-
-// XCD mapping of grouped problems (A/B timing): LMOE_XCD_MAP=mtile deals
-// m-tiles round-robin to the XCDs, =mrange gives each XCD a contiguous m-tile
-// range; the default stripes n-tiles over the XCDs when they divide evenly.
-enum XcdMap { kMapDefault = -1, kMapStripeN = 0, kMapMTile = 1, kMapMRange = 2 };
-XcdMap xcd_map() {
-  static const XcdMap v = [] {
-    const char* e = std::getenv("LMOE_XCD_MAP");
-    if (e && std::strcmp(e, "mtile") == 0) return kMapMTile;
-    if (e && std::strcmp(e, "mrange") == 0) return kMapMRange;
-    if (e && std::strcmp(e, "stripe") == 0) return kMapStripeN;
-    return kMapDefault;
-  }();
-  return v;
-}
-
 template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32, bool PIPE = false>
 int launch_dma(const Params& p, hipStream_t st, const char* name) {
   if constexpr (EPI == kEpiSitu && (BN / WN / MF) % 2 != 0) {
@@ -1225,17 +1196,12 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
     // XCD busy (at least one group each) with tall tiles
     const int64_t real_m = ceil_div(p.M, BM);
     while (gm > 1 && ceil_div(real_m, gm) < kXcds) gm /= 2;
-    const char* e = std::getenv("LMOE_DENSE_GM");
-    if (e && std::atoi(e) > 0) gm = std::atoi(e);
   }
   int64_t blocks = kXcds * ceil_div(ceil_div(mtiles, gm), kXcds) * gm * ntiles;
-  if (p.G > 1 && xcd_map() == kMapMRange) {
-    gm = -1;  // contiguous m-tile ranges per XCD
-    blocks = kXcds * (ceil_div(mtiles, kXcds) + 1) * ntiles;
-  } else if ((p.G > 1 || p.k_split > 1) && ntiles % kXcds == 0 &&
-             (xcd_map() == kMapStripeN || xcd_map() == kMapDefault)) {
+  if ((p.G > 1 || p.k_split > 1) && ntiles % kXcds == 0) {
     // n-tiles striped over the XCDs (split-K too: with few m-tiles the
-    // m-tile groups would leave most XCDs without work)
+    // m-tile groups would leave most XCDs without work); measured against
+    // round-robin m-tiles and per-XCD m-tile ranges, which were slower
     gm = 0;
     blocks = mtiles * ntiles;
   }
@@ -1251,27 +1217,14 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr_rc != hipSuccess)
     return fail(LMOE_ERR_HIP, "%s: LDS size attribute (%zu bytes): %s", name, lds, hipGetErrorString(attr_rc));
-  int64_t grid = blocks;
-  if (persistent_blocks()) {
-    const int64_t resident = kXcds * ((static_cast<int64_t>(cu_count()) * C::kLdsBlocks) / kXcds);
-    if (resident >= kXcds && resident < grid) grid = resident;
-  }
+  // one block per tile (measured equal to or faster than a persistent grid on
+  // the expert shapes: the hardware's block refill overlaps one block's
+  // epilogue with its neighbours' main loops)
   grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>
-      <<<dim3(static_cast<unsigned>(grid)), C::kThreads, lds, st>>>(p, ntiles, gm, blocks);
+      <<<dim3(static_cast<unsigned>(blocks)), C::kThreads, lds, st>>>(p, ntiles, gm, blocks);
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;
   }
-}
-
-// LMOE_STREAM=0 keeps the MXFP4 grouped GEMM on the one-block-per-tile
-// kernel (A/B timing); by default the streamed persistent kernel runs
-// wherever it applies.
-bool stream_enabled() {
-  static const bool v = [] {
-    const char* e = std::getenv("LMOE_STREAM");
-    return !(e && std::strcmp(e, "0") == 0);
-  }();
-  return v;
 }
 
 // The streamed persistent kernel: bf16 output, and the LDS tile table
@@ -1282,7 +1235,7 @@ template <int BM, int BN, int EPI, int NS, int MF>
 int try_stream(const Params& p, hipStream_t st, const char* name, int* rc) {
   using S = SCfg<BM, BN, EPI, NS, MF>;
   using C = typename S::C;
-  if (!stream_enabled() || p.G < 1 || p.M == 0) return 0;
+  if (p.G < 1 || p.M == 0) return 0;
   if (EPI != kEpiSitu && p.out_dtype != LMOE_BF16) return 0;
   const int64_t ring = static_cast<int64_t>(NS) * C::kSlot;
   const int64_t lds = ring + ((8 * (p.G + 1) + 15) / 16) * 16 + (p.a_index ? S::kIdxBytes : 0);
@@ -1294,14 +1247,10 @@ int try_stream(const Params& p, hipStream_t st, const char* name, int* rc) {
   int gm = p.G == 1 ? 4 : 1;
   int64_t blocks = kXcds * ceil_div(ceil_div(mtiles, gm), kXcds) * gm * ntiles;
   // grouped problems: n-tiles striped over the XCDs (each weight slice read
-  // by one XCD; measured fastest at config 5, 137.8 us for the gate/up).
-  // LMOE_XCD_MAP=mrange gives each XCD a balanced contiguous m-tile range
-  // instead: 21% less HBM traffic (297 against 377 MB for the gate/up) but
-  // 4% slower on the same box.
-  if (p.G > 1 && xcd_map() == kMapMRange) {
-    gm = -1;
-    blocks = kXcds * (ceil_div(mtiles, kXcds) + 1) * ntiles;
-  } else if (p.G > 1 && ntiles % kXcds == 0 && xcd_map() != kMapMTile) {
+  // by one XCD; measured fastest at config 5, 137.8 us for the gate/up).  A
+  // balanced contiguous m-tile range per XCD (gm < 0) moved 21% less HBM
+  // traffic (297 against 377 MB for the gate/up) but measured 4% slower.
+  if (p.G > 1 && ntiles % kXcds == 0) {
     gm = 0;
     blocks = mtiles * ntiles;
   }
@@ -1366,101 +1315,34 @@ __global__ __launch_bounds__(256) void tile_mxfp4_kernel(const uint8_t* __restri
   }
 }
 
-// Tile shape / ring depth of the MXFP4 kernel: LMOE_DMA_CFG = "BMxBNxNS"
-// picks one of the instantiated variants ("p": fragments read one step
-// ahead), LMOE_MFMA=16 the 16x16x32 MFMA instead of 32x32x16 (tuning
-// sweeps).  The defaults are chosen in run_mx_shape.
-int mx_variant() {
-  static const int v = [] {
-    const char* e = std::getenv("LMOE_DMA_CFG");
-    if (!e) return -1;
-    const char* names[] = {"64x128x4", "64x128x6", "64x256x4", "64x256x3", "64x128x3", "32x128x4", "32x256x4",
-                           "64x256x5", "128x256x3", "128x128x4", "64x256x4p", "128x256x2", "128x128x3"};
-    for (int i = 0; i < 13; ++i)
-      if (std::strcmp(e, names[i]) == 0) return i;
-    return -1;
-  }();
-  return v;
-}
-
-bool mfma16() {
-  static const bool v = [] {
-    const char* e = std::getenv("LMOE_MFMA");
-    return e && std::strcmp(e, "16") == 0;
-  }();
-  return v;
-}
-
-template <int EPI, int MF>
-int run_mx_shape(const Params& p, hipStream_t st, const char* name) {
-  // Defaults, from sweeps on the LatentMoE expert shapes: the streamed
-  // kernel with 64x256 tiles and a 3-deep ring (3 blocks per CU) where it
-  // applies, else the one-block-per-tile kernel with 64x256 tiles, ring depth
-  // 3 for the fused gate/up and 4 for the down projection.
-  int v = mx_variant();
-  int rc = LMOE_OK;
-  if (p.a_index) {
-    // gathered rows: the streamed kernel only
-    if constexpr (MF == 32) {
-      if (try_stream<64, 256, EPI, 3, MF>(p, st, name, &rc)) return rc;
-    }
-    return fail(LMOE_ERR_UNSUPPORTED, "%s: gathered rows need the streamed 64x256 kernel", name);
-  }
-  if ((v < 0 || v == 3) && try_stream<64, 256, EPI, 3, MF>(p, st, name, &rc)) return rc;
-  if (v == 2 && try_stream<64, 256, EPI, 4, MF>(p, st, name, &rc)) return rc;
-  if (v < 0) v = EPI == kEpiSitu ? 3 : 2;
-  switch (v) {
-    case 1: return launch_dma<64, 128, kDMX, EPI, 6, 1, 4, MF>(p, st, name);
-    case 2: return launch_dma<64, 256, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
-    case 3: return launch_dma<64, 256, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
-    case 4: return launch_dma<64, 128, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
-    case 5: return launch_dma<32, 128, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
-    case 6: return launch_dma<32, 256, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
-    case 7: return launch_dma<64, 256, kDMX, EPI, 5, 1, 4, MF>(p, st, name);
-    case 8: return launch_dma<128, 256, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
-    case 9: return launch_dma<128, 128, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
-    case 10: return launch_dma<64, 256, kDMX, EPI, 4, 1, 4, MF, true>(p, st, name);
-    case 11: return launch_dma<128, 256, kDMX, EPI, 2, 1, 4, MF>(p, st, name);
-    case 12: return launch_dma<128, 128, kDMX, EPI, 3, 1, 4, MF>(p, st, name);
-    default: return launch_dma<64, 128, kDMX, EPI, 4, 1, 4, MF>(p, st, name);
-  }
-}
-
+// Tile shapes of the MXFP4 kernel, from sweeps on the LatentMoE expert shapes
+// (64x128 / 64x256 / 128x128 / 128x256 / 32x128 / 32x256 tiles, ring depths
+// 2-6, 16x16x32 against 32x32x16 MFMAs, fragments read one step ahead): the
+// streamed kernel with 64x256 tiles and a 3-deep ring (3 blocks per CU) where
+// it applies, else the one-block-per-tile kernel with 64x256 tiles, ring depth
+// 3 for the fused gate/up and 4 for the down projection.
 template <int EPI>
 int run_mx(const Params& p, hipStream_t st, const char* name) {
-  return mfma16() ? run_mx_shape<EPI, 16>(p, st, name) : run_mx_shape<EPI, 32>(p, st, name);
+  int rc = LMOE_OK;
+  if (try_stream<64, 256, EPI, 3, 32>(p, st, name, &rc)) return rc;
+  // gathered rows: the streamed kernel only
+  if (p.a_index) return fail(LMOE_ERR_UNSUPPORTED, "%s: gathered rows need the streamed 64x256 kernel", name);
+  if constexpr (EPI == kEpiSitu)
+    return launch_dma<64, 256, kDMX, EPI, 3, 1, 4, 32>(p, st, name);
+  else
+    return launch_dma<64, 256, kDMX, EPI, 4, 1, 4, 32>(p, st, name);
 }
 
-// Tile shape of the bf16 (GNK) kernel: LMOE_GNK_CFG picks a variant
-// "BMxBNxNS_WMxWN_MF" (tuning sweeps); the defaults are the sweep winners on
-// the LatentMoE dense projections and bf16 expert shapes.
-int gnk_variant() {
-  static const int v = [] {
-    const char* e = std::getenv("LMOE_GNK_CFG");
-    if (!e) return -1;
-    const char* names[] = {"64x128x3_1x4_16", "64x128x3_1x4_32", "128x128x2_2x2_32", "128x128x3_2x2_32",
-                           "128x256x2_2x4_32", "64x256x2_1x4_32", "128x128x2_1x4_32"};
-    for (int i = 0; i < 7; ++i)
-      if (std::strcmp(e, names[i]) == 0) return i;
-    return -1;
-  }();
-  return v;
-}
-
+// Tile shapes of the bf16 (GNK) kernel, the sweep winners on the LatentMoE
+// dense projections and bf16 expert shapes: 128x128 tiles of 2x2 waves for a
+// short K (the 1024-deep up-projection as one group), else 64x128 tiles of
+// 1x4 waves on 16x16x32 MFMAs.
 template <int EPI>
 int run_gnk(const Params& p, hipStream_t st, const char* name) {
-  int v = gnk_variant();
-  // short K (the 1024-deep up-projection): 128x128 tiles of 2x2 waves
-  if (v < 0) v = (EPI == kEpiNone && p.K <= 1024 && p.G == 1) ? 2 : 0;
-  switch (v) {
-    case 1: return launch_dma<64, 128, kDGNK, EPI, 3, 1, 4, 32>(p, st, name);
-    case 2: return launch_dma<128, 128, kDGNK, EPI, 2, 2, 2, 32>(p, st, name);
-    case 3: return launch_dma<128, 128, kDGNK, EPI, 3, 2, 2, 32>(p, st, name);
-    case 4: return launch_dma<128, 256, kDGNK, EPI, 2, 2, 4, 32>(p, st, name);
-    case 5: return launch_dma<64, 256, kDGNK, EPI, 2, 1, 4, 32>(p, st, name);
-    case 6: return launch_dma<128, 128, kDGNK, EPI, 2, 1, 4, 32>(p, st, name);
-    default: return launch_dma<64, 128, kDGNK, EPI, 3, 1, 4, 16>(p, st, name);
+  if constexpr (EPI == kEpiNone) {
+    if (p.K <= 1024 && p.G == 1) return launch_dma<128, 128, kDGNK, EPI, 2, 2, 2, 32>(p, st, name);
   }
+  return launch_dma<64, 128, kDGNK, EPI, 3, 1, 4, 16>(p, st, name);
 }
 
 // Split-K reduction: out = epilogue(plane 0 + plane 1 + ... + plane S-1),
@@ -1513,34 +1395,13 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   }
 }
 
-// Tile shape of the bf16 (G, K, N) kernel: LMOE_GKN_CFG picks a variant
-// "BMxBNxNS_WMxWN" (tuning sweeps); 32x32 MFMAs throughout.
-int gkn_variant() {
-  static const int v = [] {
-    const char* e = std::getenv("LMOE_GKN_CFG");
-    if (!e) return -1;
-    const char* names[] = {"64x128x3_1x4", "128x128x2_2x2", "128x128x3_2x2", "64x256x2_1x4", "128x256x2_2x4"};
-    for (int i = 0; i < 5; ++i)
-      if (std::strcmp(e, names[i]) == 0) return i;
-    return -1;
-  }();
-  return v;
-}
-
+// The bf16 (G, K, N) kernel: 128x256 tiles of 2x4 waves, 32x32 MFMAs
+// (config 2, the reference-layout ragged_dot: 71.8 us, the speed of the
+// prepared (G, N, K) layout; 64x128 tiles 77.2 us; 128x128 and 64x256 tiles
+// slower; transpose + (G, N, K) kernel 118.2 us).
 template <int EPI>
 int run_gkn(const Params& p, hipStream_t st, const char* name) {
-  // default: 128x256 tiles of 2x4 waves (config 2, the reference-layout
-  // ragged_dot: 71.8 us, the speed of the prepared (G, N, K) layout; 64x128
-  // tiles 77.2 us; transpose + (G, N, K) kernel 118.2 us)
-  int v = gkn_variant();
-  if (v < 0) v = 4;
-  switch (v) {
-    case 1: return launch_dma<128, 128, kDGKN, EPI, 2, 2, 2, 32>(p, st, name);
-    case 2: return launch_dma<128, 128, kDGKN, EPI, 3, 2, 2, 32>(p, st, name);
-    case 3: return launch_dma<64, 256, kDGKN, EPI, 2, 1, 4, 32>(p, st, name);
-    case 4: return launch_dma<128, 256, kDGKN, EPI, 2, 2, 4, 32>(p, st, name);
-    default: return launch_dma<64, 128, kDGKN, EPI, 3, 1, 4, 32>(p, st, name);
-  }
+  return launch_dma<128, 256, kDGKN, EPI, 2, 2, 4, 32>(p, st, name);
 }
 
 }  // namespace

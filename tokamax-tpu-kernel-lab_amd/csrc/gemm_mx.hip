@@ -21,8 +21,6 @@
 // and block: A codes BM x 128 B (rows XOR-swizzled in 16-byte chunks), A scales
 // BM x 4 B (one dword DMA lane per row), B = the two 64-k records of the
 // k-step-major MXFP4 layout (lmoe_mxfp4_tile), B scales 2 x BN x 2 B.
-#include <cstdlib>
-#include <cstring>
 
 #include "dma_util.h"
 #include "gemm_tile.h"
@@ -356,14 +354,6 @@ void grouped_gemm_mx_kernel(Params p, int64_t n_tiles, int gm) {
   }
 }
 
-bool xcd_stripe_n_mx() {
-  static const bool v = [] {
-    const char* e = std::getenv("LMOE_XCD_MAP");
-    return !(e && std::strcmp(e, "mtile") == 0);
-  }();
-  return v;
-}
-
 template <int BM, int BN, int EPI, int NS>
 int launch_mx(const Params& p, hipStream_t st, const char* name) {
   using C = XCfg<BM, BN, EPI, NS>;
@@ -374,7 +364,9 @@ int launch_mx(const Params& p, hipStream_t st, const char* name) {
   if (ntiles == 0 || p.M == 0) return LMOE_OK;
   int gm = p.G == 1 ? 4 : 1;
   int64_t blocks = kXcds * ceil_div(ceil_div(mtiles, gm), kXcds) * gm * ntiles;
-  if (p.G > 1 && ntiles % kXcds == 0 && xcd_stripe_n_mx()) {
+  // grouped problems: n-tiles striped over the XCDs (each weight slice read
+  // by one XCD), as in the bf16-dequant kernels
+  if (p.G > 1 && ntiles % kXcds == 0) {
     gm = 0;
     blocks = mtiles * ntiles;
   }

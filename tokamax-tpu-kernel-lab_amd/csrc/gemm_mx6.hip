@@ -37,8 +37,6 @@
 // their 16-byte chunks rotated by one position for rows 8..15 and 24..31 of
 // every 32: the three 8-byte reads that fetch a lane's 24-byte run then fall
 // on all 64 banks twice (the minimum for 512 bytes).
-#include <cstdlib>
-#include <cstring>
 
 #include "dma_util.h"
 #include "gemm_tile.h"
@@ -388,27 +386,11 @@ int launch_mx6(const Params& p, hipStream_t st, const char* name) {
   return LMOE_OK;
 }
 
-// Tile shape: LMOE_MX6_CFG = "BMxBN_WMxWN_NS" picks an instantiated variant
-// (tuning sweeps).
-int mx6_variant() {
-  static const int v = [] {
-    const char* e = std::getenv("LMOE_MX6_CFG");
-    if (!e) return -1;
-    const char* names[] = {"128x128_2x2_3", "256x128_4x2_3", "256x128_4x2_2", "256x256_4x2_2"};
-    for (int i = 0; i < 4; ++i)
-      if (std::strcmp(e, names[i]) == 0) return i;
-    return -1;
-  }();
-  return v;
-}
-
+// Tile shape: 128x128 tiles of 2x2 waves with a 3-deep ring (swept against
+// 256x128 with 2- and 3-deep rings and 256x256 with a 2-deep ring; 256x256
+// is faster only from M = 8192 on).
 int run_mx6(const Params& p, hipStream_t st, const char* name) {
-  switch (mx6_variant()) {
-    case 1: return launch_mx6<256, 128, 4, 2, 3>(p, st, name);
-    case 2: return launch_mx6<256, 128, 4, 2, 2>(p, st, name);
-    case 3: return launch_mx6<256, 256, 4, 2, 2>(p, st, name);
-    default: return launch_mx6<128, 128, 2, 2, 3>(p, st, name);
-  }
+  return launch_mx6<128, 128, 2, 2, 3>(p, st, name);
 }
 
 }  // namespace

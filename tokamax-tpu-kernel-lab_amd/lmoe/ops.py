@@ -13,7 +13,6 @@ stream; nothing falls back to torch or the CPU.
 from __future__ import annotations
 
 import math
-import os
 from typing import NamedTuple
 
 import torch
@@ -109,22 +108,13 @@ def ragged_dot(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor, 
   if rhs.dtype != lhs.dtype:
     raise NotImplementedError(f"mixed lhs {lhs.dtype} / rhs {rhs.dtype}")
   out_dtype = preferred_element_type or lhs.dtype
-  if (_GKN_VIA_TRANSPOSE and layout == _lib.RHS_GKN and lhs.dtype == torch.bfloat16 and k % 64 == 0
-      and n % 8 == 0):
-    # A/B timing only: transpose the reference-layout weights into the
-    # k-contiguous layout first (lmoe_transpose), then the (G, N, K) kernel.
-    # The default reads (G, K, N) tiles as they lie and transposes them in
-    # LDS (ds_read_b64_tr_b16).
-    rhs_t = torch.empty((g, n, k), dtype=rhs.dtype, device=rhs.device)
-    check(lib().lmoe_transpose(_p(rhs), g, k, n, 2, _p(rhs_t), _stream()), "transpose")
-    rhs, layout = rhs_t, _lib.RHS_GNK
+  # reference-layout (G, K, N) weights are read as they lie: the kernel
+  # transposes each B tile in LDS (ds_read_b64_tr_b16), as fast as prepared
+  # (G, N, K) weights and faster than transposing them first
   out = torch.empty((m, n), dtype=out_dtype, device=lhs.device)
   check(lib().lmoe_ragged_dot(_p(lhs), _dt(lhs), _p(rhs), layout, _p(group_sizes), m, k, n, g,
                               zero_group, _p(out), _dt(out), _stream()), "ragged_dot")
   return out
-
-
-_GKN_VIA_TRANSPOSE = os.environ.get("LMOE_GKN_TRANSPOSE") == "1"
 
 
 def parse_fused_activation(spec: str) -> tuple[float, float]:
@@ -676,13 +666,6 @@ def _ones_group(m: int, device) -> torch.Tensor:
 _DENSE_BACKENDS = ("auto", "hip", "dense", "blaslt", "skinny")
 
 
-def _dense_backend_default() -> str:
-  b = os.environ.get("LMOE_DENSE", "auto")
-  if b not in _DENSE_BACKENDS:
-    raise ValueError(f"LMOE_DENSE={b!r}: one of {_DENSE_BACKENDS}")
-  return b
-
-
 # The skinny dense kernel's parallelism is one block per 16 output columns:
 # measured against hipBLASLt at M = 1..16 it wins from N = 4096 on (the
 # decode up-projection, 7168 columns: 5.4 vs 6.4 us) and loses below (the
@@ -698,13 +681,13 @@ def dense(x: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None
   ``backend``: "hip" runs it as a one-group grouped GEMM on the hand-written
   kernels; "blaslt" calls hipBLASLt (the ROCm library GEMM; (N, K) weights
   only); "skinny" the hand-written few-row kernel (bf16 (N, K) weights,
-  K % 128 == 0, N % 16 == 0).  "auto" (default, or $LMOE_DENSE), for bf16
+  K % 128 == 0, N % 16 == 0).  "auto" (the default), for bf16
   (N, K) weights -- the layer's router logits (f32 out), down- and
   up-projections: the skinny kernel for at most SKINNY_DENSE_ROWS rows and
   N >= SKINNY_DENSE_MIN_N, else hipBLASLt; for other weights the hand-written
   grouped kernels.  All accumulate the exact bf16 products in f32; only the
   summation order differs."""
-  backend = backend or _dense_backend_default()
+  backend = backend or "auto"
   if backend not in _DENSE_BACKENDS:
     raise ValueError(f"backend {backend!r}")
   out_dtype = out_dtype or x.dtype
