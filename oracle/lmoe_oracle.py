@@ -601,6 +601,7 @@ def single_shard_forward(hidden, w: dict, shard_gate, shard_up, shard_down, conf
     r = router_from_logits(logits, w["e_score_correction_bias"], config.top_k, config.moe_renormalize,
                            config.routed_scaling_factor, act, dtype)
   stages["router_logits"] = logits
+  stages["router_scores_for_choice"] = r.scores_for_choice
   stages["topk_idx"] = r.topk_idx
   stages["topk_weight"] = r.topk_weight
   d = filter_and_pad_to_shard_jittable(r.topk_idx, r.topk_weight, x, config.top_k,
