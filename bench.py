@@ -12,7 +12,13 @@ kernel (the MXFP4 gate/up grouped GEMM, timed in place with HIP events on its
 stream) and the CPU baseline (the oracle's restatement of the reference
 forward on a bounded token sample, timed on this host).
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--mxfp4-mode lds_dequant]
+  python bench.py [--steps K] [--warmup W] [--rounds R] [--gpus 1] [--mxfp4-mode lds_dequant]
+
+Timing: W warm-up steps, then K timed steps of each execution (HIP-graph
+replays of the whole layer, eager launches) in R rounds whose candidate order
+rotates; ms_per_step is the median over rounds of the graph replays' per-step
+time (hw_session_common.py:120-175's protocol), with the per-call median
+beside it.  The CPU baseline: one warm-up run, then the median of >= 5 runs.
 """
 
 import argparse
@@ -58,14 +64,93 @@ def load_traffic(name):
 
 
 def cpu_model() -> str:
+  """The host CPU as lscpu names it (its model name and, where the firmware
+  reports one, the BIOS model name), with the family / model / stepping
+  numbers from /proc/cpuinfo, which identify the part when a virtualised host
+  hides the model number."""
+  import subprocess
+  names = []
+  try:
+    out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+    for line in out.splitlines():
+      key, _, val = line.partition(":")
+      if key.strip() in ("Model name", "BIOS Model name") and val.strip() and val.strip() not in names:
+        names.append(val.strip())
+  except (OSError, subprocess.SubprocessError):
+    pass
+  ids = {}
   try:
     with open("/proc/cpuinfo") as f:
       for line in f:
-        if line.startswith("model name"):
-          return line.split(":", 1)[1].strip()
+        key, _, val = line.partition(":")
+        key = key.strip()
+        if key == "model name" and val.strip() not in names:
+          names.append(val.strip())
+        if key in ("cpu family", "model", "stepping") and key not in ids:
+          ids[key] = val.strip()
+        if not line.strip() and ids:
+          break
   except OSError:
     pass
-  return "unknown"
+  name = " / ".join(names) or "unknown"
+  if ids:
+    name += " (" + ", ".join(f"{k} {v}" for k, v in ids.items()) + ")"
+  return name
+
+
+def cpu_threads() -> tuple[int, int]:
+  """(threads to use, cores in this process's affinity mask): the affinity
+  mask, capped by OMP_NUM_THREADS where the host sets one (the share of a
+  shared box's CPUs that one job may use)."""
+  affinity = len(os.sched_getaffinity(0))
+  cap = os.environ.get("OMP_NUM_THREADS", "")
+  threads = min(affinity, int(cap)) if cap.isdigit() and int(cap) > 0 else affinity
+  return threads, affinity
+
+
+def rotated_rounds(candidates, steps, rounds, new_event, synchronize):
+  """``steps`` calls of every candidate, in ``rounds`` rounds; within a round
+  each candidate runs its share of calls back to back, timed by two events
+  on the current stream between device synchronisations, and the candidate
+  order rotates from round to round, so slow drifts of the device (clock,
+  temperature) fall on every candidate alike (the protocol of
+  hw_session_common.py:120-175).  ``candidates`` maps a name to a function of
+  the call index; returns, per name, the per-call milliseconds of each round
+  (pipelined: one event pair around the round's calls)."""
+  rounds = max(1, min(rounds, steps))
+  sizes = [steps // rounds + (1 if r < steps % rounds else 0) for r in range(rounds)]
+  names = list(candidates)
+  per = {n: [] for n in names}
+  done = {n: 0 for n in names}
+  for r, size in enumerate(sizes):
+    for i in range(len(names)):
+      name = names[(r + i) % len(names)]
+      fn = candidates[name]
+      synchronize()
+      start, end = new_event(), new_event()
+      start.record()
+      for j in range(size):
+        fn(done[name] + j)
+      end.record()
+      synchronize()
+      per[name].append(start.elapsed_time(end) / size)
+      done[name] += size
+  return per
+
+
+def per_call(fn, calls, new_event, synchronize):
+  """Milliseconds of single calls, each between device synchronisations and
+  timed by its own event pair."""
+  out = []
+  for i in range(calls):
+    synchronize()
+    start, end = new_event(), new_event()
+    start.record()
+    fn(i)
+    end.record()
+    synchronize()
+    out.append(start.elapsed_time(end))
+  return out
 
 
 def oracle_inputs(layer, hidden, w, c):
@@ -92,28 +177,31 @@ def cpu_baseline(inputs, c, sample_tokens, reps):
   the same weights, ``sample_tokens`` of the 4096 tokens, median of ``reps``
   runs.  Returns (baseline dict, the last run's (output, stages))."""
   from oracle import lmoe_oracle as O
+  import contextlib
+  threads, affinity = cpu_threads()
   try:
-    from threadpoolctl import threadpool_info
-    threads = max((i.get("num_threads", 1) for i in threadpool_info()), default=1)
+    from threadpoolctl import threadpool_limits
+    limits = threadpool_limits(limits=threads)
   except Exception:  # noqa: BLE001
-    threads = len(os.sched_getaffinity(0))
+    limits = contextlib.nullcontext()
   h, wd, gate, up, down = inputs
   h = h[:sample_tokens]
   cfg = c.config()
   run = lambda: O.single_shard_forward(h, wd, gate, up, down, cfg, "bf16", c.local_start, c.local_experts,
                                        c.capacity_factor, include_shared=False)
-  res = run()
   times = []
-  for _ in range(reps):
-    t0 = time.perf_counter()
+  with limits:
     res = run()
-    times.append(time.perf_counter() - t0)
+    for _ in range(reps):
+      t0 = time.perf_counter()
+      res = run()
+      times.append(time.perf_counter() - t0)
   med = statistics.median(times)
   return {"value": round(sample_tokens / med, 2), "unit": "tokens/s", "cores": int(threads),
-          "cpu_model": cpu_model(), "kind": "port",
+          "affinity_cores": int(affinity), "cpu_model": cpu_model(), "kind": "port",
           "sample": f"{sample_tokens} of {c.tokens} tokens through the numpy oracle's single-shard "
-                    f"forward (all stages, bf16 rounding emulated), median of {reps} runs "
-                    f"({med:.2f} s each)"}, res
+                    f"forward (all stages, bf16 rounding emulated), one warm-up run, then the median of "
+                    f"{reps} runs ({med:.2f} s each; min {min(times):.2f}, max {max(times):.2f} s)"}, res
 
 
 def parity(inputs, c, out, st, own):
@@ -189,9 +277,10 @@ def main():
   ap.add_argument("--gpus", type=int, default=1)
   ap.add_argument("--steps", type=int, default=100)
   ap.add_argument("--warmup", type=int, default=20)
+  ap.add_argument("--rounds", type=int, default=10, help="timing rounds the steps are split into")
   ap.add_argument("--mxfp4-mode", default="lds_dequant", choices=["lds_dequant", "scaled_mfma"])
   ap.add_argument("--cpu-sample-tokens", type=int, default=4096)
-  ap.add_argument("--cpu-reps", type=int, default=3)
+  ap.add_argument("--cpu-reps", type=int, default=5)
   ap.add_argument("--no-cpu-baseline", action="store_true")
   ap.add_argument("--eager", action="store_true",
                   help="time eager launches instead of replays of the layer captured as one HIP graph")
@@ -230,36 +319,43 @@ def main():
   for _ in range(args.warmup):
     layer.forward(hidden)
   torch.cuda.synchronize()
-  # eager steps with events around the two expert GEMMs (their in-layer times)
+  graph = None if args.eager else capture_layer(torch, layer, hidden)
+  if graph is not None:
+    replay = graph[0]
+    for _ in range(args.warmup):
+      replay()
+    torch.cuda.synchronize()
+  # Timed: `steps` calls of each execution (graph replays of the whole layer,
+  # eager launches) in rotated rounds; the eager steps record events around
+  # the two expert GEMMs (their in-layer times)
   events = [{k: (torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for k in ("gateup", "down")}
             for _ in range(args.steps)]
+  candidates = {"eager": lambda i: layer.forward(hidden, kernel_events=events[i])}
+  if graph is not None:
+    candidates = {"graph": lambda i: replay(), **candidates}
+  main_exec = "graph" if graph is not None else "eager"
+  new_event = lambda: torch.cuda.Event(enable_timing=True)
   t0 = time.perf_counter()
-  for i in range(args.steps):
-    layer.forward(hidden, kernel_events=events[i])
-  torch.cuda.synchronize()
-  t1 = time.perf_counter()
-  eager_ms = (t1 - t0) * 1000.0 / args.steps
-  gateup_ms = statistics.mean(e["gateup"][0].elapsed_time(e["gateup"][1]) for e in events)
-  down_ms = statistics.mean(e["down"][0].elapsed_time(e["down"][1]) for e in events)
-  log(f"eager: {eager_ms:.3f} ms/step, gate/up kernel {gateup_ms * 1000:.1f} us, down kernel {down_ms * 1000:.1f} us")
-
-  execution = "eager launches"
-  ms_per_step = eager_ms
-  if not args.eager:
-    graph = capture_layer(torch, layer, hidden)
-    if graph is not None:
-      replay, out = graph
-      for _ in range(args.warmup):
-        replay()
-      torch.cuda.synchronize()
-      t0 = time.perf_counter()
-      for _ in range(args.steps):
-        replay()
-      torch.cuda.synchronize()
-      t1 = time.perf_counter()
-      ms_per_step = (t1 - t0) * 1000.0 / args.steps
-      execution = "HIP-graph replay of the whole layer (captured once; replays checked bit-exact against eager)"
-      log(f"graph replay: {ms_per_step:.3f} ms/step")
+  per = rotated_rounds(candidates, args.steps, args.rounds, new_event, torch.cuda.synchronize)
+  wall_s = time.perf_counter() - t0
+  ms_per_step = statistics.median(per[main_exec])
+  eager_ms = statistics.median(per["eager"])
+  single = per_call((lambda i: replay()) if graph is not None else (lambda i: layer.forward(hidden)),
+                    min(args.steps, 50), new_event, torch.cuda.synchronize)
+  gateup_ms = statistics.median(e["gateup"][0].elapsed_time(e["gateup"][1]) for e in events)
+  down_ms = statistics.median(e["down"][0].elapsed_time(e["down"][1]) for e in events)
+  execution = ("HIP-graph replay of the whole layer (captured once; replays checked bit-exact against eager)"
+               if graph is not None else "eager launches")
+  timing = {"protocol": f"{len(per[main_exec])} rounds, candidates {list(candidates)} rotated per round, "
+                        "each round's calls back to back between device synchronisations, HIP events; "
+                        "ms_per_step = median over rounds",
+            "rounds_ms_per_step": [round(v, 4) for v in per[main_exec]],
+            "pipelined_mean_ms": round(statistics.mean(per[main_exec]), 4),
+            "per_call_median_ms": round(statistics.median(single), 4), "per_call_calls": len(single),
+            "eager_pipelined_median_ms": round(eager_ms, 4), "wall_s": round(wall_s, 3)}
+  log(f"{main_exec}: {ms_per_step:.4f} ms/step (median of {len(per[main_exec])} rounds; per call "
+      f"{timing['per_call_median_ms']:.4f}), eager {eager_ms:.4f} ms/step, gate/up kernel "
+      f"{gateup_ms * 1000:.1f} us, down kernel {down_ms * 1000:.1f} us")
   tokens_per_s = c.tokens / (ms_per_step / 1000.0)
 
   # the timed forward (no stage outputs: gathered-row expert GEMM, no sorted
@@ -327,7 +423,7 @@ def main():
                  "m_padded": m_padded, "routed_rows": rows, "router_skew": "zipf(1.2) on logits",
                  "shared_experts": 0, "parallelism": "single GPU (one expert shard)",
                  "execution": execution, "eager_ms_per_step": round(eager_ms, 4)},
-      "roofline": roofline, "grouped_gemm": grouped, "cpu_baseline": cpu, "parity": par,
+      "timing": timing, "roofline": roofline, "grouped_gemm": grouped, "cpu_baseline": cpu, "parity": par,
   }
   print(json.dumps(line), flush=True)
 
