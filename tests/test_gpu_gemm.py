@@ -75,6 +75,31 @@ def test_ragged_dot_matches_oracle(gpu_device, name, m, k, n, g, spec, layout, d
   assert np.all(out[tail:] == 0)
 
 
+@pytest.mark.parametrize("dt", ["f32", "bf16"])
+@pytest.mark.parametrize("dist", ["uniform", "mild_skew", "heavy_skew", "empty_groups", "single_dominant"])
+@pytest.mark.parametrize("shape", ["small", "medium_a", "medium_b"])
+def test_ragged_dot_harness_matrix(gpu_device, shape, dist, dt):
+  """The reference's ragged_dot correctness matrix (benchmark_harness.py:100-205):
+  its three shapes x its five group distributions, in its call shape (lhs
+  (M, K), rhs (G, K, N), both N(0, 1)), checked as check_correctness does
+  (max|out - ref| / max|ref|; bf16 against 2e-2, f32 here against 1e-5
+  instead of the harness's 1e-4), against the oracle's ragged_dot."""
+  from lmoe import ops
+  from lmoe import workloads as W
+  m, k, n, g = W.HARNESS_SHAPES[shape]
+  banner(f"ragged_dot harness {shape} {dist} {dt}")
+  gs = W.harness_group_sizes(m, g, dist, seed=0)
+  rng = np.random.default_rng(m + g)
+  lhs = O.cast(rng.standard_normal((m, k)), dt)
+  rhs = O.cast(rng.standard_normal((g, k, n)), dt)
+  ref = O.ragged_dot(lhs, rhs, gs, dt)
+  out = to_np(ops.ragged_dot(to_dev(lhs, dt), to_dev(rhs, dt), to_dev(gs)))
+  assert out.shape == ref.shape
+  err = max_rel(out, ref)
+  banner(f"  group sizes {gs.tolist()} max-rel {err:.2e}")
+  assert err <= (BF16_TOL if dt == "bf16" else F32_TOL)
+
+
 def test_ragged_dot_config2_full(gpu_device):
   """BASELINE config 2 at full size: M=8192, K=2048, N=1024, G=32 Zipf(1.1)."""
   from lmoe import ops

@@ -39,6 +39,39 @@ def test_zipf_group_sizes():
   assert gs.max() > 4 * 8192 / 32  # skewed
 
 
+def test_harness_distributions_are_the_reference_vectors():
+  """benchmark_harness.py:116-150, written out for G = 4: mild skew doubles
+  group 0's weight, heavy skew gives it weight G, empty_groups zeroes the
+  second half, single_dominant puts everything in group 0."""
+  assert W.harness_distribution("uniform", 4) is None
+  assert W.harness_distribution("mild_skew", 4) == [2 / 5, 1 / 5, 1 / 5, 1 / 5]
+  assert W.harness_distribution("heavy_skew", 4) == [4 / 7, 1 / 7, 1 / 7, 1 / 7]
+  assert W.harness_distribution("empty_groups", 4) == [0.5, 0.5, 0.0, 0.0]
+  assert W.harness_distribution("empty_groups", 1) == [1.0]
+  assert W.harness_distribution("single_dominant", 4) == [1.0, 0.0, 0.0, 0.0]
+  with pytest.raises(ValueError):
+    W.harness_distribution("zipf", 4)
+
+
+@pytest.mark.parametrize("shape", list(W.HARNESS_SHAPES))
+@pytest.mark.parametrize("dist", W.HARNESS_DISTRIBUTIONS)
+def test_harness_group_sizes(shape, dist):
+  m, _, _, g = W.HARNESS_SHAPES[shape]
+  gs = W.harness_group_sizes(m, g, dist, seed=5)
+  assert gs.dtype == np.int32 and gs.shape == (g,) and gs.sum() == m and gs.min() >= 0
+  assert np.array_equal(gs, W.harness_group_sizes(m, g, dist, seed=5))  # seeded
+  if dist == "uniform":
+    assert gs.max() - gs.min() <= 1
+  if dist == "empty_groups":
+    assert np.all(gs[g // 2:] == 0) and np.all(gs[: g // 2] > 0)
+  if dist == "single_dominant":
+    assert gs[0] == m
+  if dist in ("mild_skew", "heavy_skew"):
+    # group 0's share within 5 binomial sigmas of its probability
+    p0 = W.harness_distribution(dist, g)[0]
+    assert abs(gs[0] - m * p0) <= 5 * np.sqrt(m * p0 * (1 - p0))
+
+
 def test_global_picks_uniform_without_replacement():
   """Every token's picks are distinct, and over many tokens each expert is
   picked T*k/E times within a chi-square bound (uniform draw)."""

@@ -5,7 +5,7 @@ warm-up, then rounds of back-to-back calls timed with device events, median
 over rounds) and its metrics (bf16 TFLOP/s, GB/s, fraction of the binding
 roofline: valid rows only, each weight byte counted once).
 
-  python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5,decode,copy] [--rounds 10] [--calls 20]
+  python -m lmoe.kernel_bench [--only cfg2,cfg3,cfg4,cfg5,decode,prefill,dist,dense,copy] [--rounds 10] [--calls 20]
 
 Prints one JSON object per measured kernel.
 """
@@ -31,6 +31,7 @@ _PROFILE = False  # run each selected kernel a few times, no timing
 
 
 _DECODE_TOKENS = (1, 2, 4, 8, 16, 32, 64, 128)
+_PREFILL_TOKENS = (128, 512, 2048, 4096)
 
 
 def time_fn(fn, rounds=10, calls=20, name="", graph=True):
@@ -261,12 +262,13 @@ def _capture(layer, hidden):
   return g.replay, out
 
 
-def bench_decode(dev, rounds, calls):
-  """The config-5 layer in the decode regime (rd.py:553-577 sweeps
-  num_tokens 1..128): T tokens through the full local-shard forward, timed as
+def _layer_sweep(dev, rounds, calls, tokens, label):
+  """The config-5 layer at each token count of ``tokens``: the first T of the
+  4096 config-5 tokens through the full local-shard forward, timed as
   HIP-graph replays (the serving loop's launch mode).  Bytes per step = the
   dense projection weights (router, down, up) + the MXFP4 weights of the
-  local experts that receive rows; the roofline is those bytes at 8 TB/s."""
+  local experts that receive rows + the hidden rows in and out; FLOPs = the
+  dense projections + the expert GEMMs on the routed rows."""
   from .forward import LocalShardLatentMoE
   c = Config5()
   hidden, w, experts = make_config5(dev, c, "mxfp4")
@@ -278,16 +280,50 @@ def bench_decode(dev, rounds, calls):
   L, lat, inter, H = c.local_experts, c.latent, c.intermediate, c.hidden
   dense_bytes = 2 * H * (c.experts + 2 * lat)
   expert_bytes = (2 * inter * lat + lat * inter) * (0.5 + 1 / 32)
-  for t in _DECODE_TOKENS:
+  for t in tokens:
     h = hidden[:t].contiguous()
     _, st = layer.forward(h, return_stages=True)
     gs = st["dispatch"].group_sizes.cpu().numpy()
-    hit = int((gs[:L] > 0).sum())
+    hit, rows = int((gs[:L] > 0).sum()), int(gs[:L].sum())
     replay, _ = _capture(layer, h)
-    nm = f"decode layer T={t}"
+    nm = f"{label} layer T={t}"
     ms = time_fn(replay, rounds, calls, name=nm, graph=False)
-    report(nm, ms, 0, dense_bytes + hit * expert_bytes + t * H * 4, tokens=t, experts_hit=hit,
-           skinny_expert_gemms=layer._decode_path(t), tokens_per_s=round(t / (ms / 1000)) if ms else None)
+    flops = 2.0 * t * H * (c.experts + 2 * lat) + 2.0 * rows * 3 * inter * lat
+    report(nm, ms, flops, dense_bytes + hit * expert_bytes + t * H * 4, tokens=t, experts_hit=hit,
+           routed_rows=rows, skinny_expert_gemms=layer._decode_path(t),
+           tokens_per_s=round(t / (ms / 1000)) if ms else None)
+
+
+def bench_decode(dev, rounds, calls):
+  """The decode half of the reference's latency sweep (rd.py:553-577:
+  num_tokens 1..128 through the same layer)."""
+  _layer_sweep(dev, rounds, calls, _DECODE_TOKENS, "decode")
+
+
+def bench_prefill(dev, rounds, calls):
+  """The prefill half of the reference's latency sweep (rd.py:553-577: batch
+  1 at seq 128 / 512 / 2048 / 4096 through the same layer)."""
+  _layer_sweep(dev, rounds, calls, _PREFILL_TOKENS, "prefill")
+
+
+def bench_dist(dev, rounds, calls):
+  """The reference's ragged_dot group-distribution matrix
+  (benchmark_harness.py:100-153): three shapes x five distributions, in its
+  call shape (rhs (G, K, N)), bf16 and f32 inputs."""
+  from .workloads import HARNESS_DISTRIBUTIONS, HARNESS_SHAPES, harness_group_sizes
+  gen = torch.Generator(device=dev).manual_seed(11)
+  for shape, (m, k, n, g) in HARNESS_SHAPES.items():
+    for dt, tdt in (("bf16", torch.bfloat16), ("f32", torch.float32)):
+      lhs = torch.randn((m, k), generator=gen, device=dev).to(tdt)
+      rhs = torch.randn((g, k, n), generator=gen, device=dev).to(tdt)
+      esz = 2 if dt == "bf16" else 4
+      for dist in HARNESS_DISTRIBUTIONS:
+        gs = harness_group_sizes(m, g, dist, seed=0)
+        gsd = torch.from_numpy(gs).to(dev)
+        nm = f"dist ragged_dot {shape} {m}x{k}x{n} G={g} {dist} {dt}"
+        ms = time_fn(lambda: ops.ragged_dot(lhs, rhs, gsd), rounds, calls, name=nm)
+        report(nm, ms, 2.0 * m * k * n, (int((gs > 0).sum()) * k * n + m * k + m * n) * esz,
+               group_sizes=gs.tolist())
 
 
 def bench_dense(dev, rounds, calls):

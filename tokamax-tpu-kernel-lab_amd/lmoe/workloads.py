@@ -85,6 +85,61 @@ def zipf_group_sizes(m: int, g: int, seed: int, s: float = 1.1, n_zero: int = 3)
   return gs.astype(np.int32)
 
 
+# ---------------------------------------------------------------------------
+# The reference's ragged_dot group-distribution matrix
+# (05_ragged_dot_on_tpu/benchmark_harness.py:100-153): three shapes, five
+# ways of splitting the M rows over the G groups.  The harness draws the sizes
+# with tokamax.generate_ragged_dot_group_sizes (tokamax is not installed
+# here); this restates its call contract -- an even split when p is None,
+# otherwise M rows drawn over the groups with probabilities p -- as a seeded
+# multinomial, so the probability vectors are the harness's own but the
+# per-seed vectors are this generator's.
+# ---------------------------------------------------------------------------
+
+# name -> (M, K, N, G); the harness runs them in float32 (its ShapeCase
+# default) and compares against a bf16 tolerance for bf16 inputs
+HARNESS_SHAPES = {"small": (512, 256, 384, 4), "medium_a": (2048, 512, 512, 8), "medium_b": (4096, 1024, 1024, 16)}
+
+
+def harness_distribution(name: str, g: int) -> list[float] | None:
+  """The probability vector of one of the harness's distributions
+  (benchmark_harness.py:116-150); None for "uniform" (an even split)."""
+  if name == "uniform":
+    return None
+  if name == "mild_skew":  # group 0 gets about twice the average
+    p = [1.0] * g
+    p[0] = 2.0
+  elif name == "heavy_skew":  # group 0 takes most of the rows
+    p = [1.0] * g
+    p[0] = float(g)
+  elif name == "empty_groups":  # the second half of the groups gets nothing
+    half = max(g // 2, 1)
+    p = [1.0] * half + [0.0] * (g - half)
+  elif name == "single_dominant":  # every row in group 0
+    p = [0.0] * g
+    p[0] = 1.0
+  else:
+    raise ValueError(f"distribution {name!r}")
+  s = sum(p)
+  return [x / s for x in p]
+
+
+HARNESS_DISTRIBUTIONS = ("uniform", "mild_skew", "heavy_skew", "empty_groups", "single_dominant")
+
+
+def harness_group_sizes(m: int, g: int, dist: str, seed: int = 0) -> np.ndarray:
+  """int32 group sizes summing to m: an even split (the first m % g groups one
+  row larger) for "uniform", a seeded multinomial over the distribution's
+  probabilities otherwise."""
+  p = harness_distribution(dist, g)
+  if p is None:
+    gs = np.full(g, m // g, np.int64)
+    gs[: m % g] += 1
+  else:
+    gs = np.random.default_rng(seed).multinomial(m, p)
+  return gs.astype(np.int32)
+
+
 def _normal(shape, std, gen, device, dtype=torch.bfloat16):
   return (torch.randn(shape, generator=gen, device=device, dtype=torch.float32) * std).to(dtype)
 
