@@ -97,6 +97,54 @@ def check_single_shard(name, hidden, w, gate, up, down, cfg, dtype, start, L, cf
   return errs
 
 
+def _np(a):
+  return to_np(a) if hasattr(a, "detach") else np.asarray(a)
+
+
+def check_single_shard_mx8(name, hidden, w, experts, cfg, start, L, cf, out, st, act="sigmoid"):
+  """The bf16 layer with ``mxfp4_mode="scaled_mfma"``: both expert GEMMs take
+  MXFP8 activations (E4M3 + E8M0 per 32, quantised on the device) x MXFP4
+  weights.  The oracle runs each stage on the device's own input to it:
+  routing and dispatch from the device's logits and latent rows (bit-exact);
+  gate/up + SiTU on the dispatched rows and the down projection on the
+  device's SiTU output through the oracle's MXFP8 x MXFP4 product (the
+  device's quantiser is bit-exact against the oracle's, the product exact up
+  to the block-scaled instruction's accumulation); the combine on the
+  device's shard output and the RMSNorm + up-projection on the device's
+  combined rows.  Every stage within the bf16 bar.  ``experts``: numpy
+  checkpoint-layout gu/down packed codes and scales of the L + 1 experts;
+  ``out`` / ``st`` as in ``check_single_shard`` (torch or numpy arrays)."""
+  tol = 2e-2
+  x_dev, lg_dev = _np(st["x"]), _np(st["router_logits"])
+  r = O.router_from_logits(lg_dev, w["e_score_correction_bias"], cfg.top_k, cfg.moe_renormalize,
+                           cfg.routed_scaling_factor, act, "bf16")
+  assert np.array_equal(_np(st["topk_idx"]), r.topk_idx), "routing differs on identical logits"
+  assert np.array_equal(_np(st["topk_weight"]), r.topk_weight), "routing weights differ on identical logits"
+  d = O.filter_and_pad_to_shard_jittable(r.topk_idx, r.topk_weight, O.cast(x_dev, "bf16"), cfg.top_k,
+                                         cfg.num_experts, start, L, cf)
+  for field, a, b in zip(d._fields, st["dispatch"][:6], d):
+    assert np.array_equal(_np(a), b), f"dispatch {field}"
+  situ = (cfg.activation_situ_beta, cfg.activation_situ_linear_beta)
+  codes, scales = O.quantize_mxfp8(d.sorted_tokens)
+  act_ref = O.ragged_dot_mxfp8_mxfp4(codes, scales, experts["gu_packed"], experts["gu_scale"], d.group_sizes,
+                                     "bf16", situ=situ)
+  act_dev = _np(st["act"])
+  codes, scales = O.quantize_mxfp8(act_dev)
+  shard_ref = O.ragged_dot_mxfp8_mxfp4(codes, scales, experts["down_packed"], experts["down_scale"], d.group_sizes,
+                                       "bf16")
+  shard_dev = _np(st["shard_out"])
+  routed_ref = O.combine_shard_contribution(np.zeros((hidden.shape[0], cfg.latent_size), np.float32), shard_dev,
+                                            d.padded_token_idx, d.padded_combine_weight, "bf16", "bf16", "bf16")
+  routed_dev = _np(st["routed_out"])
+  final_ref = O.matmul(O.rms_norm(routed_dev, w["norm_scale"], cfg.rms_norm_eps, "bf16"), w["up_proj"], "bf16")
+  errs = {"act": max_rel(act_dev, act_ref), "shard_out": max_rel(shard_dev, shard_ref),
+          "routed_out": max_rel(routed_dev, routed_ref), "final": max_rel(_np(out), final_ref)}
+  banner(f"{name}: on the device's stage inputs: " + " ".join(f"{k} {v:.2e}" for k, v in errs.items()))
+  for k, v in errs.items():
+    assert v <= tol, (k, v)
+  return errs
+
+
 def check_unsharded(name, hidden, w, cfg, dtype, act, out, inter):
   """The unsharded forward (ref.py:330-435): ``inter`` as returned by
   ``latent_moe_forward(..., return_intermediates=True)``."""

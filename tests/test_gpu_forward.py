@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import _golden
-from _layer_check import check_single_shard, check_unsharded
+from _layer_check import check_single_shard, check_single_shard_mx8, check_unsharded
 from _util import banner, max_rel, to_dev, to_np
 from oracle import lmoe_oracle as O
 
@@ -161,6 +161,28 @@ def test_local_shard_layer_mxfp4_matches_oracle(gpu_device):
   assert torch.equal(out, out_st)
   check_single_shard("layer mxfp4 (reduced config 5)", to_np(hidden), wn, gate, up, down, c.config(), "bf16",
                      c.local_start, c.local_experts, c.capacity_factor, False, out, gs)
+
+
+def test_local_shard_layer_scaled_mfma_matches_oracle(gpu_device):
+  """The layer with ``mxfp4_mode="scaled_mfma"`` (both expert GEMMs on MXFP8
+  activations x MXFP4 weights, the block-scaled MFMA): every stage against
+  the oracle's MXFP8 arithmetic on the device's own input to that stage; the
+  deviation of its output from the bf16-activation layer is printed (a
+  property of MXFP8 activations, not checked against the bf16 bar)."""
+  from lmoe.forward import LocalShardLatentMoE
+  c, hidden, w, experts, layer = _mxfp4_layer(gpu_device)
+  scaled = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                               e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
+                               up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,
+                               local_num_experts=c.local_experts, expert_format="mxfp4", experts=experts,
+                               capacity_factor=c.capacity_factor, mxfp4_mode="scaled_mfma")
+  out, st = scaled.forward(hidden, return_stages=True)
+  wn = {k: to_np(v) for k, v in w.items()}
+  ex = {k: to_np(experts[k]) for k in ("gu_packed", "gu_scale", "down_packed", "down_scale")}
+  check_single_shard_mx8("layer scaled_mfma (reduced config 5)", to_np(hidden), wn, ex, c.config(), c.local_start,
+                         c.local_experts, c.capacity_factor, out, st)
+  dev = max_rel(to_np(out), to_np(layer.forward(hidden)))
+  print(f"  deviation of MXFP8 activations from the bf16-activation layer: {dev:.3e}")
 
 
 def test_local_shard_layer_graph_replay(gpu_device):

@@ -71,6 +71,7 @@ MX6_CASES = [
     (1024, 1024, 384, 9, 5, 8),    # trailing zero group
     (130, 2048, 1024, 4, 3, 3),
     (1, 7168, 2048, 1, 0, -1),     # one row
+    (4096, 7168, 2048, 1, 0, -1),  # BASELINE config 4 at the size its throughput is quoted at
 ]
 
 

@@ -68,3 +68,55 @@ def test_the_bound_follows_the_gate_slope():
     p = np.exp(z - z.max()) / np.exp(z - z.max()).sum()
     q = np.exp(z + d - (z + d).max()) / np.exp(z + d - (z + d).max()).sum()
     assert np.max(np.abs(q - p)) <= gate_lipschitz("softmax") * np.max(np.abs(d)) * (1 + 1e-3)
+
+
+def _mx8_layer_stages(seed=3, t=64, h=128, lat=64, inter=64, e=32, k=4, start=8, L=8):
+  """A small local-shard layer run through the oracle with MXFP8 activations
+  in both expert GEMMs, staged the way the device layer returns its stages."""
+  from lmoe.config import LatentMoEConfig
+  rng = np.random.default_rng(seed)
+  cfg = LatentMoEConfig(hidden_size=h, latent_size=lat, intermediate_size=inter, num_experts=e, top_k=k,
+                        num_shared_experts=0)
+  bf = lambda *s: O.bf16_round(rng.standard_normal(s) * 0.1)
+  w = {"router_weight": bf(h, e), "e_score_correction_bias": np.zeros(e, np.float32), "down_proj": bf(h, lat),
+       "up_proj": bf(lat, h), "norm_scale": O.bf16_round(1 + rng.standard_normal(lat) * 0.1)}
+  ex = {"gu_packed": rng.integers(0, 256, (L + 1, 2 * inter, lat // 2), dtype=np.uint8),
+        "gu_scale": rng.integers(120, 126, (L + 1, 2 * inter, lat // 32), dtype=np.uint8),
+        "down_packed": rng.integers(0, 256, (L + 1, lat, inter // 2), dtype=np.uint8),
+        "down_scale": rng.integers(120, 126, (L + 1, lat, inter // 32), dtype=np.uint8)}
+  for key in ("gu_packed", "down_packed"):
+    ex[key][L] = 0  # the padding expert: zero codes
+  hidden = O.bf16_round(rng.standard_normal((t, h)))
+  x = O.matmul(hidden, w["down_proj"], "bf16")
+  logits = O.matmul(hidden, w["router_weight"], "f32")
+  r = O.router_from_logits(logits, w["e_score_correction_bias"], k, True, 1.0, "sigmoid", "bf16")
+  d = O.filter_and_pad_to_shard_jittable(r.topk_idx, r.topk_weight, x, k, e, start, L, 2.0)
+  q, s = O.quantize_mxfp8(d.sorted_tokens)
+  act = O.ragged_dot_mxfp8_mxfp4(q, s, ex["gu_packed"], ex["gu_scale"], d.group_sizes, "bf16", situ=(4.0, 25.0))
+  q, s = O.quantize_mxfp8(act)
+  shard = O.ragged_dot_mxfp8_mxfp4(q, s, ex["down_packed"], ex["down_scale"], d.group_sizes, "bf16")
+  routed = O.combine_shard_contribution(np.zeros((t, lat), np.float32), shard, d.padded_token_idx,
+                                        d.padded_combine_weight, "bf16", "bf16", "bf16")
+  out = O.matmul(O.rms_norm(routed, w["norm_scale"], cfg.rms_norm_eps, "bf16"), w["up_proj"], "bf16")
+  st = {"x": x, "router_logits": logits, "topk_idx": r.topk_idx, "topk_weight": r.topk_weight, "dispatch": d,
+        "act": act, "shard_out": shard, "routed_out": routed}
+  return hidden, w, ex, cfg, start, L, out, st
+
+
+def test_scaled_layer_checker_accepts_the_oracle_and_rejects_a_planted_error():
+  """The scaled-MFMA layer check (used on the device's stages) passes the
+  oracle's own MXFP8 pipeline and fails when one row of one stage is off."""
+  from _layer_check import check_single_shard_mx8
+  hidden, w, ex, cfg, start, L, out, st = _mx8_layer_stages()
+  assert int(st["dispatch"].group_sizes[:L].sum()) > 0  # the shard receives rows
+  errs = check_single_shard_mx8("oracle as device", hidden, w, ex, cfg, start, L, 2.0, out, st)
+  assert max(errs.values()) == 0.0
+  row = int(np.argmax(np.abs(st["act"]).sum(axis=1)))
+  bad = dict(st, act=st["act"].copy())
+  bad["act"][row] *= 1.1
+  with pytest.raises(AssertionError, match="act"):
+    check_single_shard_mx8("planted", hidden, w, ex, cfg, start, L, 2.0, out, bad)
+  bad = dict(st, topk_idx=st["topk_idx"].copy())
+  bad["topk_idx"][0, 0] = (bad["topk_idx"][0, 0] + 1) % cfg.num_experts
+  with pytest.raises(AssertionError, match="routing"):
+    check_single_shard_mx8("planted", hidden, w, ex, cfg, start, L, 2.0, out, bad)
