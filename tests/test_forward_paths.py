@@ -1,0 +1,130 @@
+"""The layer's path selection (LocalShardLatentMoE.forward) on the CPU: the
+host logic runs on CPU tensors against a stand-in for liblmoe.so that records
+every entry point it is asked for and launches nothing, so each configuration
+is checked to reach only entry points whose size limits it meets -- e.g. a
+decode step with more than 1024 latent columns must not ask the one-launch
+router + latent cast (lmoe_router_topk_proj), which refuses it."""
+import pytest
+import torch
+
+from lmoe import forward, ops
+from lmoe.workloads import Config5, make_config5
+
+
+class RecordingLib:
+  """Every lmoe_* entry returns success (workspace sizes: 4 KiB) and is
+  recorded with its arguments."""
+
+  def __init__(self):
+    self.calls = []
+
+  def __getattr__(self, name):
+    if not name.startswith("lmoe_"):
+      raise AttributeError(name)
+
+    def entry(*args):
+      self.calls.append((name, args))
+      return 4096 if name.endswith("workspace_size") else 0
+    return entry
+
+  def names(self):
+    return [n for n, _ in self.calls if not n.endswith("workspace_size")]
+
+
+@pytest.fixture
+def rec(monkeypatch):
+  lib = RecordingLib()
+
+  def dev(*ts):
+    for t in ts:
+      if t is not None and not t.is_contiguous():
+        raise ValueError("LatentMoE operators need contiguous tensors")
+
+  def dev_rows(t):
+    if t.dim() != 2:
+      raise ValueError("expected a 2-D tensor")
+    return t.contiguous() if t.stride(1) != 1 or t.stride(0) < t.shape[1] else t
+
+  monkeypatch.setattr(ops, "lib", lambda: lib)
+  monkeypatch.setattr(ops, "_stream", lambda: 0)
+  monkeypatch.setattr(ops, "_dev", dev)
+  monkeypatch.setattr(ops, "_dev_rows", dev_rows)
+  return lib
+
+
+def _layer(lat, tokens, experts=128, mode="lds_dequant"):
+  c = Config5(tokens=tokens, hidden=256, latent=lat, intermediate=256, experts=experts, top_k=16, local_start=16,
+              local_experts=16)
+  hidden, w, ex = make_config5("cpu", c, "mxfp4")
+  layer = forward.LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                                      e_score_correction_bias=w["e_score_correction_bias"],
+                                      down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                                      local_expert_start=c.local_start, local_num_experts=c.local_experts,
+                                      expert_format="mxfp4", experts=ex, capacity_factor=c.capacity_factor,
+                                      mxfp4_mode=mode)
+  return layer, hidden
+
+
+def _proj_calls(rec):
+  return [a for n, a in rec.calls if n == "lmoe_router_topk_proj"]
+
+
+def test_decode_step_fuses_dispatch_into_the_skinny_gateup(rec):
+  layer, hidden = _layer(256, 16)
+  rec.calls.clear()
+  layer.forward(hidden[:1].contiguous())
+  assert rec.names() == ["lmoe_dense_blaslt", "lmoe_router_topk_proj", "lmoe_dispatch_mxfp4_skinny",
+                         "lmoe_ragged_dot_mxfp4_skinny", "lmoe_combine_slots_rms_norm", "lmoe_dense_blaslt"]
+
+
+@pytest.mark.parametrize("tokens", [1, 64, 512])
+def test_latent_above_1024_never_asks_the_one_launch_projection(rec, tokens):
+  """2048 latent columns: the router top-k reads the logits columns and the
+  dispatch rounds the latent columns itself, at decode and prefill sizes."""
+  layer, hidden = _layer(2048, max(tokens, 16))
+  rec.calls.clear()
+  layer.forward(hidden[:tokens].contiguous())
+  names = rec.names()
+  assert "lmoe_router_topk_proj" not in names and "lmoe_router_topk_ld" in names
+  if tokens <= 64:
+    assert "lmoe_dispatch_local_small" in names and names.count("lmoe_ragged_dot_mxfp4_skinny") == 2
+  else:
+    assert "lmoe_dispatch_local_rows" in names and names.count("lmoe_ragged_dot_mxfp4") == 2
+
+
+def test_expert_count_not_a_multiple_of_4_never_asks_the_one_launch_projection(rec):
+  """E % 4 != 0: the latent columns of the fused output start at 4 E bytes,
+  off the 16-byte alignment the one-launch projection needs."""
+  layer, hidden = _layer(256, 512, experts=126)
+  rec.calls.clear()
+  for t in (1, 512):
+    layer.forward(hidden[:t].contiguous())
+  assert not _proj_calls(rec)
+
+
+def test_prefill_gathers_rows_in_the_gateup_kernel(rec):
+  layer, hidden = _layer(256, 512)
+  rec.calls.clear()
+  layer.forward(hidden)
+  assert rec.names() == ["lmoe_dense_blaslt", "lmoe_router_topk_proj", "lmoe_dispatch_local_rows",
+                         "lmoe_ragged_dot_mxfp4_rows", "lmoe_ragged_dot_mxfp4", "lmoe_combine_slots_rms_norm",
+                         "lmoe_dense_blaslt"]
+  (args,) = _proj_calls(rec)
+  # lmoe_router_topk_proj(logits, ld, bias, T, E, k, act, renorm, scale, wdt, idx, w, x_src, x_ld, lat, ...)
+  x_ld, lat = args[13], args[14]
+  assert lat == 256 and lat <= ops.ROUTER_PROJECT_MAX_LAT and x_ld % 4 == 0 and args[12] % 16 == 0
+
+
+def test_stage_returning_forward_and_scaled_mode_take_the_sort_dispatch(rec):
+  layer, hidden = _layer(256, 512)
+  rec.calls.clear()
+  layer.forward(hidden, return_stages=True)
+  names = rec.names()
+  assert "lmoe_router_topk_proj" not in names and "lmoe_cast_rows" in names
+  assert "lmoe_ragged_dot_mxfp4_rows" not in names
+  scaled, hidden = _layer(256, 512, mode="scaled_mfma")
+  rec.calls.clear()
+  scaled.forward(hidden)
+  names = rec.names()
+  assert names.count("lmoe_quantize_mxfp8") == 2 and names.count("lmoe_ragged_dot_mxfp8_mxfp4") == 2
+  assert "lmoe_ragged_dot_mxfp4_rows" not in names and "lmoe_ragged_dot_mxfp4_skinny" not in names
