@@ -3,17 +3,19 @@ host logic runs on CPU tensors against a stand-in for liblmoe.so that records
 every entry point it is asked for and launches nothing, so each configuration
 is checked to reach only entry points whose size limits it meets -- e.g. a
 decode step with more than 1024 latent columns must not ask the one-launch
-router + latent cast (lmoe_router_topk_proj), which refuses it."""
+router + latent cast (lmoe_router_topk_proj), which refuses it.  The recorded
+calls are then re-issued to the real library, whose host-side argument and
+size checks must all pass (without a device it stops at its first HIP call)."""
 import pytest
 import torch
 
-from lmoe import forward, ops
+from lmoe import _lib, forward, ops
 from lmoe.workloads import Config5, make_config5
 
 
 class RecordingLib:
-  """Every lmoe_* entry returns success (workspace sizes: 4 KiB) and is
-  recorded with its arguments."""
+  """Every lmoe_* entry returns success and is recorded with its arguments;
+  workspace-size queries are answered by the real library (host arithmetic)."""
 
   def __init__(self):
     self.calls = []
@@ -21,14 +23,16 @@ class RecordingLib:
   def __getattr__(self, name):
     if not name.startswith("lmoe_"):
       raise AttributeError(name)
+    if name.endswith("workspace_size"):
+      return getattr(_lib.lib(), name)
 
     def entry(*args):
       self.calls.append((name, args))
-      return 4096 if name.endswith("workspace_size") else 0
+      return 0
     return entry
 
   def names(self):
-    return [n for n, _ in self.calls if not n.endswith("workspace_size")]
+    return [n for n, _ in self.calls]
 
 
 @pytest.fixture
@@ -128,3 +132,44 @@ def test_stage_returning_forward_and_scaled_mode_take_the_sort_dispatch(rec):
   names = rec.names()
   assert names.count("lmoe_quantize_mxfp8") == 2 and names.count("lmoe_ragged_dot_mxfp8_mxfp4") == 2
   assert "lmoe_ragged_dot_mxfp4_rows" not in names and "lmoe_ragged_dot_mxfp4_skinny" not in names
+
+
+@pytest.mark.parametrize("lat,tokens,mode,stages", [
+    (256, 1, "lds_dequant", False), (256, 16, "lds_dequant", True), (256, 64, "lds_dequant", False),
+    (256, 512, "lds_dequant", False), (256, 512, "lds_dequant", True), (256, 512, "scaled_mfma", False),
+    (1024, 1, "lds_dequant", False), (1024, 512, "lds_dequant", False), (2048, 1, "lds_dequant", False),
+    (2048, 512, "lds_dequant", False), (2048, 512, "lds_dequant", True)])
+def test_every_call_passes_the_library_checks(rec, lat, tokens, mode, stages):
+  """Each entry point the layer asks for, re-issued to the real library with
+  the same arguments (host pointers of the CPU tensors), must get past the
+  library's own argument and size checks: without a device the library then
+  returns LMOE_ERR_HIP at its first HIP call, never LMOE_ERR_INVALID /
+  UNSUPPORTED / WORKSPACE.  On a machine with a GPU the replay would launch
+  kernels on host pointers, so it runs only where there is none."""
+  if torch.cuda.device_count() > 0:
+    return
+  layer, hidden = _layer(lat, max(tokens, 16), mode=mode)
+  rec.calls.clear()
+  layer.forward(hidden[:tokens].contiguous(), return_stages=stages)
+  real = _lib.lib()
+  assert rec.calls
+  for name, args in rec.calls:
+    rc = getattr(real, name)(*args)
+    assert rc in (_lib.OK, _lib.ERR_HIP), (name, rc, real.lmoe_last_error())
+
+
+def test_the_replay_sees_a_refusal(rec):
+  """The replay above can fail: the same recorded projection call with 2048
+  latent columns is refused by the library's host check."""
+  if torch.cuda.device_count() > 0:
+    return
+  layer, hidden = _layer(256, 16)
+  rec.calls.clear()
+  layer.forward(hidden[:1].contiguous())
+  (args,) = _proj_calls(rec)
+  real = _lib.lib()
+  assert real.lmoe_router_topk_proj(*args) in (_lib.OK, _lib.ERR_HIP)
+  bad = list(args)
+  bad[14] = 2048
+  assert real.lmoe_router_topk_proj(*bad) == _lib.ERR_INVALID
+  assert b"latent" in real.lmoe_last_error()
