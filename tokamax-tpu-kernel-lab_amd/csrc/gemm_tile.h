@@ -367,13 +367,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
 // saturated in f32), so the tanh quotient cannot overflow.  For beta != 4 the
 // sigmoid keeps its own reciprocal and goes to 0 where e^-g overflows
 // (g < -88).  For beta == 4 the sigmoid is built from the same clamped
-// exponential a = e^(g/2) (below), so for g < -36 it stays at 2^-52 instead of
-// decaying as e^g: the result there is at most beta*beta_lin*2^-52 in
-// magnitude instead of about 0, far below the bf16 rounding of any output of
-// ordinary size.  Near
-// g = 0 (u = 0) a - 1 (c - 1) cancels: the absolute error of the result stays
-// below beta*beta_lin*2^-23, far below the bf16 rounding of results of
-// ordinary size.  Hardware exp2 / reciprocal: a few f32 ulp.  A NaN gate or
+// exponential a = e^(g/2) (below), so below g = -36.04 (a = 2^-26) it stays at
+// 2^-52 instead of decaying as e^g: the result there is at most
+// beta*beta_lin*2^-52 in magnitude instead of about 0, far below the bf16
+// rounding of any output of ordinary size.  Near g = 0 (u = 0) a - 1 (c - 1)
+// cancels: the absolute error of the result stays below beta*beta_lin*2^-23,
+// far below the bf16 rounding of results of ordinary size.  Hardware exp2 / reciprocal: a few f32 ulp.  A NaN gate or
 // up value gives NaN.  Every GEMM epilogue uses this one function, so the
 // kernels agree bit for bit on equal accumulators.
 struct SituConsts {
@@ -391,7 +390,7 @@ __device__ __forceinline__ SituConsts situ_consts(float beta, float beta_lin) {
 // a = e^(g/2) gives tanh(g/4) = (a-1)/(a+1) and sigmoid(g) = a^2/(1+a^2), so
 // the pair costs two exponentials and one reciprocal (numerator and
 // denominator stay below 2^104; with a clamped at 2^-26, sigmoid(g) bottoms
-// out at 2^-52 for g < -36); otherwise sigmoid takes its own exponential
+// out at 2^-52 for g < -36.04); otherwise sigmoid takes its own exponential
 // and reciprocal.  NaN in either input gives NaN.  Every fused kernel uses
 // this one function, so they agree bit for bit.
 __device__ __forceinline__ float situ_epi(float g, float u, const SituConsts& c) {
