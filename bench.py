@@ -34,6 +34,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "LatentMoE layer tokens/s @1 GPU; grouped-GEMM TFLOP/s as % of MFMA peak"
 HBM_PEAK_GBS = 8000.0
+DEVICE = "cuda:0"  # the one GPU this benchmark measures
 PEAK_TFLOPS = {"bf16": 2500.0, "mxfp4": 10100.0}
 
 
@@ -298,7 +299,7 @@ def main():
   from lmoe.workloads import Config5, make_config5
 
   _lib.lib()
-  dev = torch.device("cuda:0")
+  dev = torch.device(DEVICE)
   c = Config5()
   log("generating config 5 inputs and MXFP4 expert weights")
   hidden, w, experts = make_config5(dev, c, "mxfp4")

@@ -9,51 +9,14 @@ size checks must all pass (without a device it stops at its first HIP call)."""
 import pytest
 import torch
 
+import _stand_in
 from lmoe import _lib, forward, ops
 from lmoe.workloads import Config5, make_config5
 
 
-class RecordingLib:
-  """Every lmoe_* entry returns success and is recorded with its arguments;
-  workspace-size queries are answered by the real library (host arithmetic)."""
-
-  def __init__(self):
-    self.calls = []
-
-  def __getattr__(self, name):
-    if not name.startswith("lmoe_"):
-      raise AttributeError(name)
-    if name.endswith("workspace_size"):
-      return getattr(_lib.lib(), name)
-
-    def entry(*args):
-      self.calls.append((name, args))
-      return 0
-    return entry
-
-  def names(self):
-    return [n for n, _ in self.calls]
-
-
 @pytest.fixture
 def rec(monkeypatch):
-  lib = RecordingLib()
-
-  def dev(*ts):
-    for t in ts:
-      if t is not None and not t.is_contiguous():
-        raise ValueError("LatentMoE operators need contiguous tensors")
-
-  def dev_rows(t):
-    if t.dim() != 2:
-      raise ValueError("expected a 2-D tensor")
-    return t.contiguous() if t.stride(1) != 1 or t.stride(0) < t.shape[1] else t
-
-  monkeypatch.setattr(ops, "lib", lambda: lib)
-  monkeypatch.setattr(ops, "_stream", lambda: 0)
-  monkeypatch.setattr(ops, "_dev", dev)
-  monkeypatch.setattr(ops, "_dev_rows", dev_rows)
-  return lib
+  return _stand_in.install(monkeypatch)
 
 
 def _layer(lat, tokens, experts=128, mode="lds_dequant"):
