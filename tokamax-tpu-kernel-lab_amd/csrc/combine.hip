@@ -236,8 +236,6 @@ struct TokenKey {
 struct OrderSink {
   int32_t* order;
   __device__ __forceinline__ uint32_t load(int64_t) const { return 0u; }
-  __device__ __forceinline__ void bin_kept(int, int32_t) const {}
-  __device__ __forceinline__ void positions(int64_t, int, int) const {}
   __device__ __forceinline__ void operator()(int64_t s, int key, int pos, bool real, uint32_t) const {
     if (real) order[pos] = static_cast<int32_t>(s);
   }
