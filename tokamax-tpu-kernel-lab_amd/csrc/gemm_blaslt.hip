@@ -13,7 +13,6 @@
 // on first use and kept until the process ends.
 #include <hipblaslt/hipblaslt.h>
 
-#include <cstdlib>
 #include <map>
 #include <mutex>
 #include <tuple>
