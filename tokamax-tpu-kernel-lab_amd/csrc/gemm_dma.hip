@@ -32,6 +32,7 @@
 // (G, K/64, N, 32) and scales (G, K/64, N, 2), so that one step's weights for
 // a run of columns are one contiguous stretch of memory.  K % 64 == 0.
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 #include <utility>
 
@@ -1165,17 +1166,18 @@ void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_vir
   }
 }
 
-// Compute units of the current device (cached per device).
+// Compute units of the current device (cached per device; threads that race
+// on the first query store the same value).
 int cu_count() {
-  static int cache[64] = {0};
+  static std::atomic<int> cache[64] = {};
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cache[dev] == 0) {
-    int v = 0;
+  int v = cache[dev].load(std::memory_order_relaxed);
+  if (v == 0) {
     if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    cache[dev] = v;
+    cache[dev].store(v, std::memory_order_relaxed);
   }
-  return cache[dev];
+  return v;
 }
 
 template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32, bool PIPE = false>
@@ -1264,18 +1266,24 @@ int try_stream(const Params& p, hipStream_t st, const char* name, int* rc) {
     *rc = fail(LMOE_ERR_UNSUPPORTED, "%s: group too large for the DMA path", name);
     return 1;
   }
-  // raise the kernel's dynamic LDS limit when a larger table needs it
+  // raise the kernel's dynamic LDS limit when a larger table needs it; the
+  // raise and its record happen under one lock, so the limit only grows and a
+  // thread that needs less never lowers it under one that needs more
+  static std::mutex lds_mu;
   static std::atomic<int64_t> lds_set{0};
-  if (lds > lds_set.load()) {
-    const hipError_t attr_rc =
-        hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_stream_kernel<BM, BN, EPI, NS, MF>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
-    if (attr_rc != hipSuccess) {
-      *rc = fail(LMOE_ERR_HIP, "%s: LDS size attribute (%lld bytes): %s", name, (long long)lds,
-                 hipGetErrorString(attr_rc));
-      return 1;
+  if (lds > lds_set.load(std::memory_order_acquire)) {
+    std::lock_guard<std::mutex> lock(lds_mu);
+    if (lds > lds_set.load(std::memory_order_relaxed)) {
+      const hipError_t attr_rc =
+          hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_stream_kernel<BM, BN, EPI, NS, MF>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
+      if (attr_rc != hipSuccess) {
+        *rc = fail(LMOE_ERR_HIP, "%s: LDS size attribute (%lld bytes): %s", name, (long long)lds,
+                   hipGetErrorString(attr_rc));
+        return 1;
+      }
+      lds_set.store(lds, std::memory_order_release);
     }
-    lds_set.store(lds);
   }
   const int64_t resident = kXcds * ((static_cast<int64_t>(cu_count()) * C::kLdsBlocks) / kXcds);
   const int64_t grid = resident >= kXcds && resident < blocks ? resident : blocks;
