@@ -416,7 +416,10 @@ int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* topk_w, int w_
  * (no sort needed): mode LMOE_COMBINE_SCATTER_ADD reproduces
  * _combine_shard_contribution (weights padded_w[row]); mode
  * LMOE_COMBINE_SLOT_SUM reproduces the unsharded f32 weighted sum of
- * ref.py:413-416 (weights topk_w[t, j], f32), writing routed_out.
+ * ref.py:413-416 (weights topk_w[t, j], f32), writing routed_out.  With
+ * T > 0, shard_out holds at least one row (slots that were not kept re-read
+ * row 0, whose value they do not use; a dispatch's m_padded is at least one
+ * tile).  The same holds for lmoe_combine_slots_rms_norm.
  */
 int64_t lmoe_combine_workspace_size(int64_t m, int64_t T);
 int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype, const int32_t* padded_token_idx,

@@ -422,6 +422,7 @@ extern "C" int lmoe_combine_slots(const void* shard_out, int shard_dtype, const 
                  "combine_slots: bad mode %d", mode);
   LMOE_CHECK_SUPPORTED(T < (1ll << 31), "combine_slots: T too large");
   if (T == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(shard_out && slot_pos && w && routed_out, "combine_slots: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned blocks = static_cast<unsigned>(ceil_div(T, kTokensPerBlock));
   if (vec8_ok(shard_out, routed_out, lat, shard_dtype, out_dtype) && shard_dtype == LMOE_BF16 &&
@@ -451,6 +452,7 @@ extern "C" int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype,
                        (long long)T);
   LMOE_CHECK_SUPPORTED(m < (1ll << 31), "combine_scatter_add: m too large");
   if (T == 0 || m == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(shard_out && padded_token_idx && padded_w && routed_out, "combine_scatter_add: null pointer");
   const int64_t need = combine_ws_bytes(m, T);
   if (!workspace || workspace_size < need)
     return fail(LMOE_ERR_WORKSPACE, "combine_scatter_add: workspace %lld < %lld",

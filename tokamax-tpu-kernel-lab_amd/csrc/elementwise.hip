@@ -116,6 +116,7 @@ extern "C" int lmoe_rms_norm(const void* x, const void* scale, int64_t rows, int
   LMOE_CHECK_ARG(rows >= 0 && n > 0 && valid_dtype(dtype), "rms_norm: bad arguments");
   LMOE_CHECK_SUPPORTED(rows < (1ll << 33), "rms_norm: too many rows");
   if (rows == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(x && scale && out, "rms_norm: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned blocks = static_cast<unsigned>(ceil_div(rows, 4));
   const bool a16 = aligned(x, 16) && aligned(scale, 16);
@@ -133,6 +134,7 @@ extern "C" int lmoe_situ_and_mul(const void* gate, const void* up, int64_t count
                                  float beta_lin, int dtype, void* out, void* stream) {
   LMOE_CHECK_ARG(count >= 0 && valid_dtype(dtype), "situ_and_mul: bad arguments");
   if (count == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(gate && up && out, "situ_and_mul: null pointer");
   situ_kernel<<<grid_for(count), 256, 0, static_cast<hipStream_t>(stream)>>>(gate, up, count, beta,
                                                                             beta_lin, dtype, out);
   LMOE_CHECK_LAUNCH("situ_and_mul");
@@ -142,6 +144,7 @@ extern "C" int lmoe_situ_and_mul(const void* gate, const void* up, int64_t count
 extern "C" int lmoe_add(const void* a, const void* b, int64_t count, int dtype, void* out, void* stream) {
   LMOE_CHECK_ARG(count >= 0 && valid_dtype(dtype), "add: bad arguments");
   if (count == 0) return LMOE_OK;
+  LMOE_CHECK_ARG(a && b && out, "add: null pointer");
   add_kernel<<<grid_for(count), 256, 0, static_cast<hipStream_t>(stream)>>>(a, b, count, dtype, out);
   LMOE_CHECK_LAUNCH("add");
   return LMOE_OK;
