@@ -232,12 +232,12 @@ int scratch_on_current_device(void** out) {
   return LMOE_OK;
 }
 
-// Every argument check of lmoe_dispatch_local but the workspace's, so the
-// allocation-free variant refuses the same calls before it touches a device.
-int check_dispatch_local(const char* name, const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
-                         int x_dtype, int64_t T, int64_t k, int64_t lat, int64_t local_start, int64_t L,
-                         int64_t m_padded, const void* sorted_tokens, const int32_t* group_sizes, const uint8_t* valid,
-                         const int32_t* per_expert_counts, const int32_t* padded_token_idx, const void* padded_w) {
+// The argument checks of lmoe_dispatch_local, shared with the
+// allocation-free variant so that it refuses the same calls before it touches
+// a device: sizes and dtypes first, then (after the workspace check) the
+// pointers.
+int check_dispatch_sizes(const char* name, int w_dtype, int x_dtype, int64_t T, int64_t k, int64_t lat,
+                         int64_t local_start, int64_t L, int64_t m_padded) {
   LMOE_CHECK_ARG(T >= 0 && k > 0 && lat > 0 && L > 0 && m_padded >= 0 && local_start >= 0,
                  "%s: bad sizes T=%lld k=%lld lat=%lld L=%lld m_padded=%lld", name, (long long)T, (long long)k,
                  (long long)lat, (long long)L, (long long)m_padded);
@@ -245,6 +245,13 @@ int check_dispatch_local(const char* name, const int32_t* topk_idx, const void* 
   LMOE_CHECK_SUPPORTED(T * k < (1ll << 31) && m_padded < (1ll << 31) && L < (1 << 20),
                        "%s: sizes exceed int32 indexing", name);
   LMOE_CHECK_SUPPORTED(L + 1 <= 12288, "%s: L=%lld exceeds the LDS histogram", name, (long long)L);
+  return LMOE_OK;
+}
+
+int check_dispatch_pointers(const char* name, const int32_t* topk_idx, const void* topk_w, const void* x, int64_t T,
+                            int64_t m_padded, const void* sorted_tokens, const int32_t* group_sizes,
+                            const uint8_t* valid, const int32_t* per_expert_counts, const int32_t* padded_token_idx,
+                            const void* padded_w) {
   LMOE_CHECK_ARG(group_sizes && valid && per_expert_counts && padded_token_idx && padded_w &&
                      (sorted_tokens || m_padded == 0),
                  "%s: null output", name);
@@ -268,14 +275,15 @@ extern "C" int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, 
                                    void* padded_w, int32_t* slot_pos, void* workspace,
                                    int64_t workspace_size, void* stream) {
   using namespace lmoe;
-  const int rc = check_dispatch_local("dispatch_local", topk_idx, topk_w, w_dtype, x, x_dtype, T, k, lat, local_start,
-                                      L, m_padded, sorted_tokens, group_sizes, valid, per_expert_counts,
-                                      padded_token_idx, padded_w);
+  int rc = check_dispatch_sizes("dispatch_local", w_dtype, x_dtype, T, k, lat, local_start, L, m_padded);
   if (rc != LMOE_OK) return rc;
   const int64_t need = workspace_bytes(T * k, L);
   if (!workspace || workspace_size < need)
     return fail(LMOE_ERR_WORKSPACE, "dispatch_local: workspace %lld bytes < %lld", (long long)workspace_size,
                 (long long)need);
+  rc = check_dispatch_pointers("dispatch_local", topk_idx, topk_w, x, T, m_padded, sorted_tokens, group_sizes, valid,
+                               per_expert_counts, padded_token_idx, padded_w);
+  if (rc != LMOE_OK) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t n = T * k;
   const int64_t chunks = csort::num_chunks<kDispatchChunk>(n > 0 ? n : 1);
@@ -321,9 +329,8 @@ extern "C" int lmoe_dispatch_local_noalloc(const int32_t* topk_idx, const void* 
                                            int32_t* per_expert_counts, int32_t* padded_token_idx,
                                            void* padded_w, int32_t* slot_pos, void* stream) {
   using namespace lmoe;
-  int rc = check_dispatch_local("dispatch_local_noalloc", topk_idx, topk_w, w_dtype, x, x_dtype, T, k, lat,
-                                local_start, L, m_padded, sorted_tokens, group_sizes, valid, per_expert_counts,
-                                padded_token_idx, padded_w);
+  const char* name = "dispatch_local_noalloc";
+  int rc = check_dispatch_sizes(name, w_dtype, x_dtype, T, k, lat, local_start, L, m_padded);
   if (rc != LMOE_OK) return rc;
   const int64_t need = workspace_bytes(T * k, L);
   if (need > kNoAllocScratchBytes)
@@ -331,6 +338,9 @@ extern "C" int lmoe_dispatch_local_noalloc(const int32_t* topk_idx, const void* 
                 "dispatch_local_noalloc: T*k=%lld, L=%lld need %lld bytes of scratch, more than the %lld-byte "
                 "static array; call lmoe_dispatch_local with a workspace",
                 (long long)(T * k), (long long)L, (long long)need, (long long)kNoAllocScratchBytes);
+  rc = check_dispatch_pointers(name, topk_idx, topk_w, x, T, m_padded, sorted_tokens, group_sizes, valid,
+                               per_expert_counts, padded_token_idx, padded_w);
+  if (rc != LMOE_OK) return rc;
   void* ws = nullptr;
   rc = scratch_on_current_device(&ws);
   if (rc != LMOE_OK) return rc;
