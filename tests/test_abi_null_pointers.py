@@ -12,7 +12,6 @@ import torch
 
 import _stand_in
 from lmoe import _lib, ops
-from lmoe.config import LatentMoEConfig
 
 # (entry point, argument index) pairs that may be null; the stream (the last
 # argument) may always be null
@@ -71,6 +70,11 @@ def _collect(monkeypatch):
       lambda: ops.dispatch_local(idx, w, R(T, lat), 16, L, mpad, path="sort"),
       lambda: ops.dispatch_local(idx, w, R(T, lat), 16, L, mpad, path="small"),
       lambda: ops.dispatch_local(idx, w, None, 16, L, mpad, gather_rows=False, lat=lat),
+      lambda: ops.dispatch_local(idx, w, R(T, lat), 16, L, mpad, skip_padding_rows=True),
+      # bf16 rows through lmoe_dispatch_local_rows' counting-sort path (T*k > 8192, past the
+      # one-launch kernel)
+      lambda: ops.dispatch_local(idx.repeat(17, 1), w.repeat(17, 1), R(17 * T, lat), 16, L,
+                                 ops.compute_m_padded(17 * T, k, E, L, 2.0), skip_padding_rows=True),
       lambda: ops.combine_slots(shard, slot, w, T, k, mode="slot_sum"),
       lambda: ops.combine_slots_rms_norm(shard, slot, w, T, k, torch.ones(lat, dtype=bf), 1e-6, mode="slot_sum",
                                          return_routed=True),
@@ -96,6 +100,8 @@ def _collect(monkeypatch):
   # entry points without an operator of their own
   a = by_name["lmoe_router_topk_ld"][0]
   by_name["lmoe_router_topk"] = [(a[0],) + tuple(a[2:])]
+  s = by_name["lmoe_dispatch_local_small"][0]
+  by_name["lmoe_dispatch_local_rows"].append(tuple(s[:20]) + (None, 0, s[20]))  # its one-launch path, no workspace
   d = by_name["lmoe_dispatch_local"][0]
   by_name["lmoe_dispatch_local_noalloc"] = [tuple(d[:18]) + (d[20],)]
   buf = (torch.zeros(4 * 16 * 32, dtype=torch.bfloat16), torch.zeros(4 * 16 * 32, dtype=torch.bfloat16))
@@ -130,9 +136,13 @@ def test_null_pointers_are_refused_on_the_host(recorded):
     for args in variants:
       rc = getattr(real, name)(*args)
       assert rc in (_lib.OK, _lib.ERR_HIP), (name, rc, real.lmoe_last_error())
-      # the one-launch path of lmoe_dispatch_local_rows takes no workspace
-      small_rows = name == "lmoe_dispatch_local_rows" and (args[19] & _lib.DISPATCH_FLAG_NO_ROWS) == 0
-      no_rows = name == "lmoe_dispatch_local_rows" and (args[19] & _lib.DISPATCH_FLAG_NO_ROWS) != 0
+      # lmoe_dispatch_local_rows(idx, w, wdt, x, xdt, x_ld, T, k, lat, start, L, m_padded, sorted, ...,
+      # flags 19, workspace 20, ...): its one-launch path (T*k <= 8192, m_padded <= 8192, L + 1 <= 1024,
+      # rows wanted) takes no workspace; without rows, x and sorted_tokens may be null
+      rows_call = name == "lmoe_dispatch_local_rows"
+      no_rows = rows_call and (args[19] & _lib.DISPATCH_FLAG_NO_ROWS) != 0
+      small_rows = (rows_call and not no_rows and args[6] * args[7] <= 8192 and args[11] <= 8192
+                    and args[10] + 1 <= 1024)
       optional = OPTIONAL.get(name, set()) | ({20} if small_rows else set()) | ({3, 12} if no_rows else set())
       for i, t in enumerate(argt):
         if t is not _lib.P or not args[i] or i == len(argt) - 1:
@@ -146,3 +156,27 @@ def test_null_pointers_are_refused_on_the_host(recorded):
           assert rc in (_lib.ERR_INVALID, _lib.ERR_WORKSPACE), (name, i, rc, real.lmoe_last_error())
         checked += 1
   assert checked > 150, checked
+  rows_paths = {(a[6] * a[7] <= 8192, (a[19] & _lib.DISPATCH_FLAG_NO_ROWS) != 0)
+                for a in by_name["lmoe_dispatch_local_rows"]}
+  assert {(True, False), (False, False), (True, True)} <= rows_paths, rows_paths
+
+
+def test_empty_batches_pass_the_host_checks(monkeypatch):
+  """T = 0 (empty top-k and token tensors, whose data pointers are null) is
+  a valid dispatch on both paths: every row is padding."""
+  if torch.cuda.device_count() > 0:
+    return
+  rec = _stand_in.install(monkeypatch)
+  L, lat, m_padded = 16, 64, 128
+  idx = torch.empty((0, 4), dtype=torch.int32)
+  w = torch.empty((0, 4), dtype=torch.float32)
+  x = torch.empty((0, lat), dtype=torch.bfloat16)
+  assert idx.data_ptr() == 0 and x.data_ptr() == 0
+  for path in ("sort", "small"):
+    ops.dispatch_local(idx, w, x, 0, L, m_padded, path=path)
+  ops.dispatch_local(idx, w, None, 0, L, m_padded, gather_rows=False, lat=lat)
+  real = _lib.lib()
+  names = rec.names()
+  assert {"lmoe_dispatch_local", "lmoe_dispatch_local_small", "lmoe_dispatch_local_rows"} <= set(names)
+  for name, args in rec.calls:
+    assert getattr(real, name)(*args) in (_lib.OK, _lib.ERR_HIP), (name, real.lmoe_last_error())

@@ -378,9 +378,11 @@ extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* top
   if (!workspace || workspace_size < need)
     return fail(LMOE_ERR_WORKSPACE, "%s: workspace %lld bytes < %lld", name, (long long)workspace_size,
                 (long long)need);
-  LMOE_CHECK_ARG(group_sizes && valid && per_expert_counts && padded_token_idx && padded_w && topk_idx && topk_w &&
+  LMOE_CHECK_ARG(group_sizes && valid && per_expert_counts && padded_token_idx && padded_w &&
                      (no_rows || sorted_tokens || m_padded == 0),
                  "%s: null output", name);
+  LMOE_CHECK_ARG(T == 0 || (topk_idx && topk_w), "%s: null top-k input", name);
+  LMOE_CHECK_ARG(no_rows || T == 0 || m_padded == 0 || x, "%s: null x", name);
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t n = T * k;
   const int64_t chunks = csort::num_chunks<kDispatchChunk>(n > 0 ? n : 1);
