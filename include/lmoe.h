@@ -14,6 +14,12 @@
  * Data types: bf16 is stored as its 16-bit pattern (torch.bfloat16 layout),
  * f32 as IEEE float.  Index arrays are int32.  Booleans are one byte.
  *
+ * Sizes are int64.  A call whose buffers would hold more than 2^48 elements
+ * (beyond any device's memory), or whose sizes exceed a limit stated at its
+ * declaration, returns LMOE_ERR_UNSUPPORTED before anything is launched; the
+ * size products are formed with overflow checks, so no size wraps around.
+ * A null pointer for a buffer a call needs returns LMOE_ERR_INVALID.
+ *
  * The reference interface each entry point replaces is cited as file:line
  * relative to the reference repository (Yog-Sothothftgn/tokamax-tpu-kernel-lab),
  * with these aliases:
@@ -345,7 +351,8 @@ int lmoe_router_topk_proj(const float* logits, int64_t ld, const float* bias, in
  *   valid (m_padded,) u8, per_expert_counts (L,) int32
  *   padded_token_idx (m_padded,) int32 (-1 on padding), padded_w (m_padded,) w_dtype
  *   slot_pos (T*k,) int32 or NULL: sorted row of each (token, slot), -1 if not kept
- * Workspace: lmoe_dispatch_workspace_size(T, k, L) bytes, no initialisation needed.
+ * Workspace: lmoe_dispatch_workspace_size(T, k, L) bytes, no initialisation needed
+ * (-1 for sizes the dispatch refuses).
  */
 int64_t lmoe_dispatch_workspace_size(int64_t T, int64_t k, int64_t L);
 int lmoe_dispatch_local(const int32_t* topk_idx, const void* topk_w, int w_dtype, const void* x,
@@ -410,7 +417,8 @@ int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* topk_w, int w_
  * in place on routed_out (T, lat).  Deterministic: each token's rows are added
  * in ascending row order, each add rounded to out_dtype (the scatter order of
  * the reference).  idx -1 rows (padding, weight 0) are skipped, other indices
- * outside [0, T) are dropped.  Workspace: lmoe_combine_workspace_size(m, T).
+ * outside [0, T) are dropped.  Workspace: lmoe_combine_workspace_size(m, T)
+ * (-1 for sizes the combine refuses).
  *
  * lmoe_combine_slots is the same combine driven by the dispatch's slot_pos
  * (no sort needed): mode LMOE_COMBINE_SCATTER_ADD reproduces

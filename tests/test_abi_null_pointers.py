@@ -180,3 +180,48 @@ def test_empty_batches_pass_the_host_checks(monkeypatch):
   assert {"lmoe_dispatch_local", "lmoe_dispatch_local_small", "lmoe_dispatch_local_rows"} <= set(names)
   for name, args in rec.calls:
     assert getattr(real, name)(*args) in (_lib.OK, _lib.ERR_HIP), (name, real.lmoe_last_error())
+
+
+# int64 arguments that may be arbitrarily large: workspace sizes, and the
+# skinny GEMM's bound on any group's rows (a hint; the kernel uses min(M, bound))
+UNBOUNDED = {
+    "lmoe_combine_scatter_add": {11},
+    "lmoe_dispatch_local": {19},
+    "lmoe_dispatch_local_rows": {21},
+    "lmoe_ragged_dot_mxfp4_splitk": {11},
+    "lmoe_ragged_dot_mxfp4_skinny": {13},
+}
+
+
+def test_oversized_sizes_are_refused_on_the_host(recorded):
+  """Each int64 size of each recorded call set to 2^62 (one at a time): the
+  call is refused on the host -- its buffers would exceed 2^48 elements, or a
+  product of two sizes would wrap around int64 (e.g. T * k in the dispatch),
+  which the checks must not let through."""
+  if torch.cuda.device_count() > 0:
+    return
+  by_name, _ = recorded
+  real = _lib.lib()
+  checked = 0
+  for name, variants in sorted(by_name.items()):
+    argt = _lib.SIGNATURES[name][0]
+    for args in variants:
+      for i, t in enumerate(argt):
+        if t is not _lib.I64 or i in UNBOUNDED.get(name, set()):
+          continue
+        bad = list(args)
+        bad[i] = 1 << 62
+        rc = getattr(real, name)(*bad)
+        assert rc in (_lib.ERR_INVALID, _lib.ERR_UNSUPPORTED, _lib.ERR_WORKSPACE), (name, i, rc)
+        checked += 1
+  assert checked > 100, checked
+
+
+def test_workspace_size_queries_refuse_what_the_entry_points_refuse():
+  L = _lib.lib()
+  assert L.lmoe_dispatch_workspace_size(4096, 16, 112) > 0
+  for T, k, Lx in [(1 << 62, 8, 16), (8, 1 << 62, 16), (1 << 31, 2, 16), (-1, 8, 16), (64, 8, 1 << 20)]:
+    assert L.lmoe_dispatch_workspace_size(T, k, Lx) == -1, (T, k, Lx)
+  assert L.lmoe_combine_workspace_size(16384, 4096) > 0
+  assert L.lmoe_combine_workspace_size(1 << 62, 4096) == -1 and L.lmoe_combine_workspace_size(64, -1) == -1
+  assert L.lmoe_mxfp8_scale_bytes(4096, 7168) > 0 and L.lmoe_mxfp8_scale_bytes(1 << 62, 128) == -1

@@ -407,6 +407,7 @@ bool vec8_ok(const void* a, const void* b, int64_t lat, int adt, int bdt) {
 }  // namespace lmoe
 
 extern "C" int64_t lmoe_combine_workspace_size(int64_t m, int64_t T) {
+  if (m < 0 || T < 0 || m >= (1ll << 31) || T >= (1ll << 31)) return -1;
   return lmoe::combine_ws_bytes(m, T);
 }
 
@@ -421,6 +422,7 @@ extern "C" int lmoe_combine_slots(const void* shard_out, int shard_dtype, const 
   LMOE_CHECK_ARG(mode == LMOE_COMBINE_SCATTER_ADD || mode == LMOE_COMBINE_SLOT_SUM,
                  "combine_slots: bad mode %d", mode);
   LMOE_CHECK_SUPPORTED(T < (1ll << 31), "combine_slots: T too large");
+  LMOE_CHECK_SUPPORTED(extent_ok({T, lat}), "combine_slots: sizes beyond device memory");
   if (T == 0) return LMOE_OK;
   LMOE_CHECK_ARG(shard_out && slot_pos && w && routed_out, "combine_slots: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -451,6 +453,7 @@ extern "C" int lmoe_combine_scatter_add(const void* shard_out, int shard_dtype,
   LMOE_CHECK_SUPPORTED(T + 1 <= 16384, "combine_scatter_add: T=%lld exceeds the LDS histogram",
                        (long long)T);
   LMOE_CHECK_SUPPORTED(m < (1ll << 31), "combine_scatter_add: m too large");
+  LMOE_CHECK_SUPPORTED(extent_ok({m, lat}) && extent_ok({T, lat}), "combine_scatter_add: sizes beyond device memory");
   if (T == 0 || m == 0) return LMOE_OK;
   LMOE_CHECK_ARG(shard_out && padded_token_idx && padded_w && routed_out, "combine_scatter_add: null pointer");
   const int64_t need = combine_ws_bytes(m, T);

@@ -242,8 +242,10 @@ int check_dispatch_sizes(const char* name, int w_dtype, int x_dtype, int64_t T, 
                  "%s: bad sizes T=%lld k=%lld lat=%lld L=%lld m_padded=%lld", name, (long long)T, (long long)k,
                  (long long)lat, (long long)L, (long long)m_padded);
   LMOE_CHECK_ARG(valid_dtype(w_dtype) && valid_dtype(x_dtype), "%s: bad dtype", name);
-  LMOE_CHECK_SUPPORTED(T * k < (1ll << 31) && m_padded < (1ll << 31) && L < (1 << 20),
+  LMOE_CHECK_SUPPORTED(T < (1ll << 31) && k < (1ll << 31) && T * k < (1ll << 31) && m_padded < (1ll << 31) &&
+                           L < (1 << 20) && local_start < (1ll << 31) - L,
                        "%s: sizes exceed int32 indexing", name);
+  LMOE_CHECK_SUPPORTED(extent_ok({T, lat}) && extent_ok({m_padded, lat}), "%s: sizes beyond device memory", name);
   LMOE_CHECK_SUPPORTED(L + 1 <= 12288, "%s: L=%lld exceeds the LDS histogram", name, (long long)L);
   return LMOE_OK;
 }
@@ -264,6 +266,8 @@ int check_dispatch_pointers(const char* name, const int32_t* topk_idx, const voi
 }  // namespace lmoe
 
 extern "C" int64_t lmoe_dispatch_workspace_size(int64_t T, int64_t k, int64_t L) {
+  if (T < 0 || k <= 0 || L <= 0 || T >= (1ll << 31) || k >= (1ll << 31) || T * k >= (1ll << 31) || L >= (1 << 20))
+    return -1;
   return lmoe::workspace_bytes(T * k, L);
 }
 
@@ -363,12 +367,16 @@ extern "C" int lmoe_dispatch_local_rows(const int32_t* topk_idx, const void* top
   LMOE_CHECK_ARG((flags & ~(LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS | LMOE_DISPATCH_FLAG_NO_ROWS)) == 0,
                  "%s: unknown flags 0x%x", name, flags);
   const bool no_rows = (flags & LMOE_DISPATCH_FLAG_NO_ROWS) != 0;
+  LMOE_CHECK_SUPPORTED(T < (1ll << 31) && k < (1ll << 31) && extent_ok({T, x_ld}) && extent_ok({m_padded, lat}),
+                       "%s: sizes beyond device memory (T=%lld k=%lld x_ld=%lld)", name, (long long)T, (long long)k,
+                       (long long)x_ld);
   // decode-sized batches: one launch
   if (!no_rows && T * k <= 8192 && m_padded <= 8192 && L + 1 <= 1024)
     return lmoe_dispatch_local_small(topk_idx, topk_w, w_dtype, x, x_dtype, x_ld, T, k, lat, local_start, L,
                                      m_padded, sorted_tokens, group_sizes, valid, per_expert_counts,
                                      padded_token_idx, padded_w, slot_pos, flags, stream);
-  LMOE_CHECK_SUPPORTED(T * k < (1ll << 31) && m_padded < (1ll << 31) && L < (1 << 20),
+  LMOE_CHECK_SUPPORTED(T * k < (1ll << 31) && m_padded < (1ll << 31) && L < (1 << 20) &&
+                           local_start < (1ll << 31) - L,
                        "%s: sizes exceed int32 indexing", name);
   LMOE_CHECK_SUPPORTED(L + 1 <= 12288, "%s: L=%lld exceeds the LDS histogram", name, (long long)L);
   LMOE_CHECK_SUPPORTED(no_rows || (lat % 8 == 0 && x_ld % (x_dtype == LMOE_F32 ? 4 : 8) == 0 && aligned(x, 16) &&

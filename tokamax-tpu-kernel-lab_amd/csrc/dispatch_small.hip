@@ -176,10 +176,14 @@ extern "C" int lmoe_dispatch_local_small(const int32_t* topk_idx, const void* to
                  (long long)k, (long long)lat, (long long)L, (long long)m_padded, (long long)x_ld);
   LMOE_CHECK_ARG(valid_dtype(w_dtype) && valid_dtype(x_dtype), "%s: bad dtype", name);
   LMOE_CHECK_ARG((flags & ~LMOE_DISPATCH_FLAG_SKIP_PADDING_ROWS) == 0, "%s: unknown flags 0x%x", name, flags);
-  LMOE_CHECK_SUPPORTED(T * k <= kSmallSlots && m_padded <= kSmallRows && L + 1 <= kSmallKeys,
-                       "%s: at most %d slots, %d rows and %d experts (T*k=%lld m_padded=%lld L=%lld)", name,
-                       kSmallSlots, kSmallRows, kSmallKeys - 1, (long long)(T * k), (long long)m_padded,
+  LMOE_CHECK_SUPPORTED(T <= kSmallSlots && k <= kSmallSlots && T * k <= kSmallSlots && m_padded <= kSmallRows &&
+                           L + 1 <= kSmallKeys,
+                       "%s: at most %d slots, %d rows and %d experts (T=%lld k=%lld m_padded=%lld L=%lld)", name,
+                       kSmallSlots, kSmallRows, kSmallKeys - 1, (long long)T, (long long)k, (long long)m_padded,
                        (long long)L);
+  LMOE_CHECK_SUPPORTED(local_start < (1ll << 31) - L && extent_ok({T, x_ld}) && extent_ok({m_padded, lat}),
+                       "%s: sizes beyond device memory (local_start=%lld lat=%lld x_ld=%lld)", name,
+                       (long long)local_start, (long long)lat, (long long)x_ld);
   LMOE_CHECK_SUPPORTED(lat % 8 == 0 && x_ld % (x_dtype == LMOE_F32 ? 4 : 8) == 0,
                        "%s: lat %% 8 == 0 and 16-byte aligned rows (lat=%lld x_ld=%lld)", name, (long long)lat,
                        (long long)x_ld);

@@ -114,7 +114,7 @@ using namespace lmoe;
 extern "C" int lmoe_rms_norm(const void* x, const void* scale, int64_t rows, int64_t n, float eps,
                              int dtype, void* out, void* stream) {
   LMOE_CHECK_ARG(rows >= 0 && n > 0 && valid_dtype(dtype), "rms_norm: bad arguments");
-  LMOE_CHECK_SUPPORTED(rows < (1ll << 33), "rms_norm: too many rows");
+  LMOE_CHECK_SUPPORTED(rows < (1ll << 33) && extent_ok({rows, n}), "rms_norm: too many rows");
   if (rows == 0) return LMOE_OK;
   LMOE_CHECK_ARG(x && scale && out, "rms_norm: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -133,6 +133,7 @@ extern "C" int lmoe_rms_norm(const void* x, const void* scale, int64_t rows, int
 extern "C" int lmoe_situ_and_mul(const void* gate, const void* up, int64_t count, float beta,
                                  float beta_lin, int dtype, void* out, void* stream) {
   LMOE_CHECK_ARG(count >= 0 && valid_dtype(dtype), "situ_and_mul: bad arguments");
+  LMOE_CHECK_SUPPORTED(extent_ok({count}), "situ_and_mul: sizes beyond device memory");
   if (count == 0) return LMOE_OK;
   LMOE_CHECK_ARG(gate && up && out, "situ_and_mul: null pointer");
   situ_kernel<<<grid_for(count), 256, 0, static_cast<hipStream_t>(stream)>>>(gate, up, count, beta,
@@ -143,6 +144,7 @@ extern "C" int lmoe_situ_and_mul(const void* gate, const void* up, int64_t count
 
 extern "C" int lmoe_add(const void* a, const void* b, int64_t count, int dtype, void* out, void* stream) {
   LMOE_CHECK_ARG(count >= 0 && valid_dtype(dtype), "add: bad arguments");
+  LMOE_CHECK_SUPPORTED(extent_ok({count}), "add: sizes beyond device memory");
   if (count == 0) return LMOE_OK;
   LMOE_CHECK_ARG(a && b && out, "add: null pointer");
   add_kernel<<<grid_for(count), 256, 0, static_cast<hipStream_t>(stream)>>>(a, b, count, dtype, out);
@@ -154,6 +156,7 @@ extern "C" int lmoe_cast_rows(const void* x, int x_dtype, int64_t rows, int64_t 
                               int out_dtype, void* stream) {
   LMOE_CHECK_ARG(rows >= 0 && cols >= 0 && ld >= cols && valid_dtype(x_dtype) && valid_dtype(out_dtype),
                  "cast_rows: bad arguments");
+  LMOE_CHECK_SUPPORTED(extent_ok({rows, ld}), "cast_rows: sizes beyond device memory");
   if (rows == 0 || cols == 0) return LMOE_OK;
   LMOE_CHECK_ARG(x && out, "cast_rows: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -233,6 +236,8 @@ extern "C" int lmoe_transpose(const void* in, int64_t G, int64_t R, int64_t C, i
   LMOE_CHECK_ARG(G >= 0 && R >= 0 && C >= 0, "transpose: bad sizes");
   LMOE_CHECK_ARG(elem_bytes == 2 || elem_bytes == 4, "transpose: elem_bytes %d", elem_bytes);
   LMOE_CHECK_SUPPORTED(G < 65536, "transpose: G=%lld batches", (long long)G);
+  LMOE_CHECK_SUPPORTED(extent_ok({G, R, C}) && ceil_div(R, 64) < 65536 && ceil_div(C, 64) < (1ll << 31),
+                       "transpose: sizes beyond device memory or the grid (R=%lld C=%lld)", (long long)R, (long long)C);
   if (G * R * C == 0) return LMOE_OK;
   LMOE_CHECK_ARG(in && out && in != out, "transpose: null or aliased pointer");
   const dim3 grid(static_cast<unsigned>(ceil_div(C, 64)), static_cast<unsigned>(ceil_div(R, 64)),

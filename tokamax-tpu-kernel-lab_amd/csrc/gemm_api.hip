@@ -53,6 +53,9 @@ int check_common(const void* lhs, const void* rhs, const int32_t* gs, int64_t M,
   LMOE_CHECK_ARG(M >= 0 && K > 0 && N > 0 && G > 0, "%s: bad sizes M=%lld K=%lld N=%lld G=%lld", name,
                  (long long)M, (long long)K, (long long)N, (long long)G);
   LMOE_CHECK_ARG(zero_group >= -1 && zero_group < G, "%s: bad zero_group %d", name, zero_group);
+  LMOE_CHECK_SUPPORTED(extent_ok({M, K}) && extent_ok({G, K, N}) && extent_ok({M, N}),
+                       "%s: sizes beyond device memory (M=%lld K=%lld N=%lld G=%lld)", name, (long long)M,
+                       (long long)K, (long long)N, (long long)G);
   LMOE_CHECK_ARG(M == 0 || (lhs && rhs && gs && out), "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(M < (1ll << 31), "%s: M=%lld rows (the tile scan counts rows in 32 bits)", name, (long long)M);
   return LMOE_OK;
@@ -179,8 +182,8 @@ extern "C" int lmoe_ragged_dot_mxfp4_rows(const void* lhs, int64_t lhs_rows, con
   LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(w_packed, 16) && aligned(w_scale, 16), "%s: 16-byte alignment",
                        name);
   // per-lane DMA offsets are 32-bit: any row of lhs
-  LMOE_CHECK_SUPPORTED(lhs_rows * K * 2 < (1ll << 32) && lhs_rows <= 65536, "%s: lhs too large (%lld rows)", name,
-                       (long long)lhs_rows);
+  LMOE_CHECK_SUPPORTED(lhs_rows <= 65536 && extent_ok({lhs_rows, K}) && lhs_rows * K * 2 < (1ll << 32),
+                       "%s: lhs too large (%lld rows)", name, (long long)lhs_rows);
   if (M == 0) return LMOE_OK;
   Params p{static_cast<const uint16_t*>(lhs), w_packed, w_scale, group_sizes, M, K, N, G, zero_group,
            out, LMOE_BF16, beta, beta_lin, 1};
@@ -215,6 +218,7 @@ extern "C" int lmoe_ragged_dot_mxfp4_splitk(const void* lhs, const uint8_t* w_pa
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (splits == 1) return run_dma(p, kMXFP4, epi, st, name);
   LMOE_CHECK_ARG(workspace && aligned(workspace, 16), "%s: workspace must be non-null and 16-byte aligned", name);
+  LMOE_CHECK_SUPPORTED(extent_ok({splits, M, N}), "%s: partial planes beyond device memory", name);
   LMOE_CHECK_ARG(workspace_bytes >= splits * M * N * 4, "%s: workspace %lld bytes < %lld (k_split * M * N * 4)",
                  name, (long long)workspace_bytes, (long long)(splits * M * N * 4));
   return run_dma_splitk(p, kMXFP4, epi, splits, workspace, st, name);
@@ -228,6 +232,7 @@ extern "C" int lmoe_mxfp4_dequant(const uint8_t* packed, const uint8_t* scale, i
                  "%s: bad sizes N=%lld K=%lld gs=%lld", name, (long long)N, (long long)K,
                  (long long)group_size);
   LMOE_CHECK_ARG(valid_dtype(out_dtype), "%s: bad dtype", name);
+  LMOE_CHECK_SUPPORTED(extent_ok({batch, N, K}), "%s: sizes beyond device memory", name);
   const int64_t rows = batch * N;
   if (rows == 0) return LMOE_OK;
   LMOE_CHECK_ARG(packed && scale && out, "%s: null pointer", name);
@@ -246,6 +251,7 @@ extern "C" int lmoe_mxfp4_tile(const uint8_t* packed, const uint8_t* scale, int6
   const char* name = "mxfp4_tile";
   LMOE_CHECK_ARG(G >= 0 && N >= 0 && K > 0, "%s: bad sizes", name);
   LMOE_CHECK_SUPPORTED(K % 64 == 0, "%s: needs K %% 64 == 0 (K=%lld)", name, (long long)K);
+  LMOE_CHECK_SUPPORTED(extent_ok({G, N, K}), "%s: sizes beyond device memory", name);
   if (G * N == 0) return LMOE_OK;
   LMOE_CHECK_ARG(packed && scale && packed_out && scale_out, "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(aligned(packed, 16) && aligned(packed_out, 16), "%s: packed buffers must be 16-byte aligned",

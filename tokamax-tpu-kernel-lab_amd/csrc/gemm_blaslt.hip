@@ -102,6 +102,8 @@ extern "C" int lmoe_dense_blaslt(const void* x, int x_dtype, const void* w_nk, i
                  (long long)K, (long long)N);
   LMOE_CHECK_ARG(valid_dtype(x_dtype) && valid_dtype(w_dtype) && valid_dtype(out_dtype), "dense_blaslt: bad dtype");
   LMOE_CHECK_SUPPORTED(x_dtype == w_dtype, "dense_blaslt: x and W dtypes differ");
+  LMOE_CHECK_SUPPORTED(extent_ok({M, K}) && extent_ok({N, K}) && extent_ok({M, N}),
+                       "dense_blaslt: sizes beyond device memory");
   if (M == 0) return LMOE_OK;
   LMOE_CHECK_ARG(x && w_nk && out, "dense_blaslt: null pointer");
   int dev = 0;

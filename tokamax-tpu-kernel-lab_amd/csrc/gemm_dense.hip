@@ -293,7 +293,8 @@ extern "C" int lmoe_dense(const void* x, const void* w_nk, int64_t M, int64_t K,
                        (long long)K, (long long)N);
   LMOE_CHECK_SUPPORTED(aligned(x, 16) && aligned(w_nk, 16) && aligned(out, 16), "dense: 16-byte aligned buffers");
   // per-lane DMA offsets are 32-bit: one tile's rows of x and w
-  LMOE_CHECK_SUPPORTED(256 * K * 2 < (1ll << 32) && M < (1ll << 31) && N < (1ll << 31), "dense: sizes too large");
+  LMOE_CHECK_SUPPORTED(K < (1ll << 23) && 256 * K * 2 < (1ll << 32) && M < (1ll << 31) && N < (1ll << 31),
+                       "dense: sizes too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(w_nk);

@@ -391,7 +391,7 @@ using namespace lmoe;
 using namespace lmoe::gemm;
 
 extern "C" int64_t lmoe_mxfp8_scale_bytes(int64_t M, int64_t K) {
-  if (M < 0 || K <= 0 || K % 128) return -1;
+  if (M < 0 || K <= 0 || K % 128 || !extent_ok({M + 3, K})) return -1;
   return (K / 128) * ((M + 3) / 4 * 4) * 4;
 }
 
@@ -401,6 +401,7 @@ extern "C" int lmoe_quantize_mxfp8(const void* x, int x_dtype, int64_t M, int64_
   LMOE_CHECK_ARG(M >= 0 && K > 0, "%s: bad sizes M=%lld K=%lld", name, (long long)M, (long long)K);
   LMOE_CHECK_ARG(valid_dtype(x_dtype), "%s: bad dtype", name);
   LMOE_CHECK_SUPPORTED(K % 128 == 0, "%s: needs K %% 128 == 0 (K=%lld)", name, (long long)K);
+  LMOE_CHECK_SUPPORTED(extent_ok({M + 3, K}), "%s: sizes beyond device memory", name);
   if (M == 0) return LMOE_OK;
   LMOE_CHECK_ARG(x && q && scale_t, "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(aligned(x, 16) && aligned(q, 16), "%s: x and q must be 16-byte aligned", name);
@@ -431,6 +432,8 @@ extern "C" int lmoe_ragged_dot_mxfp8_mxfp4(const uint8_t* lhs_q, const uint8_t* 
   LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || out_dtype == LMOE_BF16, "%s: SiTU output is bf16", name);
   LMOE_CHECK_SUPPORTED(K % 128 == 0, "%s: needs K %% 128 == 0 (K=%lld)", name, (long long)K);
   LMOE_CHECK_SUPPORTED(N % (epilogue == LMOE_EPI_SITU ? 16 : 8) == 0 && N >= 8, "%s: N=%lld", name, (long long)N);
+  LMOE_CHECK_SUPPORTED(extent_ok({M, K}) && extent_ok({G, K, N}) && extent_ok({M, N}),
+                       "%s: sizes beyond device memory", name);
   if (M == 0) return LMOE_OK;
   LMOE_CHECK_ARG(lhs_q && lhs_scale_t && w_packed_t && w_scale_t && group_sizes && out, "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(aligned(lhs_q, 16) && aligned(w_packed_t, 16) && aligned(w_scale_t, 16) &&

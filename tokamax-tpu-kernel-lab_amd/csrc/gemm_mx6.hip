@@ -406,6 +406,7 @@ extern "C" int lmoe_quantize_mxfp6(const void* x, int x_dtype, int64_t M, int64_
   LMOE_CHECK_ARG(M >= 0 && K > 0, "%s: bad sizes M=%lld K=%lld", name, (long long)M, (long long)K);
   LMOE_CHECK_ARG(valid_dtype(x_dtype), "%s: bad dtype", name);
   LMOE_CHECK_SUPPORTED(K % 128 == 0, "%s: needs K %% 128 == 0 (K=%lld)", name, (long long)K);
+  LMOE_CHECK_SUPPORTED(extent_ok({M + 3, K}), "%s: sizes beyond device memory", name);
   if (M == 0) return LMOE_OK;
   LMOE_CHECK_ARG(x && q && scale_t, "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(aligned(x, 16) && aligned(q, 8), "%s: x 16-byte and q 8-byte alignment", name);
@@ -433,6 +434,8 @@ extern "C" int lmoe_ragged_dot_mxfp6_mxfp4(const uint8_t* lhs_q, const uint8_t* 
   LMOE_CHECK_ARG(valid_dtype(out_dtype), "%s: bad out dtype", name);
   LMOE_CHECK_SUPPORTED(K % 128 == 0, "%s: needs K %% 128 == 0 (K=%lld)", name, (long long)K);
   LMOE_CHECK_SUPPORTED(N % 8 == 0, "%s: N=%lld", name, (long long)N);
+  LMOE_CHECK_SUPPORTED(extent_ok({M, K}) && extent_ok({G, K, N}) && extent_ok({M, N}),
+                       "%s: sizes beyond device memory", name);
   if (M == 0) return LMOE_OK;
   LMOE_CHECK_ARG(lhs_q && lhs_scale_t && w_packed_t && w_scale_t && group_sizes && out, "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(aligned(lhs_q, 16) && aligned(w_packed_t, 16) && aligned(w_scale_t, 16) &&

@@ -606,7 +606,10 @@ extern "C" int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_ti
   LMOE_CHECK_SUPPORTED(N % (epi == kEpiSitu ? 32 : 16) == 0, "%s: needs 16-column output tiles (N=%lld)", name,
                        (long long)N);
   LMOE_CHECK_SUPPORTED(G <= kSkMaxGroups, "%s: at most %d groups (G=%lld)", name, kSkMaxGroups, (long long)G);
-  LMOE_CHECK_SUPPORTED(M < (1ll << 31), "%s: M=%lld", name, (long long)M);
+  LMOE_CHECK_SUPPORTED(M < (1ll << 31) && K < (1ll << 31) && N < (1ll << 31) && extent_ok({M, K}) &&
+                           extent_ok({G, K, N}) && extent_ok({M, N}),
+                       "%s: sizes beyond device memory (M=%lld K=%lld N=%lld)", name, (long long)M, (long long)K,
+                       (long long)N);
   if (M == 0) return LMOE_OK;
   LMOE_CHECK_ARG(lhs && w_tiled && s_tiled && group_sizes && out, "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(aligned(lhs, 16) && aligned(w_tiled, 16) && aligned(out, 16) && aligned(s_tiled, 2),
@@ -653,10 +656,15 @@ extern "C" int lmoe_dispatch_mxfp4_skinny(const int32_t* topk_idx, const void* t
   LMOE_CHECK_ARG(epilogue == LMOE_EPI_NONE || epilogue == LMOE_EPI_SITU, "%s: bad epilogue", name);
   LMOE_CHECK_ARG((flags & ~LMOE_MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS) == 0, "%s: unknown flags 0x%x", name, flags);
   const int epi = epilogue == LMOE_EPI_SITU ? kEpiSitu : kEpiNone;
-  LMOE_CHECK_SUPPORTED(T * k <= kSkDispSlots && m_padded <= kSkDispRows && L + 1 <= kSkMaxGroups,
-                       "%s: at most %d slots, %d rows and %d experts (T*k=%lld m_padded=%lld L=%lld)", name,
-                       kSkDispSlots, kSkDispRows, kSkMaxGroups - 1, (long long)(T * k), (long long)m_padded,
+  LMOE_CHECK_SUPPORTED(T <= kSkDispSlots && k <= kSkDispSlots && T * k <= kSkDispSlots && m_padded <= kSkDispRows &&
+                           L + 1 <= kSkMaxGroups,
+                       "%s: at most %d slots, %d rows and %d experts (T=%lld k=%lld m_padded=%lld L=%lld)", name,
+                       kSkDispSlots, kSkDispRows, kSkMaxGroups - 1, (long long)T, (long long)k, (long long)m_padded,
                        (long long)L);
+  LMOE_CHECK_SUPPORTED(local_start < (1ll << 31) - L && K < (1ll << 31) && N < (1ll << 31) && extent_ok({T, x_ld}) &&
+                           extent_ok({L + 1, K, N}) && extent_ok({m_padded, N}),
+                       "%s: sizes beyond device memory (local_start=%lld K=%lld N=%lld x_ld=%lld)", name,
+                       (long long)local_start, (long long)K, (long long)N, (long long)x_ld);
   LMOE_CHECK_SUPPORTED(K % 128 == 0 && x_ld % 8 == 0, "%s: needs K %% 128 == 0 and 16-byte rows (K=%lld x_ld=%lld)",
                        name, (long long)K, (long long)x_ld);
   LMOE_CHECK_SUPPORTED(N % (epi == kEpiSitu ? 32 : 16) == 0, "%s: needs 16-column output tiles (N=%lld)", name,
@@ -714,6 +722,10 @@ extern "C" int lmoe_dense_skinny(const void* x, const void* w_nk, int64_t M, int
   LMOE_CHECK_ARG(out_dtype == LMOE_BF16 || out_dtype == LMOE_F32, "%s: bad out dtype", name);
   LMOE_CHECK_SUPPORTED(K % 128 == 0 && N % 16 == 0, "%s: needs K %% 128 == 0 and N %% 16 == 0 (K=%lld N=%lld)",
                        name, (long long)K, (long long)N);
+  LMOE_CHECK_SUPPORTED(M < (1ll << 31) && K < (1ll << 31) && N < (1ll << 31) && extent_ok({M, K}) &&
+                           extent_ok({N, K}) && extent_ok({M, N}),
+                       "%s: sizes beyond device memory (M=%lld K=%lld N=%lld)", name, (long long)M, (long long)K,
+                       (long long)N);
   if (M == 0) return LMOE_OK;
   LMOE_CHECK_ARG(x && w_nk && out, "%s: null pointer", name);
   LMOE_CHECK_SUPPORTED(aligned(x, 16) && aligned(w_nk, 16) && aligned(out, 16), "%s: 16-byte alignment", name);

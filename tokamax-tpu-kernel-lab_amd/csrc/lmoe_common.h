@@ -7,6 +7,7 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <initializer_list>
 
 #include "../../include/lmoe.h"
 
@@ -34,6 +35,23 @@ int fail(int code, const char* fmt, ...);
   } while (0)
 
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// A buffer of these (non-negative) dimensions has at most 2^48 elements --
+// beyond any device's memory, so every entry point refuses larger sizes, and
+// every index and byte offset computed from accepted sizes fits in int64.
+// The product is formed with overflow checks; a zero dimension makes the
+// buffer empty.
+constexpr int64_t kMaxElems = int64_t{1} << 48;
+inline bool extent_ok(std::initializer_list<int64_t> dims) {
+  for (int64_t d : dims) {
+    if (d < 0) return false;
+    if (d == 0) return true;
+  }
+  int64_t n = 1;
+  for (int64_t d : dims)
+    if (__builtin_mul_overflow(n, d, &n) || n > kMaxElems) return false;
+  return true;
+}
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -329,6 +329,7 @@ int router_impl(const float* logits, int64_t ld, const float* bias, int64_t T, i
   LMOE_CHECK_ARG(act == LMOE_ACT_SIGMOID || act == LMOE_ACT_SOFTMAX, "router_topk: bad act %d", act);
   LMOE_CHECK_ARG(valid_dtype(weight_dtype), "router_topk: bad weight dtype %d", weight_dtype);
   LMOE_CHECK_ARG(T <= (1ll << 30), "router_topk: T too large");
+  LMOE_CHECK_SUPPORTED(extent_ok({T, ld}) && extent_ok({T, x_ld}), "router_topk: sizes beyond device memory");
   if (T == 0) return LMOE_OK;
   LMOE_CHECK_ARG(logits && topk_idx && topk_w, "router_topk: null pointer");
   hipStream_t st = static_cast<hipStream_t>(stream);
