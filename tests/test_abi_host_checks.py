@@ -1,12 +1,18 @@
-"""Every C-ABI entry point turns a null pointer for a buffer it needs into
-LMOE_ERR_INVALID (or LMOE_ERR_WORKSPACE for a workspace) on the host, instead
-of launching a kernel that would dereference it.  One valid call per entry
-point is recorded through the Python operators, the layer and three calls
-built by hand (the recording stand-in library on CPU tensors); each call is
-re-issued to the real liblmoe.so first as recorded (it must pass the host
-checks: LMOE_OK, or LMOE_ERR_HIP at the first HIP call on a machine without a
-device), then once per pointer argument with that pointer null.  The pointers
-include/lmoe.h documents as optional must still be accepted."""
+"""The C-ABI's host-side argument checks, which stand between a bad call and
+a kernel launch.  One valid call per entry point is recorded through the
+Python operators, the layer and a few calls built by hand (the recording
+stand-in library on CPU tensors); each call is re-issued to the real
+liblmoe.so first as recorded (it must pass the host checks: LMOE_OK, or
+LMOE_ERR_HIP at the first HIP call on a machine without a device), then with
+one argument spoiled at a time, which the library must refuse before it
+launches anything:
+  * a null pointer for a buffer the call needs -> LMOE_ERR_INVALID (or
+    LMOE_ERR_WORKSPACE); the pointers include/lmoe.h marks optional are
+    accepted;
+  * an int64 size of 2^62 -> refused (buffers beyond 2^48 elements, and no
+    size product may wrap around int64);
+  * an out-of-range enum (dtype, layout, mode, epilogue, activation, flags,
+    zero_group) -> refused."""
 import pytest
 import torch
 
@@ -225,3 +231,35 @@ def test_workspace_size_queries_refuse_what_the_entry_points_refuse():
   assert L.lmoe_combine_workspace_size(16384, 4096) > 0
   assert L.lmoe_combine_workspace_size(1 << 62, 4096) == -1 and L.lmoe_combine_workspace_size(64, -1) == -1
   assert L.lmoe_mxfp8_scale_bytes(4096, 7168) > 0 and L.lmoe_mxfp8_scale_bytes(1 << 62, 128) == -1
+
+
+# int arguments read as booleans (any nonzero value is true)
+BOOLEANS = {
+    "lmoe_ragged_dot_gateup_situ": {11},  # round_before_act
+    "lmoe_router_topk": {6},              # renorm
+    "lmoe_router_topk_ld": {7},
+    "lmoe_router_topk_proj": {7},
+}
+
+
+def test_out_of_range_enums_are_refused_on_the_host(recorded):
+  """Every int argument (dtype, layout, mode, epilogue, activation, flags,
+  zero_group) set to 12345 or -7 is refused, but for the boolean ones."""
+  if torch.cuda.device_count() > 0:
+    return
+  by_name, _ = recorded
+  real = _lib.lib()
+  checked = 0
+  for name, variants in sorted(by_name.items()):
+    argt = _lib.SIGNATURES[name][0]
+    for args in variants:
+      for i, t in enumerate(argt):
+        if t is not _lib.I32 or i in BOOLEANS.get(name, set()):
+          continue
+        for v in (12345, -7):
+          bad = list(args)
+          bad[i] = v
+          rc = getattr(real, name)(*bad)
+          assert rc in (_lib.ERR_INVALID, _lib.ERR_UNSUPPORTED), (name, i, v, rc)
+          checked += 1
+  assert checked > 100, checked
