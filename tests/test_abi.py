@@ -103,3 +103,38 @@ def test_router_project_predicate_matches_library(L, e, lat):
                                ctypes.c_void_p(2 * base), None)
   want = _lib.OK if ops.router_topk_project_supported(e, lat) else _lib.ERR_UNSUPPORTED
   assert rc == want, L.lmoe_last_error()
+
+
+@pytest.mark.parametrize("compiler,flags", [("gcc", ["-std=c99", "-pedantic"]), ("g++", ["-std=c++17", "-x", "c++"])])
+def test_header_builds_a_c_host_that_links_and_runs(tmp_path, compiler, flags):
+  """include/lmoe.h as a C (or C++) host uses it: a program that takes the
+  address of every declared function compiles warning-free, links against
+  liblmoe.so and runs the host-side calls (version, a refused call and its
+  message, the workspace-size queries) without a device."""
+  import os
+  import re
+  import subprocess
+  root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+  inc = os.path.join(root, "include")
+  libdir = os.path.dirname(_lib.LIB_PATH)
+  names = sorted(set(re.findall(r"\b(lmoe_[a-z0-9_]+)\s*\(", open(os.path.join(inc, "lmoe.h")).read())))
+  src = tmp_path / "host.c"
+  src.write_text("\n".join(
+      ["#include <stdio.h>", "#include <string.h>", '#include "lmoe.h"', "typedef void (*fn_t)(void);",
+       "static fn_t all[] = {"] + [f"  (fn_t){n}," for n in names] +
+      ["};", "int main(void) {",
+       "  int rc = lmoe_router_topk(NULL, NULL, 4, 8, 9, LMOE_ACT_SIGMOID, 1, 1.0f, LMOE_F32, NULL, NULL, NULL, NULL);",
+       '  printf("%d %d %d %lld %lld\\n", (int)(sizeof(all) / sizeof(all[0])), lmoe_version(), rc,',
+       "         (long long)lmoe_dispatch_workspace_size(4096, 16, 112),",
+       "         (long long)lmoe_dispatch_workspace_size(-1, 16, 112));",
+       '  return rc == LMOE_ERR_INVALID && strstr(lmoe_last_error(), "k=9") != NULL ? 0 : 1;', "}"]) + "\n")
+  exe = tmp_path / "host"
+  cmd = [compiler, *flags, "-Wall", "-Wextra", "-Werror", f"-I{inc}", str(src), f"-L{libdir}", "-llmoe",
+         f"-Wl,-rpath,{libdir}", "-Wl,-rpath-link,/opt/rocm/lib", "-o", str(exe)]
+  r = subprocess.run(cmd, capture_output=True, text=True, timeout=120)
+  assert r.returncode == 0, r.stderr
+  r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=60)
+  assert r.returncode == 0, (r.stdout, r.stderr)
+  count, version, rc, ws, ws_bad = (int(v) for v in r.stdout.split())
+  assert count == len(names) == len(_lib.SIGNATURES) and version >= 1 and rc == _lib.ERR_INVALID
+  assert ws == _lib.lib().lmoe_dispatch_workspace_size(4096, 16, 112) and ws_bad == -1
