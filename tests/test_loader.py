@@ -172,3 +172,58 @@ def test_errors(tmp_path):
   (tmp_path / "huge.safetensors").write_bytes((1 << 40).to_bytes(8, "little") + b"{}")
   with pytest.raises(ValueError, match="exceeds"):
     loader.read_header(str(tmp_path / "huge.safetensors"))
+
+
+def _raw_file(path, header, data=b""):
+  h = json.dumps(header).encode()
+  path.write_bytes(len(h).to_bytes(8, "little") + h + data)
+  return str(path)
+
+
+def test_malformed_headers_are_refused(tmp_path):
+  """Headers that are valid JSON but not the safetensors layout are refused
+  with ValueError naming the entry, before any tensor is read."""
+  good = {"dtype": "U8", "shape": [2, 4], "data_offsets": [0, 8]}
+  assert loader.read_header(_raw_file(tmp_path / "ok.safetensors", {"t": good}, bytes(8)))[0] == {"t": good}
+  bad_entries = [
+      [1, 2],                                               # not an object
+      {"t": "U8"},                                          # entry not an object
+      {"t": {"shape": [2, 4], "data_offsets": [0, 8]}},     # no dtype
+      {"t": dict(good, shape=[2, -4])},                     # negative dim
+      {"t": dict(good, shape=[2, 4.0])},                    # float dim
+      {"t": dict(good, data_offsets=[8, 0])},               # hi < lo
+      {"t": dict(good, data_offsets=[-8, 0])},              # negative offset
+      {"t": dict(good, data_offsets=[0, 8, 16])},           # three offsets
+      {"t": dict(good, data_offsets=[0, True])},            # bool offset
+  ]
+  for i, h in enumerate(bad_entries):
+    with pytest.raises(ValueError, match="header"):
+      loader.read_header(_raw_file(tmp_path / f"bad{i}.safetensors", h, bytes(8)))
+
+
+def test_byte_count_must_match_the_shape(tmp_path):
+  names = {f"{w}.weight_{p}": (n, m) for w, n, m in (("w1", I, LAT), ("w3", I, LAT), ("w2", LAT, I))
+           for p in ("packed", "scale")}
+  header, off, blob = {}, 0, b""
+  for name, (n, m) in names.items():
+    cols = m // 2 if name.endswith("packed") else m // 32
+    nbytes = n * cols - (1 if name == "w2.weight_scale" else 0)  # one byte short
+    header[_key(0, name)] = {"dtype": "U8", "shape": [n, cols], "data_offsets": [off, off + nbytes]}
+    off += nbytes
+    blob += bytes(nbytes)
+  path = _raw_file(tmp_path / "short_tensor.safetensors", header, blob)
+  with pytest.raises(ValueError, match="bytes for shape"):
+    loader.load_mxfp4_experts(path, LAYER, [0], device="cpu")
+
+
+def test_index_cannot_name_files_outside_the_checkpoint(tmp_path):
+  rng = np.random.default_rng(5)
+  tensors, _ = _checkpoint(rng, 1)
+  (tmp_path / "elsewhere").mkdir()
+  save_file(tensors, str(tmp_path / "elsewhere" / "x.safetensors"))
+  ckpt = tmp_path / "ckpt"
+  ckpt.mkdir()
+  (ckpt / "model.safetensors.index.json").write_text(
+      json.dumps({"weight_map": {k: "../elsewhere/x.safetensors" for k in tensors}}))
+  with pytest.raises(ValueError, match="not a file of the checkpoint directory"):
+    loader.load_mxfp4_experts(str(ckpt), LAYER, [0], device="cpu")

@@ -42,7 +42,10 @@ _DTYPES = {"U8": np.uint8, "I8": np.int8, "BF16": np.uint16, "F16": np.float16, 
 
 
 def read_header(path: str) -> tuple[dict, int]:
-  """(header without "__metadata__", absolute offset of the data section)."""
+  """(header without "__metadata__", absolute offset of the data section).
+  Every entry is checked to be {dtype: str, shape: [int >= 0, ...],
+  data_offsets: [lo, hi]} with 0 <= lo <= hi; the offsets are checked against
+  the file when a tensor is read."""
   with open(path, "rb") as f:
     raw = f.read(8)
     if len(raw) != 8:
@@ -52,7 +55,17 @@ def read_header(path: str) -> tuple[dict, int]:
     if n > size - 8:
       raise ValueError(f"{path}: header length {n} exceeds the file size {size}")
     header = json.loads(f.read(n))
+  if not isinstance(header, dict):
+    raise ValueError(f"{path}: the header is not a JSON object")
   header.pop("__metadata__", None)
+  is_int = lambda v: isinstance(v, int) and not isinstance(v, bool)
+  for name, meta in header.items():
+    ok = (isinstance(meta, dict) and isinstance(meta.get("dtype"), str) and isinstance(meta.get("shape"), list)
+          and all(is_int(d) and d >= 0 for d in meta["shape"]) and isinstance(meta.get("data_offsets"), list)
+          and len(meta["data_offsets"]) == 2 and all(is_int(o) for o in meta["data_offsets"])
+          and 0 <= meta["data_offsets"][0] <= meta["data_offsets"][1])
+    if not ok:
+      raise ValueError(f"{path}: malformed header entry {name!r}: {meta!r}")
   return header, 8 + n
 
 
@@ -93,6 +106,10 @@ def _open_checkpoint(path: str) -> tuple[list[_File], dict[str, _File]]:
       with open(index) as f:
         wm = json.load(f)["weight_map"]
       files = sorted({os.path.join(path, v) for v in wm.values()})
+      root = os.path.realpath(path)
+      for fp in files:
+        if os.path.dirname(os.path.realpath(fp)) != root:
+          raise ValueError(f"{index}: shard {fp!r} is not a file of the checkpoint directory")
     else:
       files = sorted(os.path.join(path, f) for f in os.listdir(path) if f.endswith(".safetensors"))
   else:
