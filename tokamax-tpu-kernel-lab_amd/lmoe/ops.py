@@ -62,6 +62,30 @@ def _stream() -> int:
   return torch.cuda.current_stream().cuda_stream
 
 
+def _check_groups(group_sizes: torch.Tensor, g: int) -> None:
+  """The kernels read exactly g group sizes."""
+  if group_sizes.dtype != torch.int32:
+    raise ValueError("group_sizes must be int32")
+  if tuple(group_sizes.shape) != (g,):
+    raise ValueError(f"group_sizes {tuple(group_sizes.shape)} for {g} groups")
+
+
+def _check_topk(topk_idx: torch.Tensor, topk_weight: torch.Tensor) -> None:
+  """The dispatch reads T*k ids and T*k weights."""
+  if topk_idx.dtype != torch.int32 or topk_idx.dim() != 2:
+    raise ValueError(f"topk_idx must be int32 (T, k), got {topk_idx.dtype} {tuple(topk_idx.shape)}")
+  if tuple(topk_weight.shape) != tuple(topk_idx.shape):
+    raise ValueError(f"topk_weight {tuple(topk_weight.shape)} vs topk_idx {tuple(topk_idx.shape)}")
+  if topk_weight.dtype not in (torch.float32, torch.bfloat16):
+    raise ValueError(f"topk_weight must be float32 or bfloat16, got {topk_weight.dtype}")
+
+
+def _check_rows(x: torch.Tensor, t: int) -> None:
+  """Token rows: one per token."""
+  if x.dim() != 2 or x.shape[0] != t:
+    raise ValueError(f"x {tuple(x.shape)}: want ({t}, lat) token rows")
+
+
 def _workspace(nbytes: int, device) -> torch.Tensor:
   return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
@@ -144,6 +168,7 @@ def ragged_dot_gateup_situ(lhs: torch.Tensor, rhs_gu: torch.Tensor, group_sizes:
     raise ValueError(f"rhs_layout {rhs_layout!r}")
   if kk != k or n2 % 2:
     raise ValueError(f"gateup shapes lhs {tuple(lhs.shape)} rhs {tuple(rhs_gu.shape)}")
+  _check_groups(group_sizes, g)
   inter = n2 // 2
   out = torch.empty((m, inter), dtype=torch.bfloat16, device=lhs.device)
   check(lib().lmoe_ragged_dot_gateup_situ(_p(lhs), _p(rhs_gu), layout, _p(group_sizes), m, k, inter,
@@ -345,6 +370,7 @@ def ragged_dot_mxfp8_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
       or tuple(w_packed.shape) != (g, k // 64, n, 32) or tuple(w_scale.shape) != (g, k // 64, n, 2)):
     raise ValueError(f"shapes: lhs {tuple(lhs_q.shape)} scale {tuple(lhs_scale.shape)} "
                      f"w {tuple(w_packed.shape)} w_scale {tuple(w_scale.shape)}")
+  _check_groups(group_sizes, g)
   epi, b, bl, width = _lib.EPI_NONE, 0.0, 0.0, n
   if fuse_gateup_activation is not None:
     b, bl = parse_fused_activation(fuse_gateup_activation)
@@ -393,6 +419,7 @@ def ragged_dot_mxfp6_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
       or tuple(w_packed.shape) != (g, k // 64, n, 32) or tuple(w_scale.shape) != (g, k // 64, n, 2)):
     raise ValueError(f"shapes: lhs {tuple(lhs_q.shape)} scale {tuple(lhs_scale.shape)} "
                      f"w {tuple(w_packed.shape)} w_scale {tuple(w_scale.shape)}")
+  _check_groups(group_sizes, g)
   out = torch.empty((m, n), dtype=out_dtype, device=lhs_q.device)
   check(lib().lmoe_ragged_dot_mxfp6_mxfp4(_p(lhs_q), _p(lhs_scale), _p(w_packed), _p(w_scale), _p(group_sizes),
                                           m, k, n, g, zero_group, _p(out), _dt(out), _stream()),
@@ -481,6 +508,7 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   if (tuple(w_packed.shape), tuple(w_scale.shape)) != want:
     raise ValueError(f"mxfp4 shapes lhs {tuple(lhs.shape)} packed {tuple(w_packed.shape)} "
                      f"scale {tuple(w_scale.shape)} ({weight_layout} layout wants {want})")
+  _check_groups(group_sizes, g)
   epi, b, bl = _lib.EPI_NONE, 0.0, 0.0
   width = n
   if fuse_gateup_activation is not None:
@@ -554,6 +582,7 @@ def _ragged_dot_mxfp4_rows(lhs, row_index, w_packed, w_scale, group_sizes, *, fu
   g, _, n, _ = w_packed.shape
   if (tuple(w_packed.shape), tuple(w_scale.shape)) != ((g, k // 64, n, 32), (g, k // 64, n, 2)):
     raise ValueError(f"mxfp4 shapes lhs {tuple(lhs.shape)} packed {tuple(w_packed.shape)} scale {tuple(w_scale.shape)}")
+  _check_groups(group_sizes, g)
   epi, b, bl, width = _lib.EPI_NONE, 0.0, 0.0, n
   if fuse_gateup_activation is not None:
     b, bl = parse_fused_activation(fuse_gateup_activation)
@@ -587,6 +616,8 @@ def router_topk_from_logits(logits: torch.Tensor, bias: torch.Tensor | None, top
   if bias is not None and bias.dtype != torch.float32:
     bias = bias.float().contiguous()
   t, e = logits.shape
+  if bias is not None and bias.numel() != e:
+    raise ValueError(f"bias has {bias.numel()} entries for {e} experts")
   idx = torch.empty((t, top_k), dtype=torch.int32, device=logits.device)
   w = torch.empty((t, top_k), dtype=weight_dtype, device=logits.device)
   scores = torch.empty((t, e), dtype=torch.float32, device=logits.device) if return_scores else None
@@ -624,6 +655,8 @@ def router_topk_project(logits: torch.Tensor, x: torch.Tensor, bias: torch.Tenso
   if bias is not None and bias.dtype != torch.float32:
     bias = bias.float().contiguous()
   t, e = logits.shape
+  if bias is not None and bias.numel() != e:
+    raise ValueError(f"bias has {bias.numel()} entries for {e} experts")
   lat = x.shape[1]
   if x.shape[0] != t:
     raise ValueError(f"logits {tuple(logits.shape)} and x {tuple(x.shape)} differ in rows")
@@ -839,8 +872,8 @@ def dispatch_ragged_dot_mxfp4_skinny(topk_idx: torch.Tensor, topk_weight: torch.
   except ``sorted_tokens`` (None: each block reads its rows' token rows of x
   itself) and the same expert GEMM output, bit for bit.  x: bf16 token rows
   (T, >= lat), unit column stride.  Sizes: ``dispatch_skinny_supported``."""
-  if topk_idx.dtype != torch.int32:
-    raise ValueError("topk_idx must be int32")
+  _check_topk(topk_idx, topk_weight)
+  _check_rows(x, topk_idx.shape[0])
   if x.dtype != torch.bfloat16:
     raise NotImplementedError("the fused decode dispatch reads bf16 token rows")
   if w_tiled.dtype != torch.uint8 or s_tiled.dtype != torch.uint8:
@@ -893,12 +926,15 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
   None; ``x`` may be None, then ``lat`` gives the row width), for an expert
   GEMM that gathers the token rows itself (``ragged_dot_mxfp4(...,
   lhs_row_index=padded_token_idx)``); the counting-sort path at every size."""
-  if topk_idx.dtype != torch.int32:
-    raise ValueError("topk_idx must be int32")
+  _check_topk(topk_idx, topk_weight)
   t, k = topk_idx.shape
+  if x is not None:
+    _check_rows(x, t)
   if not gather_rows:
     return _dispatch_metadata(topk_idx, topk_weight, local_expert_start, local_num_experts, m_padded,
                               x.shape[-1] if x is not None else lat)
+  if x is None:
+    raise ValueError("dispatch with rows: x is required")
   lat = x.shape[-1]
   L = local_num_experts
   small_ok = small_dispatch_supported(t, k, lat, L, m_padded)
@@ -1009,8 +1045,13 @@ def _combine_shard_contribution(routed_out: torch.Tensor, shard_out: torch.Tenso
   with the output dtype's rounding after every add (the reference's scatter
   order); idx -1 rows (padding, weight 0) are skipped."""
   _dev(routed_out, shard_out, padded_token_idx, padded_combine_weight)
-  out = routed_out.clone()
+  if shard_out.dim() != 2 or routed_out.dim() != 2 or routed_out.shape[1] != shard_out.shape[1]:
+    raise ValueError(f"routed_out {tuple(routed_out.shape)} / shard_out {tuple(shard_out.shape)}: want (T, lat) / (m, lat)")
   m, lat = shard_out.shape
+  if padded_token_idx.dtype != torch.int32 or padded_token_idx.numel() != m or padded_combine_weight.numel() != m:
+    raise ValueError(f"padded_token_idx (int32) and padded_combine_weight need {m} entries, got "
+                     f"{padded_token_idx.dtype} {padded_token_idx.numel()} / {padded_combine_weight.numel()}")
+  out = routed_out.clone()
   t = routed_out.shape[0]
   ws = _workspace(lib().lmoe_combine_workspace_size(m, t), routed_out.device)
   check(lib().lmoe_combine_scatter_add(_p(shard_out), _dt(shard_out), _p(padded_token_idx),
@@ -1018,6 +1059,20 @@ def _combine_shard_contribution(routed_out: torch.Tensor, shard_out: torch.Tenso
                                        _p(out), _dt(out), _p(ws), ws.numel(), _stream()),
         "combine_scatter_add")
   return out
+
+
+def _check_slots(shard_out, slot_pos, weights, num_tokens, top_k, mode):
+  """The slot combine reads T*k slot positions, T*k weights (slot_sum) or one
+  weight per shard row (scatter_add), and at least one shard row (dropped
+  slots re-read row 0)."""
+  if shard_out.dim() != 2 or (num_tokens > 0 and shard_out.shape[0] == 0):
+    raise ValueError(f"shard_out {tuple(shard_out.shape)}: want (m >= 1, lat)")
+  if slot_pos.dtype != torch.int32 or slot_pos.numel() != num_tokens * top_k:
+    raise ValueError(f"slot_pos must be int32 with T*k = {num_tokens * top_k} entries, got "
+                     f"{slot_pos.dtype} {slot_pos.numel()}")
+  want = num_tokens * top_k if mode == "slot_sum" else shard_out.shape[0]
+  if mode in ("slot_sum", "scatter_add") and weights.numel() != want:
+    raise ValueError(f"{mode} weights need {want} entries, got {weights.numel()}")
 
 
 def combine_slots(shard_out: torch.Tensor, slot_pos: torch.Tensor, weights: torch.Tensor,
@@ -1028,11 +1083,14 @@ def combine_slots(shard_out: torch.Tensor, slot_pos: torch.Tensor, weights: torc
   padded per-row weights); mode="slot_sum": the unsharded f32 weighted sum of
   ref.py:413-416 (weights are topk_weight (T, k) f32)."""
   _dev(shard_out, slot_pos, weights)
+  _check_slots(shard_out, slot_pos, weights, num_tokens, top_k, mode)
   lat = shard_out.shape[-1]
   if mode == "scatter_add":
     if routed_out is None:
       routed_out = torch.zeros((num_tokens, lat), dtype=out_dtype or shard_out.dtype,
                                device=shard_out.device)
+    if tuple(routed_out.shape) != (num_tokens, lat):
+      raise ValueError(f"routed_out {tuple(routed_out.shape)}: want ({num_tokens}, {lat})")
     out = routed_out.clone()
     m = _lib.COMBINE_SCATTER_ADD
   elif mode == "slot_sum":
@@ -1053,7 +1111,10 @@ def combine_slots_rms_norm(shard_out: torch.Tensor, slot_pos: torch.Tensor, weig
   kernel (bit-identical to the two calls): returns normed (T, lat), or
   (normed, routed) with ``return_routed``."""
   _dev(shard_out, slot_pos, weights, norm_scale)
+  _check_slots(shard_out, slot_pos, weights, num_tokens, top_k, mode)
   lat = shard_out.shape[-1]
+  if norm_scale.numel() != lat:
+    raise ValueError(f"norm_scale has {norm_scale.numel()} entries for {lat} columns")
   dt = out_dtype or shard_out.dtype
   m = {"scatter_add": _lib.COMBINE_SCATTER_ADD, "slot_sum": _lib.COMBINE_SLOT_SUM}[mode]
   normed = torch.empty((num_tokens, lat), dtype=dt, device=shard_out.device)
@@ -1076,8 +1137,10 @@ def combine_rms_norm_supported(lat: int) -> bool:
 def _rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
   """ref.py:286-293."""
   _dev(x, scale)
-  out = torch.empty_like(x)
   n = x.shape[-1]
+  if scale.numel() != n:
+    raise ValueError(f"scale has {scale.numel()} entries for rows of {n}")
+  out = torch.empty_like(x)
   check(lib().lmoe_rms_norm(_p(x), _p(scale.to(x.dtype).contiguous()), x.numel() // n, n, eps, _dt(x),
                             _p(out), _stream()), "rms_norm")
   return out
@@ -1086,6 +1149,8 @@ def _rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
 def _situ_and_mul(gate: torch.Tensor, up: torch.Tensor, beta: float, linear_beta: float) -> torch.Tensor:
   """ref.py:296-310: f32 SiTU-GLU, cast back to the input dtype."""
   _dev(gate, up)
+  if gate.shape != up.shape or gate.dtype != up.dtype:
+    raise ValueError(f"gate {tuple(gate.shape)} {gate.dtype} / up {tuple(up.shape)} {up.dtype} differ")
   out = torch.empty_like(gate)
   check(lib().lmoe_situ_and_mul(_p(gate), _p(up), gate.numel(), beta, linear_beta, _dt(gate), _p(out),
                                 _stream()), "situ_and_mul")
@@ -1095,6 +1160,8 @@ def _situ_and_mul(gate: torch.Tensor, up: torch.Tensor, beta: float, linear_beta
 def add(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
   """a + b rounded to the dtype (the residual add of ref.py:435)."""
   _dev(a, b)
+  if a.shape != b.shape or a.dtype != b.dtype:
+    raise ValueError(f"a {tuple(a.shape)} {a.dtype} / b {tuple(b.shape)} {b.dtype} differ")
   out = torch.empty_like(a)
   check(lib().lmoe_add(_p(a), _p(b), a.numel(), _dt(a), _p(out), _stream()), "add")
   return out
