@@ -117,3 +117,30 @@ def test_the_same_calls_with_good_inputs_reach_the_library(monkeypatch):
     rec.calls.clear()
     fn()
     assert rec.calls, i
+
+
+@pytest.mark.parametrize("case", ["router E", "router hidden", "bias", "down_proj", "up_proj", "norm_scale",
+                                  "local range past E", "no local experts"])
+def test_layer_refuses_weights_that_disagree_with_its_config(monkeypatch, case):
+  """LocalShardLatentMoE checks its dense weights against the config and its
+  local expert range against the expert count when it is built."""
+  from lmoe import forward
+  from lmoe.workloads import Config5, make_config5
+  rec = _stand_in.install(monkeypatch)
+  c = Config5(tokens=16, hidden=256, latent=256, intermediate=256, experts=128, top_k=16, local_start=16,
+              local_experts=16)
+  hidden, w, ex = make_config5("cpu", c, "mxfp4")
+  kw = dict(router_weight=w["router_weight"], e_score_correction_bias=w["e_score_correction_bias"],
+            down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+            local_expert_start=c.local_start, local_num_experts=c.local_experts, expert_format="mxfp4", experts=ex)
+  forward.LocalShardLatentMoE(c.config(), **kw)  # consistent: builds
+  bad = {"router E": dict(router_weight=w["router_weight"][:, :120]),
+         "router hidden": dict(router_weight=w["router_weight"][:200]),
+         "bias": dict(e_score_correction_bias=w["e_score_correction_bias"][:100]),
+         "down_proj": dict(down_proj=w["down_proj"][:, :128]), "up_proj": dict(up_proj=w["up_proj"][:128]),
+         "norm_scale": dict(norm_scale=w["norm_scale"][:128]), "local range past E": dict(local_expert_start=120),
+         "no local experts": dict(local_num_experts=0)}[case]
+  rec.calls.clear()
+  with pytest.raises(ValueError):
+    forward.LocalShardLatentMoE(c.config(), **dict(kw, **bad))
+  assert not rec.calls

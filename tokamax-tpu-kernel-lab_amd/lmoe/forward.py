@@ -148,6 +148,15 @@ class LocalShardLatentMoE:
                expert_format: str, experts: dict, shared: dict | None = None,
                capacity_factor: float = 2.0, act: str = "sigmoid", mxfp4_mode: str = "lds_dequant",
                decode_tokens: int = 64):
+    h, lat, e = config.hidden_size, config.latent_size, config.num_experts
+    want = {"router_weight": (router_weight, (h, e)), "e_score_correction_bias": (e_score_correction_bias, (e,)),
+            "down_proj": (down_proj, (h, lat)), "up_proj": (up_proj, (lat, h)), "norm_scale": (norm_scale, (lat,))}
+    for name, (t, shape) in want.items():
+      if tuple(t.shape) != shape:
+        raise ValueError(f"{name} {tuple(t.shape)}: the config wants {shape}")
+    if not (local_num_experts > 0 and 0 <= local_expert_start and local_expert_start + local_num_experts <= e):
+      raise ValueError(f"local experts [{local_expert_start}, {local_expert_start + local_num_experts}) "
+                       f"outside the {e} experts")
     self.config = config
     self.L = local_num_experts
     self.start = local_expert_start
