@@ -43,10 +43,12 @@ inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_
 // buffer empty.
 constexpr int64_t kMaxElems = int64_t{1} << 48;
 inline bool extent_ok(std::initializer_list<int64_t> dims) {
+  bool empty = false;
   for (int64_t d : dims) {
     if (d < 0) return false;
-    if (d == 0) return true;
+    empty = empty || d == 0;
   }
+  if (empty) return true;
   int64_t n = 1;
   for (int64_t d : dims)
     if (__builtin_mul_overflow(n, d, &n) || n > kMaxElems) return false;
