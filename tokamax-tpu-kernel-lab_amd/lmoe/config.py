@@ -108,6 +108,31 @@ class LatentMoEWeights:
     return {f: getattr(self, f) for f in WEIGHT_FIELDS}
 
 
+def init_weights(config: LatentMoEConfig, key=0, dtype=None, device="cuda") -> LatentMoEWeights:
+  """``init_weights`` (ref.py:255-283): every field in the (in, out) layout
+  with the reference's shapes and law -- each matrix N(0, 0.02^2), the
+  correction bias zero, the norm scale one, the shared-expert matrices
+  (hidden, intermediate * num_shared_experts) / transposed -- as torch
+  tensors of ``dtype`` (default float32) on ``device``.  ``key`` is an int
+  seed or a torch.Generator; the reference's JAX PRNG stream is not
+  reproduced (no expected output depends on the particular draws)."""
+  import torch
+  dtype = dtype or torch.float32
+  gen = key if isinstance(key, torch.Generator) else torch.Generator(device=device).manual_seed(int(key))
+  h, lat, inter, e = config.hidden_size, config.latent_size, config.intermediate_size, config.num_experts
+  shared = inter * config.num_shared_experts
+
+  def normal(*shape):
+    return (torch.randn(shape, generator=gen, device=gen.device) * 0.02).to(device=device, dtype=dtype)
+
+  return LatentMoEWeights(
+      router_weight=normal(h, e), e_score_correction_bias=torch.zeros(e, dtype=dtype, device=device),
+      down_proj=normal(h, lat), up_proj=normal(lat, h), expert_gate=normal(e, lat, inter),
+      expert_up=normal(e, lat, inter), expert_down=normal(e, inter, lat),
+      norm_scale=torch.ones(lat, dtype=dtype, device=device), shared_gate=normal(h, shared),
+      shared_up=normal(h, shared), shared_down=normal(shared, h))
+
+
 def weights_from_official_state_dict(sd: dict, config: LatentMoEConfig) -> dict:
   """Official (out, in) nn.Linear layout -> reference (in, out) layout, with the
   per-expert stacking of test_jax_reference_against_pytorch_golden.py:139-170

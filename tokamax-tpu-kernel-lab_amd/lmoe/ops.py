@@ -21,6 +21,7 @@ from . import _lib
 from ._lib import check, lib
 
 MOSAIC_TILE_SIZE = 128  # ref.py:149
+_MOSAIC_TILE_SIZE = MOSAIC_TILE_SIZE  # the reference's name
 
 _DT = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16}
 
@@ -807,6 +808,9 @@ def round_up_to_tile(value: int, tile_size: int = MOSAIC_TILE_SIZE) -> int:
   return -(-value // tile_size) * tile_size
 
 
+_round_up_to_tile = round_up_to_tile  # the reference's name (ref.py:152)
+
+
 def compute_m_padded(num_tokens: int, top_k: int, num_experts: int, local_num_experts: int,
                      capacity_factor: float = 2.0, tile_size: int = MOSAIC_TILE_SIZE) -> int:
   """ref.py:825-826: round_up(ceil(T*k*L/E * cf), tile), static per config."""
@@ -1175,6 +1179,16 @@ def _situ_glu_mlp(x, w_gate, w_up, w_down, beta, linear_beta):
 # ---------------------------------------------------------------------------
 # a11: expert FFN over one shard
 # ---------------------------------------------------------------------------
+
+
+def _local_shard_expert_ffn(sorted_tokens, expert_gate, expert_up, expert_down, group_sizes, config):
+  """ref.py:1486-1528, the reference's per-expert-loop form of the shard FFN
+  (the oracle its ragged_dot form, rd.py:580-607, is checked against): the
+  same function, so here both names run the grouped GEMMs -- gate / up,
+  SiTU-GLU, down -- over the sorted rows, the trailing padding group included
+  (its rows are zero, so are its outputs)."""
+  return _local_shard_expert_ffn_ragged_dot(sorted_tokens, expert_gate, expert_up, expert_down, group_sizes,
+                                            config)
 
 
 def _local_shard_expert_ffn_ragged_dot(sorted_tokens, expert_gate, expert_up, expert_down,
