@@ -100,3 +100,30 @@ def test_mxfp4_matmul_orientation_and_values():
 @pytest.mark.parametrize("v,t,want", [(0, 128, 0), (1, 128, 128), (128, 128, 128), (129, 128, 256), (5, 4, 8)])
 def test_round_up_to_tile(v, t, want):
   assert O.round_up_to_tile(v, t) == want
+
+
+def test_grouped_mxfp4_with_situ_against_brute_force():
+  """The grouped MXFP4 oracle with the SiTU epilogue (the config-5 gate/up:
+  N = [gate | up] of each checkpoint expert, rd.py:610-723 on MXFP4 weights):
+  per-row float64 dots over the E2M1 table, rounded to bf16 before a float64
+  SiTU, within 2 bf16 ulp; the padding rows past sum(group_sizes) are zero."""
+  rng = np.random.default_rng(2)
+  gs = np.array([2, 0, 3, 1], np.int32)
+  m, inter, k, b, bl = 8, 6, 64, 4.0, 25.0
+  packed = rng.integers(0, 256, (4, 2 * inter, k // 2), dtype=np.uint8)
+  scale = rng.integers(118, 124, (4, 2 * inter, k // 32), dtype=np.uint8)
+  x = O.bf16_round(rng.standard_normal((m, k)))
+  got = O.ragged_dot_mxfp4(x, packed, scale, gs, "bf16", situ=(b, bl)).astype(np.float64)
+  want = np.zeros((m, inter))
+  start = 0
+  for g, n in enumerate(gs):
+    w = _dequant_brute(packed[g], scale[g], k)
+    for r in range(start, start + n):
+      acc = x[r].astype(np.float64) @ w.T
+      want[r] = _situ64(O.bf16_round(acc[:inter]), O.bf16_round(acc[inter:]), b, bl)
+    start += int(n)
+  valid = int(gs.sum())
+  scale_ = np.maximum(np.abs(want[:valid]), 1e-3)
+  assert got.shape == (m, inter)
+  assert np.max(np.abs(got[:valid] - want[:valid]) / scale_) <= 2 * 2.0 ** -8
+  assert not got[valid:].any()
