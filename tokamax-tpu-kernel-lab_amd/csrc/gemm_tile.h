@@ -204,7 +204,7 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs; consecutive blocks go to consecutiv
 // dealt round-robin.  An XCD then reads an expert's weights and a tile's
 // activation rows from its own L2.
 template <class Locate>
-__device__ __forceinline__ TileInfo schedule_tile_with(int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt,
+__host__ __device__ __forceinline__ TileInfo schedule_tile_with(int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt,
                                                        Locate&& locate, int64_t tm_work = -1) {
   // grids and tile counts are < 2^31 (checked on the host): 32-bit index math
   const uint32_t v32 = static_cast<uint32_t>(vb), nt32 = static_cast<uint32_t>(n_tiles);
