@@ -138,3 +138,28 @@ def test_header_builds_a_c_host_that_links_and_runs(tmp_path, compiler, flags):
   count, version, rc, ws, ws_bad = (int(v) for v in r.stdout.split())
   assert count == len(names) == len(_lib.SIGNATURES) and version >= 1 and rc == _lib.ERR_INVALID
   assert ws == _lib.lib().lmoe_dispatch_workspace_size(4096, 16, 112) and ws_bad == -1
+
+
+def test_integration_bindings_match_the_library():
+  """The ctypes bindings INTEGRATION.md shows a maintainer (argtypes lists and
+  example calls) agree with the library's signatures, so copying them binds
+  the entry points correctly."""
+  import os
+  import re
+  root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+  txt = open(os.path.join(root, "INTEGRATION.md")).read()
+  kinds = {"P": _lib.P, "I64": _lib.I64, "I32": _lib.I32, "ctypes.c_float": _lib.F}
+  bound = re.findall(r"lib\.(lmoe_\w+)\.argtypes = \[(.*?)\]", txt, re.S)
+  assert len(bound) >= 5
+  for name, body in bound:
+    toks = [t.strip() for t in body.replace("\n", " ").split(",") if t.strip()]
+    assert [kinds[t] for t in toks] == _lib.SIGNATURES[name][0], name
+  calls = re.findall(r"rc = lib\.(lmoe_\w+)\((.*?)\)\n", txt, re.S)
+  assert len(calls) >= 5
+  for name, body in calls:
+    depth, n = 0, 1
+    for ch in body:
+      depth += ch in "(["
+      depth -= ch in ")]"
+      n += ch == "," and depth == 0
+    assert n == len(_lib.SIGNATURES[name][0]), (name, n)
