@@ -163,3 +163,29 @@ def test_integration_bindings_match_the_library():
       depth -= ch in ")]"
       n += ch == "," and depth == 0
     assert n == len(_lib.SIGNATURES[name][0]), (name, n)
+
+
+def test_header_prototypes_match_the_ctypes_bindings():
+  """Every prototype in include/lmoe.h has the parameter list and return
+  type the ctypes binding declares (pointer / int64_t / int / float, in
+  order): a binding that disagreed would pass its arguments in the wrong
+  registers without any error."""
+  import os
+  import re
+  root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+  hdr = re.sub(r"/\*.*?\*/", "", open(os.path.join(root, "include", "lmoe.h")).read(), flags=re.S)
+  protos = re.findall(r"([\w\s\*]+?)\b(lmoe_\w+)\s*\(([^;{]*?)\)\s*;", hdr, re.S)
+  scalar = {"int64_t": _lib.I64, "int": _lib.I32, "float": _lib.F}
+
+  def kind(decl):
+    decl = " ".join(decl.replace("const ", "").split())
+    if "*" in decl:
+      return _lib.P
+    return scalar.get(decl.split(" ")[0], decl)
+
+  assert len(protos) == len(_lib.SIGNATURES)
+  for ret, name, params in protos:
+    args = [kind(p) for p in params.split(",") if p.strip() and p.strip() != "void"]
+    ret = " ".join(ret.split())
+    ret_kind = ctypes.c_char_p if "char" in ret else scalar.get(ret.split(" ")[-1], ret)
+    assert (args, ret_kind) == _lib.SIGNATURES[name], name
