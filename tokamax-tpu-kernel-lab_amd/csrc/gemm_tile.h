@@ -202,7 +202,10 @@ constexpr int kXcds = 8;  // MI355X: 8 XCDs; consecutive blocks go to consecutiv
 // trailing zero group, so the ranges hold equal real work), each m-tile's
 // n-tiles in turn; the m-tiles from tm_work on (zero group, tail rows) follow,
 // dealt round-robin.  An XCD then reads an expert's weights and a tile's
-// activation rows from its own L2.
+// activation rows from its own L2.  No launch selects gm < 0 today (it moved
+// 21% less HBM traffic for the config-5 gate/up but measured 4% slower than
+// gm == 0); the branch stays because the measured kernels were compiled with
+// it, and taking it out changes their code.
 template <class Locate>
 __host__ __device__ __forceinline__ TileInfo schedule_tile_with(int64_t n_tiles, int gm, int64_t vb, int64_t tm, int64_t& nt,
                                                        Locate&& locate, int64_t tm_work = -1) {
