@@ -147,7 +147,11 @@ def parse_fused_activation(spec: str) -> tuple[float, float]:
   parts = spec.split(":")
   if len(parts) != 3 or parts[0] != "situ":
     raise NotImplementedError(f"fuse_gateup_activation={spec!r}: only 'situ:<beta>:<beta_lin>'")
-  return float(parts[1]), float(parts[2])
+  beta, beta_lin = float(parts[1]), float(parts[2])
+  if not (0.0 < beta < math.inf and 0.0 < beta_lin < math.inf):
+    raise ValueError(f"fuse_gateup_activation={spec!r}: beta and beta_lin must be positive and finite "
+                     "(each divides a tanh argument)")
+  return beta, beta_lin
 
 
 def ragged_dot_gateup_situ(lhs: torch.Tensor, rhs_gu: torch.Tensor, group_sizes: torch.Tensor,
