@@ -136,3 +136,36 @@ def test_the_replay_sees_a_refusal(rec):
   bad[14] = 2048
   assert real.lmoe_router_topk_proj(*bad) == _lib.ERR_INVALID
   assert b"latent" in real.lmoe_last_error()
+
+
+@pytest.mark.parametrize("fused,shared", [(False, True), (True, True), (False, False), (True, False)])
+def test_single_shard_functional_forward_path(rec, fused, shared):
+  """latent_moe_forward_ragged_dot_single_shard_jittable (rd.py:1035-1137):
+  down-projection, router logits, top-k, dispatch, the shard FFN (three
+  grouped GEMMs, or the fused gate/up + SiTU and the down GEMM), combine,
+  RMSNorm, up-projection, and the shared-expert MLP when given; every
+  recorded call then passes the real library's host checks."""
+  from lmoe import config as C
+  cfg = C.mosaic_correctness_config()
+  w = C.init_weights(cfg, 5, torch.bfloat16, device="cpu")
+  start, L = 2, 4
+  shard = lambda t: torch.cat([t[start:start + L], torch.zeros_like(t[:1])]).contiguous()
+  hidden = torch.randn(32, cfg.hidden_size).to(torch.bfloat16)
+  forward.latent_moe_forward_ragged_dot_single_shard_jittable(
+      hidden, w.router_weight, w.e_score_correction_bias, w.down_proj, shard(w.expert_gate), shard(w.expert_up),
+      shard(w.expert_down), w.norm_scale, w.up_proj, w.shared_gate if shared else None,
+      w.shared_up if shared else None, w.shared_down if shared else None, cfg, start, L, fused_gateup=fused)
+  names = rec.names()
+  ffn = (["lmoe_ragged_dot_gateup_situ", "lmoe_ragged_dot"] if fused
+         else ["lmoe_ragged_dot", "lmoe_ragged_dot", "lmoe_situ_and_mul", "lmoe_ragged_dot"])
+  head = names[:4]
+  assert set(head[:2]) <= {"lmoe_ragged_dot", "lmoe_dense_blaslt"} and head[2] == "lmoe_router_topk_ld"
+  assert head[3].startswith("lmoe_dispatch_local")
+  assert names[4:4 + len(ffn)] == ffn
+  rest = names[4 + len(ffn):]
+  assert rest[0] == "lmoe_combine_slots" and rest[1] == "lmoe_rms_norm"
+  assert ("lmoe_add" in rest) == shared and ("lmoe_situ_and_mul" in rest) == shared
+  if torch.cuda.device_count() == 0:
+    real = _lib.lib()
+    for name, args in rec.calls:
+      assert getattr(real, name)(*args) in (_lib.OK, _lib.ERR_HIP), (name, real.lmoe_last_error())
