@@ -85,6 +85,7 @@ int lmoe_device_arch_ok(void); /* 1 if device 0 is gfx950, else 0 (host-side que
  * reading its weights (the trailing padding bucket, whose input rows are zero:
  * ref.py:1497-1500); pass -1 to compute every group.
  * bf16: K % 8 == 0, N % 8 == 0, 16-byte aligned lhs/rhs; f32: any shape.
+ * M < 2^31 rows (also for every grouped GEMM below).
  */
 int lmoe_ragged_dot(const void* lhs, int lhs_dtype, const void* rhs, int rhs_layout,
                     const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
@@ -193,7 +194,8 @@ int lmoe_ragged_dot_mxfp4_splitk(const void* lhs, const uint8_t* w_packed, const
  * small only costs extra passes).  Partial sums are added in a fixed order
  * (repeatable bit for bit) but not in the tile kernel's: the two agree within
  * bf16 rounding, not bit for bit.  K % 128 == 0, N % 16 == 0 (N % 32 with
- * SiTU), G <= 1024; lhs, w_tiled and out 16-byte aligned.  No workspace.
+ * SiTU), G <= 1024, M, K, N < 2^31; lhs, w_tiled and out 16-byte aligned.
+ * No workspace.
  */
 int lmoe_ragged_dot_mxfp4_skinny(const void* lhs, const uint8_t* w_tiled, const uint8_t* s_tiled,
                                  const int32_t* group_sizes, int64_t M, int64_t K, int64_t N, int64_t G,
@@ -239,7 +241,8 @@ int lmoe_dense_blaslt(const void* x, int x_dtype, const void* w_nk, int w_dtype,
  * (the layer's router logits + down-projection, ref.py:620 / ref.py:634-655,
  * and up-projection, ref.py:430).  256 x 128 output tiles on the bf16 MFMA
  * with a direct-to-LDS DMA pipeline; summation order differs from hipBLASLt's.
- * K % 64 == 0, N % 8 == 0, buffers 16-byte aligned.  No workspace.
+ * K % 64 == 0, N % 8 == 0, K < 2^23, M, N < 2^31, buffers 16-byte aligned.
+ * No workspace.
  */
 int lmoe_dense(const void* x, const void* w_nk, int64_t M, int64_t K, int64_t N, void* out, int out_dtype,
                void* stream);
@@ -248,7 +251,8 @@ int lmoe_dense(const void* x, const void* w_nk, int64_t M, int64_t K, int64_t N,
  * (N, K), f32 accumulation, out bf16 or f32.  Each weight byte is read once
  * per 16/32/64 rows; the K axis is split over a block's waves and summed in a
  * fixed order (repeatable bit for bit, another order than hipBLASLt's).
- * K % 128 == 0, N % 16 == 0, pointers 16-byte aligned.  No workspace.
+ * K % 128 == 0, N % 16 == 0, M, K, N < 2^31, pointers 16-byte aligned.  No
+ * workspace.
  */
 int lmoe_dense_skinny(const void* x, const void* w_nk, int64_t M, int64_t K, int64_t N, void* out, int out_dtype,
                       void* stream);
@@ -351,6 +355,7 @@ int lmoe_router_topk_proj(const float* logits, int64_t ld, const float* bias, in
  *   valid (m_padded,) u8, per_expert_counts (L,) int32
  *   padded_token_idx (m_padded,) int32 (-1 on padding), padded_w (m_padded,) w_dtype
  *   slot_pos (T*k,) int32 or NULL: sorted row of each (token, slot), -1 if not kept
+ * T, k, T*k and m_padded < 2^31, L + 1 <= 12288, local_start + L < 2^31.
  * Workspace: lmoe_dispatch_workspace_size(T, k, L) bytes, no initialisation needed
  * (-1 for sizes the dispatch refuses).
  */
