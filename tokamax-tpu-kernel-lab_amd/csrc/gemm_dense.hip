@@ -295,6 +295,8 @@ extern "C" int lmoe_dense(const void* x, const void* w_nk, int64_t M, int64_t K,
   // per-lane DMA offsets are 32-bit: one tile's rows of x and w
   LMOE_CHECK_SUPPORTED(K < (1ll << 23) && 256 * K * 2 < (1ll << 32) && M < (1ll << 31) && N < (1ll << 31),
                        "dense: sizes too large");
+  // tile counts and the grid are passed as int: 256 x 128 output tiles
+  LMOE_CHECK_SUPPORTED(ceil_div(M, 256) * ceil_div(N, 128) < (1ll << 31) - 8, "dense: grid too large");
   hipStream_t st = static_cast<hipStream_t>(stream);
   const uint16_t* xp = static_cast<const uint16_t*>(x);
   const uint16_t* wp = static_cast<const uint16_t*>(w_nk);
