@@ -263,3 +263,32 @@ def test_out_of_range_enums_are_refused_on_the_host(recorded):
           assert rc in (_lib.ERR_INVALID, _lib.ERR_UNSUPPORTED), (name, i, v, rc)
           checked += 1
   assert checked > 100, checked
+
+
+def test_last_error_is_per_thread():
+  """``lmoe_last_error`` is thread-local: two host threads that each make a
+  call the library refuses (null buffers) read their own message, though the
+  other thread's call failed in between."""
+  import threading
+  real = _lib.lib()
+  calls = {
+      "rms_norm": lambda: real.lmoe_rms_norm(None, None, 4, 8, 1e-6, _lib.BF16, None, None),
+      "add": lambda: real.lmoe_add(None, None, 8, _lib.BF16, None, None),
+  }
+  barrier = threading.Barrier(2, timeout=30)
+  seen = {name: [] for name in calls}
+
+  def run(name):
+    for _ in range(20):
+      rc = calls[name]()
+      barrier.wait()  # both calls have failed before either thread reads
+      seen[name].append((rc, real.lmoe_last_error().decode()))
+      barrier.wait()
+
+  threads = [threading.Thread(target=run, args=(n,)) for n in calls]
+  for t in threads:
+    t.start()
+  for t in threads:
+    t.join(60)
+  for name, got in seen.items():
+    assert len(got) == 20 and all(rc == _lib.ERR_INVALID and msg.startswith(name + ":") for rc, msg in got), got
