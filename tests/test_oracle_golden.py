@@ -41,3 +41,22 @@ def test_golden_bias_is_extreme():
   config, dtype, hidden, w, golden = _golden.load("golden_bundle_small")
   assert w["e_score_correction_bias"][0] > 1e5
   assert np.all(golden["topk_indices"][:, 0] == 0) or np.all((golden["topk_indices"] == 0).any(-1))
+
+
+def test_committed_bundles_match_their_provenance():
+  """Every committed golden file is byte-identical to the reference file that
+  SHA256SUMS names, and every bundle the tests load is listed there."""
+  import hashlib
+  import os
+  listed = {}
+  with open(os.path.join(_golden.GOLDEN_DIR, "SHA256SUMS")) as f:
+    for line in f:
+      digest, path = line.split()
+      listed[path.split("/", 1)[1]] = digest
+  on_disk = {f"{b}/{n}" for b in os.listdir(_golden.GOLDEN_DIR) if b.startswith("golden_bundle_")
+             for n in os.listdir(os.path.join(_golden.GOLDEN_DIR, b))}
+  assert on_disk == set(listed)
+  for rel, digest in listed.items():
+    with open(os.path.join(_golden.GOLDEN_DIR, rel), "rb") as f:
+      assert hashlib.sha256(f.read()).hexdigest() == digest, rel
+  assert {rel.split("/")[0] for rel in listed} == set(_golden.BUNDLES)
