@@ -6,6 +6,10 @@ registers no longer leave room for the waves per SIMD its schedule counts
 on, loses time without changing a single output bit, so no parity test can
 see it; here it fails on the CPU.
 
+The same code objects, disassembled, show that the build's
+``-packed-fp32-ops`` target feature holds: no packed FP32 add / multiply /
+FMA anywhere (those have given silent wrong results on the target boxes).
+
 The code objects come out of the library's .hip_fatbin section: one clang
 offload bundle per source file, each holding a host entry and the gfx950 ELF
 code object."""
@@ -57,11 +61,18 @@ def _code_objects(tmp_path):
   return objs
 
 
-def _kernels(tmp_path):
-  kernels = []
+def _write_code_objects(tmp_path):
+  paths = []
   for i, obj in enumerate(_code_objects(tmp_path)):
     path = tmp_path / f"co_{i}.o"
     path.write_bytes(obj)
+    paths.append(path)
+  return paths
+
+
+def _kernels(paths):
+  kernels = []
+  for path in paths:
     notes = subprocess.run([f"{LLVM}/llvm-readelf", "--notes", str(path)], capture_output=True, text=True,
                            timeout=120).stdout
     doc = notes[notes.index("---"):]
@@ -84,11 +95,18 @@ def _waves_per_simd(k):
 
 
 @pytest.fixture(scope="module")
-def kernels(tmp_path_factory):
+def code_objects(tmp_path_factory):
   if not os.path.exists(_lib.LIB_PATH):
     pytest.fail(f"{_lib.LIB_PATH} is not built")
-  ks = _kernels(tmp_path_factory.mktemp("codeobj"))
-  assert len(ks) > 100  # every source with device code contributes its kernels
+  paths = _write_code_objects(tmp_path_factory.mktemp("codeobj"))
+  assert len(paths) >= 10  # one per source file with device code
+  return paths
+
+
+@pytest.fixture(scope="module")
+def kernels(code_objects):
+  ks = _kernels(code_objects)
+  assert len(ks) > 100
   return ks
 
 
@@ -129,3 +147,34 @@ def test_streamed_gemm_keeps_three_waves_per_simd(kernels):
   for k in streamed:
     assert k[".private_segment_fixed_size"] == 0, k[".name"]
     assert _waves_per_simd(k) >= 3, (k[".name"], k[".vgpr_count"], k[".agpr_count"])
+
+
+PACKED_FP32 = re.compile(r"\bv_pk_(add|mul|fma)_f32\b")
+
+AXPY2 = r"""
+#include <hip/hip_runtime.h>
+__global__ void axpy2(const float2* __restrict__ x, float2* __restrict__ y, float a, int n) {
+  int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) { float2 v = x[i], w = y[i]; w.x = a * v.x + w.x; w.y = a * v.y + w.y; y[i] = w; }
+}
+"""
+
+
+def test_no_packed_fp32_in_the_library(code_objects, tmp_path):
+  """The control first: the same compiler, without the feature switch, turns
+  a float2 a*x + y into a packed FP32 FMA that this pattern finds; the
+  library's code, built with the switch, holds none."""
+  src = tmp_path / "axpy2.hip"
+  src.write_text(AXPY2)
+  r = subprocess.run(["/opt/rocm/bin/hipcc", "--offload-arch=gfx950", "-O3", "--cuda-device-only", "-S", str(src),
+                      "-o", str(tmp_path / "axpy2.s")], capture_output=True, text=True, timeout=300)
+  assert r.returncode == 0, r.stderr[-2000:]
+  assert PACKED_FP32.search((tmp_path / "axpy2.s").read_text())
+  instructions = 0
+  for path in code_objects:
+    dis = subprocess.run([f"{LLVM}/llvm-objdump", "-d", "--mcpu=gfx950", str(path)], capture_output=True, text=True,
+                         timeout=300).stdout
+    instructions += dis.count("\n")
+    hit = PACKED_FP32.search(dis)
+    assert hit is None, f"{path.name}: {hit.group(0)}"
+  assert instructions > 100000  # the disassembly is the whole library
