@@ -34,6 +34,16 @@ BAD = {
     "mxfp4 rows: 3 group sizes": lambda: ops.ragged_dot_mxfp4(R(64, 128), U8(4, 2, 64, 32), U8(4, 2, 64, 2), GS[:3],
                                                                weight_layout="tiled", lhs_row_index=I32(64)),
     "mxfp4: unknown mode": lambda: ops.ragged_dot_mxfp4(R(64, 128), U8(4, 64, 64), U8(4, 64, 4), GS, mode="fast"),
+    # K = 65 with weights for K = 64: K / 64 and K / 32 round down to the weights' shapes
+    "mxfp4 tiled: K not a multiple of 64": lambda: ops.ragged_dot_mxfp4(R(64, 65), U8(4, 1, 64, 32), U8(4, 1, 64, 2),
+                                                                         GS, weight_layout="tiled"),
+    "mxfp4: K not a multiple of 64": lambda: ops.ragged_dot_mxfp4(R(64, 65), U8(4, 64, 32), U8(4, 64, 2), GS),
+    "mxfp4 rows: K not a multiple of 64": lambda: ops.ragged_dot_mxfp4(R(64, 65), U8(4, 1, 64, 32), U8(4, 1, 64, 2),
+                                                                        GS, weight_layout="tiled",
+                                                                        lhs_row_index=I32(64)),
+    "mxfp8 x mxfp4: K not a multiple of 128": lambda: ops.ragged_dot_mxfp8_mxfp4(U8(64, 130), U8(1, 64, 4),
+                                                                                  U8(4, 2, 64, 32), U8(4, 2, 64, 2),
+                                                                                  GS),
     "mxfp8 x mxfp4: 3 group sizes": lambda: ops.ragged_dot_mxfp8_mxfp4(U8(64, 128), U8(1, 64, 4), U8(4, 2, 64, 32),
                                                                         U8(4, 2, 64, 2), GS[:3]),
     "mxfp6 x mxfp4: 3 group sizes": lambda: ops.ragged_dot_mxfp6_mxfp4(U8(64, 96), U8(1, 64, 4), U8(4, 2, 64, 32),
@@ -143,4 +153,15 @@ def test_layer_refuses_weights_that_disagree_with_its_config(monkeypatch, case):
   rec.calls.clear()
   with pytest.raises(ValueError):
     forward.LocalShardLatentMoE(c.config(), **dict(kw, **bad))
+  assert not rec.calls
+
+
+@pytest.mark.parametrize("shape", [(0, 0), (5, 0), (0, 64)])
+def test_empty_rms_norm_returns_its_empty_output(monkeypatch, shape):
+  """Normalising no elements (no rows, or rows of width 0) gives an empty
+  output of the input's shape without a library call (the library refuses
+  a width of 0)."""
+  rec = _stand_in.install(monkeypatch)
+  out = ops._rms_norm(R(*shape), torch.ones(shape[1], dtype=bf), 1e-6)
+  assert out.shape == shape and out.dtype == bf
   assert not rec.calls

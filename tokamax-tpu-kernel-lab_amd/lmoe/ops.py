@@ -371,7 +371,7 @@ def ragged_dot_mxfp8_mxfp4(lhs_q: torch.Tensor, lhs_scale: torch.Tensor, w_packe
     raise ValueError(f"weights must be tiled (G, K/64, N, 32), got {tuple(w_packed.shape)}")
   g, _, n, _ = w_packed.shape
   m4 = (m + 3) // 4 * 4
-  if (lhs_q.dtype != torch.uint8 or tuple(lhs_scale.shape) != (k // 128, m4, 4)
+  if (lhs_q.dtype != torch.uint8 or k % 128 or tuple(lhs_scale.shape) != (k // 128, m4, 4)
       or tuple(w_packed.shape) != (g, k // 64, n, 32) or tuple(w_scale.shape) != (g, k // 64, n, 2)):
     raise ValueError(f"shapes: lhs {tuple(lhs_q.shape)} scale {tuple(lhs_scale.shape)} "
                      f"w {tuple(w_packed.shape)} w_scale {tuple(w_scale.shape)}")
@@ -500,6 +500,8 @@ def ragged_dot_mxfp4(lhs: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.T
   if group_sizes.dtype != torch.int32:
     raise ValueError("group_sizes must be int32")
   m, k = lhs.shape
+  if k % 64:  # the weight shapes below are formed with K / 64 and K / 32
+    raise NotImplementedError(f"MXFP4 GEMM needs K % 64 == 0 (K={k})")
   if weight_layout == "tiled":
     if w_packed.dim() != 4 or w_packed.shape[3] != 32:
       raise ValueError(f"tiled packed weights must be (G, K/64, N, 32), got {tuple(w_packed.shape)}")
@@ -581,6 +583,8 @@ def _ragged_dot_mxfp4_rows(lhs, row_index, w_packed, w_scale, group_sizes, *, fu
   if weight_layout != "tiled" or mode != "lds_dequant":
     raise NotImplementedError("gathered rows: tiled weights on the lds_dequant streamed kernel only")
   rows, k = lhs.shape
+  if k % 64:
+    raise NotImplementedError(f"MXFP4 GEMM needs K % 64 == 0 (K={k})")
   m = row_index.shape[0]
   if w_packed.dim() != 4 or w_packed.shape[3] != 32:
     raise ValueError(f"tiled packed weights must be (G, K/64, N, 32), got {tuple(w_packed.shape)}")
@@ -1149,6 +1153,8 @@ def _rms_norm(x: torch.Tensor, scale: torch.Tensor, eps: float) -> torch.Tensor:
   if scale.numel() != n:
     raise ValueError(f"scale has {scale.numel()} entries for rows of {n}")
   out = torch.empty_like(x)
+  if x.numel() == 0:  # no rows, or rows of width 0: nothing to normalise
+    return out
   check(lib().lmoe_rms_norm(_p(x), _p(scale.to(x.dtype).contiguous()), x.numel() // n, n, eps, _dt(x),
                             _p(out), _stream()), "rms_norm")
   return out
