@@ -1,0 +1,108 @@
+"""The local-shard layer across its configuration space, on the CPU: hidden,
+latent and intermediate sizes, expert count, top-k, local expert range,
+token count (decode and prefill), capacity factor, expert format (MXFP4 or
+bf16), MXFP4 mode and stage return drawn by hypothesis.  A configuration the
+layer cannot run is refused when it is built (ValueError /
+NotImplementedError); one it builds runs its forward against the recording
+stand-in library without raising, every buffer it hands the library holds
+what the call's sizes say, and (where no GPU is present) every call passes
+the real library's host checks.  The forward chooses among several paths by
+size (the one-launch decode dispatch, the gathered-rows gate/up, the fused
+router projection, the stage-returning path); this checks that each
+combination it can choose is one the library takes."""
+import pytest
+import torch
+from hypothesis import HealthCheck, given, settings
+from hypothesis import strategies as st
+
+import test_buffer_extents as X
+from lmoe import _lib, forward, ops
+from lmoe.workloads import Config5, make_config5
+
+NO_GPU = torch.cuda.device_count() == 0
+
+
+def _build(c, fmt, mode):
+  hidden, w, ex = make_config5("cpu", c, fmt)
+  layer = forward.LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                                      e_score_correction_bias=w["e_score_correction_bias"],
+                                      down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                                      local_expert_start=c.local_start, local_num_experts=c.local_experts,
+                                      expert_format=fmt, experts=ex, capacity_factor=c.capacity_factor,
+                                      mxfp4_mode=mode)
+  return layer, hidden
+
+
+def _replay_refusals(calls):
+  real = _lib.lib()
+  out = []
+  for name, args, _ in calls:
+    rc = getattr(real, name)(*args)
+    if rc not in (_lib.OK, _lib.ERR_HIP):
+      out.append((name, rc, real.lmoe_last_error().decode()))
+  return out
+
+
+def test_configurations(monkeypatch):
+  log = X.ExtentLog(monkeypatch)
+  stats = {"ran": 0, "refused": 0}
+
+  @settings(max_examples=120, deadline=None, derandomize=True, database=None,
+            suppress_health_check=[HealthCheck.too_slow, HealthCheck.function_scoped_fixture])
+  @given(st.data())
+  def run(data):
+    pick = lambda xs: data.draw(st.sampled_from(xs))
+    e = pick([8, 16, 60, 128, 256])
+    L = pick([n for n in (1, 4, 15, 16, 60, 128) if n <= e])
+    c = Config5(tokens=pick([1, 2, 5, 16, 63, 64, 65, 200, 512]), hidden=pick([64, 128, 256]),
+                latent=pick([64, 128, 192, 256, 1024, 1088, 2048]), intermediate=pick([64, 128, 192, 256]),
+                experts=e, top_k=pick([k for k in (1, 2, 4, 8, 16) if k <= e]),
+                local_start=pick(sorted({0, min(3, e - L), e - L})), local_experts=L,
+                capacity_factor=pick([1.0, 2.0, 4.0]))
+    fmt = pick(["mxfp4", "mxfp4", "bf16"])
+    mode = pick(["lds_dequant", "lds_dequant", "scaled_mfma"]) if fmt == "mxfp4" else "lds_dequant"
+    stages = pick([False, False, True])
+    try:
+      layer, hidden = _build(c, fmt, mode)
+    except (ValueError, NotImplementedError):
+      stats["refused"] += 1
+      return
+    log.clear()
+    layer.forward(hidden, return_stages=stages)  # a layer that builds runs
+    X.check_extents(log.calls)
+    if NO_GPU:
+      assert not _replay_refusals(log.calls), (c, fmt, mode, stages)
+    stats["ran"] += 1
+
+  run()
+  assert stats["ran"] >= 80, stats
+
+
+def test_one_token_bf16_experts(monkeypatch):
+  """One token through a layer with bf16 expert weights: the latent rows are
+  a one-row slice of the fused router + down-projection output, rounded to
+  bf16 by the dispatch as for any other batch (a single-row slice counts as
+  contiguous to torch)."""
+  log = X.ExtentLog(monkeypatch)
+  c = Config5(tokens=1, hidden=128, latent=128, intermediate=64, experts=16, top_k=2, local_start=0,
+              local_experts=16)
+  layer, hidden = _build(c, "bf16", "lds_dequant")
+  log.clear()
+  layer.forward(hidden)
+  assert "lmoe_ragged_dot_gateup_situ" in [n for n, _, _ in log.calls]
+
+
+@pytest.mark.parametrize("t", [1, 2])
+def test_dispatch_rounds_a_row_slice_to_bf16_at_every_batch_size(monkeypatch, t):
+  X.ExtentLog(monkeypatch)
+  wide = torch.zeros(t, 16 + 64)
+  d = ops.dispatch_local(torch.zeros(t, 2, dtype=torch.int32), torch.zeros(t, 2), wide[:, 16:], 0, 4, 128,
+                         path="sort")
+  assert d.sorted_tokens.dtype == torch.bfloat16
+
+
+def test_scaled_mode_refuses_sizes_it_cannot_quantise():
+  c = Config5(tokens=4, hidden=128, latent=192, intermediate=128, experts=16, top_k=2, local_start=0,
+              local_experts=16)
+  with pytest.raises(NotImplementedError, match="multiples of 128"):
+    _build(c, "mxfp4", "scaled_mfma")

@@ -157,6 +157,11 @@ class LocalShardLatentMoE:
     if not (local_num_experts > 0 and 0 <= local_expert_start and local_expert_start + local_num_experts <= e):
       raise ValueError(f"local experts [{local_expert_start}, {local_expert_start + local_num_experts}) "
                        f"outside the {e} experts")
+    if expert_format == "mxfp4" and mxfp4_mode.startswith("scaled_mfma") and (
+        lat % 128 or config.intermediate_size % 128):
+      # the activations of both expert GEMMs are quantised in blocks of 128 along K
+      raise NotImplementedError(f"mxfp4_mode={mxfp4_mode!r} needs latent and intermediate sizes that are "
+                                f"multiples of 128 (got {lat}, {config.intermediate_size})")
     self.config = config
     self.L = local_num_experts
     self.start = local_expert_start

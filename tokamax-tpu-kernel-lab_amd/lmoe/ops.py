@@ -87,6 +87,14 @@ def _check_rows(x: torch.Tensor, t: int) -> None:
     raise ValueError(f"x {tuple(x.shape)}: want ({t}, lat) token rows")
 
 
+def _row_strided(x: torch.Tensor) -> bool:
+  """Rows further apart than their width (e.g. a column slice of a wider
+  array), judged by the strides themselves: torch calls a single-row slice
+  contiguous whatever its row stride, and a one-token batch must take the
+  same path as a larger one."""
+  return x.stride(-1) != 1 or (x.shape[0] > 0 and x.stride(0) != x.shape[-1])
+
+
 def _workspace(nbytes: int, device) -> torch.Tensor:
   return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
@@ -951,7 +959,7 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
   L = local_num_experts
   small_ok = small_dispatch_supported(t, k, lat, L, m_padded)
   if path == "auto":
-    path = "small" if small_ok and x.dtype == torch.bfloat16 and x.is_contiguous() else "sort"
+    path = "small" if small_ok and x.dtype == torch.bfloat16 and not _row_strided(x) else "sort"
   if path == "small":
     if not small_ok:
       raise NotImplementedError(f"one-launch dispatch: T*k={t * k}, m_padded={m_padded}, L={L}, lat={lat}")
@@ -973,7 +981,7 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
     return Dispatch(sorted_tokens, group_sizes, valid, counts, tok, w, slot_pos)
   if path != "sort":
     raise ValueError(f"path {path!r}")
-  if skip_padding_rows or not x.is_contiguous():
+  if skip_padding_rows or _row_strided(x):
     # row-strided bf16 / f32 rows, written as bf16: the counting sort with a
     # converting gather (the one-launch kernel when the sizes fit it)
     x = _dev_rows(x)
