@@ -9,7 +9,9 @@ what the call's sizes say, and (where no GPU is present) every call passes
 the real library's host checks.  The forward chooses among several paths by
 size (the one-launch decode dispatch, the gathered-rows gate/up, the fused
 router projection, the stage-returning path); this checks that each
-combination it can choose is one the library takes."""
+combination it can choose is one the library takes.  The reference-API
+forwards (unsharded and functional single-shard) are swept the same way
+over the configurations the reference allows."""
 import pytest
 import torch
 from hypothesis import HealthCheck, given, settings
@@ -106,3 +108,50 @@ def test_scaled_mode_refuses_sizes_it_cannot_quantise():
               local_experts=16)
   with pytest.raises(NotImplementedError, match="multiples of 128"):
     _build(c, "mxfp4", "scaled_mfma")
+
+
+def test_reference_api_forwards(monkeypatch):
+  """``latent_moe_forward`` (unsharded) and the functional single-shard
+  forward across configurations the reference allows -- f32 or bf16
+  weights, 1 to 128 experts, sizes off the 8-element grid (hidden 72,
+  latent 24, intermediate 40), no / one / two shared experts, sigmoid or
+  softmax gate, renormalised or not, fused gate/up or not: each runs without
+  raising, with large-enough buffers and every call past the real library's
+  host checks."""
+  from lmoe.config import LatentMoEConfig, init_weights
+  log = X.ExtentLog(monkeypatch)
+  stats = {"ran": 0}
+
+  @settings(max_examples=150, deadline=None, derandomize=True, database=None,
+            suppress_health_check=[HealthCheck.too_slow, HealthCheck.function_scoped_fixture])
+  @given(st.data())
+  def run(data):
+    pick = lambda xs: data.draw(st.sampled_from(xs))
+    e = pick([1, 2, 8, 16, 60, 128])
+    cfg = LatentMoEConfig(hidden_size=pick([8, 32, 48, 64, 72, 256]), latent_size=pick([8, 16, 24, 32, 48, 128]),
+                          intermediate_size=pick([8, 16, 40, 48, 128]), num_experts=e,
+                          top_k=pick([k for k in (1, 2, 4, 8, 16) if k <= e]), num_shared_experts=pick([0, 1, 2]),
+                          moe_renormalize=pick([True, False]), routed_scaling_factor=pick([1.0, 2.5]))
+    dt = pick([torch.float32, torch.bfloat16])
+    W = init_weights(cfg, dtype=dt, device="cpu")
+    h = torch.zeros(pick([1, 2, 5, 20, 64, 300]), cfg.hidden_size, dtype=dt)
+    act = pick(["sigmoid", "softmax"])
+    log.clear()
+    if pick(["unsharded", "shard"]) == "unsharded":
+      forward.latent_moe_forward(h, W, cfg, act=act)
+    else:
+      L = pick([n for n in (1, 4, e) if n <= e])
+      start = pick(sorted({0, e - L}))
+      pad = lambda w: torch.cat([w[start:start + L], torch.zeros_like(w[:1])])
+      forward.latent_moe_forward_ragged_dot_single_shard_jittable(
+          h, W.router_weight, W.e_score_correction_bias, W.down_proj, pad(W.expert_gate), pad(W.expert_up),
+          pad(W.expert_down), W.norm_scale, W.up_proj, W.shared_gate if cfg.num_shared_experts else None,
+          W.shared_up, W.shared_down, cfg, start, L, capacity_factor=pick([1.0, 2.0]), act=act,
+          fused_gateup=pick([False, True]))
+    X.check_extents(log.calls)
+    if NO_GPU:
+      assert not _replay_refusals(log.calls), (cfg, dt, h.shape)
+    stats["ran"] += 1
+
+  run()
+  assert stats["ran"] == 150

@@ -141,6 +141,15 @@ def ragged_dot(lhs: torch.Tensor, rhs: torch.Tensor, group_sizes: torch.Tensor, 
   if rhs.dtype != lhs.dtype:
     raise NotImplementedError(f"mixed lhs {lhs.dtype} / rhs {rhs.dtype}")
   out_dtype = preferred_element_type or lhs.dtype
+  if m == 0 or n == 0 or k == 0:  # nothing to read: an empty sum is zero
+    return torch.zeros((m, n), dtype=out_dtype, device=lhs.device)
+  if lhs.dtype == torch.bfloat16 and (k % 8 or n % 8):
+    # off the bf16 kernels' 8-element grid: the any-shape f32 kernel on the
+    # same values (bf16 products are exact in f32, accumulated in f32 as on
+    # the bf16 path), then one rounding to the output dtype
+    out = ragged_dot(lhs.float(), rhs.float(), group_sizes, preferred_element_type=torch.float32,
+                     rhs_layout=rhs_layout, zero_group=zero_group)
+    return out if out_dtype == torch.float32 else out.to(out_dtype)
   # reference-layout (G, K, N) weights are read as they lie: the kernel
   # transposes each B tile in LDS (ds_read_b64_tr_b16), as fast as prepared
   # (G, N, K) weights and faster than transposing them first
@@ -169,8 +178,11 @@ def ragged_dot_gateup_situ(lhs: torch.Tensor, rhs_gu: torch.Tensor, group_sizes:
   epilogue in registers (rd.py:644-723; gate/up rounded to bf16 before SiTU as
   in gk.py:114-125).  rhs_gu (G, K, 2I) ("gkn") or (G, 2I, K) ("gnk"); out (M, I)."""
   _dev(lhs, rhs_gu, group_sizes)
-  if lhs.dtype != torch.bfloat16 or rhs_gu.dtype != torch.bfloat16:
-    raise NotImplementedError("fused gate/up SiTU is bf16 only")
+  f32 = lhs.dtype == torch.float32 and rhs_gu.dtype == torch.float32
+  if not f32 and (lhs.dtype != torch.bfloat16 or rhs_gu.dtype != torch.bfloat16):
+    raise NotImplementedError("fused gate/up SiTU takes bf16 (or f32) lhs and weights of one dtype")
+  if lhs.dim() != 2 or rhs_gu.dim() != 3:
+    raise ValueError(f"gateup: lhs {tuple(lhs.shape)} / rhs {tuple(rhs_gu.shape)} ranks")
   m, k = lhs.shape
   g = rhs_gu.shape[0]
   if rhs_layout == "gkn":
@@ -183,6 +195,21 @@ def ragged_dot_gateup_situ(lhs: torch.Tensor, rhs_gu: torch.Tensor, group_sizes:
     raise ValueError(f"gateup shapes lhs {tuple(lhs.shape)} rhs {tuple(rhs_gu.shape)}")
   _check_groups(group_sizes, g)
   inter = n2 // 2
+  if f32 or m == 0 or k == 0 or inter == 0 or k % 8 or inter % 8:
+    # f32 (rounding to f32 before the activation is the identity), empty or
+    # off-grid problems: the two halves as ragged_dots, then the SiTU-GLU
+    if rhs_layout == "gkn":
+      gate, up = rhs_gu[:, :, :inter].contiguous(), rhs_gu[:, :, inter:].contiguous()
+    else:
+      gate, up = rhs_gu[:, :inter].contiguous(), rhs_gu[:, inter:].contiguous()
+    # gate / up rounded to the lhs dtype before the activation, or kept f32
+    pet = None if f32 or round_before_act else torch.float32
+    gate_out = ragged_dot(lhs, gate, group_sizes, preferred_element_type=pet, rhs_layout=rhs_layout,
+                          zero_group=zero_group)
+    up_out = ragged_dot(lhs, up, group_sizes, preferred_element_type=pet, rhs_layout=rhs_layout,
+                        zero_group=zero_group)
+    act = _situ_and_mul(gate_out, up_out, beta, linear_beta)
+    return act if act.dtype == lhs.dtype else act.to(lhs.dtype)
   out = torch.empty((m, inter), dtype=torch.bfloat16, device=lhs.device)
   check(lib().lmoe_ragged_dot_gateup_situ(_p(lhs), _p(rhs_gu), layout, _p(group_sizes), m, k, inter,
                                           g, zero_group, beta, linear_beta, int(round_before_act),
@@ -741,6 +768,10 @@ def dense(x: torch.Tensor, w: torch.Tensor, out_dtype: torch.dtype | None = None
   if backend not in _DENSE_BACKENDS:
     raise ValueError(f"backend {backend!r}")
   out_dtype = out_dtype or x.dtype
+  if x.dim() == 2 and w.dim() == 2 and x.shape[1] == w.shape[1 if w_layout == "nk" else 0]:
+    n = w.shape[0 if w_layout == "nk" else 1]
+    if x.shape[0] == 0 or x.shape[1] == 0 or n == 0:  # nothing to read: an empty sum is zero
+      return torch.zeros((x.shape[0], n), dtype=out_dtype, device=x.device)
   nk_bf16 = w_layout == "nk" and x.dtype == torch.bfloat16 and w.dtype == torch.bfloat16
   if backend == "auto" and nk_bf16 and x.dim() == 2 and x.shape[0] <= SKINNY_DENSE_ROWS \
      and x.shape[1] % 128 == 0 and w.shape[0] % 16 == 0 and w.shape[0] >= SKINNY_DENSE_MIN_N:
