@@ -1,8 +1,10 @@
-"""A stand-in for liblmoe.so that computes, on the CPU, for the few entry
-points the operators' host-side fallbacks reach: lmoe_ragged_dot (f32 and
-bf16, both weight layouts, zero_group), lmoe_situ_and_mul and lmoe_add,
-each reading and writing the host buffers behind the pointers the operators
-pass, with the oracle's definitions.  Test infrastructure only: it lets the
+"""A stand-in for liblmoe.so that computes, on the CPU, the entry points of
+the bf16 / f32 forwards -- router top-k (with the projection's bf16 rows),
+the four dispatch entry points, the three combines, the grouped GEMM and
+fused gate/up, the dense projections, RMSNorm, SiTU-GLU, add and the row
+cast -- each reading and writing the host buffers behind the pointers the
+operators pass, with the oracle's definitions (the slot-driven combine
+restates the header's add order directly).  Test infrastructure only: it lets the
 Python layer's composition (which entry point, which views, dtypes and
 casts) be checked for values on a machine without a GPU; the kernels
 themselves are checked on the GPU.  Where no GPU is present each call is
@@ -49,6 +51,32 @@ def _dt(code):
   return "f32" if code == _lib.F32 else "bf16"
 
 
+def _ints(ptr, count, ctype=ctypes.c_int32):
+  if count == 0 or not ptr:
+    return np.zeros(0, np.int64)
+  return np.ctypeslib.as_array((ctype * count).from_address(ptr)).astype(np.int64)
+
+
+def _put_ints(ptr, values, ctype=ctypes.c_int32):
+  v = np.asarray(values).ravel()
+  if v.size and ptr:
+    np.ctypeslib.as_array((ctype * v.size).from_address(ptr))[:] = v
+
+
+def _rows(ptr, n, ld, width, dtype):
+  """n rows of `width` elements, ld elements apart, as float32 (n, width)."""
+  if n == 0 or width == 0:
+    return np.zeros((n, width), np.float32)
+  flat = _read(ptr, (n - 1) * ld + width, dtype)
+  return np.stack([flat[i * ld:i * ld + width] for i in range(n)])
+
+
+def _gkn(ptr, G, K, N, dtype, layout):
+  """Grouped weights as (G, K, N) in memory order, whichever layout they have."""
+  w = _read(ptr, G * K * N, dtype)
+  return w.reshape(G, K, N) if layout == _lib.RHS_GKN else np.ascontiguousarray(w.reshape(G, N, K).transpose(0, 2, 1))
+
+
 class EmulatedLib:
   def __init__(self):
     self.calls = []
@@ -75,17 +103,160 @@ class EmulatedLib:
   def names(self):
     return list(self.calls)
 
-  def _lmoe_ragged_dot(self, lhs, lhs_dt, rhs, layout, gs, M, K, N, G, zero_group, out, out_dt, stream):
-    a = _read(lhs, M * K, lhs_dt).reshape(M, K)
-    w = _read(rhs, G * K * N, lhs_dt)
-    # (G, K, N) in memory order, so numpy sums each dot product as the oracle does
-    w = w.reshape(G, K, N) if layout == _lib.RHS_GKN else np.ascontiguousarray(w.reshape(G, N, K).transpose(0, 2, 1))
-    sizes = np.ctypeslib.as_array((ctypes.c_int32 * G).from_address(gs)).copy() if G else np.zeros(0, np.int32)
-    res = O.ragged_dot(a, w, sizes, "f32")
-    if 0 <= zero_group < G:
+  @staticmethod
+  def _zero_group_rows(res, sizes, zero_group):
+    if 0 <= zero_group < len(sizes):
       start = int(sizes[:zero_group].sum())
       res[start:start + int(sizes[zero_group])] = 0
+    return res
+
+  def _lmoe_ragged_dot(self, lhs, lhs_dt, rhs, layout, gs, M, K, N, G, zero_group, out, out_dt, stream):
+    a = _read(lhs, M * K, lhs_dt).reshape(M, K)
+    # (G, K, N) in memory order, so numpy sums each dot product as the oracle does
+    w = _gkn(rhs, G, K, N, lhs_dt, layout)
+    sizes = _ints(gs, G)
+    res = self._zero_group_rows(O.ragged_dot(a, w, sizes, "f32"), sizes, zero_group)
     _write(out, O.cast(res, _dt(out_dt)), out_dt)
+    return _lib.OK
+
+  def _lmoe_ragged_dot_gateup_situ(self, lhs, rhs, layout, gs, M, K, I, G, zero_group, beta, beta_lin, rba, out,
+                                   stream):
+    a = _read(lhs, M * K, _lib.BF16).reshape(M, K)
+    sizes = _ints(gs, G)
+    res = O.ragged_dot_gateup_situ(a, _gkn(rhs, G, K, 2 * I, _lib.BF16, layout), sizes, beta, beta_lin, "bf16",
+                                   round_before_act=bool(rba))
+    _write(out, self._zero_group_rows(res, sizes, zero_group), _lib.BF16)
+    return _lib.OK
+
+  # ---- dense projections: x (M, K) @ w_nk^T, f32 accumulation
+  def _lmoe_dense_blaslt(self, x, x_dt, w, w_dt, M, K, N, out, out_dt, stream):
+    a = _read(x, M * K, x_dt).reshape(M, K)
+    b = _read(w, N * K, w_dt).reshape(N, K)
+    _write(out, O.matmul(a, np.ascontiguousarray(b.T), _dt(out_dt)), out_dt)
+    return _lib.OK
+
+  def _lmoe_dense(self, x, w, M, K, N, out, out_dt, stream):
+    return self._lmoe_dense_blaslt(x, _lib.BF16, w, _lib.BF16, M, K, N, out, out_dt, stream)
+
+  _lmoe_dense_skinny = _lmoe_dense
+
+  # ---- router
+  def _lmoe_router_topk_ld(self, logits, ld, bias, T, E, k, act, renorm, scale, w_dt, idx, w, scores, stream):
+    if T == 0:
+      return _lib.OK
+    lg = _rows(logits, T, ld, E, _lib.F32)
+    b = _read(bias, E, _lib.F32) if bias else None
+    r = O.router_from_logits(lg, b, k, bool(renorm), scale, "sigmoid" if act == _lib.ACT_SIGMOID else "softmax",
+                             _dt(w_dt))
+    _put_ints(idx, r.topk_idx)
+    _write(w, r.topk_weight, w_dt)
+    if scores:
+      _write(scores, r.scores, _lib.F32)
+    return _lib.OK
+
+  def _lmoe_router_topk(self, logits, bias, T, E, k, act, renorm, scale, w_dt, idx, w, scores, stream):
+    return self._lmoe_router_topk_ld(logits, E, bias, T, E, k, act, renorm, scale, w_dt, idx, w, scores, stream)
+
+  def _lmoe_router_topk_proj(self, logits, ld, bias, T, E, k, act, renorm, scale, w_dt, idx, w, x_src, x_ld, lat,
+                             x_out, stream):
+    self._lmoe_router_topk_ld(logits, ld, bias, T, E, k, act, renorm, scale, w_dt, idx, w, None, stream)
+    _write(x_out, O.cast(_rows(x_src, T, x_ld, lat, _lib.F32), "bf16"), _lib.BF16)
+    return _lib.OK
+
+  # ---- dispatch (ref.py:754-877): the oracle's jittable dispatch
+  def _dispatch(self, idx, w, w_dt, xrows, T, k, start, L, m_padded, sorted_tokens, sorted_dt, gs, valid, counts,
+                tok, pw, slot, skip_padding):
+    ids = _ints(idx, T * k).reshape(T, k)
+    wts = _read(w, T * k, w_dt).reshape(T, k)
+    x = xrows if xrows is not None else np.zeros((T, 1), np.float32)
+    d, slot_pos = O.filter_and_pad_to_shard_jittable(ids, wts, x, k, start + L, start, L, m_padded=m_padded,
+                                                     return_slot_pos=True)
+    sorted_x, sizes, ok, cnt, tk, wk = d
+    if sorted_tokens and xrows is not None:
+      rows = int(cnt.sum()) if skip_padding else m_padded
+      _write(sorted_tokens, O.cast(sorted_x[:rows], _dt(sorted_dt)), sorted_dt)
+    _put_ints(gs, sizes)
+    _put_ints(valid, ok.astype(np.uint8), ctypes.c_uint8)
+    _put_ints(counts, cnt)
+    _put_ints(tok, tk)
+    _write(pw, O.cast(wk, _dt(w_dt)), w_dt)
+    _put_ints(slot, slot_pos)
+    return _lib.OK
+
+  def _lmoe_dispatch_local_noalloc(self, idx, w, w_dt, x, x_dt, T, k, lat, start, L, m_padded, sorted_tokens, gs,
+                                   valid, counts, tok, pw, slot, stream):
+    return self._dispatch(idx, w, w_dt, _rows(x, T, lat, lat, x_dt), T, k, start, L, m_padded, sorted_tokens,
+                          x_dt, gs, valid, counts, tok, pw, slot, False)
+
+  def _lmoe_dispatch_local(self, idx, w, w_dt, x, x_dt, T, k, lat, start, L, m_padded, sorted_tokens, gs, valid,
+                           counts, tok, pw, slot, ws, ws_size, stream):
+    return self._lmoe_dispatch_local_noalloc(idx, w, w_dt, x, x_dt, T, k, lat, start, L, m_padded, sorted_tokens,
+                                             gs, valid, counts, tok, pw, slot, stream)
+
+  def _lmoe_dispatch_local_small(self, idx, w, w_dt, x, x_dt, x_ld, T, k, lat, start, L, m_padded, sorted_tokens,
+                                 gs, valid, counts, tok, pw, slot, flags, stream):
+    xrows = None if flags & _lib.DISPATCH_FLAG_NO_ROWS or not x else _rows(x, T, x_ld, lat, x_dt)
+    return self._dispatch(idx, w, w_dt, xrows, T, k, start, L, m_padded, sorted_tokens, _lib.BF16, gs, valid,
+                          counts, tok, pw, slot, bool(flags & _lib.DISPATCH_FLAG_SKIP_PADDING_ROWS))
+
+  def _lmoe_dispatch_local_rows(self, idx, w, w_dt, x, x_dt, x_ld, T, k, lat, start, L, m_padded, sorted_tokens,
+                                gs, valid, counts, tok, pw, slot, flags, ws, ws_size, stream):
+    return self._lmoe_dispatch_local_small(idx, w, w_dt, x, x_dt, x_ld, T, k, lat, start, L, m_padded,
+                                           sorted_tokens, gs, valid, counts, tok, pw, slot, flags, stream)
+
+  # ---- combine
+  @staticmethod
+  def _combine(shard, shard_dt, slot, w, w_dt, T, k, lat, mode, routed, out_dt):
+    """routed (T, lat) float32 values before the combine -> after it."""
+    sp = _ints(slot, T * k).reshape(T, k)
+    kept = sp[sp >= 0]
+    m = int(kept.max()) + 1 if kept.size else 1
+    rows = _read(shard, m * lat, shard_dt).reshape(m, lat)
+    if mode == _lib.COMBINE_SLOT_SUM:
+      # ref.py:413-416: f32 weighted sum over the k slots in slot order, one cast
+      wt = _read(w, T * k, w_dt).reshape(T, k)
+      acc = np.zeros((T, lat), np.float32)
+      for j in range(k):
+        vals = np.where((sp[:, j] >= 0)[:, None], rows[np.maximum(sp[:, j], 0)], np.float32(0))
+        acc = (acc + vals * wt[:, j:j + 1]).astype(np.float32)
+      return O.cast(acc, _dt(out_dt))
+    # ref.py:1113-1141: each token's kept rows added in ascending row order
+    pw = _read(w, m, w_dt)
+    pti = np.full(m, -1, np.int64)
+    for t in range(T):
+      for j in range(k):
+        if sp[t, j] >= 0:
+          pti[sp[t, j]] = t
+    return O.combine_shard_contribution(routed, rows, pti, pw, _dt(out_dt), _dt(shard_dt), _dt(w_dt))
+
+  def _lmoe_combine_slots(self, shard, shard_dt, slot, w, w_dt, T, k, lat, mode, routed, out_dt, stream):
+    cur = _read(routed, T * lat, out_dt).reshape(T, lat) if mode == _lib.COMBINE_SCATTER_ADD else None
+    _write(routed, self._combine(shard, shard_dt, slot, w, w_dt, T, k, lat, mode, cur, out_dt), out_dt)
+    return _lib.OK
+
+  def _lmoe_combine_slots_rms_norm(self, shard, shard_dt, slot, w, w_dt, T, k, lat, mode, scale, eps, routed,
+                                   normed, dt, stream):
+    res = self._combine(shard, shard_dt, slot, w, w_dt, T, k, lat, mode, np.zeros((T, lat), np.float32), dt)
+    if routed:
+      _write(routed, res, dt)
+    _write(normed, O.rms_norm(res, _read(scale, lat, dt), eps, _dt(dt)), dt)
+    return _lib.OK
+
+  def _lmoe_combine_scatter_add(self, shard, shard_dt, pti, pw, w_dt, m, lat, T, routed, out_dt, ws, ws_size,
+                                stream):
+    cur = _read(routed, T * lat, out_dt).reshape(T, lat)
+    res = O.combine_shard_contribution(cur, _read(shard, m * lat, shard_dt).reshape(m, lat), _ints(pti, m),
+                                       _read(pw, m, w_dt), _dt(out_dt), _dt(shard_dt), _dt(w_dt))
+    _write(routed, res, out_dt)
+    return _lib.OK
+
+  # ---- elementwise
+  def _lmoe_rms_norm(self, x, scale, rows, n, eps, dt, out, stream):
+    _write(out, O.rms_norm(_read(x, rows * n, dt).reshape(rows, n), _read(scale, n, dt), eps, _dt(dt)), dt)
+    return _lib.OK
+
+  def _lmoe_cast_rows(self, x, x_dt, rows, cols, ld, out, out_dt, stream):
+    _write(out, O.cast(_rows(x, rows, ld, cols, x_dt), _dt(out_dt)), out_dt)
     return _lib.OK
 
   def _lmoe_situ_and_mul(self, gate, up, count, beta, beta_lin, dt, out, stream):
@@ -106,7 +277,13 @@ def install(monkeypatch) -> EmulatedLib:
       if t is not None and not t.is_contiguous():
         raise ValueError("LatentMoE operators need contiguous tensors")
 
+  def dev_rows(t):
+    if t.dim() != 2:
+      raise ValueError("expected a 2-D tensor")
+    return t.contiguous() if t.stride(1) != 1 or t.stride(0) < t.shape[1] else t
+
   monkeypatch.setattr(ops, "lib", lambda: lib)
   monkeypatch.setattr(ops, "_stream", lambda: 0)
   monkeypatch.setattr(ops, "_dev", dev)
+  monkeypatch.setattr(ops, "_dev_rows", dev_rows)
   return lib

@@ -1,0 +1,117 @@
+"""The Python layer's composition of the library, checked for values on the
+CPU: the forwards run with the emulating stand-in library (each entry point
+computed by the oracle's definition on the operators' host buffers, behind
+the real library's host checks where no GPU is present), and their outputs
+go through the same checks as the GPU suite's forward tests -- the six
+golden bundles stage by stage at the reference's tolerances, the unsharded
+and single-shard forwards against the oracle on their own logits (routing,
+weights and every dispatch output bit for bit), and the prepared-weight
+layer with bf16 experts at one token and larger batches.  A mistake in how
+the operators chain the entry points (an argument order, a stride, a dtype,
+a combine mode, a padding group) fails here without a GPU; the kernels
+themselves are the GPU suite's."""
+import numpy as np
+import pytest
+import torch
+
+import _emulated_lib
+import _golden
+from _layer_check import check_single_shard, check_unsharded
+from _util import to_dev, to_np
+from lmoe.config import LatentMoEConfig, LatentMoEWeights
+from oracle import lmoe_oracle as O
+
+
+def _dev(a, dt="f32"):
+  return to_dev(a, dt, device="cpu")
+
+
+def _weights(w, dt):
+  return LatentMoEWeights(**{k: _dev(O.cast(v, dt), dt) for k, v in w.items()})
+
+
+@pytest.mark.parametrize("bundle", _golden.BUNDLES)
+def test_unsharded_forward_on_golden_bundles(monkeypatch, bundle):
+  from lmoe.forward import latent_moe_forward
+  lib = _emulated_lib.install(monkeypatch)
+  config, dtype, hidden, w, golden = _golden.load(bundle)
+  final, inter = latent_moe_forward(_dev(O.cast(hidden, dtype), dtype), _weights(w, dtype), config,
+                                    return_intermediates=True)
+  ours = {k: to_np(v) for k, v in inter.items()}
+  ours["sorted_token_indices"] = ours["sorted_token_indices"].astype(np.int64)
+  atol, rtol = _golden.TOLERANCES[dtype]
+  known = _golden.KNOWN_RESIDUALS.get(bundle, {})
+  failures = []
+
+  def check(name, g, o, exact):
+    assert g.shape == o.shape, (name, g.shape, o.shape)
+    if exact:
+      if not np.array_equal(g, o):
+        failures.append(f"{name}: exact mismatch")
+      return
+    max_abs = float(np.max(np.abs(g.astype(np.float64) - o))) if g.size else 0.0
+    bound = known.get(name)
+    if bound is not None:
+      if max_abs > bound:
+        failures.append(f"{name}: {max_abs:.3e} > documented {bound:.3e}")
+    elif not np.allclose(g, o, atol=atol, rtol=rtol):
+      failures.append(f"{name}: max_abs={max_abs:.3e}")
+
+  _golden.compare_stages(golden, ours, config, dtype, check)
+  assert not failures, failures
+  wc = {k: O.cast(v, dtype) for k, v in w.items()}
+  check_unsharded(f"emulated unsharded {bundle}", O.cast(hidden, dtype), wc, config, dtype, "sigmoid", final, inter)
+  assert {"lmoe_router_topk_ld", "lmoe_ragged_dot", "lmoe_combine_slots", "lmoe_rms_norm"} <= set(lib.names())
+
+
+def _shard_problem(rng, cfg, t, start, L):
+  """The GPU suite's shard problem with the latent projection and the expert
+  weights scaled by powers of two (bf16 values stay exact) so that gate and
+  up are of order one: at its N(0, 0.02^2) weights they are near 0.02, where
+  SiTU-GLU is close to the symmetric g * u / 2 and a gate / up swap moves
+  the output by less than the bf16 bound."""
+  import test_gpu_forward as G
+  hidden, w, gate, up, down = G._shard_problem(rng, cfg, t, start, L)
+  w = dict(w, down_proj=w["down_proj"] * 8)
+  return hidden, w, gate * 16, up * 16, down * 4
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_single_shard_forward(monkeypatch, fused):
+  from lmoe.forward import latent_moe_forward_ragged_dot_single_shard_jittable as fwd
+  _emulated_lib.install(monkeypatch)
+  cfg = LatentMoEConfig(hidden_size=64, latent_size=32, intermediate_size=48, num_experts=32, top_k=4,
+                        num_shared_experts=1)
+  t, start, L = 40, 8, 8
+  hidden, w, gate, up, down = _shard_problem(np.random.default_rng(21), cfg, t, start, L)
+  d = lambda a: _dev(a, "bf16")
+  out, st = fwd(d(hidden), d(w["router_weight"]), _dev(w["e_score_correction_bias"]), d(w["down_proj"]), d(gate),
+                d(up), d(down), d(w["norm_scale"]), d(w["up_proj"]), d(w["shared_gate"]), d(w["shared_up"]),
+                d(w["shared_down"]), cfg, start, L, return_stages=True, fused_gateup=fused)
+  check_single_shard(f"emulated single shard fused={fused}", hidden, w, gate, up, down, cfg, "bf16", start, L, 2.0,
+                     True, out, st)
+
+
+@pytest.mark.parametrize("t", [1, 5, 96])
+def test_local_shard_layer_bf16_experts(monkeypatch, t):
+  """The prepared-weight layer (fused router + down-projection GEMM, the
+  dispatch rounding the f32 latent columns to bf16, the fused gate/up, the
+  combine fused with the RMSNorm), one token included."""
+  from lmoe import ops
+  from lmoe.forward import LocalShardLatentMoE
+  lib = _emulated_lib.install(monkeypatch)
+  cfg = LatentMoEConfig(hidden_size=64, latent_size=32, intermediate_size=32, num_experts=32, top_k=4,
+                        num_shared_experts=0)
+  start, L = 0, 8
+  hidden, w, gate, up, down = _shard_problem(np.random.default_rng(22 + t), cfg, t, start, L)
+  d = lambda a: _dev(a, "bf16")
+  experts = {"gu_nk": ops.prefuse_gateup_weights_gnk(d(gate), d(up)), "down_nk": ops.to_gnk(d(down))}
+  layer = LocalShardLatentMoE(cfg, router_weight=d(w["router_weight"]),
+                              e_score_correction_bias=_dev(w["e_score_correction_bias"]), down_proj=d(w["down_proj"]),
+                              up_proj=d(w["up_proj"]), norm_scale=d(w["norm_scale"]), local_expert_start=start,
+                              local_num_experts=L, expert_format="bf16", experts=experts)
+  out, st = layer.forward(d(hidden), return_stages=True)
+  check_single_shard(f"emulated layer bf16 experts T={t}", hidden, w, gate, up, down, cfg, "bf16", start, L, 2.0,
+                     False, out, st)
+  assert "lmoe_ragged_dot_gateup_situ" in lib.names()
+  assert torch.equal(layer.forward(d(hidden)), out)  # without the stages: the same output
