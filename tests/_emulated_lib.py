@@ -2,7 +2,10 @@
 the bf16 / f32 forwards -- router top-k (with the projection's bf16 rows),
 the four dispatch entry points, the three combines, the grouped GEMM and
 fused gate/up, the dense projections, RMSNorm, SiTU-GLU, add and the row
-cast -- each reading and writing the host buffers behind the pointers the
+cast -- and of the MXFP4 expert paths (weight tiling and dequantisation, the
+grouped GEMM in both weight layouts and its gathered-rows, skinny and
+split-K forms, the fused decode dispatch, MXFP8 / MXFP6 activation
+quantisation and their scaled GEMMs) -- each reading and writing the host buffers behind the pointers the
 operators pass, with the oracle's definitions (the slot-driven combine
 restates the header's add order directly).  Test infrastructure only: it lets the
 Python layer's composition (which entry point, which views, dtypes and
@@ -248,6 +251,124 @@ class EmulatedLib:
     res = O.combine_shard_contribution(cur, _read(shard, m * lat, shard_dt).reshape(m, lat), _ints(pti, m),
                                        _read(pw, m, w_dt), _dt(out_dt), _dt(shard_dt), _dt(w_dt))
     _write(routed, res, out_dt)
+    return _lib.OK
+
+  # ---- MXFP4 weights: checkpoint (G, N, K/2) + (G, N, K/32); tiled (G, K/64, N, 32) + (G, K/64, N, 2),
+  # each 32-byte record holding the checkpoint's eight 4-byte groups in the order below
+  _RECORD = np.array([0, 2, 4, 6, 1, 3, 5, 7])
+
+  @classmethod
+  def _untile(cls, wp, ws, G, N, K):
+    tp = _ints(wp, G * (K // 64) * N * 32, ctypes.c_uint8).astype(np.uint8).reshape(G, K // 64, N, 8, 4)
+    ts = _ints(ws, G * (K // 64) * N * 2, ctypes.c_uint8).astype(np.uint8).reshape(G, K // 64, N, 2)
+    packed = np.empty_like(tp)
+    packed[:, :, :, cls._RECORD] = tp
+    packed = packed.transpose(0, 2, 1, 3, 4).reshape(G, N, K // 2)
+    return packed, np.ascontiguousarray(ts.transpose(0, 2, 1, 3).reshape(G, N, K // 32))
+
+  @staticmethod
+  def _checkpoint(wp, ws, G, N, K):
+    return (_ints(wp, G * N * (K // 2), ctypes.c_uint8).astype(np.uint8).reshape(G, N, K // 2),
+            _ints(ws, G * N * (K // 32), ctypes.c_uint8).astype(np.uint8).reshape(G, N, K // 32))
+
+  def _lmoe_mxfp4_tile(self, packed, scale, G, N, K, packed_out, scale_out, stream):
+    pk, sc = self._checkpoint(packed, scale, G, N, K)
+    rec = pk.reshape(G, N, K // 64, 8, 4)[:, :, :, self._RECORD].transpose(0, 2, 1, 3, 4)
+    _put_ints(packed_out, rec.reshape(-1), ctypes.c_uint8)
+    _put_ints(scale_out, sc.reshape(G, N, K // 64, 2).transpose(0, 2, 1, 3).reshape(-1), ctypes.c_uint8)
+    return _lib.OK
+
+  def _lmoe_mxfp4_dequant(self, packed, scale, batch, N, K, group_size, out, out_dt, stream):
+    pk = _ints(packed, batch * N * (K // 2), ctypes.c_uint8).astype(np.uint8).reshape(batch, N, K // 2)
+    sc = _ints(scale, batch * N * (K // group_size), ctypes.c_uint8).astype(np.uint8).reshape(batch, N, -1)
+    _write(out, O.cast(O.dequantize_mxfp4(pk, sc), _dt(out_dt)), out_dt)
+    return _lib.OK
+
+  def _mx_gemm(self, a, pk, sc, sizes, zero_group, epi, beta, beta_lin, out):
+    res = O.ragged_dot_mxfp4(a, pk, sc, sizes, "bf16", situ=(beta, beta_lin) if epi == _lib.EPI_SITU else None)
+    _write(out, self._zero_group_rows(res, sizes, zero_group), _lib.BF16)
+    return _lib.OK
+
+  def _lmoe_ragged_dot_mxfp4(self, lhs, wp, ws, gs, M, K, N, G, zero_group, mode, epi, beta, beta_lin, out,
+                             stream):
+    mode &= ~_lib.MXFP4_FLAG_SKIP_ZERO_GROUP_ROWS  # rows it lets go unwritten are written (as zeros)
+    pk, sc = (self._untile if mode == _lib.MXFP4_LDS_DEQUANT_TILED else self._checkpoint)(wp, ws, G, N, K)
+    return self._mx_gemm(_read(lhs, M * K, _lib.BF16).reshape(M, K), pk, sc, _ints(gs, G), zero_group, epi, beta,
+                         beta_lin, out)
+
+  def _lmoe_ragged_dot_mxfp4_rows(self, lhs, lhs_rows, row_index, wp, ws, gs, M, K, N, G, zero_group, mode, epi,
+                                  beta, beta_lin, out, stream):
+    tokens = _read(lhs, lhs_rows * K, _lib.BF16).reshape(lhs_rows, K)
+    a = tokens[np.clip(_ints(row_index, M), 0, max(lhs_rows - 1, 0))] if lhs_rows else np.zeros((M, K), np.float32)
+    pk, sc = self._untile(wp, ws, G, N, K)
+    return self._mx_gemm(a, pk, sc, _ints(gs, G), zero_group, epi, beta, beta_lin, out)
+
+  def _lmoe_ragged_dot_mxfp4_skinny(self, lhs, wt, st, gs, M, K, N, G, zero_group, flags, epi, beta, beta_lin,
+                                    max_group_rows, out, stream):
+    pk, sc = self._untile(wt, st, G, N, K)
+    return self._mx_gemm(_read(lhs, M * K, _lib.BF16).reshape(M, K), pk, sc, _ints(gs, G), zero_group, epi, beta,
+                         beta_lin, out)
+
+  def _lmoe_ragged_dot_mxfp4_splitk(self, lhs, wp, ws, gs, M, K, N, G, zero_group, k_split, work, work_bytes, epi,
+                                    beta, beta_lin, out, stream):
+    return self._lmoe_ragged_dot_mxfp4_skinny(lhs, wp, ws, gs, M, K, N, G, zero_group, 0, epi, beta, beta_lin, 0,
+                                              out, stream)
+
+  def _lmoe_dispatch_mxfp4_skinny(self, idx, w, w_dt, x, x_ld, T, k, start, L, m_padded, wt, st, K, N, epi, beta,
+                                  beta_lin, flags, gs, valid, counts, tok, pw, slot, out, stream):
+    self._dispatch(idx, w, w_dt, None, T, k, start, L, m_padded, None, _lib.BF16, gs, valid, counts, tok, pw, slot,
+                   False)
+    rows = _rows(x, T, x_ld, K, _lib.BF16)
+    t = _ints(tok, m_padded)
+    a = np.where((t >= 0)[:, None], rows[np.maximum(t, 0)] if T else 0, np.float32(0)).astype(np.float32)
+    pk, sc = self._untile(wt, st, L + 1, N, K)
+    return self._mx_gemm(a, pk, sc, _ints(gs, L + 1), L, epi, beta, beta_lin, out)
+
+  # ---- MXFP8 / MXFP6 activations: codes (M, K) / packed (M, K*3/4), E8M0 scales k-step-major
+  # (K/128, roundup(M, 4), 4): scale_t[s, m, j] = scale[m, 4 s + j], pad rows 0
+  @staticmethod
+  def _put_scales(ptr, scales, M, K):
+    m4 = -(-M // 4) * 4
+    st = np.zeros((K // 128, m4, 4), np.uint8)
+    st[:, :M, :] = np.asarray(scales, np.uint8).reshape(M, K // 128, 4).transpose(1, 0, 2)
+    _put_ints(ptr, st.reshape(-1), ctypes.c_uint8)
+
+  @staticmethod
+  def _get_scales(ptr, M, K):
+    m4 = -(-M // 4) * 4
+    st = _ints(ptr, (K // 128) * m4 * 4, ctypes.c_uint8).astype(np.uint8).reshape(K // 128, m4, 4)
+    return np.ascontiguousarray(st.transpose(1, 0, 2).reshape(m4, K // 32)[:M])
+
+  def _lmoe_quantize_mxfp8(self, x, x_dt, M, K, q, scale_t, stream):
+    codes, scales = O.quantize_mxfp8(_read(x, M * K, x_dt).reshape(M, K))
+    _put_ints(q, codes.reshape(-1), ctypes.c_uint8)
+    self._put_scales(scale_t, scales, M, K)
+    return _lib.OK
+
+  def _lmoe_quantize_mxfp6(self, x, x_dt, M, K, q, scale_t, stream):
+    codes, scales = O.quantize_mxfp6(_read(x, M * K, x_dt).reshape(M, K))
+    _put_ints(q, O.pack_fp6(codes).reshape(-1), ctypes.c_uint8)
+    self._put_scales(scale_t, scales, M, K)
+    return _lib.OK
+
+  def _lmoe_ragged_dot_mxfp8_mxfp4(self, q, qs, wp, ws, gs, M, K, N, G, zero_group, epi, beta, beta_lin, out,
+                                   out_dt, stream):
+    codes = _ints(q, M * K, ctypes.c_uint8).astype(np.uint8).reshape(M, K)
+    pk, sc = self._untile(wp, ws, G, N, K)
+    sizes = _ints(gs, G)
+    situ = epi == _lib.EPI_SITU
+    dt = _lib.BF16 if situ else out_dt
+    res = O.ragged_dot_mxfp8_mxfp4(codes, self._get_scales(qs, M, K), pk, sc, sizes, _dt(dt),
+                                   situ=(beta, beta_lin) if situ else None)
+    _write(out, self._zero_group_rows(res, sizes, zero_group), dt)
+    return _lib.OK
+
+  def _lmoe_ragged_dot_mxfp6_mxfp4(self, q, qs, wp, ws, gs, M, K, N, G, zero_group, out, out_dt, stream):
+    codes = O.unpack_fp6(_ints(q, M * K * 3 // 4, ctypes.c_uint8).astype(np.uint8).reshape(M, K * 3 // 4), K)
+    pk, sc = self._untile(wp, ws, G, N, K)
+    sizes = _ints(gs, G)
+    res = O.ragged_dot_mxfp6_mxfp4(codes, self._get_scales(qs, M, K), pk, sc, sizes, _dt(out_dt))
+    _write(out, self._zero_group_rows(res, sizes, zero_group), out_dt)
     return _lib.OK
 
   # ---- elementwise

@@ -115,3 +115,66 @@ def test_local_shard_layer_bf16_experts(monkeypatch, t):
                      False, out, st)
   assert "lmoe_ragged_dot_gateup_situ" in lib.names()
   assert torch.equal(layer.forward(d(hidden)), out)  # without the stages: the same output
+
+
+def _mxfp4_layer(tokens, mode="lds_dequant"):
+  """A small config-5-shaped layer with MXFP4 experts: each E8M0 scale byte
+  raised by 4 (every dequantised weight times 16, exactly) and the latent
+  projection times 8, so gate and up are of order one."""
+  from lmoe.forward import LocalShardLatentMoE
+  from lmoe.workloads import Config5, make_config5
+  c = Config5(tokens=tokens, hidden=128, latent=128, intermediate=128, experts=32, top_k=4, local_start=8,
+              local_experts=8)
+  hidden, w, experts = make_config5("cpu", c, "mxfp4")
+  for key in ("gu_scale", "down_scale"):
+    experts[key] = experts[key] + 4
+  w["down_proj"] = w["down_proj"] * 8
+  layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                              e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
+                              up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,
+                              local_num_experts=c.local_experts, expert_format="mxfp4", experts=experts,
+                              capacity_factor=c.capacity_factor, mxfp4_mode=mode)
+  return c, hidden, w, experts, layer
+
+
+def _dequantized_shard(c, experts):
+  inter = c.intermediate
+  gu = O.dequantize_mxfp4(to_np(experts["gu_packed"]), to_np(experts["gu_scale"]))
+  dn = O.dequantize_mxfp4(to_np(experts["down_packed"]), to_np(experts["down_scale"]))
+  return gu[:, :inter, :].transpose(0, 2, 1), gu[:, inter:, :].transpose(0, 2, 1), dn.transpose(0, 2, 1)
+
+
+# token counts: the decode step (fused dispatch + skinny expert GEMMs), the
+# prefill step (rows gathered by the gate/up kernel), past the decode bound
+@pytest.mark.parametrize("tokens,path", [(1, "lmoe_dispatch_mxfp4_skinny"), (16, "lmoe_dispatch_mxfp4_skinny"),
+                                         (64, "lmoe_dispatch_mxfp4_skinny"), (65, "lmoe_ragged_dot_mxfp4_rows"),
+                                         (200, "lmoe_ragged_dot_mxfp4_rows")])
+def test_local_shard_layer_mxfp4(monkeypatch, tokens, path):
+  """The benchmarked layer's composition at decode and prefill sizes against
+  the oracle's single-shard forward on the dequantised experts; the
+  stage-returning run (the sort dispatch, padding rows written) gives the
+  same output bit for bit."""
+  lib = _emulated_lib.install(monkeypatch)
+  c, hidden, w, experts, layer = _mxfp4_layer(tokens)
+  out = layer.forward(hidden)
+  assert path in lib.names()
+  lib.calls.clear()
+  out_st, st = layer.forward(hidden, return_stages=True)
+  assert path not in lib.names()  # the stages come from the sort dispatch
+  assert torch.equal(out, out_st)
+  gate, up, down = _dequantized_shard(c, experts)
+  wn = {k: to_np(v) for k, v in w.items()}
+  check_single_shard(f"emulated mxfp4 layer T={tokens}", to_np(hidden), wn, gate, up, down, c.config(), "bf16",
+                     c.local_start, c.local_experts, c.capacity_factor, False, out, st)
+
+
+def test_local_shard_layer_scaled_mfma(monkeypatch):
+  from _layer_check import check_single_shard_mx8
+  lib = _emulated_lib.install(monkeypatch)
+  c, hidden, w, experts, layer = _mxfp4_layer(96, mode="scaled_mfma")
+  out, st = layer.forward(hidden, return_stages=True)
+  assert {"lmoe_quantize_mxfp8", "lmoe_ragged_dot_mxfp8_mxfp4"} <= set(lib.names())
+  wn = {k: to_np(v) for k, v in w.items()}
+  ex = {k: to_np(experts[k]) for k in ("gu_packed", "gu_scale", "down_packed", "down_scale")}
+  check_single_shard_mx8("emulated scaled_mfma layer", to_np(hidden), wn, ex, c.config(), c.local_start,
+                         c.local_experts, c.capacity_factor, out, st)
