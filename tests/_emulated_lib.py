@@ -131,6 +131,16 @@ class EmulatedLib:
     _write(out, self._zero_group_rows(res, sizes, zero_group), _lib.BF16)
     return _lib.OK
 
+  def _lmoe_ragged_dot_fp8_scaled(self, lhs, rhs_q, rhs_scale, block_size, gs, M, K, N, G, zero_group, epi, beta,
+                                  beta_lin, out, stream):
+    a = _read(lhs, M * K, _lib.BF16).reshape(M, K)
+    q = _ints(rhs_q, G * K * N, ctypes.c_uint8).astype(np.uint8).reshape(G, K, N)
+    sc = _read(rhs_scale, G * (K // block_size) * N, _lib.F32).reshape(G, K // block_size, 1, N)
+    sizes = _ints(gs, G)
+    res = O.ragged_dot_fp8_scaled(a, q, sc, sizes, "bf16", situ=(beta, beta_lin) if epi == _lib.EPI_SITU else None)
+    _write(out, self._zero_group_rows(res, sizes, zero_group), _lib.BF16)
+    return _lib.OK
+
   # ---- dense projections: x (M, K) @ w_nk^T, f32 accumulation
   def _lmoe_dense_blaslt(self, x, x_dt, w, w_dt, M, K, N, out, out_dt, stream):
     a = _read(x, M * K, x_dt).reshape(M, K)
@@ -169,12 +179,19 @@ class EmulatedLib:
   # ---- dispatch (ref.py:754-877): the oracle's jittable dispatch
   def _dispatch(self, idx, w, w_dt, xrows, T, k, start, L, m_padded, sorted_tokens, sorted_dt, gs, valid, counts,
                 tok, pw, slot, skip_padding):
-    ids = _ints(idx, T * k).reshape(T, k)
-    wts = _read(w, T * k, w_dt).reshape(T, k)
-    x = xrows if xrows is not None else np.zeros((T, 1), np.float32)
-    d, slot_pos = O.filter_and_pad_to_shard_jittable(ids, wts, x, k, start + L, start, L, m_padded=m_padded,
-                                                     return_slot_pos=True)
-    sorted_x, sizes, ok, cnt, tk, wk = d
+    if T == 0:  # no slots: every row is padding
+      width = xrows.shape[1] if xrows is not None else 1
+      sorted_x, sizes = np.zeros((m_padded, width), np.float32), np.zeros(L + 1, np.int32)
+      sizes[L] = m_padded
+      ok, cnt = np.zeros(m_padded, bool), np.zeros(L, np.int32)
+      tk, wk, slot_pos = np.full(m_padded, -1, np.int32), np.zeros(m_padded, np.float32), np.zeros(0, np.int32)
+    else:
+      ids = _ints(idx, T * k).reshape(T, k)
+      wts = _read(w, T * k, w_dt).reshape(T, k)
+      x = xrows if xrows is not None else np.zeros((T, 1), np.float32)
+      d, slot_pos = O.filter_and_pad_to_shard_jittable(ids, wts, x, k, start + L, start, L, m_padded=m_padded,
+                                                       return_slot_pos=True)
+      sorted_x, sizes, ok, cnt, tk, wk = d
     if sorted_tokens and xrows is not None:
       rows = int(cnt.sum()) if skip_padding else m_padded
       _write(sorted_tokens, O.cast(sorted_x[:rows], _dt(sorted_dt)), sorted_dt)
@@ -198,7 +215,10 @@ class EmulatedLib:
 
   def _lmoe_dispatch_local_small(self, idx, w, w_dt, x, x_dt, x_ld, T, k, lat, start, L, m_padded, sorted_tokens,
                                  gs, valid, counts, tok, pw, slot, flags, stream):
-    xrows = None if flags & _lib.DISPATCH_FLAG_NO_ROWS or not x else _rows(x, T, x_ld, lat, x_dt)
+    if flags & _lib.DISPATCH_FLAG_NO_ROWS:
+      xrows = None
+    else:
+      xrows = _rows(x, T, x_ld, lat, x_dt) if T else np.zeros((0, lat), np.float32)
     return self._dispatch(idx, w, w_dt, xrows, T, k, start, L, m_padded, sorted_tokens, _lib.BF16, gs, valid,
                           counts, tok, pw, slot, bool(flags & _lib.DISPATCH_FLAG_SKIP_PADDING_ROWS))
 
