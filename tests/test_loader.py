@@ -227,3 +227,67 @@ def test_index_cannot_name_files_outside_the_checkpoint(tmp_path):
       json.dumps({"weight_map": {k: "../elsewhere/x.safetensors" for k in tensors}}))
   with pytest.raises(ValueError, match="not a file of the checkpoint directory"):
     loader.load_mxfp4_experts(str(ckpt), LAYER, [0], device="cpu")
+
+
+def test_hostile_headers_are_refused(tmp_path):
+  """A header nested past the JSON parser's recursion limit, and a header
+  longer than the format's 100 MB cap (a sparse file, so nothing that large
+  is written or read), raise ValueError like any other malformed header."""
+  import struct
+  deep = tmp_path / "deep.safetensors"
+  body = b"[" * 200000 + b"]" * 200000
+  deep.write_bytes(struct.pack("<Q", len(body)) + body)
+  with pytest.raises(ValueError, match="nests too deeply"):
+    loader.read_header(str(deep))
+  big = tmp_path / "big.safetensors"
+  n = loader.MAX_HEADER_BYTES + 1
+  with open(big, "wb") as f:
+    f.write(struct.pack("<Q", n))
+    f.seek(8 + n)
+    f.write(b"\0")
+  with pytest.raises(ValueError, match="exceeds the format's"):
+    loader.read_header(str(big))
+
+
+def test_arbitrary_headers_parse_or_raise_value_error(tmp_path):
+  """Random header entries (dtype, shape, offsets inside and outside the
+  data) over random data bytes: every file parses and every tensor reads, or
+  the loader raises ValueError / NotImplementedError (an unknown dtype) --
+  nothing else escapes."""
+  import json
+  import struct
+  from hypothesis import HealthCheck, given, settings
+  from hypothesis import strategies as st
+  path = tmp_path / "f.safetensors"
+  seen = {"ok": 0}
+  size = {"U8": 1, "F32": 4, "BF16": 2, "I32": 4}
+  shape = st.lists(st.integers(0, 6), max_size=3)
+
+  @settings(max_examples=300, deadline=None, derandomize=True, database=None,
+            suppress_health_check=[HealthCheck.function_scoped_fixture])
+  @given(st.lists(st.tuples(st.sampled_from(["U8", "F32", "BF16", "I32", "U8", "F32", "F8_E4M3", 7]),
+                            st.one_of(shape, shape, shape, st.integers(0, 3)),
+                            st.integers(-2, 40), st.integers(-2, 40), st.sampled_from([True, True, True, False])),
+                  max_size=4),
+         st.binary(min_size=64, max_size=96), st.sampled_from([0, 0, 0, -1, 1, -3]))
+  def run(entries, payload, skew):
+    h = {}
+    for i, (dt, sh, lo, hi, fits) in enumerate(entries):
+      if fits and isinstance(sh, list) and dt in size and lo >= 0:  # offsets that match the shape
+        hi = lo + int(np.prod(sh)) * size[dt]
+      h[f"t{i}"] = {"dtype": dt, "shape": sh, "data_offsets": [lo, hi]}
+    body = json.dumps(h).encode()
+    path.write_bytes(struct.pack("<Q", max(len(body) + skew, 0)) + body + payload)
+    try:
+      f = loader._File(str(path))
+    except ValueError:
+      return
+    for name in f.header:
+      try:
+        f.tensor(name)
+        seen["ok"] += 1
+      except (ValueError, NotImplementedError):
+        pass
+
+  run()
+  assert seen["ok"] > 20

@@ -39,6 +39,8 @@ DEFAULT_PREFIX = "language_model.model."
 _ROLES = {"gate": "w1", "up": "w3", "down": "w2"}
 _DTYPES = {"U8": np.uint8, "I8": np.int8, "BF16": np.uint16, "F16": np.float16, "F32": np.float32,
            "I32": np.int32, "I64": np.int64}
+# the safetensors format's limit on the JSON header
+MAX_HEADER_BYTES = 100_000_000
 
 
 def read_header(path: str) -> tuple[dict, int]:
@@ -54,7 +56,12 @@ def read_header(path: str) -> tuple[dict, int]:
     size = os.fstat(f.fileno()).st_size
     if n > size - 8:
       raise ValueError(f"{path}: header length {n} exceeds the file size {size}")
-    header = json.loads(f.read(n))
+    if n > MAX_HEADER_BYTES:
+      raise ValueError(f"{path}: header length {n} exceeds the format's {MAX_HEADER_BYTES} bytes")
+    try:
+      header = json.loads(f.read(n))
+    except RecursionError:
+      raise ValueError(f"{path}: the header nests too deeply") from None
   if not isinstance(header, dict):
     raise ValueError(f"{path}: the header is not a JSON object")
   header.pop("__metadata__", None)
