@@ -66,10 +66,9 @@ __device__ __forceinline__ int swzk(int row) { return 4 * (row % 4); }
 // by exactly one wave.  MF is the MFMA tile edge: 32 (v_mfma_f32_32x32x16_bf16,
 // the one a single wave issues at the full matrix rate) or 16
 // (v_mfma_f32_16x16x32_bf16, which one wave issues at half rate).
-template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32, bool PIPE = false>
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32>
 struct DCfg {
   static constexpr int kWM = WM, kWN = WN, kMF = MF;
-  static constexpr bool kPipe = PIPE;  // operand fragments read one step ahead
   static constexpr int kWaves = WM * WN, kThreads = 64 * WM * WN;
   static constexpr int kWTM = BM / kWM, kWTN = BN / kWN;
   static constexpr int kTM = kWTM / MF, kTN = kWTN / MF;
@@ -101,9 +100,8 @@ struct DCfg {
   // capped so that the same number of waves fits on each SIMD
   static constexpr int kLdsBlocks = 163840 / (NS * kSlot + 64);
   static constexpr int kWavesPerEuRaw = kLdsBlocks * kWaves / 4;
-  // at most 3 waves per SIMD (at most 2 with the software pipeline, whose two
-  // fragment sets plus the accumulators need up to 256 VGPRs)
-  static constexpr int kWavesCap = PIPE ? 2 : 3;
+  // at most 3 waves per SIMD
+  static constexpr int kWavesCap = 3;
   static constexpr int kWavesPerEu =
       kWavesPerEuRaw < 1 ? 1 : (kWavesPerEuRaw > kWavesCap ? kWavesCap : kWavesPerEuRaw);
 };
@@ -161,11 +159,11 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* base, int byte) {
   return __builtin_bit_cast(uint2, v);
 }
 
-template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM, int WN, int MF, bool PIPE>
-__global__ __launch_bounds__((DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>::kThreads))
-__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>::kWavesPerEu)))
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM, int WN, int MF>
+__global__ __launch_bounds__((DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF>::kThreads))
+__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF>::kWavesPerEu)))
 void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtual) {
-  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>;
+  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF>;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   __shared__ TileInfo s_tile;
   __shared__ int64_t s_nt;
@@ -306,20 +304,10 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
       }
     };
 
-    // Software pipeline over K steps (PIPE; otherwise each step lands, refills
-    // the slot of the previous step and reads + computes its own fragments).
-    // The ring has NS slots; the prologue fills all of them (steps
-    // 0 .. NS-1).  Step k's operand fragments are read from LDS into
-    // registers one step early, so iteration k
-    //   waits for step k+1's DMA (s_waitcnt vmcnt) and s_barrier: step k+1
-    //     has landed for every wave, and every wave has its step-k
-    //     fragments in registers (lgkmcnt(0) before the barrier), so slot
-    //     k % NS is free;
-    //   issues the DMA of step k+NS into slot k % NS;
-    //   issues the LDS reads of step k+1's fragments;
-    //   runs step k's conversions and MFMAs from registers, overlapping the
-    //     LDS latency of those reads and NS-1 steps of DMA.
-    static_for<PIPE ? NS : NS - 1>([&](auto sc) __attribute__((always_inline)) {
+    // The ring has NS slots; the prologue fills NS-1 of them (steps
+    // 0 .. NS-2).  Each K step lands, refills the slot of the previous step
+    // (step k+NS-1) and reads + computes its own fragments.
+    static_for<NS - 1>([&](auto sc) __attribute__((always_inline)) {
       constexpr int s = decltype(sc)::value;
       issue(s, s);
       return true;
@@ -473,11 +461,9 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
     // Wait for step k's DMA with `ahead` younger steps still allowed in
     // flight, then barrier.
     auto land = [&](int64_t k) __attribute__((always_inline)) {
-      // youngest step whose DMA has been issued.  Pipelined: the prologue
-      // issues steps 0 .. NS-1, and before land(k), k >= 1, the last issue
-      // was step k+NS-2.  Otherwise: the prologue issues 0 .. NS-2 and step
-      // j issues j+NS-1 after its land.
-      const int64_t youngest = (PIPE && k == 0) ? NS - 1 : k + NS - 2;
+      // youngest step whose DMA has been issued: the prologue issues 0 ..
+      // NS-2 and step j issues j+NS-1 after its land
+      const int64_t youngest = k + NS - 2;
       const int64_t last = nk - 1 < youngest ? nk - 1 : youngest;
       const int ahead = static_cast<int>(last - k);
       if (wave == 0)
@@ -490,33 +476,15 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
     // rows and once for the last, partial tile of a group (one wave-uniform
     // test per tile instead of one per MFMA).
     auto k_loop = [&](auto full_tag) __attribute__((always_inline)) {
-      if constexpr (PIPE) {
-        auto step = [&](int64_t k, const Frags& cur, Frags& nxt) __attribute__((always_inline)) {
-          if (k + 1 < nk) {
-            land(k + 1);
-            issue(k + NS, static_cast<int>(k % NS));
-            read_frags(static_cast<int>((k + 1) % NS), nxt);
-          }
-          compute(cur, full_tag);
-        };
-        Frags fa, fb;
-        land(0);
-        read_frags(0, fa);
-        for (int64_t kt = 0; kt < nk; kt += 2) {
-          step(kt, fa, fb);
-          if (kt + 1 < nk) step(kt + 1, fb, fa);
-        }
-      } else {
-        // land step k, refill the slot of step k-1, read and compute step k
-        int cur = 0;  // slot of step k
-        for (int64_t kt = 0; kt < nk; ++kt) {
-          land(kt);
-          issue(kt + NS - 1, cur == 0 ? NS - 1 : cur - 1);
-          Frags f;
-          read_frags(cur, f);
-          compute(f, full_tag);
-          cur = cur == NS - 1 ? 0 : cur + 1;
-        }
+      // land step k, refill the slot of step k-1, read and compute step k
+      int cur = 0;  // slot of step k
+      for (int64_t kt = 0; kt < nk; ++kt) {
+        land(kt);
+        issue(kt + NS - 1, cur == 0 ? NS - 1 : cur - 1);
+        Frags f;
+        read_frags(cur, f);
+        compute(f, full_tag);
+        cur = cur == NS - 1 ? 0 : cur + 1;
       }
     };
     if (tm_eff >= C::kTM)
@@ -650,7 +618,7 @@ void grouped_gemm_dma_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtua
 // ---------------------------------------------------------------------------
 template <int BM, int BN, int EPI, int NS, int MF>
 struct SCfg {
-  using C = DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF, false>;
+  using C = DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF>;
   static constexpr int kOutCols = EPI == kEpiSitu ? BN / 2 : BN;  // bf16 output columns of a tile
   static constexpr int kChunks = kOutCols / 8;                     // 16-byte chunks per output row
   // staged rows: 8 bytes of padding put row r's dword 0 in bank 2r (mod 64),
@@ -690,8 +658,8 @@ __device__ __forceinline__ void wait_stream(int a, int r) {
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" : : : "memory"); }
 
 template <int BM, int BN, int EPI, int NS, int MF>
-__global__ __launch_bounds__((DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF, false>::kThreads))
-__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF, false>::kWavesPerEu)))
+__global__ __launch_bounds__((DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF>::kThreads))
+__attribute__((amdgpu_waves_per_eu(DCfg<BM, BN, kDMX, EPI, NS, 1, 4, MF>::kWavesPerEu)))
 void grouped_gemm_stream_kernel(Params p, int64_t n_tiles, int gm, int64_t n_virtual) {
   using S = SCfg<BM, BN, EPI, NS, MF>;
   using C = typename S::C;
@@ -1180,13 +1148,13 @@ int cu_count() {
   return v;
 }
 
-template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32, bool PIPE = false>
+template <int BM, int BN, int LAYOUT, int EPI, int NS, int WM = 1, int WN = 4, int MF = 32>
 int launch_dma(const Params& p, hipStream_t st, const char* name) {
   if constexpr (EPI == kEpiSitu && (BN / WN / MF) % 2 != 0) {
     return fail(LMOE_ERR_UNSUPPORTED, "%s: SiTU tile %dx%d with %dx%d MFMAs has no gate/up pairing", name, BM, BN, MF,
                 MF);
   } else {
-  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>;
+  using C = DCfg<BM, BN, LAYOUT, EPI, NS, WM, WN, MF>;
   const int64_t out_cols = EPI == kEpiSitu ? p.N / 2 : p.N;
   const int64_t cols_per_tile = EPI == kEpiSitu ? BN / 2 : BN;
   const int64_t ntiles = ceil_div(out_cols, cols_per_tile);
@@ -1215,14 +1183,14 @@ int launch_dma(const Params& p, hipStream_t st, const char* name) {
                        name);
   const size_t lds = static_cast<size_t>(NS) * C::kSlot;
   static const hipError_t attr_rc =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN, MF>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(lds));
   if (attr_rc != hipSuccess)
     return fail(LMOE_ERR_HIP, "%s: LDS size attribute (%zu bytes): %s", name, lds, hipGetErrorString(attr_rc));
   // one block per tile (measured equal to or faster than a persistent grid on
   // the expert shapes: the hardware's block refill overlaps one block's
   // epilogue with its neighbours' main loops)
-  grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN, MF, PIPE>
+  grouped_gemm_dma_kernel<BM, BN, LAYOUT, EPI, NS, WM, WN, MF>
       <<<dim3(static_cast<unsigned>(blocks)), C::kThreads, lds, st>>>(p, ntiles, gm, blocks);
   LMOE_CHECK_LAUNCH(name);
   return LMOE_OK;
