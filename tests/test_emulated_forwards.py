@@ -178,3 +178,60 @@ def test_local_shard_layer_scaled_mfma(monkeypatch):
   ex = {k: to_np(experts[k]) for k in ("gu_packed", "gu_scale", "down_packed", "down_scale")}
   check_single_shard_mx8("emulated scaled_mfma layer", to_np(hidden), wn, ex, c.config(), c.local_start,
                          c.local_experts, c.capacity_factor, out, st)
+
+
+def test_mxfp4_layer_values_across_configurations(monkeypatch):
+  """The MXFP4 layer over random configurations (expert count, shard size
+  and position, top-k, token count, latent / intermediate / hidden sizes,
+  capacity factors that truncate, lds_dequant or scaled mode): every forward
+  equals its stage-returning run and passes the same oracle checks as above."""
+  import contextlib
+  import io
+  from hypothesis import HealthCheck, given, settings
+  from hypothesis import strategies as st
+  from _layer_check import check_single_shard_mx8
+  from lmoe.forward import LocalShardLatentMoE
+  from lmoe.workloads import Config5, make_config5
+  _emulated_lib.install(monkeypatch)
+  stats = {"ran": 0}
+
+  @settings(max_examples=30, deadline=None, derandomize=True, database=None,
+            suppress_health_check=[HealthCheck.too_slow, HealthCheck.function_scoped_fixture])
+  @given(st.data())
+  def run(data):
+    pick = lambda xs: data.draw(st.sampled_from(xs))
+    e = pick([8, 16, 60, 128])
+    L = pick([n for n in (1, 4, 15, 16) if n <= e])
+    c = Config5(tokens=pick([1, 2, 5, 16, 63, 64, 65, 130]), hidden=pick([64, 128]), latent=pick([64, 128, 256]),
+                intermediate=pick([64, 128]), experts=e, top_k=pick([k for k in (1, 2, 4, 8) if k <= e]),
+                local_start=pick(sorted({0, e - L})), local_experts=L, capacity_factor=pick([0.25, 1.0, 2.0]))
+    mode = pick(["lds_dequant", "lds_dequant", "scaled_mfma"])
+    hidden, w, ex = make_config5("cpu", c, "mxfp4")
+    for key in ("gu_scale", "down_scale"):
+      ex[key] = ex[key] + 4
+    w["down_proj"] = w["down_proj"] * 8
+    try:
+      layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                                  e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
+                                  up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,
+                                  local_num_experts=L, expert_format="mxfp4", experts=ex,
+                                  capacity_factor=c.capacity_factor, mxfp4_mode=mode)
+    except NotImplementedError:  # the scaled mode's sizes
+      return
+    out = layer.forward(hidden)
+    out_st, st_ = layer.forward(hidden, return_stages=True)
+    assert torch.equal(out, out_st), (c, mode)
+    wn = {k: to_np(v) for k, v in w.items()}
+    with contextlib.redirect_stdout(io.StringIO()):
+      if mode == "scaled_mfma":
+        exn = {k: to_np(ex[k]) for k in ("gu_packed", "gu_scale", "down_packed", "down_scale")}
+        check_single_shard_mx8("sweep", to_np(hidden), wn, exn, c.config(), c.local_start, L, c.capacity_factor,
+                               out_st, st_)
+      else:
+        gate, up, down = _dequantized_shard(c, ex)
+        check_single_shard("sweep", to_np(hidden), wn, gate, up, down, c.config(), "bf16", c.local_start, L,
+                           c.capacity_factor, False, out_st, st_)
+    stats["ran"] += 1
+
+  run()
+  assert stats["ran"] >= 20, stats
