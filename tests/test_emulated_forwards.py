@@ -235,3 +235,24 @@ def test_mxfp4_layer_values_across_configurations(monkeypatch):
 
   run()
   assert stats["ran"] >= 20, stats
+
+
+@pytest.mark.parametrize("act,renorm,scaling,dt", [("softmax", True, 1.0, "bf16"), ("softmax", False, 2.5, "f32"),
+                                                   ("sigmoid", False, 2.5, "bf16")])
+def test_unsharded_forward_gate_options(monkeypatch, act, renorm, scaling, dt):
+  """The unsharded forward's gate options the golden bundles do not hold
+  (softmax, no renormalisation, a routed scaling factor): against the oracle
+  on its own logits, routing bit for bit."""
+  from lmoe.config import init_weights
+  from lmoe.forward import latent_moe_forward
+  _emulated_lib.install(monkeypatch)
+  cfg = LatentMoEConfig(hidden_size=64, latent_size=32, intermediate_size=48, num_experts=16, top_k=4,
+                        num_shared_experts=1, moe_renormalize=renorm, routed_scaling_factor=scaling)
+  tdt = torch.float32 if dt == "f32" else torch.bfloat16
+  import dataclasses
+  W = init_weights(cfg, key=3, dtype=tdt, device="cpu")
+  W = dataclasses.replace(W, router_weight=W.router_weight * 8)  # logits of order one: the gate's shape matters
+  hidden = O.cast(np.random.default_rng(3).standard_normal((24, 64)), dt)
+  final, inter = latent_moe_forward(_dev(hidden, dt), W, cfg, act=act, return_intermediates=True)
+  wn = {k: to_np(v) for k, v in W.as_dict().items()}
+  check_unsharded(f"emulated unsharded {act}", hidden, wn, cfg, dt, act, final, inter)
