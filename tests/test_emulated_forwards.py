@@ -67,9 +67,10 @@ def test_unsharded_forward_on_golden_bundles(monkeypatch, bundle):
 def _shard_problem(rng, cfg, t, start, L):
   """The GPU suite's shard problem with the latent projection and the expert
   weights scaled by powers of two (bf16 values stay exact) so that gate and
-  up are of order one: at its N(0, 0.02^2) weights they are near 0.02, where
-  SiTU-GLU is close to the symmetric g * u / 2 and a gate / up swap moves
-  the output by less than the bf16 bound."""
+  up are of order one: at the small sizes used here (hidden 64, latent 32)
+  and N(0, 0.02^2) weights they are near 0.02, where SiTU-GLU is close to
+  the symmetric g * u / 2 and a gate / up swap moves the output by less than
+  the bf16 bound."""
   import test_gpu_forward as G
   hidden, w, gate, up, down = G._shard_problem(rng, cfg, t, start, L)
   w = dict(w, down_proj=w["down_proj"] * 8)
