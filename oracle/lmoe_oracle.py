@@ -933,19 +933,59 @@ def ragged_dot_fp8_scaled(lhs, rhs_q, rhs_scale, group_sizes, dtype: str = "bf16
 
 
 PINNING = {
-    "bf16_round": "closed form: exhaustive bf16 neighbours, torch.bfloat16 cast (tests/test_oracle_basics.py)",
-    "router_from_logits / router_gate": "golden bundles router_* / topk_* (6 stages), softmax closed form",
-    "filter_and_pad_to_shard(_jittable)": "literal KATs from test_sharded_routing_local.py, brute force, eager==jittable",
-    "unsharded_dispatch": "golden group_sizes + canonical sorted_token_indices",
-    "ragged_dot / situ / ffn": "golden expert_* / situ_output stages, brute-force per-row dot",
-    "combine_shard_contribution": "golden routed_output_after_combine via sharded==unsharded, literal padding KAT",
-    "rms_norm / forward": "golden normalized/up_projection/shared/final stages",
-    "dequantize_mxfp4": "closed form OCP MX E2M1/E8M0 table, exhaustive 256 bytes x edge scales",
-    "fp8_e4m3_to_f32 / f32_to_fp8_e4m3": "all 256 codes and a dense sweep incl. ties and subnormals vs torch.float8_e4m3fn",
-    "quantize_mxfp8": "OCP MX closed form (exponent choice, saturation, zero block), grid values round-trip exactly",
-    "ragged_dot_mxfp8_mxfp4": "brute-force triple loop on small inputs; equals the bf16 oracle when the activations are on the E4M3 grid",
-    "gate_exp64 / gate_sigmoid / gate_softmax": "libm exp within 1 ulp (planted ln2/Taylor mistakes fail), sigmoid correctly rounded vs extended precision, softmax within 1 ulp",
-    "dequantize_fp8_blockscaled / ragged_dot_fp8_scaled": "torch float8_e4m3fn -> f32 * scale -> bf16 casts, all 256 codes x block sizes K and 32",
-    "fp6_e2m3_to_f32 / f32_to_fp6_e2m3 / quantize_mxfp6 / pack_fp6": "the OCP E2M3 value table (monotone codes, spacing 1/8, 1/4, 1/2), brute-force nearest-even search over a dense sweep with every midpoint, the MX exponent closed form (amax / 2^X in [4, 8)), grid values round-trip, a planted emax mistake fails, one-hot bit placement of the packing",
-    "ragged_dot_mxfp6_mxfp4": "brute-force triple loop on small inputs",
+    # Keys name every public function of this module ("a / b" when one check
+    # pins several); ``tests/test_oracle_basics.py`` asserts the coverage.
+    "bf16_round / bf16_bits / bits_to_f32 / cast":
+        "torch's bfloat16 cast over random, denormal and edge floats, ties to even; all 65536 bf16 bit "
+        "patterns decoded against torch's bfloat16 view and round-tripped (test_oracle_basics.py)",
+    "promote": "torch.promote_types over every bf16/f32 pair, which JAX's promotion lattice agrees with "
+               "for these two types (test_oracle_basics.py)",
+    "matmul": "a float64 product: the f32 result within f32 accumulation error, the bf16 result its "
+              "single rounding, within half a bf16 ulp plus that error (test_oracle_basics.py)",
+    "sigmoid / softmax / situ_and_mul / rms_norm": "float64 closed forms (test_oracle_basics.py)",
+    "gate_exp64 / gate_sigmoid / gate_softmax":
+        "libm exp within 1 ulp (planted ln2/Taylor mistakes fail), sigmoid correctly rounded vs extended "
+        "precision, softmax within 1 ulp (test_oracle_basics.py)",
+    "top_k": "brute-force sort by (-value, index) with ties (test_oracle_basics.py)",
+    "router_from_logits / router_gate": "golden bundles router_* / topk_* (6 stages); renormalisation "
+                                        "order KAT (test_oracle_golden.py, test_oracle_basics.py)",
+    "round_up_to_tile / compute_m_padded":
+        "literal values; the reference's m_padded table (expert_ffn_roofline.py:42-47) at its token sweep "
+        "(rd.py:1843) (test_oracle_composites.py, test_oracle_dispatch.py)",
+    "filter_and_pad_to_shard / filter_and_pad_to_shard_jittable":
+        "literal KATs from test_sharded_routing_local.py, brute force, eager == jittable "
+        "(test_oracle_dispatch.py)",
+    "unsharded_dispatch / unsharded_combine / latent_moe_forward / situ_glu_mlp":
+        "golden group_sizes, canonical sorted_token_indices and every stage of the six bundles "
+        "(test_oracle_golden.py)",
+    "ragged_dot / local_shard_expert_ffn": "golden expert_* / situ_output stages, brute-force per-row "
+                                           "dot (test_oracle_basics.py, test_oracle_dispatch.py)",
+    "combine_shard_contribution": "sharded sum == unsharded forward over 4 configs, literal padding KAT, "
+                                  "rounding-order KAT (test_oracle_dispatch.py)",
+    "single_shard_forward": "one shard holding every expert equals latent_moe_forward stage by stage; "
+                            "the routed outputs of all shards sum to the unsharded one "
+                            "(test_oracle_dispatch.py)",
+    "prefuse_gateup_weights / ragged_dot_gateup_situ / mxfp4_matmul / ragged_dot_mxfp4":
+        "explicit [gate | up] layout; float64 per-row brute force with the OCP E2M1 table, gate/up swap "
+        "and nibble-order mistakes fail (test_oracle_composites.py)",
+    "e8m0_to_f32 / fp4_e2m1_to_f32 / dequantize_mxfp4":
+        "OCP MX v1.0 bit formulas over all 256 scale bytes and all 16 codes; exhaustive 256 bytes x edge "
+        "scales; literal KAT (test_oracle_basics.py)",
+    "fp8_e4m3_to_f32 / f32_to_fp8_e4m3":
+        "all 256 codes and a dense sweep incl. ties and subnormals vs torch.float8_e4m3fn "
+        "(test_oracle_mxfp8.py)",
+    "quantize_mxfp8 / dequantize_mxfp8":
+        "OCP MX closed form (exponent choice, saturation, zero block), grid values round-trip exactly, "
+        "planted exponent mistake fails (test_oracle_mxfp8.py)",
+    "ragged_dot_mxfp8_mxfp4": "brute-force triple loop on small inputs; equals the bf16 oracle when the "
+                              "activations are on the E4M3 grid (test_oracle_mxfp8.py)",
+    "dequantize_fp8_blockscaled / ragged_dot_fp8_scaled":
+        "torch float8_e4m3fn -> f32 * scale -> bf16 casts, all 256 codes x block sizes K and 32 "
+        "(test_oracle_mxfp8.py)",
+    "fp6_e2m3_to_f32 / f32_to_fp6_e2m3 / quantize_mxfp6 / dequantize_mxfp6 / pack_fp6 / unpack_fp6":
+        "the OCP E2M3 value table (monotone codes, spacing 1/8, 1/4, 1/2), brute-force nearest-even search "
+        "over a dense sweep with every midpoint, the MX exponent closed form (amax / 2^X in [4, 8)), grid "
+        "values round-trip, a planted emax mistake fails, one-hot bit placement of the packing "
+        "(test_oracle_mxfp6.py)",
+    "ragged_dot_mxfp6_mxfp4": "brute-force triple loop on small inputs (test_oracle_mxfp6.py)",
 }

@@ -249,3 +249,64 @@ def test_planted_mistake_is_caught(monkeypatch, mutation):
       return out._replace(topk_weight=w.astype(np.float32))
     monkeypatch.setattr(O, "router_from_logits", with_bias)
   assert _golden_failures() != []
+
+
+def test_bits_to_f32_every_bf16_pattern():
+  """All 65536 bf16 bit patterns: decoded as torch's bfloat16 view decodes
+  them, and (NaNs aside) encoded back to the same bits by ``bf16_bits``;
+  ``cast`` is ``bf16_round`` for bf16 and the identity on float32."""
+  u = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+  got = O.bits_to_f32(u)
+  theirs = torch.from_numpy(u.view(np.int16)).view(torch.bfloat16).float().numpy()
+  assert np.array_equal(got.view(np.uint32), theirs.view(np.uint32))
+  finite = ~np.isnan(got)
+  assert np.array_equal(O.bf16_bits(got[finite]), u[finite])
+  assert np.isnan(O.bits_to_f32(O.bf16_bits(got[~finite]))).all()
+  x = np.random.default_rng(7).standard_normal(1000).astype(np.float32)
+  assert np.array_equal(O.cast(x, "bf16"), torch.from_numpy(x).bfloat16().float().numpy())
+  assert np.array_equal(O.cast(x, "f32"), x)
+
+
+def test_promote_matches_torch():
+  t = {"bf16": torch.bfloat16, "f32": torch.float32}
+  for a in t:
+    for b in t:
+      assert t[O.promote(a, b)] == torch.promote_types(t[a], t[b]), (a, b)
+
+
+def test_matmul_rounds_once_from_f32_accumulation():
+  rng = np.random.default_rng(8)
+  a = O.bf16_round(rng.standard_normal((33, 200)))
+  b = O.bf16_round(rng.standard_normal((200, 17)))
+  exact = a.astype(np.float64) @ b.astype(np.float64)
+  acc_err = 200 * 2.0 ** -24 * (np.abs(a).astype(np.float64) @ np.abs(b))  # f32 accumulation bound
+  f32 = O.matmul(a, b, "f32")
+  assert f32.dtype == np.float32 and np.all(np.abs(f32 - exact) <= acc_err)
+  bf = O.matmul(a, b, "bf16")
+  half_ulp = 2.0 ** (np.floor(np.log2(np.abs(exact))) - 8)
+  assert np.array_equal(bf, O.bf16_round(bf)) and np.all(np.abs(bf - exact) <= half_ulp + 2 * acc_err)
+
+
+def test_e8m0_and_e2m1_decoders_every_code():
+  """OCP MX v1.0: an E8M0 byte s is 2^(s-127) (byte 0 the float32 denormal
+  2^-127; 255 overflows float32 to inf as the reference's 2^(s-127) does),
+  an E2M1 nibble is given by ``_e2m1_spec``."""
+  s = np.arange(256)
+  got = O.e8m0_to_f32(s.astype(np.uint8))
+  with np.errstate(over="ignore"):
+    want = np.array([np.float32(math.ldexp(1.0, int(v) - 127)) for v in s[:255]] + [np.float32(np.inf)])
+  assert got.dtype == np.float32 and np.array_equal(got, want)
+  codes = np.arange(16, dtype=np.uint8)
+  got = O.fp4_e2m1_to_f32(codes)
+  want = np.array([_e2m1_spec(int(c)) for c in codes], np.float32)
+  assert np.array_equal(got, want) and np.array_equal(np.signbit(got), codes >= 8)
+
+
+def test_every_public_oracle_function_is_pinned():
+  """``PINNING`` names every public function of the oracle, and nothing else."""
+  import inspect
+  public = {n for n, f in vars(O).items()
+            if inspect.isfunction(f) and f.__module__ == O.__name__ and not n.startswith("_")}
+  named = [n.strip() for key in O.PINNING for n in key.split(" / ")]
+  assert len(named) == len(set(named))
+  assert set(named) == public, (sorted(public - set(named)), sorted(set(named) - public))

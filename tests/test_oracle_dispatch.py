@@ -290,3 +290,38 @@ def test_combine_scatter_add_rounds_each_add_in_order():
                                      np.ones(2, np.float32), "bf16", "bf16", "bf16")
   assert out[0, 0] == np.float32(1 + 2.0 ** -6)
   assert O.bf16_round(np.float32(1 + 10 * 2.0 ** -10)) == np.float32(1 + 2.0 ** -7)
+
+
+@pytest.mark.parametrize("t,k,want", [(128, 16, 384), (2048, 16, 4736), (4096, 16, 9472)])
+def test_compute_m_padded_reference_table(t, k, want):
+  """The reference's Stage C table (expert_ffn_roofline.py:42-47, a 64-expert
+  shard of 896, top-16, capacity factor 2) at its prefill token sweep
+  (rd.py:1843: 128, 2048, 4096 tokens)."""
+  assert O.compute_m_padded(t, k, 896, 64, 2.0) == want
+
+
+@pytest.mark.parametrize("seed,num_tokens,global_e,local_e,top_k", [(0, 32, 16, 4, 2), (3, 200, 64, 8, 16)])
+def test_single_shard_forward_against_unsharded(seed, num_tokens, global_e, local_e, top_k):
+  """One shard holding every expert reproduces ``latent_moe_forward`` stage by
+  stage (f32; only the combine's summation order differs), and the routed
+  outputs of all shards of a split sum to the unsharded routed output."""
+  cfg = _toy_shard_config(top_k=top_k, num_experts=global_e)
+  rng = np.random.default_rng(seed)
+  w = _init_weights(cfg, rng)
+  hidden = rng.standard_normal((num_tokens, cfg.hidden_size)).astype(np.float32)
+  want, inter = O.latent_moe_forward(hidden, w, cfg, "f32")
+  pad = lambda a, s, n: np.concatenate([a[s:s + n], np.zeros_like(a[:1])])
+  shard = lambda s, n: [pad(w[k], s, n) for k in ("expert_gate", "expert_up", "expert_down")]
+  got, st = O.single_shard_forward(hidden, w, *shard(0, global_e), cfg, "f32", 0, global_e,
+                                   capacity_factor=float(global_e))
+  assert np.array_equal(st["x"], inter["latent_projection"])
+  assert np.array_equal(st["router_logits"], inter["router_logits"])
+  assert np.array_equal(st["topk_idx"], inter["topk_indices"])
+  assert np.array_equal(st["topk_weight"], inter["topk_weights"])
+  assert int(st["dispatch"].valid_mask.sum()) == num_tokens * top_k
+  assert np.max(np.abs(st["routed_out"] - inter["routed_output_after_combine"])) < 1e-5
+  assert np.max(np.abs(got - want)) < 1e-4
+  routed = sum(O.single_shard_forward(hidden, w, *shard(s, local_e), cfg, "f32", s, local_e,
+                                      capacity_factor=float(global_e // local_e), include_shared=False)[1]["routed_out"]
+               for s in range(0, global_e, local_e))
+  assert np.max(np.abs(routed - inter["routed_output_after_combine"])) < 1e-5
