@@ -25,6 +25,13 @@ def to_np(t):
   return t.cpu().numpy()
 
 
+def agreement(out, ref):
+  """Fraction of the elements of ``out`` bit-equal to ``ref`` (NaN never is)."""
+  out, ref = np.asarray(out), np.asarray(ref)
+  assert out.shape == ref.shape, (out.shape, ref.shape)
+  return float(np.mean(out == ref)) if ref.size else 1.0
+
+
 def max_rel(out, ref):
   """max|out - ref| / max|ref| (benchmark_harness.py:192-199)."""
   out = np.asarray(out, np.float64)

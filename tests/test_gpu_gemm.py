@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import banner, max_rel, to_dev, to_np
+from _util import agreement, banner, max_rel, to_dev, to_np
 from oracle import lmoe_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -131,8 +131,15 @@ def test_ragged_dot_f32_out_and_zero_group(gpu_device, layout):
   assert max_rel(z[:40], O.bf16_round(ref[:40])) <= BF16_TOL
 
 
+@pytest.mark.parametrize("round_first", [True, False])
 @pytest.mark.parametrize("layout", ["gkn", "gnk"])
-def test_gateup_situ_matches_oracle(gpu_device, layout):
+def test_gateup_situ_matches_oracle(gpu_device, layout, round_first):
+  """The fused gate/up + SiTU against the oracle at the bf16 bar, and its
+  rounding of the gate/up accumulators before the activation (gk.py:114-125)
+  as asked: nearly every element equals the matching oracle bit for bit,
+  while about a third differ from the other choice -- a difference of one
+  bf16 ulp on the activation's inputs, below the bf16 bar.  (A float32 model
+  of the device epilogue puts the agreements at 0.999 and 0.67 here.)"""
   from lmoe import ops
   rng = np.random.default_rng(4)
   m, k, inter, g = 700, 256, 192, 9
@@ -142,11 +149,15 @@ def test_gateup_situ_matches_oracle(gpu_device, layout):
   wg = O.bf16_round(rng.standard_normal((g, k, inter)) * 0.05)
   wu = O.bf16_round(rng.standard_normal((g, k, inter)) * 0.05)
   fused = O.prefuse_gateup_weights(wg, wu)
-  ref = O.ragged_dot_gateup_situ(lhs, fused, gs, 4.0, 25.0, "bf16")
+  ref = O.ragged_dot_gateup_situ(lhs, fused, gs, 4.0, 25.0, "bf16", round_before_act=round_first)
+  other = O.ragged_dot_gateup_situ(lhs, fused, gs, 4.0, 25.0, "bf16", round_before_act=not round_first)
   rhs = fused if layout == "gkn" else np.ascontiguousarray(fused.transpose(0, 2, 1))
   out = to_np(ops.ragged_dot_gateup_situ(to_dev(lhs, "bf16"), to_dev(rhs, "bf16"), to_dev(gs), 4.0, 25.0,
-                                         rhs_layout=layout))
+                                         rhs_layout=layout, round_before_act=round_first))
   assert max_rel(out, ref) <= BF16_TOL
+  assert agreement(out, ref) >= 0.95 and agreement(out, other) <= 0.9, (agreement(out, ref), agreement(out, other))
+  if not round_first:
+    return
   # the unfused oracle (separate rounded gate/up) is the same function
   unfused = O.situ_and_mul(O.ragged_dot(lhs, wg, gs, "bf16"), O.ragged_dot(lhs, wu, gs, "bf16"), 4.0, 25.0,
                            "bf16")
