@@ -257,3 +257,81 @@ def test_unsharded_forward_gate_options(monkeypatch, act, renorm, scaling, dt):
   final, inter = latent_moe_forward(_dev(hidden, dt), W, cfg, act=act, return_intermediates=True)
   wn = {k: to_np(v) for k, v in W.as_dict().items()}
   check_unsharded(f"emulated unsharded {act}", hidden, wn, cfg, dt, act, final, inter)
+
+
+def _launch_free_log(monkeypatch):
+  """Records, for each library call, the real library's own status on the
+  same arguments: where no GPU is present any launch fails with ERR_HIP, so
+  OK means the call returned before launching anything."""
+  from lmoe import _lib
+  real, log = _lib.lib(), []
+  emulated = _emulated_lib.EmulatedLib.__getattr__
+
+  def getattr_(self, name):
+    entry = emulated(self, name)
+    if not name.startswith("lmoe_") or name.endswith("workspace_size"):
+      return entry
+
+    def call(*args):
+      log.append((name, getattr(real, name)(*args)))
+      return entry(*args)
+    return call
+  monkeypatch.setattr(_emulated_lib.EmulatedLib, "__getattr__", getattr_)
+  return log
+
+
+@pytest.mark.skipif(torch.cuda.device_count() > 0, reason="reads the real library's status without a device")
+def test_empty_batch(monkeypatch):
+  """A batch of no tokens through every forward (unsharded, functional
+  single shard with and without the fused gate/up, the prepared layer with
+  bf16 experts and with MXFP4 experts in both modes, stages returned or
+  not): an empty output of the hidden width and the input's dtype, the
+  dispatch of no slots as the oracle gives it at m_padded = 0, and no call
+  that launches a kernel (every entry point returns before its launch on
+  empty sizes)."""
+  from lmoe import _lib, forward
+  from lmoe.config import init_weights
+  from lmoe.workloads import Config5, make_config5
+  _emulated_lib.install(monkeypatch)
+  log = _launch_free_log(monkeypatch)
+  cfg = LatentMoEConfig(hidden_size=64, latent_size=32, intermediate_size=48, num_experts=16, top_k=2,
+                        num_shared_experts=1)
+  want = O.filter_and_pad_to_shard_jittable(np.zeros((0, 2), np.int32), np.zeros((0, 2), np.float32),
+                                            np.zeros((0, 32), np.float32), 2, 16, 0, 4, m_padded=0)
+  outs = []
+  for dt in (torch.float32, torch.bfloat16):
+    W = init_weights(cfg, dtype=dt, device="cpu")
+    h = torch.zeros(0, 64, dtype=dt)
+    final, inter = forward.latent_moe_forward(h, W, cfg, return_intermediates=True)
+    outs.append((final, dt, 64))
+    assert all(v.shape[0] == 0 for k, v in inter.items() if k != "group_sizes")
+    assert not inter["group_sizes"].any()
+    pad = lambda w: torch.cat([w[0:4], torch.zeros_like(w[:1])])
+    for fused in (False, True):
+      final, st = forward.latent_moe_forward_ragged_dot_single_shard_jittable(
+          h, W.router_weight, W.e_score_correction_bias, W.down_proj, pad(W.expert_gate), pad(W.expert_up),
+          pad(W.expert_down), W.norm_scale, W.up_proj, W.shared_gate, W.shared_up, W.shared_down, cfg, 0, 4,
+          fused_gateup=fused, return_stages=True)
+      outs.append((final, dt, 64))
+      for name, a, b in zip(want._fields, st["dispatch"], want):
+        assert np.array_equal(to_np(a), b) and tuple(a.shape) == b.shape, name
+      assert st["dispatch"].slot_pos.numel() == 0
+  assert log and all(rc == _lib.OK for _, rc in log), log
+  for fmt, mode in (("bf16", "lds_dequant"), ("mxfp4", "lds_dequant"), ("mxfp4", "scaled_mfma")):
+    c = Config5(tokens=4, hidden=128, latent=128, intermediate=128, experts=16, top_k=2, local_start=0,
+                local_experts=8)
+    hidden, w, ex = make_config5("cpu", c, fmt)
+    layer = forward.LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                                        e_score_correction_bias=w["e_score_correction_bias"],
+                                        down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                                        local_expert_start=0, local_num_experts=8, expert_format=fmt, experts=ex,
+                                        capacity_factor=c.capacity_factor, mxfp4_mode=mode)
+    log.clear()  # (re-tiling the MXFP4 weights at construction launches)
+    outs.append((layer.forward(hidden[:0]), hidden.dtype, 128))
+    out, st = layer.forward(hidden[:0], return_stages=True)
+    outs.append((out, hidden.dtype, 128))
+    assert st["dispatch"].group_sizes.tolist() == [0] * 9
+    assert all(rc == _lib.OK for _, rc in log), log
+  for out, dt, width in outs:
+    assert tuple(out.shape) == (0, width) and out.dtype == dt
+  assert len(outs) == 12

@@ -243,6 +243,20 @@ def test_local_shard_layer_from_safetensors_checkpoint(gpu_device, tmp_path):
   assert torch.equal(layer2.forward(hidden), layer.forward(hidden))
 
 
+def test_local_shard_layer_empty_batch(gpu_device):
+  """No tokens: an empty (0, hidden) bf16 output and an empty dispatch, with
+  the stages returned or not; every library call returns before its launch
+  on empty sizes, so nothing runs on the device but torch's allocations."""
+  c, hidden, w, experts, layer = _mxfp4_layer(gpu_device, tokens=4)
+  out = layer.forward(hidden[:0])
+  out_st, st = layer.forward(hidden[:0], return_stages=True)
+  torch.cuda.synchronize()
+  for o in (out, out_st):
+    assert tuple(o.shape) == (0, c.hidden) and o.dtype == torch.bfloat16
+  assert st["dispatch"].group_sizes.tolist() == [0] * (c.local_experts + 1)
+  assert st["dispatch"].slot_pos.numel() == 0 and st["shard_out"].shape[0] == 0
+
+
 @pytest.mark.parametrize("tokens", [1, 16, 64])
 def test_local_shard_layer_decode_matches_oracle(gpu_device, tokens):
   """Decode regime (rd.py:553-577: num_tokens 1..128 through the same layer):

@@ -12,6 +12,7 @@ router projection, the stage-returning path); this checks that each
 combination it can choose is one the library takes.  The reference-API
 forwards (unsharded and functional single-shard) are swept the same way
 over the configurations the reference allows."""
+
 import pytest
 import torch
 from hypothesis import HealthCheck, given, settings
@@ -24,8 +25,26 @@ from lmoe.workloads import Config5, make_config5
 NO_GPU = torch.cuda.device_count() == 0
 
 
-def _build(c, fmt, mode):
-  hidden, w, ex = make_config5("cpu", c, fmt)
+def _zero_config5(c, fmt):
+  """``make_config5``'s shapes and dtypes, zero-filled: the recording stand-in
+  computes nothing, so the values do not matter and drawing the random
+  weights would take most of the sweep's time."""
+  bf, u8, L, i2 = torch.bfloat16, torch.uint8, c.local_experts, 2 * c.intermediate
+  z = torch.zeros
+  w = {"router_weight": z(c.hidden, c.experts, dtype=bf), "e_score_correction_bias": z(c.experts),
+       "down_proj": z(c.hidden, c.latent, dtype=bf), "up_proj": z(c.latent, c.hidden, dtype=bf),
+       "norm_scale": torch.ones(c.latent, dtype=bf)}
+  if fmt == "mxfp4":
+    ex = {"gu_packed": z(L + 1, i2, c.latent // 2, dtype=u8), "gu_scale": z(L + 1, i2, c.latent // 32, dtype=u8),
+          "down_packed": z(L + 1, c.latent, c.intermediate // 2, dtype=u8),
+          "down_scale": z(L + 1, c.latent, c.intermediate // 32, dtype=u8)}
+  else:
+    ex = {"gu_nk": z(L + 1, i2, c.latent, dtype=bf), "down_nk": z(L + 1, c.latent, c.intermediate, dtype=bf)}
+  return z(c.tokens, c.hidden, dtype=bf), w, ex
+
+
+def _build(c, fmt, mode, zero_weights=False):
+  hidden, w, ex = (_zero_config5 if zero_weights else lambda c, fmt: make_config5("cpu", c, fmt))(c, fmt)
   layer = forward.LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
                                       e_score_correction_bias=w["e_score_correction_bias"],
                                       down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
@@ -55,9 +74,10 @@ def test_configurations(monkeypatch):
   def run(data):
     pick = lambda xs: data.draw(st.sampled_from(xs))
     e = pick([8, 16, 60, 128, 256])
+    lat, inter = pick([64, 128, 192, 256, 1024, 1088, 2048]), pick([64, 128, 192, 256])
     L = pick([n for n in (1, 4, 15, 16, 60, 128) if n <= e])
     c = Config5(tokens=pick([1, 2, 5, 16, 63, 64, 65, 200, 512]), hidden=pick([64, 128, 256]),
-                latent=pick([64, 128, 192, 256, 1024, 1088, 2048]), intermediate=pick([64, 128, 192, 256]),
+                latent=lat, intermediate=inter,
                 experts=e, top_k=pick([k for k in (1, 2, 4, 8, 16) if k <= e]),
                 local_start=pick(sorted({0, min(3, e - L), e - L})), local_experts=L,
                 capacity_factor=pick([1.0, 2.0, 4.0]))
@@ -65,7 +85,7 @@ def test_configurations(monkeypatch):
     mode = pick(["lds_dequant", "lds_dequant", "scaled_mfma"]) if fmt == "mxfp4" else "lds_dequant"
     stages = pick([False, False, True])
     try:
-      layer, hidden = _build(c, fmt, mode)
+      layer, hidden = _build(c, fmt, mode, zero_weights=True)
     except (ValueError, NotImplementedError):
       stats["refused"] += 1
       return
@@ -108,6 +128,23 @@ def test_scaled_mode_refuses_sizes_it_cannot_quantise():
               local_experts=16)
   with pytest.raises(NotImplementedError, match="multiples of 128"):
     _build(c, "mxfp4", "scaled_mfma")
+
+
+@pytest.mark.parametrize("fmt,mode,error", [("mxfp4", "skinny", NotImplementedError),
+                                            ("mxfp4", "scaled_mfma_fp6", NotImplementedError),
+                                            ("mxfp4", "bogus", NotImplementedError), ("fp8", "lds_dequant", ValueError)])
+def test_layer_refuses_modes_it_cannot_run(fmt, mode, error):
+  """Expert formats and MXFP4 modes the layer has no forward for are refused
+  when it is built (the skinny decode kernel is chosen by size, not by mode;
+  the MXFP6 path has no fused SiTU epilogue for the gate/up GEMM)."""
+  c = Config5(tokens=4, hidden=128, latent=128, intermediate=128, experts=16, top_k=2, local_start=0,
+              local_experts=16)
+  hidden, w, ex = make_config5("cpu", c, "mxfp4" if fmt == "mxfp4" else "bf16")
+  with pytest.raises(error, match="mxfp4_mode" if fmt == "mxfp4" else "expert_format"):
+    forward.LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                                e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
+                                up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=0,
+                                local_num_experts=16, expert_format=fmt, experts=ex, mxfp4_mode=mode)
 
 
 def test_reference_api_forwards(monkeypatch):

@@ -157,6 +157,12 @@ class LocalShardLatentMoE:
     if not (local_num_experts > 0 and 0 <= local_expert_start and local_expert_start + local_num_experts <= e):
       raise ValueError(f"local experts [{local_expert_start}, {local_expert_start + local_num_experts}) "
                        f"outside the {e} experts")
+    if expert_format not in ("bf16", "mxfp4"):
+      raise ValueError(f"expert_format={expert_format!r}: the layer takes 'bf16' or 'mxfp4' experts")
+    if expert_format == "mxfp4" and mxfp4_mode not in ("lds_dequant", "scaled_mfma"):
+      # the skinny decode kernel is chosen by size under "lds_dequant"; the
+      # MXFP6 path has no fused SiTU epilogue for the gate/up GEMM
+      raise NotImplementedError(f"mxfp4_mode={mxfp4_mode!r}: the layer runs 'lds_dequant' or 'scaled_mfma'")
     if expert_format == "mxfp4" and mxfp4_mode.startswith("scaled_mfma") and (
         lat % 128 or config.intermediate_size % 128):
       # the activations of both expert GEMMs are quantised in blocks of 128 along K

@@ -883,12 +883,25 @@ def small_dispatch_supported(t: int, k: int, lat: int, L: int, m_padded: int) ->
   return t * k <= SMALL_DISPATCH_SLOTS and m_padded <= 8192 and L + 1 <= 1024 and lat % 8 == 0
 
 
+def _no_slot_dispatch(t, k, L, lat, rows_dtype, w_dtype, dev, gather_rows=True) -> Dispatch:
+  """m_padded == 0 (an empty batch): no slot is kept, so every output is
+  known without a launch -- zero group sizes and counts, every slot_pos -1,
+  the per-row outputs empty (ref.py:816-868 at m_padded 0)."""
+  empty = lambda dtype, *shape: torch.empty(shape or (0,), dtype=dtype, device=dev)
+  return Dispatch(empty(rows_dtype, 0, lat) if gather_rows else None,
+                  torch.zeros((L + 1,), dtype=torch.int32, device=dev), empty(torch.bool),
+                  torch.zeros((L,), dtype=torch.int32, device=dev), empty(torch.int32), empty(w_dtype),
+                  torch.full((t * k,), -1, dtype=torch.int32, device=dev))
+
+
 def _dispatch_metadata(topk_idx, topk_weight, local_expert_start, L, m_padded, lat):
   _dev(topk_idx, topk_weight)
   if lat is None:
     raise ValueError("dispatch without rows: give x or lat")
   t, k = topk_idx.shape
   dev = topk_idx.device
+  if m_padded == 0:
+    return _no_slot_dispatch(t, k, L, lat, torch.bfloat16, topk_weight.dtype, dev, gather_rows=False)
   group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
   valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
   counts = torch.empty((L,), dtype=torch.int32, device=dev)
@@ -944,6 +957,9 @@ def dispatch_ragged_dot_mxfp4_skinny(topk_idx: torch.Tensor, topk_weight: torch.
   x = _dev_rows(x)
   _dev(topk_idx, topk_weight, w_tiled, s_tiled)
   dev = x.device
+  if m_padded == 0:
+    d = _no_slot_dispatch(t, k, L, lat, torch.bfloat16, topk_weight.dtype, dev, gather_rows=False)
+    return d, torch.empty((0, width), dtype=torch.bfloat16, device=dev)
   group_sizes = torch.empty((L + 1,), dtype=torch.int32, device=dev)
   valid = torch.empty((m_padded,), dtype=torch.bool, device=dev)
   counts = torch.empty((L,), dtype=torch.int32, device=dev)
@@ -988,6 +1004,13 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
     raise ValueError("dispatch with rows: x is required")
   lat = x.shape[-1]
   L = local_num_experts
+  if m_padded == 0:
+    _dev(topk_idx, topk_weight, x)
+    # the dtype the gather would write: bf16 for a row-strided view (judged
+    # by its strides alone, the view having no rows) or skipped padding rows
+    strided = x.stride(-1) != 1 or x.stride(0) != x.shape[-1]
+    rows_dtype = torch.bfloat16 if skip_padding_rows or strided else x.dtype
+    return _no_slot_dispatch(t, k, L, lat, rows_dtype, topk_weight.dtype, x.device)
   small_ok = small_dispatch_supported(t, k, lat, L, m_padded)
   if path == "auto":
     path = "small" if small_ok and x.dtype == torch.bfloat16 and not _row_strided(x) else "sort"
