@@ -145,3 +145,23 @@ def test_router_on_a_row_slice(lib, act):
   r = O.router_from_logits(wide[:, :40], bias, 6, True, 1.0, act)
   assert np.array_equal(to_np(idx), r.topk_idx) and np.array_equal(to_np(w), r.topk_weight)
   assert np.array_equal(to_np(scores), r.scores)
+
+
+@pytest.mark.parametrize("gather_rows", [True, False])
+def test_dispatch_with_no_capacity(lib, gather_rows):
+  """m_padded = 0 with tokens routed (a capacity factor of 0): every slot is
+  dropped -- zero group sizes and counts, every slot_pos -1 -- as the oracle
+  gives it, with no library call."""
+  t, k, L = 6, 2, 4
+  idx = np.stack([RNG.permutation(8)[:k] for _ in range(t)]).astype(np.int32)
+  w = RNG.uniform(size=(t, k)).astype(np.float32)
+  x = O.bf16_round(RNG.standard_normal((t, 16)))
+  want, slot_pos = O.filter_and_pad_to_shard_jittable(idx, w, x, k, 8, 0, L, m_padded=0, return_slot_pos=True)
+  got = ops.dispatch_local(torch.from_numpy(idx), _t(w, "f32"), _t(x), 0, L, 0, gather_rows=gather_rows, lat=16)
+  assert lib.names() == []
+  for name, a, b in zip(want._fields, got, want):
+    if a is None:
+      assert name == "sorted_tokens" and not gather_rows
+      continue
+    assert tuple(a.shape) == b.shape and np.array_equal(to_np(a), b), name
+  assert np.array_equal(to_np(got.slot_pos), slot_pos)
