@@ -335,3 +335,43 @@ def test_empty_batch(monkeypatch):
   for out, dt, width in outs:
     assert tuple(out.shape) == (0, width) and out.dtype == dt
   assert len(outs) == 12
+
+
+def test_no_capacity(monkeypatch):
+  """capacity_factor 0: m_padded is 0 and every slot is dropped (ref.py:825-826
+  rounds 0 up to 0), so the routed output is zero and the output is the
+  shared experts' alone -- the oracle's single-shard forward at the same
+  capacity, for the functional forward (fused gate/up or not) and the
+  prepared layer with bf16 or MXFP4 experts."""
+  from lmoe import forward
+  from lmoe.config import init_weights
+  from lmoe.workloads import Config5, make_config5
+  _emulated_lib.install(monkeypatch)
+  cfg = LatentMoEConfig(hidden_size=64, latent_size=32, intermediate_size=48, num_experts=16, top_k=2,
+                        num_shared_experts=1)
+  W = init_weights(cfg, dtype=torch.bfloat16, device="cpu")
+  h = torch.randn(5, 64, generator=torch.Generator().manual_seed(0)).bfloat16()
+  pad = lambda w: torch.cat([w[0:4], torch.zeros_like(w[:1])])
+  wn = {k: to_np(v) for k, v in vars(W).items()}
+  want, _ = O.single_shard_forward(to_np(h), wn, to_np(pad(W.expert_gate)), to_np(pad(W.expert_up)),
+                                   to_np(pad(W.expert_down)), cfg, "bf16", 0, 4, capacity_factor=0.0)
+  assert np.any(want != 0)
+  for fused in (False, True):
+    got, st = forward.latent_moe_forward_ragged_dot_single_shard_jittable(
+        h, W.router_weight, W.e_score_correction_bias, W.down_proj, pad(W.expert_gate), pad(W.expert_up),
+        pad(W.expert_down), W.norm_scale, W.up_proj, W.shared_gate, W.shared_up, W.shared_down, cfg, 0, 4,
+        capacity_factor=0.0, fused_gateup=fused, return_stages=True)
+    assert not st["routed_out"].any() and st["shard_out"].shape[0] == 0
+    assert np.array_equal(to_np(got), want)
+  for fmt in ("bf16", "mxfp4"):
+    c = Config5(tokens=4, hidden=128, latent=128, intermediate=128, experts=16, top_k=2, local_start=0,
+                local_experts=8, capacity_factor=0.0)
+    hidden, w, ex = make_config5("cpu", c, fmt)
+    layer = forward.LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                                        e_score_correction_bias=w["e_score_correction_bias"],
+                                        down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                                        local_expert_start=0, local_num_experts=8, expert_format=fmt, experts=ex,
+                                        capacity_factor=0.0)
+    out, st = layer.forward(hidden, return_stages=True)
+    assert torch.equal(layer.forward(hidden), out)
+    assert tuple(out.shape) == (4, 128) and not out.any() and not st["routed_out"].any()

@@ -1005,7 +1005,8 @@ def dispatch_local(topk_idx: torch.Tensor, topk_weight: torch.Tensor, x: torch.T
   lat = x.shape[-1]
   L = local_num_experts
   if m_padded == 0:
-    _dev(topk_idx, topk_weight, x)
+    _dev(topk_idx, topk_weight)
+    _dev_rows(x)
     # the dtype the gather would write: bf16 for a row-strided view (judged
     # by its strides alone, the view having no rows) or skipped padding rows
     strided = x.stride(-1) != 1 or x.stride(0) != x.shape[-1]
@@ -1138,8 +1139,10 @@ def _combine_shard_contribution(routed_out: torch.Tensor, shard_out: torch.Tenso
 def _check_slots(shard_out, slot_pos, weights, num_tokens, top_k, mode):
   """The slot combine reads T*k slot positions, T*k weights (slot_sum) or one
   weight per shard row (scatter_add), and at least one shard row (dropped
-  slots re-read row 0)."""
-  if shard_out.dim() != 2 or (num_tokens > 0 and shard_out.shape[0] == 0):
+  slots re-read row 0).  In scatter_add mode a shard of no rows (every slot
+  dropped, m_padded == 0) adds nothing and is combined without a launch by
+  the callers; slot_sum keeps every slot, so its rows cannot be missing."""
+  if shard_out.dim() != 2 or (mode != "scatter_add" and num_tokens * top_k > 0 and shard_out.shape[0] == 0):
     raise ValueError(f"shard_out {tuple(shard_out.shape)}: want (m >= 1, lat)")
   if slot_pos.dtype != torch.int32 or slot_pos.numel() != num_tokens * top_k:
     raise ValueError(f"slot_pos must be int32 with T*k = {num_tokens * top_k} entries, got "
@@ -1172,6 +1175,8 @@ def combine_slots(shard_out: torch.Tensor, slot_pos: torch.Tensor, weights: torc
     m = _lib.COMBINE_SLOT_SUM
   else:
     raise ValueError(mode)
+  if shard_out.shape[0] == 0:  # no shard rows (no slots, or every one dropped): nothing to add
+    return out if mode == "scatter_add" else out.zero_()
   check(lib().lmoe_combine_slots(_p(shard_out), _dt(shard_out), _p(slot_pos), _p(weights),
                                  _dt(weights), num_tokens, top_k, lat, m, _p(out), _dt(out),
                                  _stream()), "combine_slots")
@@ -1191,6 +1196,10 @@ def combine_slots_rms_norm(shard_out: torch.Tensor, slot_pos: torch.Tensor, weig
     raise ValueError(f"norm_scale has {norm_scale.numel()} entries for {lat} columns")
   dt = out_dtype or shard_out.dtype
   m = {"scatter_add": _lib.COMBINE_SCATTER_ADD, "slot_sum": _lib.COMBINE_SLOT_SUM}[mode]
+  if shard_out.shape[0] == 0:  # no shard rows: the routed rows stay zero
+    routed = torch.zeros((num_tokens, lat), dtype=dt, device=shard_out.device)
+    normed = _rms_norm(routed, norm_scale.to(dt).contiguous(), eps)
+    return (normed, routed) if return_routed else normed
   normed = torch.empty((num_tokens, lat), dtype=dt, device=shard_out.device)
   routed = torch.empty_like(normed) if return_routed else None
   check(lib().lmoe_combine_slots_rms_norm(_p(shard_out), _dt(shard_out), _p(slot_pos), _p(weights), _dt(weights),
