@@ -375,3 +375,30 @@ def test_no_capacity(monkeypatch):
     out, st = layer.forward(hidden, return_stages=True)
     assert torch.equal(layer.forward(hidden), out)
     assert tuple(out.shape) == (4, 128) and not out.any() and not st["routed_out"].any()
+
+
+@pytest.mark.parametrize("tokens", [16, 200])
+def test_local_shard_layer_gate_options(monkeypatch, tokens):
+  """The prepared MXFP4 layer with the softmax gate, no renormalisation and a
+  routed scaling factor (ref.py:340-361) at a decode size (the one-launch
+  router projection and fused dispatch) and a prefill size (gathered rows),
+  stages returned and not: against the oracle's single-shard forward with the
+  same options."""
+  import dataclasses
+  from lmoe.forward import LocalShardLatentMoE
+  lib = _emulated_lib.install(monkeypatch)
+  c, hidden, w, experts, _ = _mxfp4_layer(tokens)
+  cfg = dataclasses.replace(c.config(), moe_renormalize=False, routed_scaling_factor=2.5)
+  layer = LocalShardLatentMoE(cfg, router_weight=w["router_weight"], e_score_correction_bias=w["e_score_correction_bias"],
+                              down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                              local_expert_start=c.local_start, local_num_experts=c.local_experts,
+                              expert_format="mxfp4", experts=experts, capacity_factor=c.capacity_factor,
+                              act="softmax")
+  out = layer.forward(hidden)
+  assert "lmoe_router_topk_proj" in lib.names()
+  out_st, st = layer.forward(hidden, return_stages=True)
+  assert torch.equal(out, out_st)
+  gate, up, down = _dequantized_shard(c, experts)
+  wn = {k: to_np(v) for k, v in w.items()}
+  check_single_shard(f"emulated softmax layer T={tokens}", to_np(hidden), wn, gate, up, down, cfg, "bf16",
+                     c.local_start, c.local_experts, c.capacity_factor, False, out, st, act="softmax")

@@ -243,6 +243,30 @@ def test_local_shard_layer_from_safetensors_checkpoint(gpu_device, tmp_path):
   assert torch.equal(layer2.forward(hidden), layer.forward(hidden))
 
 
+@pytest.mark.parametrize("tokens", [16, 512])
+def test_local_shard_layer_gate_options(gpu_device, tokens):
+  """The reduced config-5 layer with the softmax gate, no renormalisation and
+  a routed scaling factor (ref.py:340-361), at a decode size (router
+  projection and fused dispatch) and a prefill size (gathered rows): stage by
+  stage against the oracle's single-shard forward with the same options."""
+  import dataclasses
+  from lmoe.forward import LocalShardLatentMoE
+  c, hidden, w, experts, _ = _mxfp4_layer(gpu_device, tokens=tokens)
+  cfg = dataclasses.replace(c.config(), moe_renormalize=False, routed_scaling_factor=2.5)
+  layer = LocalShardLatentMoE(cfg, router_weight=w["router_weight"], e_score_correction_bias=w["e_score_correction_bias"],
+                              down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+                              local_expert_start=c.local_start, local_num_experts=c.local_experts,
+                              expert_format="mxfp4", experts=experts, capacity_factor=c.capacity_factor,
+                              act="softmax")
+  out = layer.forward(hidden)
+  out_st, gs = layer.forward(hidden, return_stages=True)
+  assert torch.equal(out, out_st)
+  gate, up, down = _dequantized_shard(c, experts)
+  wn = {k: to_np(v) for k, v in w.items()}
+  check_single_shard(f"layer softmax T={tokens}", to_np(hidden), wn, gate, up, down, cfg, "bf16", c.local_start,
+                     c.local_experts, c.capacity_factor, False, out, gs, act="softmax")
+
+
 def test_local_shard_layer_empty_batch(gpu_device):
   """No tokens: an empty (0, hidden) bf16 output and an empty dispatch, with
   the stages returned or not; every library call returns before its launch
