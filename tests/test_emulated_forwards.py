@@ -402,3 +402,37 @@ def test_local_shard_layer_gate_options(monkeypatch, tokens):
   wn = {k: to_np(v) for k, v in w.items()}
   check_single_shard(f"emulated softmax layer T={tokens}", to_np(hidden), wn, gate, up, down, cfg, "bf16",
                      c.local_start, c.local_experts, c.capacity_factor, False, out, st, act="softmax")
+
+
+@pytest.mark.parametrize("tokens", [16, 200])
+def test_local_shard_layer_with_shared_experts(monkeypatch, tokens):
+  """The prepared MXFP4 layer with its shared-expert MLP (ref.py:428-433,
+  given in the layout its docstring states) against the oracle's
+  single-shard forward with the shared experts included; a shared weight of
+  the wrong shape is refused when the layer is built."""
+  from lmoe import ops
+  from lmoe.forward import LocalShardLatentMoE
+  _emulated_lib.install(monkeypatch)
+  c, hidden, w, experts, _ = _mxfp4_layer(tokens)
+  rng = np.random.default_rng(tokens)
+  si = 2 * c.intermediate
+  sh = {k: O.bf16_round(rng.standard_normal(s) * 0.05) for k, s in
+        (("shared_gate", (c.hidden, si)), ("shared_up", (c.hidden, si)), ("shared_down", (si, c.hidden)))}
+  t = {k: _dev(v, "bf16") for k, v in sh.items()}
+  shared = {"gu_nk": ops.prefuse_gateup_weights_gnk(t["shared_gate"][None], t["shared_up"][None]),
+            "down_nk": t["shared_down"].t().contiguous()}
+  kw = dict(router_weight=w["router_weight"], e_score_correction_bias=w["e_score_correction_bias"],
+            down_proj=w["down_proj"], up_proj=w["up_proj"], norm_scale=w["norm_scale"],
+            local_expert_start=c.local_start, local_num_experts=c.local_experts, expert_format="mxfp4",
+            experts=experts, capacity_factor=c.capacity_factor)
+  layer = LocalShardLatentMoE(c.config(), shared=shared, **kw)
+  out = layer.forward(hidden)
+  out_st, st = layer.forward(hidden, return_stages=True)
+  assert torch.equal(out, out_st)
+  gate, up, down = _dequantized_shard(c, experts)
+  wn = {k: to_np(v) for k, v in w.items()} | sh
+  cfg = c.config()
+  check_single_shard(f"emulated layer with shared experts T={tokens}", to_np(hidden), wn, gate, up, down, cfg,
+                     "bf16", c.local_start, c.local_experts, c.capacity_factor, True, out, st)
+  with pytest.raises(ValueError, match="shared"):
+    LocalShardLatentMoE(c.config(), shared={"gu_nk": shared["gu_nk"], "down_nk": shared["down_nk"].t()}, **kw)

@@ -141,6 +141,11 @@ class LocalShardLatentMoE:
   router logits GEMM, down-projection GEMM, top-k, dispatch, fused gate/up +
   SiTU GEMM, down GEMM, combine, RMSNorm, up-projection GEMM (+ the shared
   expert MLP when given).
+
+  ``shared``: the shared-expert MLP (ref.py:428-433) as {"gu_nk": (1, 2*SI,
+  H) [gate | up] k-contiguous, "down_nk": (H, SI)}, i.e.
+  ``ops.prefuse_gateup_weights_gnk(shared_gate[None], shared_up[None])`` and
+  ``shared_down.t().contiguous()`` from the reference-layout weights.
   """
 
   def __init__(self, config: LatentMoEConfig, *, router_weight, e_score_correction_bias, down_proj,
@@ -157,6 +162,12 @@ class LocalShardLatentMoE:
     if not (local_num_experts > 0 and 0 <= local_expert_start and local_expert_start + local_num_experts <= e):
       raise ValueError(f"local experts [{local_expert_start}, {local_expert_start + local_num_experts}) "
                        f"outside the {e} experts")
+    if shared is not None:
+      gu, dn = shared.get("gu_nk"), shared.get("down_nk")
+      if (gu is None or dn is None or gu.dim() != 3 or gu.shape[0] != 1 or gu.shape[2] != h or gu.shape[1] % 2
+          or tuple(dn.shape) != (h, gu.shape[1] // 2)):
+        raise ValueError(f"shared: want gu_nk (1, 2*SI, {h}) and down_nk ({h}, SI), got "
+                         f"{None if gu is None else tuple(gu.shape)} / {None if dn is None else tuple(dn.shape)}")
     if expert_format not in ("bf16", "mxfp4"):
       raise ValueError(f"expert_format={expert_format!r}: the layer takes 'bf16' or 'mxfp4' experts")
     if expert_format == "mxfp4" and mxfp4_mode not in ("lds_dequant", "scaled_mfma"):
