@@ -267,6 +267,35 @@ def test_local_shard_layer_gate_options(gpu_device, tokens):
                      c.local_experts, c.capacity_factor, False, out, gs, act="softmax")
 
 
+@pytest.mark.parametrize("tokens", [16, 512])
+def test_local_shard_layer_with_shared_experts(gpu_device, tokens):
+  """The reduced config-5 layer with a shared-expert MLP (ref.py:428-433) in
+  the layout the layer states, at a decode and a prefill size: stage by stage
+  against the oracle's single-shard forward with the shared experts."""
+  from lmoe import ops
+  from lmoe.forward import LocalShardLatentMoE
+  c, hidden, w, experts, _ = _mxfp4_layer(gpu_device, tokens=tokens)
+  rng = np.random.default_rng(tokens)
+  si = c.intermediate
+  sh = {k: O.bf16_round(rng.standard_normal(s) * 0.05) for k, s in
+        (("shared_gate", (c.hidden, si)), ("shared_up", (c.hidden, si)), ("shared_down", (si, c.hidden)))}
+  t = {k: to_dev(v, "bf16") for k, v in sh.items()}
+  shared = {"gu_nk": ops.prefuse_gateup_weights_gnk(t["shared_gate"][None], t["shared_up"][None]),
+            "down_nk": t["shared_down"].t().contiguous()}
+  layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
+                              e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
+                              up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,
+                              local_num_experts=c.local_experts, expert_format="mxfp4", experts=experts,
+                              capacity_factor=c.capacity_factor, shared=shared)
+  out = layer.forward(hidden)
+  out_st, gs = layer.forward(hidden, return_stages=True)
+  assert torch.equal(out, out_st)
+  gate, up, down = _dequantized_shard(c, experts)
+  wn = {k: to_np(v) for k, v in w.items()} | sh
+  check_single_shard(f"layer with shared experts T={tokens}", to_np(hidden), wn, gate, up, down, c.config(), "bf16",
+                     c.local_start, c.local_experts, c.capacity_factor, True, out, gs)
+
+
 def test_local_shard_layer_empty_batch(gpu_device):
   """No tokens: an empty (0, hidden) bf16 output and an empty dispatch, with
   the stages returned or not; every library call returns before its launch
