@@ -130,6 +130,7 @@ def _mxfp4_layer(tokens, mode="lds_dequant"):
   for key in ("gu_scale", "down_scale"):
     experts[key] = experts[key] + 4
   w["down_proj"] = w["down_proj"] * 8
+  w["norm_scale"] = _dev(O.bf16_round(np.random.default_rng(7).uniform(0.5, 2.0, c.latent)), "bf16")
   layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
                               e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
                               up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,

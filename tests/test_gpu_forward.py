@@ -130,6 +130,9 @@ def _mxfp4_layer(dev, tokens=512):
   c = Config5(tokens=tokens, hidden=512, latent=256, intermediate=256, experts=128, top_k=16,
               local_start=16, local_experts=16)
   hidden, w, experts = make_config5(dev, c, "mxfp4")
+  # a norm scale other than the reference's unit init, so that a norm whose
+  # scale went unapplied would show
+  w["norm_scale"] = to_dev(O.bf16_round(np.random.default_rng(7).uniform(0.5, 2.0, c.latent)), "bf16", device=dev)
   layer = LocalShardLatentMoE(c.config(), router_weight=w["router_weight"],
                               e_score_correction_bias=w["e_score_correction_bias"], down_proj=w["down_proj"],
                               up_proj=w["up_proj"], norm_scale=w["norm_scale"], local_expert_start=c.local_start,
