@@ -356,6 +356,9 @@ int lmoe_router_topk_proj(const float* logits, int64_t ld, const float* bias, in
  *   padded_token_idx (m_padded,) int32 (-1 on padding), padded_w (m_padded,) w_dtype
  *   slot_pos (T*k,) int32 or NULL: sorted row of each (token, slot), -1 if not kept
  * T, k, T*k and m_padded < 2^31, L + 1 <= 12288, local_start + L < 2^31.
+ * m_padded == 0 allows a NULL sorted_tokens; the other outputs must still be
+ * non-NULL (a caller with no slots to keep can form the result itself: zero
+ * group sizes and counts, every slot_pos -1).
  * Workspace: lmoe_dispatch_workspace_size(T, k, L) bytes, no initialisation needed
  * (-1 for sizes the dispatch refuses).
  */
