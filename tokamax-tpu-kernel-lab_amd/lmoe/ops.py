@@ -885,9 +885,9 @@ def small_dispatch_supported(t: int, k: int, lat: int, L: int, m_padded: int) ->
 
 def _no_slot_dispatch(t, k, L, lat, rows_dtype, w_dtype, dev, gather_rows=True) -> Dispatch:
   """m_padded == 0 (an empty batch, or a capacity factor of 0): no slot is
-  kept, so every output is
-  known without a launch -- zero group sizes and counts, every slot_pos -1,
-  the per-row outputs empty (ref.py:816-868 at m_padded 0)."""
+  kept, so every output is known without a launch -- zero group sizes and
+  counts, every slot_pos -1, the per-row outputs empty (ref.py:816-868 at
+  m_padded 0)."""
   empty = lambda dtype, *shape: torch.empty(shape or (0,), dtype=dtype, device=dev)
   return Dispatch(empty(rows_dtype, 0, lat) if gather_rows else None,
                   torch.zeros((L + 1,), dtype=torch.int32, device=dev), empty(torch.bool),
