@@ -1,7 +1,8 @@
 """The local-shard layer across its configuration space, on the CPU: hidden,
 latent and intermediate sizes, expert count, top-k, local expert range,
-token count (decode and prefill), capacity factor, expert format (MXFP4 or
-bf16), MXFP4 mode and stage return drawn by hypothesis.  A configuration the
+token count (none, decode and prefill), capacity factor (0 included),
+expert format (MXFP4 or bf16), MXFP4 mode and stage return drawn by
+hypothesis.  A configuration the
 layer cannot run is refused when it is built (ValueError /
 NotImplementedError); one it builds runs its forward against the recording
 stand-in library without raising, every buffer it hands the library holds
@@ -76,11 +77,11 @@ def test_configurations(monkeypatch):
     e = pick([8, 16, 60, 128, 256])
     lat, inter = pick([64, 128, 192, 256, 1024, 1088, 2048]), pick([64, 128, 192, 256])
     L = pick([n for n in (1, 4, 15, 16, 60, 128) if n <= e])
-    c = Config5(tokens=pick([1, 2, 5, 16, 63, 64, 65, 200, 512]), hidden=pick([64, 128, 256]),
+    c = Config5(tokens=pick([0, 1, 2, 5, 16, 63, 64, 65, 200, 512]), hidden=pick([64, 128, 256]),
                 latent=lat, intermediate=inter,
                 experts=e, top_k=pick([k for k in (1, 2, 4, 8, 16) if k <= e]),
                 local_start=pick(sorted({0, min(3, e - L), e - L})), local_experts=L,
-                capacity_factor=pick([1.0, 2.0, 4.0]))
+                capacity_factor=pick([0.0, 1.0, 2.0, 4.0]))
     fmt = pick(["mxfp4", "mxfp4", "bf16"])
     mode = pick(["lds_dequant", "lds_dequant", "scaled_mfma"]) if fmt == "mxfp4" else "lds_dequant"
     stages = pick([False, False, True])
@@ -171,7 +172,7 @@ def test_reference_api_forwards(monkeypatch):
                           moe_renormalize=pick([True, False]), routed_scaling_factor=pick([1.0, 2.5]))
     dt = pick([torch.float32, torch.bfloat16])
     W = init_weights(cfg, dtype=dt, device="cpu")
-    h = torch.zeros(pick([1, 2, 5, 20, 64, 300]), cfg.hidden_size, dtype=dt)
+    h = torch.zeros(pick([0, 1, 2, 5, 20, 64, 300]), cfg.hidden_size, dtype=dt)
     act = pick(["sigmoid", "softmax"])
     log.clear()
     if pick(["unsharded", "shard"]) == "unsharded":
@@ -183,7 +184,7 @@ def test_reference_api_forwards(monkeypatch):
       forward.latent_moe_forward_ragged_dot_single_shard_jittable(
           h, W.router_weight, W.e_score_correction_bias, W.down_proj, pad(W.expert_gate), pad(W.expert_up),
           pad(W.expert_down), W.norm_scale, W.up_proj, W.shared_gate if cfg.num_shared_experts else None,
-          W.shared_up, W.shared_down, cfg, start, L, capacity_factor=pick([1.0, 2.0]), act=act,
+          W.shared_up, W.shared_down, cfg, start, L, capacity_factor=pick([0.0, 1.0, 2.0]), act=act,
           fused_gateup=pick([False, True]))
     X.check_extents(log.calls)
     if NO_GPU:
