@@ -32,3 +32,17 @@ def test_quoted_paths_exist(doc):
       if int(hi or lo) > n:
         bad.append(f"{path}:{lo}{'-' + hi if hi else ''} (file has {n} lines)")
   assert not bad, bad
+
+
+def test_profiles_name_their_commands():
+  """Each committed profile summary gives the command that made it, which
+  runs committed files only (no working-folder script)."""
+  folder = os.path.join(ROOT, "profiles")
+  names = sorted(os.listdir(folder))
+  assert names
+  for name in names:
+    text = open(os.path.join(folder, name), errors="replace").read()
+    assert re.search(r"rocprofv3|python", text), f"{name}: no command"
+    assert "_work/" not in text, f"{name}: names a working-folder file"
+    for script in re.findall(r"python3? (?:-u )?([\w./-]+\.py)", text):
+      assert os.path.exists(os.path.join(ROOT, script)), f"{name}: {script} is not in the tree"
