@@ -141,7 +141,7 @@ def test_header_builds_a_c_host_that_links_and_runs(tmp_path, compiler, flags):
 
 
 def test_integration_bindings_match_the_library():
-  """The ctypes bindings INTEGRATION.md shows a maintainer (argtypes lists and
+  """The ctypes bindings the integration guide shows a maintainer (argtypes lists and
   example calls) agree with the library's signatures, so copying them binds
   the entry points correctly."""
   import os

@@ -1,7 +1,7 @@
-"""The documents point at files of this repository that exist: every path
-under profiles/, tests/, include/, oracle/ or the package that DESIGN.md,
-README.md or INTEGRATION.md quote in backticks names a file or folder of the
-tree, and a quoted line number lies inside that file."""
+"""The documents at the repository root point at files that exist: every
+path under profiles/, tests/, include/, oracle/ or the package that they
+quote in backticks names a file or folder of the tree, and a quoted line
+number lies inside that file."""
 import os
 import re
 
@@ -11,7 +11,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 DOCS = ("DESIGN.md", "README.md", "INTEGRATION.md")
 PATH = re.compile(r"`((?:profiles|tests|include|oracle|tokamax-tpu-kernel-lab_amd)/[\w./-]+?)(?::(\d+)(?:-(\d+))?)?`")
 # named as what is absent: the reference has no C source to build there
-ABSENT_BY_DESIGN = {"oracle/_ref"}
+ABSENT_ON_PURPOSE = {"oracle/_ref"}
 
 
 @pytest.mark.parametrize("doc", DOCS)
@@ -23,7 +23,7 @@ def test_quoted_paths_exist(doc):
   for path, lo, hi in quoted:
     path = path.rstrip(".")
     full = os.path.join(ROOT, path)
-    if path in ABSENT_BY_DESIGN:
+    if path in ABSENT_ON_PURPOSE:
       continue
     if not os.path.exists(full):
       bad.append(path)
